@@ -1,0 +1,241 @@
+"""Benchmark of the q4 weight path on one MI355X.
+
+    python bench.py [--steps K] [--warmup W] [--gpus 1] [--no-cpu] [--quick]
+
+Headline (``value``): q4 decode GEMV HBM GB/s at the task's config 1,
+x bf16[1,3072] . W q4[8192,3072]^T, over ``--copies`` distinct weight copies
+(48 x 14.2 MB = 680 MB, larger than the 256 MB MALL), so every launch streams
+its weights from HBM. One step = one pass over all copies (48 launches),
+replayed as one HIP graph; event timing on the device's stream brackets the K
+timed steps. Algorithmic bytes per launch: 12,582,912 (nibbles) + 1,572,864
+(scales + biases) + 6,144 (x) + 16,384 (y) = 14,178,304.
+
+Secondary lines (same method): the LM-head GEMV (N=128256, K=3072), the q4
+embedding gather at B=4096 and the two config-3 prefill GEMMs.
+
+cpu_baseline: the reference arithmetic (oracle/liboracle.so: fp32 dequant,
+sequential-k fp32 accumulation, bf16 RNE) on the config-1 GEMV, on this
+host's cores, for a bounded number of calls.
+"""
+from __future__ import annotations
+
+import argparse
+import ctypes
+import json
+import os
+import platform
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+from foundry_amd import _lib, synth  # noqa: E402
+from foundry_amd.device import HipDevice  # noqa: E402
+
+METRIC = "q4 GEMV HBM GB/s (% of peak); decode tok/s, Llama-3.2-3B-shape q4, 1 GPU"
+HBM_PEAK_GBS = 8000.0
+BF16_PEAK_TFLOPS = 2500.0
+
+
+def gemv_bytes(m: int, n: int, k: int) -> int:
+    return n * k // 2 + 2 * 2 * n * (k // 64) + 2 * m * k + 2 * m * n
+
+
+def embed_bytes(b: int, k: int) -> int:
+    # per id: packed row, its scales and biases, the id, the bf16 row written
+    return b * (k // 2 + 2 * 2 * (k // 64) + 4 + 2 * k)
+
+
+class Weights:
+    """Device copies of one q4 weight shape, each from its own seed."""
+
+    def __init__(self, dev: HipDevice, n: int, k: int, copies: int, seed: int):
+        self.n, self.k = n, k
+        self.ptrs = []
+        self._keep = []
+        base = synth.q4_weights(seed, n, k)
+        for c in range(copies):
+            # distinct bytes per copy: xor the packed words with a per-copy pattern
+            wq = base[0] ^ np.uint32((0x9E3779B9 * (c + 1)) & 0xFFFFFFFF) if c else base[0]
+            arrs = (np.ascontiguousarray(wq), base[1], base[2])
+            sts = [dev.storage_from_bytes(a.tobytes()) for a in arrs]
+            self._keep.append(sts)
+            self.ptrs.append(tuple(st.ptr for st in sts))
+
+
+def q4_matmul(dev, x_ptr, m, k, w_ptrs, n, y_ptr, y_dtype=_lib.BF16):
+    _lib.call("fh_q4_matmul", dev.handle, ctypes.c_void_p(x_ptr), m, k, k,
+              ctypes.c_void_p(w_ptrs[0]), ctypes.c_void_p(w_ptrs[1]), ctypes.c_void_p(w_ptrs[2]),
+              n, 64, ctypes.c_void_p(y_ptr), y_dtype)
+
+
+def timed_graph(dev: HipDevice, enqueue, steps: int, warmup: int) -> float:
+    """Captures enqueue() as one graph; returns ms per replay over `steps`."""
+    dev.capture_begin()
+    enqueue()
+    graph = dev.capture_end()
+    for _ in range(warmup):
+        graph.launch()
+    dev.synchronize()
+    dev.timer_begin()
+    for _ in range(steps):
+        graph.launch()
+    ms = dev.timer_end()
+    dev.synchronize()
+    return ms / steps
+
+
+def bench_gemv(dev, n, k, copies, steps, warmup, seed):
+    w = Weights(dev, n, k, copies, seed)
+    x = dev.storage_from_bytes(synth.bf16_normal(seed + 1, (1, k)).tobytes())
+    y = dev.empty(2 * n)
+
+    def enqueue():
+        for p in w.ptrs:
+            q4_matmul(dev, x.ptr, 1, k, p, n, y.ptr)
+
+    ms_step = timed_graph(dev, enqueue, steps, warmup)
+    per_launch_ms = ms_step / copies
+    gbs = gemv_bytes(1, n, k) / (per_launch_ms * 1e-3) / 1e9
+    return {"n": n, "k": k, "copies": copies, "weight_bytes_total": copies * gemv_bytes(1, n, k),
+            "us_per_launch": per_launch_ms * 1e3, "GB_per_s": gbs, "frac_hbm_peak": gbs / HBM_PEAK_GBS,
+            "ms_per_step": ms_step}
+
+
+def bench_embed(dev, batch, steps, warmup, seed):
+    rows, k = 128256, 3072
+    wq, s, b = synth.q4_weights(seed, rows, k)
+    sts = [dev.storage_from_bytes(a.tobytes()) for a in (wq, s, b)]
+    ids = dev.storage_from_bytes(synth.token_ids(seed, batch, rows).tobytes())
+    out = dev.empty(batch * k * 2)
+    reps = 8
+
+    def enqueue():
+        for _ in range(reps):
+            _lib.call("fh_q4_embed", dev.handle, *[ctypes.c_void_p(st.ptr) for st in sts], rows, k, 64,
+                      ctypes.c_void_p(ids.ptr), batch, ctypes.c_void_p(out.ptr))
+
+    ms = timed_graph(dev, enqueue, steps, warmup) / reps
+    gbs = embed_bytes(batch, k) / (ms * 1e-3) / 1e9
+    return {"batch": batch, "us_per_launch": ms * 1e3, "GB_per_s": gbs, "frac_hbm_peak": gbs / HBM_PEAK_GBS,
+            "note": "table rows re-read across repeats may hit L2/MALL"}
+
+
+def bench_gemm(dev, m, n, k, steps, warmup, seed):
+    w = Weights(dev, n, k, 1, seed)
+    x = dev.storage_from_bytes(synth.bf16_normal(seed + 1, (m, k)).tobytes())
+    y = dev.empty(2 * m * n)
+    reps = 4
+
+    def enqueue():
+        for _ in range(reps):
+            q4_matmul(dev, x.ptr, m, k, w.ptrs[0], n, y.ptr)
+
+    ms = timed_graph(dev, enqueue, steps, warmup) / reps
+    tflops = 2.0 * m * n * k / (ms * 1e-3) / 1e12
+    return {"m": m, "n": n, "k": k, "us_per_launch": ms * 1e3, "TFLOP_per_s": tflops,
+            "frac_bf16_peak": tflops / BF16_PEAK_TFLOPS}
+
+
+def cpu_baseline(seconds: float = 12.0):
+    """Reference arithmetic of the config-1 GEMV on the host (oracle)."""
+    import oracle as O  # checker only: the bench's CPU baseline leg
+
+    n, k = 8192, 3072
+    wq, s, b = synth.q4_weights(1, n, k)
+    x = synth.bf16_normal(2, (1, k))
+    out = {}
+    cores = os.cpu_count() or 1
+    for label, threads, budget in (("1_thread", 1, seconds * 0.5), ("all_cores", cores, seconds * 0.5)):
+        calls, t0 = 0, time.perf_counter()
+        while True:
+            O.q4_linear(x, wq, s, b, threads=threads)
+            calls += 1
+            el = time.perf_counter() - t0
+            if el >= budget:
+                break
+        ms = el / calls * 1e3
+        out[label] = {"threads": threads, "calls": calls, "ms_per_call": ms,
+                      "GB_per_s": gemv_bytes(1, n, k) / (ms * 1e-3) / 1e9}
+    cpu = platform.processor() or ""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    cpu = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return out, cpu
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--copies", type=int, default=48)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--quick", action="store_true", help="headline only, no secondary lines")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not supported "
+              "(the q4 path has no multi-GPU form here)", file=sys.stderr)
+        return 2
+
+    dev = HipDevice(0)
+    head = bench_gemv(dev, 8192, 3072, args.copies, args.steps, args.warmup, seed=1)
+    print(f"[bench] gemv 8192x3072: {head['us_per_launch']:.2f} us/launch, {head['GB_per_s']:.0f} GB/s", flush=True)
+    secondary = {}
+    if not args.quick:
+        secondary["lm_head_gemv"] = bench_gemv(dev, 128256, 3072, 3, max(5, args.steps // 5), 2, seed=3)
+        print(f"[bench] lm head: {secondary['lm_head_gemv']['GB_per_s']:.0f} GB/s", flush=True)
+        secondary["embed_b4096"] = bench_embed(dev, 4096, max(5, args.steps // 5), 2, seed=5)
+        secondary["embed_b1"] = bench_embed(dev, 1, max(5, args.steps // 5), 2, seed=5)
+        print(f"[bench] embed: {secondary['embed_b4096']['GB_per_s']:.0f} GB/s", flush=True)
+        secondary["gemm_gate_up"] = bench_gemm(dev, 2048, 8192, 3072, max(5, args.steps // 5), 2, seed=7)
+        secondary["gemm_down"] = bench_gemm(dev, 2048, 3072, 8192, max(5, args.steps // 5), 2, seed=9)
+        print(f"[bench] gemm: {secondary['gemm_gate_up']['TFLOP_per_s']:.0f} TFLOP/s", flush=True)
+    dev.close()
+
+    cpu = None
+    if not args.no_cpu:
+        base, model = cpu_baseline()
+        cpu = {"value": base["1_thread"]["GB_per_s"], "unit": "GB/s", "cores": 1, "kind": "port",
+               "sample": (f"config-1 GEMV x[1,3072].W[8192,3072]^T, reference arithmetic "
+                          f"(oracle/liboracle.so), {base['1_thread']['calls']} calls single-threaded; "
+                          f"all {base['all_cores']['threads']} cores: {base['all_cores']['GB_per_s']:.2f} GB/s"),
+               "cpu_model": model, "all_cores": base["all_cores"]}
+
+    per_launch_bytes = gemv_bytes(1, 8192, 3072)
+    line = {
+        "metric": METRIC,
+        "value": round(head["GB_per_s"], 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": head["ms_per_step"],
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "u4 weights x bf16 activations, fp32 accumulate",
+        "data": "synthetic (SplitMix64-seeded, task config distributions)",
+        "config": {"workload": f"q4 decode GEMV x[1,3072].W[8192,3072]^T over {args.copies} weight copies per step",
+                   "m": 1, "n": 8192, "k": 3072, "group": 64, "copies": args.copies},
+        "roofline": {"bound": "hbm", "achieved": round(head["GB_per_s"], 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(head["GB_per_s"] / HBM_PEAK_GBS, 4), "traffic": None,
+                     "algorithmic_bytes_per_launch": per_launch_bytes,
+                     "us_per_launch": head["us_per_launch"]},
+        "cpu_baseline": cpu,
+        "secondary": secondary,
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

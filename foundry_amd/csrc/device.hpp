@@ -1,0 +1,91 @@
+// Internal state of an fh_device and the helpers every op entry point uses:
+// error reporting, ownership/bounds checks and the dispatch wrapper.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstdint>
+#include <map>
+#include <string>
+#include <utility>
+#include <vector>
+
+#include "../../include/foundry_hip.h"
+
+namespace fh {
+
+// Writes the thread-local message returned by fh_last_error and returns code.
+int fail(int code, const char *fmt, ...) __attribute__((format(printf, 2, 3)));
+void clear_error();
+
+}  // namespace fh
+
+struct fh_graph {
+    hipGraph_t graph = nullptr;
+    hipGraphExec_t exec = nullptr;
+    int ordinal = 0;
+};
+
+struct fh_device {
+    int ordinal = 0;
+    hipStream_t stream = nullptr;
+    std::string name;
+    // base address -> size of every live allocation this device made
+    std::map<uintptr_t, size_t> allocs;
+    uint64_t live_bytes = 0;
+    uint64_t peak_bytes = 0;
+    uint64_t run_peak_bytes = 0;
+    bool failed = false;
+    bool capturing = false;
+    int profile_mode = FH_PROFILE_OFF;
+    fh_profile counters{};
+    // per-dispatch event pairs (KERNELS mode) or the span of a step (STEPS)
+    std::vector<std::pair<hipEvent_t, hipEvent_t>> intervals;
+    std::vector<hipEvent_t> event_pool;
+    hipEvent_t timer_begin = nullptr;
+    hipEvent_t timer_end = nullptr;
+    bool timer_started = false;
+};
+
+namespace fh {
+
+// Sticky-failure gate at the start of every call that touches the device.
+int check_usable(fh_device *dev, const char *fn);
+
+// Makes the device's GPU current for the calling thread.
+int set_current(fh_device *dev, const char *fn);
+
+// The operand [ptr, ptr + nbytes) must lie inside one live allocation of dev.
+int check_range(const fh_device *dev, const void *ptr, uint64_t nbytes, const char *fn,
+                const char *what);
+
+// Records a HIP error from `call`, marks the device failed and returns
+// FH_ERR_FAILED; FH_OK when err is hipSuccess.
+int device_error(fh_device *dev, hipError_t err, const char *fn, const char *call);
+
+// Launch wrapper: brackets the launch with profiling events when enabled,
+// checks the launch status, and counts the dispatch.
+template <typename Launch>
+int dispatch(fh_device *dev, const char *fn, Launch &&launch);
+
+hipEvent_t take_event(fh_device *dev);
+void record_profile_begin(fh_device *dev, hipEvent_t *begin);
+void record_profile_end(fh_device *dev, hipEvent_t begin);
+
+template <typename Launch>
+int dispatch(fh_device *dev, const char *fn, Launch &&launch) {
+    hipEvent_t begin = nullptr;
+    record_profile_begin(dev, &begin);
+    launch();
+    hipError_t err = hipGetLastError();
+    if (err != hipSuccess) {
+        dev->failed = true;
+        return fail(FH_ERR_LAUNCH, "%s: kernel launch failed: %s", fn, hipGetErrorString(err));
+    }
+    record_profile_end(dev, begin);
+    dev->counters.dispatches += 1;
+    return FH_OK;
+}
+
+}  // namespace fh

@@ -1,0 +1,35 @@
+// Device-side helpers shared by the q4 kernels: the bf16 codec and the q4
+// nibble layout.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+namespace fh {
+
+// Group size the kernels implement (elements of K sharing one scale/bias).
+constexpr int kGroup = 64;
+
+// bf16 -> f32 is exact: the bf16 bits are the top half of the f32 bits
+// (src/metal/kernels/common.metal:29-31).
+__device__ __forceinline__ float bf16_to_f32(uint32_t bits16) {
+    return __uint_as_float(bits16 << 16);
+}
+
+// f32 -> bf16, round to nearest with ties to even; a NaN keeps its top bits
+// and is made quiet (src/metal/kernels/common.metal:37-43). The same rule as
+// the reference so every materialised value, NaN included, is bit-identical.
+__device__ __forceinline__ uint32_t f32_to_bf16_rne(float v) {
+    const uint32_t b = __float_as_uint(v);
+    if (v != v) return (b >> 16) | 0x0040u;
+    return (b + 0x7FFFu + ((b >> 16) & 1u)) >> 16;
+}
+
+// Dequantised weight in fp32. s*q is exact (8-bit significand times a 4-bit
+// integer), so fmaf and mul-then-add give the same bits.
+__device__ __forceinline__ float q4_dequant(float s, uint32_t q, float b) {
+    return fmaf(s, static_cast<float>(q), b);
+}
+
+}  // namespace fh

@@ -1,0 +1,260 @@
+"""HipDevice: the reference's ``Device`` trait (src/nn/primitive.rs:70-120)
+implemented over the C-ABI, for the q4 ops.
+
+Method names, argument meaning and error behaviour follow the trait and its
+Metal implementation (src/metal/mod.rs:527-725): ``run`` returns a fresh
+contiguous output; ``storage_to_bytes`` synchronises first; a device error is
+sticky. Storage is device memory owned by one device (``HipStorage``); an
+op given storage of another device fails with ``ForeignStorage``, as
+src/metal/mod.rs:187-200 does.
+"""
+from __future__ import annotations
+
+import ctypes
+from dataclasses import dataclass
+
+import numpy as np
+
+from . import _lib
+from .primitive import DType, QuantizedIndexSelect, QuantizedMatmul, TensorError, output
+
+
+class HipStorage:
+    """One device allocation. Freed when the last reference drops, as the
+    reference's Rc<Storage> is (src/nn/tensor.rs:49-53)."""
+
+    __slots__ = ("device", "ptr", "nbytes", "__weakref__")
+
+    def __init__(self, device: "HipDevice", ptr: int, nbytes: int):
+        self.device = device
+        self.ptr = ptr
+        self.nbytes = nbytes
+
+    def __del__(self):
+        dev = self.device
+        if dev is not None and dev._handle and self.ptr:
+            _lib.load().fh_free(dev._handle, ctypes.c_void_p(self.ptr))
+            self.ptr = 0
+
+
+@dataclass(frozen=True)
+class Layout:
+    """src/nn/layout.rs: shape, strides in elements, storage offset."""
+
+    shape: tuple
+    strides: tuple
+    offset: int = 0
+
+    @staticmethod
+    def contiguous(shape) -> "Layout":
+        strides, acc = [], 1
+        for d in reversed(shape):
+            strides.append(acc)
+            acc *= max(int(d), 1)
+        return Layout(tuple(int(d) for d in shape), tuple(reversed(strides)), 0)
+
+    def is_contiguous(self) -> bool:
+        return self.strides == Layout.contiguous(self.shape).strides
+
+    @property
+    def numel(self) -> int:
+        n = 1
+        for d in self.shape:
+            n *= d
+        return n
+
+
+@dataclass(frozen=True)
+class Operand:
+    """src/nn/tensor.rs:21-47: storage, layout and dtype of one op input."""
+
+    storage: HipStorage
+    layout: Layout
+    dtype: DType
+
+    def address(self) -> int:
+        return self.storage.ptr + self.layout.offset * self.dtype.itemsize
+
+
+class HipDevice:
+    """One GPU, one HIP stream."""
+
+    def __init__(self, ordinal: int = 0, profile_mode: int = _lib.PROFILE_OFF):
+        lib = _lib.load()
+        handle = ctypes.c_void_p()
+        if profile_mode == _lib.PROFILE_OFF:
+            _lib.check(lib.fh_device_create(ordinal, ctypes.byref(handle)))
+        else:
+            _lib.check(lib.fh_device_create_profiled(ordinal, profile_mode, ctypes.byref(handle)))
+        self._handle = handle.value
+        self.ordinal = ordinal
+
+    @classmethod
+    def profiled(cls, mode: int, ordinal: int = 0) -> "HipDevice":
+        """MetalDevice::profiled (src/metal/mod.rs:142-149)."""
+        return cls(ordinal, mode)
+
+    def close(self) -> None:
+        if self._handle:
+            h, self._handle = self._handle, None
+            _lib.check(_lib.load().fh_device_destroy(h))
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    @property
+    def handle(self) -> int:
+        if not self._handle:
+            raise _lib.HipError(_lib.ERR_INVALID_ARGUMENT, "device is closed")
+        return self._handle
+
+    # ---- Device trait ----
+    def device_name(self) -> str:
+        buf = ctypes.create_string_buffer(256)
+        _lib.call("fh_device_name", self.handle, buf, len(buf))
+        return buf.value.decode()
+
+    def synchronize(self) -> None:
+        _lib.call("fh_synchronize", self.handle)
+
+    def max_memory_allocated(self):
+        m = _lib.AllocatedMemory()
+        _lib.call("fh_max_memory_allocated", self.handle, ctypes.byref(m))
+        return {"bytes": m.bytes, "source": m.source.decode()}
+
+    def reset_run_memory_peak(self) -> None:
+        _lib.call("fh_reset_run_memory_peak", self.handle)
+
+    def run_memory_peak(self):
+        m = _lib.AllocatedMemory()
+        _lib.call("fh_run_memory_peak", self.handle, ctypes.byref(m))
+        return {"bytes": m.bytes, "source": m.source.decode()}
+
+    def take_profile(self):
+        """Counters since the previous call, or None when profiling is off."""
+        p = _lib.Profile()
+        rc = _lib.load().fh_take_profile(self.handle, ctypes.byref(p))
+        if rc == _lib.ERR_UNSUPPORTED:
+            return None
+        _lib.check(rc)
+        return {
+            "dispatches": p.dispatches,
+            "allocations": p.allocations,
+            "allocated_bytes": p.allocated_bytes,
+            "gpu_busy_ns": p.gpu_busy_ns,
+        }
+
+    def _alloc(self, nbytes: int, zero: bool) -> HipStorage:
+        ptr = ctypes.c_void_p()
+        _lib.call("fh_alloc", self.handle, nbytes, 1 if zero else 0, ctypes.byref(ptr))
+        return HipStorage(self, ptr.value, nbytes)
+
+    def storage_from_bytes(self, data) -> HipStorage:
+        buf = np.ascontiguousarray(np.frombuffer(memoryview(data).cast("B"), dtype=np.uint8))
+        st = self._alloc(buf.nbytes, zero=False)
+        if buf.nbytes:
+            _lib.call("fh_upload", self.handle, ctypes.c_void_p(st.ptr),
+                      buf.ctypes.data_as(ctypes.c_void_p), buf.nbytes)
+        return st
+
+    def zeros(self, nbytes: int) -> HipStorage:
+        return self._alloc(nbytes, zero=True)
+
+    def empty(self, nbytes: int) -> HipStorage:
+        """Uninitialised storage (an op's output)."""
+        return self._alloc(nbytes, zero=False)
+
+    def storage_to_bytes(self, operand: Operand) -> bytes:
+        if not operand.layout.is_contiguous():
+            raise TensorError("ToBytesNonContiguous")
+        nbytes = operand.layout.numel * operand.dtype.itemsize
+        out = np.empty(nbytes, dtype=np.uint8)
+        if nbytes:
+            _lib.call("fh_download", self.handle, out.ctypes.data_as(ctypes.c_void_p),
+                      ctypes.c_void_p(operand.address()), nbytes)
+        return out.tobytes()
+
+    def _owns(self, operand: Operand) -> None:
+        if operand.storage.device is not self:
+            raise _lib.HipError(_lib.ERR_FOREIGN_STORAGE, "storage was produced by another device")
+
+    def run(self, op, inputs, output_shape, dtype) -> HipStorage:
+        """Runs a q4 op into fresh contiguous storage (Device::run)."""
+        for operand in inputs:
+            self._owns(operand)
+        shape, out_dtype = output(op, [(o.dtype, o.layout.shape) for o in inputs])
+        if tuple(output_shape) != shape or DType(dtype) != out_dtype:
+            raise TensorError("OperandCount", f"output {output_shape}/{dtype} does not match {shape}/{out_dtype}")
+        numel = 1
+        for d in shape:
+            numel *= d
+        out = self.empty(numel * out_dtype.itemsize)
+        if isinstance(op, QuantizedMatmul):
+            x, wq, s, b = inputs
+            for w in (wq, s, b):
+                if not w.layout.is_contiguous():
+                    raise TensorError("MatmulIncompatible", "q4 weights must be contiguous")
+            rows, k = x.layout.shape
+            if x.layout.strides[1] != 1 and k > 1:
+                raise TensorError("MatmulIncompatible", "x must have unit column stride")
+            if x.dtype is not DType.BF16:
+                raise _lib.HipError(_lib.ERR_DTYPE, "the q4 kernels take bf16 activations")
+            x_ld = x.layout.strides[0] if rows > 1 else max(k, x.layout.strides[0])
+            _lib.call("fh_q4_matmul", self.handle, ctypes.c_void_p(x.address()), rows, k, x_ld,
+                      ctypes.c_void_p(wq.address()), ctypes.c_void_p(s.address()),
+                      ctypes.c_void_p(b.address()), shape[1], op.group, ctypes.c_void_p(out.ptr),
+                      _lib.BF16 if out_dtype is DType.BF16 else _lib.F32)
+            return out
+        if isinstance(op, QuantizedIndexSelect):
+            wq, s, b, ids = inputs
+            for w in (wq, s, b, ids):
+                if not w.layout.is_contiguous():
+                    raise TensorError("IndexSelectIncompatible", "operands must be contiguous")
+            rows = wq.layout.shape[0]
+            _lib.call("fh_q4_embed", self.handle, ctypes.c_void_p(wq.address()),
+                      ctypes.c_void_p(s.address()), ctypes.c_void_p(b.address()), rows, shape[1],
+                      op.group, ctypes.c_void_p(ids.address()), shape[0], ctypes.c_void_p(out.ptr))
+            return out
+        raise _lib.HipError(_lib.ERR_INVALID_ARGUMENT, f"unsupported op {op!r}")
+
+    # ---- batching and timing (CommandStream counterpart) ----
+    def capture_begin(self) -> None:
+        _lib.call("fh_capture_begin", self.handle)
+
+    def capture_end(self) -> "HipGraph":
+        g = ctypes.c_void_p()
+        _lib.call("fh_capture_end", self.handle, ctypes.byref(g))
+        return HipGraph(self, g.value)
+
+    def timer_begin(self) -> None:
+        _lib.call("fh_timer_begin", self.handle)
+
+    def timer_end(self) -> float:
+        ms = ctypes.c_double()
+        _lib.call("fh_timer_end", self.handle, ctypes.byref(ms))
+        return ms.value
+
+
+class HipGraph:
+    """A captured sequence of ops, replayed with ``launch``."""
+
+    def __init__(self, device: HipDevice, handle: int):
+        self.device = device
+        self._handle = handle
+
+    def launch(self) -> None:
+        _lib.call("fh_graph_launch", self.device.handle, ctypes.c_void_p(self._handle))
+
+    def __del__(self):
+        if self._handle:
+            _lib.load().fh_graph_destroy(ctypes.c_void_p(self._handle))
+            self._handle = None
+
+
+def device_count() -> int:
+    n = ctypes.c_int()
+    _lib.call("fh_device_count", ctypes.byref(n))
+    return n.value

@@ -1,0 +1,185 @@
+/*
+ * foundry_hip.h: the C-ABI of libfoundry_hip.so, the MI355X (gfx950) backend
+ * for Foundry's 4-bit quantized weight path.
+ *
+ * This is the one boundary a host binds. It is what the reference's `Device`
+ * trait (src/nn/primitive.rs:70-120) needs from a backend, flattened to plain
+ * pointers and sizes: a device owns one HIP stream; storage is device memory
+ * the device allocated; every op returns a fresh output the caller allocated
+ * and passes in. A Rust `src/hip` backend binds these through a thin FFI crate
+ * (see INTEGRATION.md); the Python package foundry_amd binds them with ctypes.
+ *
+ * Conventions
+ * - Every function returns an fh_status (0 = FH_OK). On error, fh_last_error()
+ *   returns a thread-local message naming the function and the cause.
+ * - Failure is sticky, as the reference's command stream is
+ *   (src/metal/stream.rs:109-115, :201-212): once a launch or a
+ *   synchronisation reports a device error, every later call on that device
+ *   returns FH_ERR_FAILED.
+ * - Ops validate shapes and dtypes before any launch (the reference does so in
+ *   `primitive::output`, src/nn/primitive.rs:146-289) and check that every
+ *   operand lies inside a live allocation of this device (the reference's
+ *   ForeignStorage check, src/metal/mod.rs:187-200). A rejected call launches
+ *   nothing.
+ * - Ops are asynchronous on the device's stream. fh_download synchronises
+ *   first (src/metal/mod.rs:614), fh_synchronize waits for everything.
+ * - One host thread per device, as in the reference (Rc-based, !Send
+ *   tensors). No internal locking.
+ *
+ * bf16 values are passed as their uint16_t bit patterns.
+ */
+#ifndef FOUNDRY_HIP_H
+#define FOUNDRY_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define FH_ABI_VERSION 1
+
+typedef struct fh_device fh_device;
+typedef struct fh_graph fh_graph;
+
+/* Error kinds. Mirrors MetalError (src/metal/error.rs:7-58) where a HIP
+ * counterpart exists, plus the Tensor-level validation errors
+ * (src/nn/error.rs) that the reference raises before the device call. */
+typedef enum fh_status {
+    FH_OK = 0,
+    FH_ERR_INVALID_ARGUMENT = 1,  /* shapes, sizes or null pointers do not fit the op */
+    FH_ERR_DEVICE_UNAVAILABLE = 2,/* MetalError::DeviceUnavailable */
+    FH_ERR_ALLOCATION = 3,        /* MetalError::BufferAllocation */
+    FH_ERR_FOREIGN_STORAGE = 4,   /* MetalError::ForeignStorage */
+    FH_ERR_OUT_OF_BOUNDS = 5,     /* MetalError::ToBytesOutOfBounds; operand past its allocation */
+    FH_ERR_LAUNCH = 6,            /* a kernel launch was refused */
+    FH_ERR_FAILED = 7,            /* MetalError::CommandBufferFailed (sticky) */
+    FH_ERR_INDEX_TOO_LARGE = 8,   /* MetalError::KernelIndexTooLarge */
+    FH_ERR_DTYPE = 9,             /* MetalError::DTypeNotFloat; TensorError::IndicesNotU32 */
+    FH_ERR_UNSUPPORTED = 10,      /* valid request the kernels do not implement (e.g. group != 64) */
+    FH_ERR_CAPTURE = 11           /* graph capture misuse */
+} fh_status;
+
+/* src/nn/dtype.rs:6-10 */
+typedef enum fh_dtype { FH_F32 = 0, FH_BF16 = 1, FH_U32 = 2 } fh_dtype;
+
+/* src/nn/profile.rs:7-13. STEPS keeps normal batching and times the span of
+ * work; KERNELS brackets every dispatch with events (per-kernel GPU time). */
+typedef enum fh_profile_mode {
+    FH_PROFILE_OFF = 0,
+    FH_PROFILE_STEPS = 1,
+    FH_PROFILE_KERNELS = 2
+} fh_profile_mode;
+
+/* src/nn/memory.rs:1-5 */
+typedef struct fh_allocated_memory {
+    uint64_t bytes;
+    const char *source; /* static string */
+} fh_allocated_memory;
+
+/* src/nn/profile.rs:15-21 (DeviceProfile) */
+typedef struct fh_profile {
+    uint64_t dispatches;      /* kernels launched since the last take */
+    uint64_t allocations;     /* fh_alloc calls since the last take */
+    uint64_t allocated_bytes; /* bytes they requested */
+    uint64_t gpu_busy_ns;     /* union of timed GPU intervals (0 when unavailable) */
+} fh_profile;
+
+/* ---- errors and version ---- */
+const char *fh_last_error(void);
+int fh_abi_version(void);
+
+/* ---- device lifecycle: MetalDevice::new / ::profiled (src/metal/mod.rs:108-149) ---- */
+int fh_device_count(int *count);
+int fh_device_create(int ordinal, fh_device **out);
+int fh_device_create_profiled(int ordinal, int mode, fh_device **out);
+/* Synchronises, frees every allocation the device still owns, destroys it. */
+int fh_device_destroy(fh_device *dev);
+/* Device::device_name (src/nn/primitive.rs:74) */
+int fh_device_name(const fh_device *dev, char *buf, size_t len);
+/* Device::synchronize (src/nn/primitive.rs:86) */
+int fh_synchronize(fh_device *dev);
+/* The device's HIP stream (hipStream_t), for callers that time with events. */
+int fh_device_stream(fh_device *dev, void **stream);
+
+/* ---- storage: Device::{zeros, storage_from_bytes, storage_to_bytes}
+ *      (src/nn/primitive.rs:88-103; src/metal/mod.rs:565-637) ---- */
+/* Allocates nbytes (at least 1) of device memory, 256-byte aligned. With
+ * zero_fill != 0 the memory is cleared before any later op on the stream
+ * reads it (Device::zeros). */
+int fh_alloc(fh_device *dev, size_t nbytes, int zero_fill, void **out);
+/* Frees an allocation of this device after the work queued on it ends. */
+int fh_free(fh_device *dev, void *ptr);
+/* Host -> device copy into an owned range; ordered on the stream. */
+int fh_upload(fh_device *dev, void *dst, const void *src, size_t nbytes);
+/* Device -> host copy of an owned range; synchronises first. */
+int fh_download(fh_device *dev, void *dst, const void *src, size_t nbytes);
+
+/* ---- memory and profile counters (src/nn/primitive.rs:75-83) ---- */
+int fh_max_memory_allocated(const fh_device *dev, fh_allocated_memory *out);
+int fh_reset_run_memory_peak(fh_device *dev);
+int fh_run_memory_peak(const fh_device *dev, fh_allocated_memory *out);
+/* Counters since the previous take, then reset. Returns FH_ERR_UNSUPPORTED
+ * (and leaves *out zeroed) when the device was not created profiled, as the
+ * reference returns None (src/nn/primitive.rs:83). */
+int fh_take_profile(fh_device *dev, fh_profile *out);
+
+/* ---- batching: the HIP counterpart of the reference's CommandStream
+ * (src/metal/stream.rs:29-215), which encodes many dispatches and commits
+ * them at once. Between begin and end, ops are validated and recorded, not
+ * run; fh_graph_launch replays the recording on the device's stream. ---- */
+int fh_capture_begin(fh_device *dev);
+int fh_capture_end(fh_device *dev, fh_graph **out);
+int fh_graph_launch(fh_device *dev, fh_graph *graph);
+int fh_graph_destroy(fh_graph *graph);
+
+/* ---- event timing on the device's stream ---- */
+/* Records a start event now, in stream order. */
+int fh_timer_begin(fh_device *dev);
+/* Records an end event, waits for it, writes the milliseconds between the two. */
+int fh_timer_end(fh_device *dev, double *elapsed_ms);
+
+/* ======================================================================
+ * q4 ops. Weight format (affine group quantisation):
+ *   wq     u32 [rows, k/8]   element j of a row = nibble j%8 (bits 4*(j%8)..+3)
+ *                            of word j/8, little-endian nibble order
+ *   scales bf16[rows, k/group]
+ *   biases bf16[rows, k/group]
+ *   w[r, j] = f32(scales[r, j/group]) * q[r, j] + f32(biases[r, j/group])
+ * The kernels implement group = 64 and k a multiple of 64.
+ * ====================================================================== */
+
+/* q4 Embedding::forward (src/nn/linear.rs:53-69) -> Op::IndexSelect{dim 0}
+ * (src/nn/primitive.rs:258-289; src/metal/mod.rs:483-500;
+ * src/metal/kernels/index_select.metal:11-29) over a q4 table.
+ * out bf16[n_ids, k]: out[i, :] = RNE_bf16(w[ids[i], :]); an id >= rows
+ * writes a zero row. Bit-exact. n_ids may be 0. */
+int fh_q4_embed(fh_device *dev, const uint32_t *wq, const uint16_t *scales,
+                const uint16_t *biases, int64_t rows, int64_t k, int64_t group,
+                const uint32_t *ids, int64_t n_ids, uint16_t *out);
+
+/* q4 Linear::forward (src/nn/linear.rs:22-35) -> Op::Matmul
+ * (src/nn/primitive.rs:234-256; src/metal/mod.rs:434-481;
+ * src/metal/kernels/matmul.metal:29-65) with a q4 right operand:
+ *   y[i, r] = sum_j x[i, j] * w[r, j]       (fp32 accumulation)
+ * x bf16[m, k] with row stride x_ld (elements, >= k); y [m, n] contiguous,
+ * y_dtype FH_BF16 (RNE of the fp32 sum, the reference's output rounding) or
+ * FH_F32 (the fp32 sum itself). m <= 8 runs the decode GEMV, larger m the
+ * prefill GEMM. m may be 0. */
+int fh_q4_matmul(fh_device *dev, const uint16_t *x, int64_t m, int64_t k,
+                 int64_t x_ld, const uint32_t *wq, const uint16_t *scales,
+                 const uint16_t *biases, int64_t n, int64_t group, void *y,
+                 int y_dtype);
+
+/* Materialised dequantisation: out bf16[rows, k] = RNE_bf16(w). Bit-exact.
+ * The value the prefill GEMM feeds to the matrix cores. */
+int fh_q4_dequant(fh_device *dev, const uint32_t *wq, const uint16_t *scales,
+                  const uint16_t *biases, int64_t rows, int64_t k, int64_t group,
+                  uint16_t *out);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif

@@ -1,0 +1,340 @@
+"""GPU parity of the q4 path against the CPU oracle, through the C-ABI.
+
+Bars (written into each check):
+- fh_q4_dequant and fh_q4_embed: bit-exact against the oracle.
+- fh_q4_matmul, fp32 output: max|y - y64| / max|y64| <= 2e-3 against the fp64
+  dequant-then-matmul oracle. (The decode GEMV keeps every weight exact in
+  fp32 and lands near 1e-6; the GEMM feeds the matrix cores the bf16 weight
+  RNE(s*q + b) and lands near 1e-3.)
+- bf16 output: bit-identical to RNE of the same kernel's fp32 output, and
+  within 1 bf16 ulp of the fp64 value plus the fp32 bound above.
+Full-size configs that the fp64 oracle cannot hold whole are compared on a
+seeded sample of output rows/columns.
+"""
+import ctypes
+import os
+
+import numpy as np
+import pytest
+
+from foundry_amd import _lib, synth
+from foundry_amd.device import HipDevice
+from foundry_amd.nn import Q4Embedding, Q4Linear, Q4Weight
+from foundry_amd.primitive import DType
+from foundry_amd.tensor import Tensor
+
+pytestmark = pytest.mark.gpu
+
+FP32_BOUND = 2e-3
+GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "q4_small.npz")
+
+
+def up(dev, arr, dtype):
+    return Tensor.from_numpy(dev, arr, dtype)
+
+
+def weight(dev, wq, s, b):
+    return Q4Weight(up(dev, wq, DType.U32), up(dev, s, DType.BF16), up(dev, b, DType.BF16))
+
+
+def matmul_raw(dev, x_t, w: Q4Weight, m, k, x_ld, y_dtype):
+    n = w.out_features
+    item = 4 if y_dtype == _lib.F32 else 2
+    out = dev.empty(max(m * n * item, 1))
+    _lib.call("fh_q4_matmul", dev.handle, ctypes.c_void_p(x_t.storage.ptr), m, k, x_ld,
+              ctypes.c_void_p(w.wq.storage.ptr), ctypes.c_void_p(w.scales.storage.ptr),
+              ctypes.c_void_p(w.biases.storage.ptr), n, 64, ctypes.c_void_p(out.ptr), y_dtype)
+    raw = np.empty(m * n * item, dtype=np.uint8)
+    if raw.size:
+        _lib.call("fh_download", dev.handle, raw.ctypes.data_as(ctypes.c_void_p), ctypes.c_void_p(out.ptr), raw.size)
+    return raw.view(np.float32 if y_dtype == _lib.F32 else np.uint16).reshape(m, n)
+
+
+def bf16_ulp(v):
+    a = np.abs(v).astype(np.float64)
+    e = np.floor(np.log2(np.maximum(a, 2.0**-126)))
+    return 2.0 ** (e - 7)
+
+
+def check_matmul(y32, y16, y64, bound=FP32_BOUND):
+    scale = float(np.max(np.abs(y64))) or 1.0
+    err32 = float(np.max(np.abs(y32.astype(np.float64) - y64))) / scale
+    assert err32 <= bound, f"fp32 rel err {err32:.3e} > {bound}"
+    assert np.array_equal(y16, synth.bf16_rne(y32)), "bf16 output is not RNE of the fp32 result"
+    err16 = np.abs(synth.bf16_to_f32(y16).astype(np.float64) - y64)
+    assert np.all(err16 <= bf16_ulp(y64) + bound * scale), "bf16 output beyond 1 ulp + bound"
+    return err32
+
+
+def run_linear(dev, oracle, m, n, k, seed, x_ld=None, sample=None):
+    wq, s, b = synth.q4_weights(seed, n, k)
+    x_ld = x_ld or k
+    x = synth.bf16_normal(seed + 1, (m, x_ld))
+    w = weight(dev, wq, s, b)
+    xt = up(dev, x, DType.BF16)
+    y32 = matmul_raw(dev, xt, w, m, k, x_ld, _lib.F32)
+    y16 = matmul_raw(dev, xt, w, m, k, x_ld, _lib.BF16)
+    xs = x[:, :k]
+    if sample is None:
+        y64 = oracle.linear_f64(xs, wq, s, b)
+        return check_matmul(y32, y16, y64)
+    rng = np.random.default_rng(seed)
+    rows = np.sort(rng.choice(m, size=min(m, sample[0]), replace=False))
+    cols = np.sort(rng.choice(n, size=min(n, sample[1]), replace=False))
+    y64 = oracle.linear_f64(np.ascontiguousarray(xs[rows]), wq, s, b, rows=cols)
+    return check_matmul(y32[np.ix_(rows, cols)], y16[np.ix_(rows, cols)], y64)
+
+
+# ---------------- dequant and gather: bit-exact ----------------
+
+def test_dequant_golden_and_config_shape(device, oracle):
+    with np.load(GOLDEN) as g:
+        for case in ("gemv", "gemm"):
+            wq, s, b = g[f"{case}_wq"], g[f"{case}_s"], g[f"{case}_b"]
+            out = dev_dequant(device, wq, s, b)
+            assert np.array_equal(out, g[f"{case}_deq"])
+    wq, s, b = synth.q4_weights(101, 8192, 3072)
+    assert np.array_equal(dev_dequant(device, wq, s, b), oracle.q4_dequant_bf16(wq, s, b))
+
+
+def dev_dequant(dev, wq, s, b):
+    rows, k = wq.shape[0], wq.shape[1] * 8
+    w = weight(dev, wq, s, b)
+    out = dev.empty(rows * k * 2)
+    _lib.call("fh_q4_dequant", dev.handle, ctypes.c_void_p(w.wq.storage.ptr),
+              ctypes.c_void_p(w.scales.storage.ptr), ctypes.c_void_p(w.biases.storage.ptr),
+              rows, k, 64, ctypes.c_void_p(out.ptr))
+    raw = np.empty(rows * k, dtype=np.uint16)
+    _lib.call("fh_download", dev.handle, raw.ctypes.data_as(ctypes.c_void_p), ctypes.c_void_p(out.ptr), raw.nbytes)
+    return raw.reshape(rows, k)
+
+
+def test_dequant_special_values(device, oracle):
+    specials = np.array([0x0000, 0x8000, 0x7F80, 0xFF80, 0x7FC0, 0x7F81, 0x0001, 0x7F7F, 0x3C80, 0xBC80,
+                         0x4700, 0xC2F0, 0x3B83, 0x0080, 0x8001, 0x3F80], dtype=np.uint16)
+    rows = 16
+    r = np.arange(rows)
+    s = np.stack([specials[r], specials[(r + 7) % 16]], axis=1).astype(np.uint16)
+    b = np.stack([specials[(r + 3) % 16], specials[(r * 5 + 1) % 16]], axis=1).astype(np.uint16)
+    wq = synth.q4_weights(5, rows, 128)[0]
+    got = dev_dequant(device, wq, s, b)
+    want = oracle.q4_dequant_bf16(wq, s, b)
+    assert np.array_equal(got, want)
+
+
+def test_embed_golden(device):
+    with np.load(GOLDEN) as g:
+        emb = Q4Embedding(weight(device, g["gemv_wq"], g["gemv_s"], g["gemv_b"]))
+        ids = up(device, g["embed_ids"], DType.U32)
+        rows = emb.forward(device, ids).to_numpy(device)
+        assert rows.shape == (g["embed_ids"].size, 128)
+        assert np.array_equal(rows, g["embed_rows"])
+
+
+def test_embed_known_answer(device, oracle):
+    q = np.zeros((3, 64), dtype=np.uint8)
+    q[:, :4] = np.arange(12).reshape(3, 4)
+    wq = oracle.q4_pack(q)
+    s = np.full((3, 1), 0x3F80, dtype=np.uint16)
+    b = np.zeros((3, 1), dtype=np.uint16)
+    emb = Q4Embedding(weight(device, wq, s, b))
+    rows = emb.forward(device, up(device, np.array([2, 0, 3], dtype=np.uint32), DType.U32)).to_numpy(device)
+    assert synth.bf16_to_f32(rows[:, :4]).tolist() == [[8, 9, 10, 11], [0, 1, 2, 3], [0, 0, 0, 0]]
+    assert not rows[:, 4:].any()
+
+
+@pytest.mark.parametrize("batch", [1, 64, 4096])
+def test_embed_config2_full_table(device, oracle, batch, _config2_table):
+    wq, s, b, w = _config2_table
+    ids = synth.token_ids(batch, batch, 128256)
+    if batch >= 64:  # edge ids: first, last, just past the end, max u32
+        ids[:4] = [0, 128255, 128256, 2**32 - 1]
+    out = Q4Embedding(w).forward(device, up(device, ids.reshape(1, -1), DType.U32)).to_numpy(device)
+    assert out.shape == (1, batch, 3072)
+    assert np.array_equal(out[0], oracle.q4_embed(wq, s, b, ids))
+
+
+@pytest.fixture(scope="module")
+def _config2_table(device):
+    wq, s, b = synth.q4_weights(2, 128256, 3072)
+    return wq, s, b, weight(device, wq, s, b)
+
+
+def test_embed_empty(device):
+    wq, s, b = synth.q4_weights(3, 8, 64)
+    emb = Q4Embedding(weight(device, wq, s, b))
+    out = emb.forward(device, up(device, np.zeros((0,), dtype=np.uint32), DType.U32))
+    assert out.shape == (0, 64)
+
+
+# ---------------- GEMV (m <= 8) ----------------
+
+@pytest.mark.parametrize(
+    "m,n,k",
+    [(1, 8192, 3072), (1, 3072, 8192), (1, 1000, 64), (1, 1024, 3072), (3, 40, 128),
+     (2, 4096, 4096), (4, 333, 192), (8, 14336, 4096), (8, 4096, 14336), (5, 3072, 8192),
+     (7, 129, 1024), (1, 17, 30720)],
+)
+def test_gemv_parity(device, oracle, m, n, k):
+    err = run_linear(device, oracle, m, n, k, seed=1000 + m * 7 + n + k)
+    assert err < 1e-4, f"GEMV keeps exact weights; rel err {err:.2e} suggests a wrong term"
+
+
+def test_gemv_config1_and_lm_head_sampled(device, oracle):
+    run_linear(device, oracle, 1, 8192, 3072, seed=1)
+    run_linear(device, oracle, 1, 128256, 3072, seed=2, sample=(1, 4096))
+
+
+def test_gemv_golden(device):
+    with np.load(GOLDEN) as g:
+        w = weight(device, g["gemv_wq"], g["gemv_s"], g["gemv_b"])
+        x = up(device, g["gemv_x"], DType.BF16)
+        m, k = g["gemv_x"].shape
+        y32 = matmul_raw(device, x, w, m, k, k, _lib.F32)
+        y16 = matmul_raw(device, x, w, m, k, k, _lib.BF16)
+        check_matmul(y32, y16, g["gemv_y64"])
+
+
+def test_gemv_strided_x(device, oracle):
+    run_linear(device, oracle, 3, 512, 1024, seed=77, x_ld=1024 + 64)
+
+
+# ---------------- GEMM (m > 8) ----------------
+
+@pytest.mark.parametrize(
+    "m,n,k", [(9, 128, 64), (20, 72, 256), (130, 200, 320), (256, 256, 3072), (512, 1000, 1024), (64, 64, 8192)]
+)
+def test_gemm_parity(device, oracle, m, n, k):
+    run_linear(device, oracle, m, n, k, seed=2000 + m + n + k)
+
+
+def test_gemm_config3_shapes_sampled(device, oracle):
+    run_linear(device, oracle, 2048, 8192, 3072, seed=3, sample=(96, 8192))
+    run_linear(device, oracle, 2048, 3072, 8192, seed=4, sample=(96, 3072))
+
+
+def test_gemm_golden(device):
+    with np.load(GOLDEN) as g:
+        w = weight(device, g["gemm_wq"], g["gemm_s"], g["gemm_b"])
+        x = up(device, g["gemm_x"], DType.BF16)
+        m, k = g["gemm_x"].shape
+        y32 = matmul_raw(device, x, w, m, k, k, _lib.F32)
+        y16 = matmul_raw(device, x, w, m, k, k, _lib.BF16)
+        check_matmul(y32, y16, g["gemm_y64"])
+
+
+def test_gemm_strided_x(device, oracle):
+    run_linear(device, oracle, 40, 256, 512, seed=78, x_ld=512 + 8)
+
+
+def test_zero_k_and_zero_m(device):
+    w = weight(device, np.zeros((16, 0), dtype=np.uint32), np.zeros((16, 0), dtype=np.uint16),
+               np.zeros((16, 0), dtype=np.uint16))
+    for m in (1, 20):
+        x = up(device, np.zeros((m, 8), dtype=np.uint16), DType.BF16)
+        y = matmul_raw(device, x, w, m, 0, 8, _lib.F32)
+        assert y.shape == (m, 16) and not y.any()
+    wq, s, b = synth.q4_weights(9, 16, 64)
+    x = up(device, np.zeros((1, 64), dtype=np.uint16), DType.BF16)
+    assert matmul_raw(device, x, weight(device, wq, s, b), 0, 64, 64, _lib.BF16).shape == (0, 16)
+
+
+# ---------------- modules, errors, batching, profiling ----------------
+
+def test_q4_linear_module_shapes(device, oracle):
+    wq, s, b = synth.q4_weights(31, 96, 256)
+    x = synth.bf16_normal(32, (2, 3, 256))
+    lin = Q4Linear(weight(device, wq, s, b))
+    y = lin.forward(device, up(device, x, DType.BF16)).to_numpy(device)
+    assert y.shape == (2, 3, 96)
+    y64 = oracle.linear_f64(x.reshape(6, 256), wq, s, b).reshape(2, 3, 96)
+    err = np.abs(synth.bf16_to_f32(y).astype(np.float64) - y64)
+    assert np.all(err <= bf16_ulp(y64) + 1e-5 * np.max(np.abs(y64)))
+
+
+def test_foreign_and_out_of_bounds_storage_are_rejected(device):
+    wq, s, b = synth.q4_weights(41, 64, 128)
+    w = weight(device, wq, s, b)
+    x = up(device, synth.bf16_normal(42, (1, 128)), DType.BF16)
+    other = HipDevice(0)
+    try:
+        xo = up(other, synth.bf16_normal(42, (1, 128)), DType.BF16)
+        with pytest.raises(_lib.HipError) as e:
+            matmul_raw(device, xo, w, 1, 128, 128, _lib.BF16)
+        assert e.value.status == _lib.ERR_FOREIGN_STORAGE
+    finally:
+        del xo
+        other.close()
+    out = device.empty(65 * 2)
+    with pytest.raises(_lib.HipError) as e:  # n=65 rows do not fit a 64-row weight
+        _lib.call("fh_q4_matmul", device.handle, ctypes.c_void_p(x.storage.ptr), 1, 128, 128,
+                  ctypes.c_void_p(w.wq.storage.ptr), ctypes.c_void_p(w.scales.storage.ptr),
+                  ctypes.c_void_p(w.biases.storage.ptr), 65, 64, ctypes.c_void_p(out.ptr), _lib.BF16)
+    assert e.value.status == _lib.ERR_OUT_OF_BOUNDS
+    with pytest.raises(_lib.HipError) as e:
+        _lib.call("fh_q4_matmul", device.handle, ctypes.c_void_p(x.storage.ptr), 1, 128, 128,
+                  ctypes.c_void_p(w.wq.storage.ptr), ctypes.c_void_p(w.scales.storage.ptr),
+                  ctypes.c_void_p(w.biases.storage.ptr), 64, 32, ctypes.c_void_p(out.ptr), _lib.BF16)
+    assert e.value.status == _lib.ERR_UNSUPPORTED
+    # validation errors launch nothing and are not sticky
+    y = matmul_raw(device, x, w, 1, 128, 128, _lib.BF16)
+    assert y.shape == (1, 64)
+
+
+def test_graph_replay_matches_eager(device):
+    wq, s, b = synth.q4_weights(51, 512, 1024)
+    w = weight(device, wq, s, b)
+    xs = {m: up(device, synth.bf16_normal(52 + m, (m, 1024)), DType.BF16) for m in (1, 4, 64)}
+    ids = up(device, np.array([5, 511, 512, 0], dtype=np.uint32), DType.U32)
+    outs = {m: device.empty(m * 512 * 2) for m in xs}
+    emb_out = device.empty(4 * 1024 * 2)
+
+    def enqueue():
+        for m, xt in xs.items():
+            _lib.call("fh_q4_matmul", device.handle, ctypes.c_void_p(xt.storage.ptr), m, 1024, 1024,
+                      ctypes.c_void_p(w.wq.storage.ptr), ctypes.c_void_p(w.scales.storage.ptr),
+                      ctypes.c_void_p(w.biases.storage.ptr), 512, 64, ctypes.c_void_p(outs[m].ptr), _lib.BF16)
+        _lib.call("fh_q4_embed", device.handle, ctypes.c_void_p(w.wq.storage.ptr),
+                  ctypes.c_void_p(w.scales.storage.ptr), ctypes.c_void_p(w.biases.storage.ptr),
+                  512, 1024, 64, ctypes.c_void_p(ids.storage.ptr), 4, ctypes.c_void_p(emb_out.ptr))
+
+    def read():
+        res = {}
+        for m, st in list(outs.items()) + [("emb", emb_out)]:
+            raw = np.empty(st.nbytes, dtype=np.uint8)
+            _lib.call("fh_download", device.handle, raw.ctypes.data_as(ctypes.c_void_p), ctypes.c_void_p(st.ptr), raw.size)
+            res[m] = raw
+        return res
+
+    enqueue()
+    eager = read()
+    device.capture_begin()
+    enqueue()
+    graph = device.capture_end()
+    for _ in range(3):
+        for st in list(outs.values()) + [emb_out]:  # clobber between replays
+            junk = np.full(st.nbytes, 0xAB, dtype=np.uint8)
+            _lib.call("fh_upload", device.handle, ctypes.c_void_p(st.ptr), junk.ctypes.data_as(ctypes.c_void_p), junk.size)
+        graph.launch()
+        device.synchronize()
+        got = read()
+        for key in eager:
+            assert np.array_equal(got[key], eager[key]), key
+
+
+def test_profiled_device_counts_dispatches(device):
+    prof = HipDevice.profiled(_lib.PROFILE_KERNELS)
+    try:
+        wq, s, b = synth.q4_weights(61, 256, 512)
+        w = weight(prof, wq, s, b)
+        x = up(prof, synth.bf16_normal(62, (1, 512)), DType.BF16)
+        assert prof.take_profile()["allocations"] == 4
+        for _ in range(3):
+            Q4Linear(w).forward(prof, x)
+        p = prof.take_profile()
+        assert p["dispatches"] == 3 and p["gpu_busy_ns"] > 0 and p["allocations"] == 3
+        assert prof.take_profile()["dispatches"] == 0
+        assert prof.max_memory_allocated()["bytes"] > 0
+    finally:
+        prof.close()
+    assert device.take_profile() is None
