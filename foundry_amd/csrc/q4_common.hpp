@@ -26,9 +26,21 @@ __device__ __forceinline__ uint32_t f32_to_bf16_rne(float v) {
     return (b + 0x7FFFu + ((b >> 16) & 1u)) >> 16;
 }
 
-// Dequantised weight in fp32. s*q is exact (8-bit significand times a 4-bit
-// integer), so fmaf and mul-then-add give the same bits.
+// Dequantised weight in fp32: the product, rounded, then the sum, rounded.
+// s*q is exact whenever it is finite (8-bit significand times a 4-bit
+// integer), so this equals fmaf(s, q, b) except when s*q overflows fp32
+// (|s| > 2^124), where the product becomes an infinity as in the reference's
+// mul-then-add order. Contraction is switched off here so the two roundings
+// stay two instructions.
 __device__ __forceinline__ float q4_dequant(float s, uint32_t q, float b) {
+#pragma clang fp contract(off)
+    const float prod = s * static_cast<float>(q);
+    return prod + b;
+}
+
+// Same value through one fma, for the GEMM's register dequantisation; equal
+// to q4_dequant whenever s*q is finite in fp32.
+__device__ __forceinline__ float q4_dequant_fma(float s, uint32_t q, float b) {
     return fmaf(s, static_cast<float>(q), b);
 }
 

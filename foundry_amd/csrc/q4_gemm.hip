@@ -38,8 +38,8 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
 __device__ __forceinline__ void dequant_word(uint32_t w, float s, float b, uint32_t out[4]) {
 #pragma unroll
     for (int p = 0; p < 4; ++p) {
-        const float lo = q4_dequant(s, (w >> (8 * p)) & 0xFu, b);
-        const float hi = q4_dequant(s, (w >> (8 * p + 4)) & 0xFu, b);
+        const float lo = q4_dequant_fma(s, (w >> (8 * p)) & 0xFu, b);
+        const float hi = q4_dequant_fma(s, (w >> (8 * p + 4)) & 0xFu, b);
         out[p] = pack_bf16x2(lo, hi);
     }
 }

@@ -89,8 +89,9 @@ void or_q4_unpack(const uint32_t *wq, int64_t rows, int64_t k, uint8_t *q) {
         for (int64_t c = 0; c < k; ++c) q[r * k + c] = (uint8_t)or_q4_get(wq, k, r, c);
 }
 
-/* f32(s) * q is exact (8-bit significand times a 4-bit integer), so this is
- * one rounding, the add; an FMA gives the same bits. */
+/* Product rounded, then sum rounded (the reference's mul-then-add order).
+ * f32(s) * q is exact whenever it is finite (8-bit significand times a 4-bit
+ * integer), so an FMA gives the same bits except when the product overflows. */
 float or_q4_dequant_one(uint16_t s, uint32_t q, uint16_t b) {
     float prod = or_bf16_to_f32(s) * (float)q;
     return prod + or_bf16_to_f32(b);
