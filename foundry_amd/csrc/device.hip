@@ -145,6 +145,7 @@ static int create(int ordinal, int mode, fh_device **out, const char *fn) {
     if (!dev) return fail(FH_ERR_ALLOCATION, "%s: out of host memory", fn);
     dev->ordinal = ordinal;
     dev->name = prop.name[0] ? prop.name : prop.gcnArchName;
+    dev->compute_units = prop.multiProcessorCount > 0 ? prop.multiProcessorCount : 256;
     dev->profile_mode = mode;
     // default priority: streams of other priorities are not used anywhere
     if (hipStreamCreateWithFlags(&dev->stream, hipStreamNonBlocking) != hipSuccess) {

@@ -31,6 +31,7 @@ struct fh_device {
     int ordinal = 0;
     hipStream_t stream = nullptr;
     std::string name;
+    uint32_t compute_units = 0;  // sizes persistent grids
     // base address -> size of every live allocation this device made
     std::map<uintptr_t, size_t> allocs;
     uint64_t live_bytes = 0;

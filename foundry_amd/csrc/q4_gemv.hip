@@ -7,12 +7,17 @@
 // Design for CDNA4:
 // - A lane owns 16-byte chunks (32 weights, half a group) of one weight row;
 //   L lanes share a row, chunk c = sub + L*i, so each load instruction of an
-//   L-lane row group reads 16*L contiguous bytes. Loads are software-pipelined
-//   one batch of kBatch chunks ahead.
-// - x is staged once per block into LDS, permuted so that the bf16 pair for
-//   nibbles (e, e+4) of a word is one dword, and laid out [m][word-in-chunk]
-//   [chunk] so neighbouring lanes read neighbouring 16 bytes (no bank
-//   conflicts). Per-chunk sums of x are staged beside it.
+//   L-lane row group reads 16*L contiguous bytes. A wavefront covers 64/L
+//   rows at once (a "row group").
+// - Blocks are persistent: the grid is sized to the chip (8 blocks of 4
+//   wavefronts per CU), each block stages x once and its wavefronts walk row
+//   groups with a stride. A lane issues all CPL chunk loads of a row group at
+//   once, and the next row group's loads before the current one's reduction;
+//   latency is hidden by occupancy (one register buffer keeps VGPRs low).
+// - x is staged into LDS, permuted so that the bf16 pair for nibbles
+//   (e, e+4) of a word is one dword, and laid out [m][word-in-chunk][chunk]
+//   so neighbouring lanes read neighbouring 16 bytes (no bank conflicts).
+//   Per-chunk sums of x are staged beside it.
 // - Dequantisation in registers without conversions: (w >> 4t) & 0x000F000F
 //   | 0x43004300 is a bf16 pair (128 + q_t, 128 + q_{t+4}), exact since q < 16;
 //   v_dot2_f32_bf16 multiplies it with the x pair and accumulates in fp32.
@@ -26,9 +31,11 @@
 namespace fh {
 
 constexpr int kGemvThreads = 256;
-constexpr int kBatch = 4;
+constexpr int kGemvWaves = kGemvThreads / 64;
 // Dynamic LDS one block may use for staged x (bytes).
 constexpr uint32_t kGemvLdsLimit = 64 * 1024;
+// Persistent blocks per CU.
+constexpr uint32_t kGemvBlocksPerCu = 8;
 
 typedef __attribute__((ext_vector_type(2))) __bf16 bf16x2_t;
 
@@ -42,13 +49,21 @@ __host__ __device__ constexpr uint32_t gemv_lds_bytes(uint32_t m, uint32_t k) {
     return m * (k / 32) * (4 * 16 + 4);
 }
 
-template <int M, int L>
+// One lane's chunks of one row group: packed words and the group scale/bias.
+template <int CPL>
+struct GemvChunks {
+    uint4 w[CPL];
+    uint32_t s[CPL], b[CPL];
+};
+
+// FULL: every lane's CPL chunks exist (k is a multiple of 32*CPL*L), so the
+// loads need no per-chunk guard and share one address with immediate offsets.
+template <int M, int L, int CPL, bool FULL>
 __global__ __launch_bounds__(kGemvThreads) void q4_gemv_kernel(
     const uint16_t *__restrict__ x, uint32_t x_ld, const uint32_t *__restrict__ wq,
     const uint16_t *__restrict__ scales, const uint16_t *__restrict__ biases, uint32_t n,
     uint32_t k, void *__restrict__ y, uint32_t y_ld, int y_is_f32) {
-    constexpr int kRowsPerWave = 64 / L;
-    constexpr int kRowsPerBlock = (kGemvThreads / 64) * kRowsPerWave;
+    constexpr uint32_t kRowsPerWave = 64 / L;
     extern __shared__ uint4 lds[];
     const uint32_t chunks = k / 32;
     uint4 *xs = lds;                                                // [M][4][chunks]
@@ -57,25 +72,32 @@ __global__ __launch_bounds__(kGemvThreads) void q4_gemv_kernel(
     const uint32_t lane = threadIdx.x & 63;
     const uint32_t wave = threadIdx.x >> 6;
     const uint32_t sub = lane % L;
-    const uint32_t row = blockIdx.x * kRowsPerBlock + wave * kRowsPerWave + lane / L;
-    const bool valid = row < n;
-    const uint32_t row_c = valid ? row : 0;  // clamped: invalid lanes load row 0, discard
-    const uint4 *wrow = reinterpret_cast<const uint4 *>(wq + static_cast<uint64_t>(row_c) * (k / 8));
-    const uint16_t *srow = scales + static_cast<uint64_t>(row_c) * (k / kGroup);
-    const uint16_t *brow = biases + static_cast<uint64_t>(row_c) * (k / kGroup);
+    const uint32_t seg_chunks = CPL * L;
+    const uint32_t segs = FULL ? chunks / seg_chunks : (chunks == 0 ? 1 : (chunks + seg_chunks - 1) / seg_chunks);
+    const uint32_t groups_total = (n + kRowsPerWave - 1) / kRowsPerWave;
+    const uint32_t group_first = blockIdx.x * kGemvWaves + wave;
+    const uint32_t group_stride = gridDim.x * kGemvWaves;
 
-    // first batch of weights goes out before x is staged
-    uint4 wv[kBatch];
-    uint32_t sv[kBatch], bv[kBatch];
+    auto load = [&](uint32_t group, uint32_t seg, GemvChunks<CPL> &buf) {
+        const uint32_t row = group * kRowsPerWave + lane / L;
+        const uint64_t row_c = row < n ? row : n - 1;  // clamped rows load, never store
+        const uint32_t c0 = seg * seg_chunks + sub;
+        const uint4 *wrow = reinterpret_cast<const uint4 *>(wq + row_c * (k / 8)) + c0;
+        const uint16_t *srow = scales + row_c * (k / kGroup);
+        const uint16_t *brow = biases + row_c * (k / kGroup);
 #pragma unroll
-    for (int u = 0; u < kBatch; ++u) {
-        const uint32_t c = sub + u * L;
-        if (c < chunks) {
-            wv[u] = wrow[c];
-            sv[u] = srow[c / 2];
-            bv[u] = brow[c / 2];
+        for (int u = 0; u < CPL; ++u) {
+            const uint32_t c = c0 + u * L;
+            if (FULL || c < chunks) {
+                buf.w[u] = wrow[u * L];
+                buf.s[u] = srow[c / 2];
+                buf.b[u] = brow[c / 2];
+            }
         }
-    }
+    };
+
+    GemvChunks<CPL> buf;
+    if (group_first < groups_total) load(group_first, 0, buf);  // in flight while x is staged
 
     // stage x: one thread per (m, chunk): four 16-byte loads, permute, sum
     for (uint32_t t = threadIdx.x; t < M * chunks; t += kGemvThreads) {
@@ -86,10 +108,10 @@ __global__ __launch_bounds__(kGemvThreads) void q4_gemv_kernel(
         for (int wi = 0; wi < 4; ++wi) {
             const uint4 v = src[wi];  // (x0,x1) (x2,x3) (x4,x5) (x6,x7)
             uint4 p;
-            p.x = (v.x & 0xFFFFu) | (v.z << 16);          // (x0, x4)
-            p.y = (v.x >> 16) | (v.z & 0xFFFF0000u);      // (x1, x5)
-            p.z = (v.y & 0xFFFFu) | (v.w << 16);          // (x2, x6)
-            p.w = (v.y >> 16) | (v.w & 0xFFFF0000u);      // (x3, x7)
+            p.x = (v.x & 0xFFFFu) | (v.z << 16);      // (x0, x4)
+            p.y = (v.x >> 16) | (v.z & 0xFFFF0000u);  // (x1, x5)
+            p.z = (v.y & 0xFFFFu) | (v.w << 16);      // (x2, x6)
+            p.w = (v.y >> 16) | (v.w & 0xFFFF0000u);  // (x3, x7)
             xs[(m * 4 + wi) * chunks + c] = p;
             sum += bf16_to_f32(v.x & 0xFFFFu) + bf16_to_f32(v.x >> 16);
             sum += bf16_to_f32(v.y & 0xFFFFu) + bf16_to_f32(v.y >> 16);
@@ -100,104 +122,128 @@ __global__ __launch_bounds__(kGemvThreads) void q4_gemv_kernel(
     }
     __syncthreads();
 
-    float acc[M];
-#pragma unroll
-    for (int m = 0; m < M; ++m) acc[m] = 0.f;
+    // The bf16 exponent constant lives in a VGPR so that mask-and-or is one
+    // v_and_or_b32 (a VOP3 on gfx9 takes no literal and at most one SGPR).
+    uint32_t magic = 0x43004300u;
+    asm volatile("" : "+v"(magic));
 
-    for (uint32_t c0 = sub; c0 < chunks; c0 += kBatch * L) {
-        // prefetch the next batch while this one is computed
-        uint4 nw[kBatch];
-        uint32_t ns[kBatch], nb[kBatch];
-        const uint32_t c1 = c0 + kBatch * L;
+    for (uint32_t group = group_first; group < groups_total; group += group_stride) {
+        float acc[M];
 #pragma unroll
-        for (int u = 0; u < kBatch; ++u) {
-            const uint32_t c = c1 + u * L;
-            if (c < chunks) {
-                nw[u] = wrow[c];
-                ns[u] = srow[c / 2];
-                nb[u] = brow[c / 2];
-            }
-        }
+        for (int m = 0; m < M; ++m) acc[m] = 0.f;
+        for (uint32_t seg = 0; seg < segs; ++seg) {
+            if (seg > 0) load(group, seg, buf);
+            const uint32_t c0 = seg * seg_chunks + sub;
 #pragma unroll
-        for (int u = 0; u < kBatch; ++u) {
-            const uint32_t c = c0 + u * L;
-            if (c < chunks) {
-                const float s = bf16_to_f32(sv[u]);
-                const float bc = fmaf(-128.f, s, bf16_to_f32(bv[u]));
-                const uint32_t words[4] = {wv[u].x, wv[u].y, wv[u].z, wv[u].w};
-                uint32_t pr[4][4];
+            for (int u = 0; u < CPL; ++u) {
+                const uint32_t c = c0 + u * L;
+                if (FULL || c < chunks) {
+                    const float s = bf16_to_f32(buf.s[u]);
+                    const float bc = fmaf(-128.f, s, bf16_to_f32(buf.b[u]));
+                    const uint32_t words[4] = {buf.w[u].x, buf.w[u].y, buf.w[u].z, buf.w[u].w};
+                    uint32_t pr[4][4];
 #pragma unroll
-                for (int wi = 0; wi < 4; ++wi)
+                    for (int wi = 0; wi < 4; ++wi)
 #pragma unroll
-                    for (int t = 0; t < 4; ++t)
-                        pr[wi][t] = ((words[wi] >> (4 * t)) & 0x000F000Fu) | 0x43004300u;
+                        for (int t = 0; t < 4; ++t)
+                            pr[wi][t] = ((words[wi] >> (4 * t)) & 0x000F000Fu) | magic;
 #pragma unroll
-                for (int m = 0; m < M; ++m) {
-                    float d0 = 0.f, d1 = 0.f;
+                    for (int m = 0; m < M; ++m) {
+                        float d0 = 0.f, d1 = 0.f;
 #pragma unroll
-                    for (int wi = 0; wi < 4; ++wi) {
-                        const uint4 xp = xs[(m * 4 + wi) * chunks + c];
-                        d0 = dot2_bf16(pr[wi][0], xp.x, d0);
-                        d1 = dot2_bf16(pr[wi][1], xp.y, d1);
-                        d0 = dot2_bf16(pr[wi][2], xp.z, d0);
-                        d1 = dot2_bf16(pr[wi][3], xp.w, d1);
+                        for (int wi = 0; wi < 4; ++wi) {
+                            const uint4 xp = xs[(m * 4 + wi) * chunks + c];
+                            d0 = dot2_bf16(pr[wi][0], xp.x, d0);
+                            d1 = dot2_bf16(pr[wi][1], xp.y, d1);
+                            d0 = dot2_bf16(pr[wi][2], xp.z, d0);
+                            d1 = dot2_bf16(pr[wi][3], xp.w, d1);
+                        }
+                        acc[m] = fmaf(s, d0 + d1, acc[m]);
+                        acc[m] = fmaf(bc, xsum[m * chunks + c], acc[m]);
                     }
-                    acc[m] = fmaf(s, d0 + d1, acc[m]);
-                    acc[m] = fmaf(bc, xsum[m * chunks + c], acc[m]);
                 }
             }
         }
-#pragma unroll
-        for (int u = 0; u < kBatch; ++u) {
-            wv[u] = nw[u];
-            sv[u] = ns[u];
-            bv[u] = nb[u];
-        }
-    }
-
-#pragma unroll
-    for (int m = 0; m < M; ++m) {
-        float v = acc[m];
-#pragma unroll
-        for (int off = L / 2; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
-        acc[m] = v;
-    }
-    if (valid && sub == 0) {
+        // next row group's loads go out before this one's reduction
+        const uint32_t next = group + group_stride;
+        if (next < groups_total) load(next, 0, buf);
 #pragma unroll
         for (int m = 0; m < M; ++m) {
-            const uint64_t o = static_cast<uint64_t>(m) * y_ld + row;
-            if (y_is_f32)
-                static_cast<float *>(y)[o] = acc[m];
-            else
-                static_cast<uint16_t *>(y)[o] = static_cast<uint16_t>(f32_to_bf16_rne(acc[m]));
+            float v = acc[m];
+#pragma unroll
+            for (int off = L / 2; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
+            acc[m] = v;
+        }
+        const uint32_t row = group * kRowsPerWave + lane / L;
+        if (row < n && sub == 0) {
+#pragma unroll
+            for (int m = 0; m < M; ++m) {
+                const uint64_t o = static_cast<uint64_t>(m) * y_ld + row;
+                if (y_is_f32)
+                    static_cast<float *>(y)[o] = acc[m];
+                else
+                    static_cast<uint16_t *>(y)[o] = static_cast<uint16_t>(f32_to_bf16_rne(acc[m]));
+            }
         }
     }
 }
 
-template <int M, int L>
-static void launch_gemv_ml(hipStream_t stream, const uint16_t *x, uint32_t x_ld,
-                           const uint32_t *wq, const uint16_t *s, const uint16_t *b, uint32_t n,
-                           uint32_t k, void *y, uint32_t y_ld, int y_is_f32) {
-    constexpr int kRowsPerBlock = (kGemvThreads / 64) * (64 / L);
-    const uint32_t blocks = (n + kRowsPerBlock - 1) / kRowsPerBlock;
-    hipLaunchKernelGGL((q4_gemv_kernel<M, L>), dim3(blocks), dim3(kGemvThreads),
-                       gemv_lds_bytes(M, k), stream, x, x_ld, wq, s, b, n, k, y, y_ld, y_is_f32);
+// Blocks of `kernel` that stay resident on one CU with `lds` bytes each,
+// capped at kGemvBlocksPerCu; a persistent grid larger than this would leave
+// the excess blocks to run after the others, as a tail.
+template <typename Kernel>
+static uint32_t resident_blocks(Kernel kernel, uint32_t lds) {
+    int per_cu = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, kGemvThreads, lds) != hipSuccess ||
+        per_cu < 1)
+        per_cu = 1;
+    return per_cu < static_cast<int>(kGemvBlocksPerCu) ? per_cu : kGemvBlocksPerCu;
 }
 
-template <int L>
-static void launch_gemv_l(int m, hipStream_t stream, const uint16_t *x, uint32_t x_ld,
-                          const uint32_t *wq, const uint16_t *s, const uint16_t *b, uint32_t n,
-                          uint32_t k, void *y, uint32_t y_ld, int y_is_f32) {
+template <int M, int L, int CPL, bool FULL>
+static void launch_gemv_full(hipStream_t stream, uint32_t cus, const uint16_t *x, uint32_t x_ld,
+                             const uint32_t *wq, const uint16_t *s, const uint16_t *b, uint32_t n,
+                             uint32_t k, void *y, uint32_t y_ld, int y_is_f32) {
+    constexpr uint32_t kRowsPerWave = 64 / L;
+    auto kernel = q4_gemv_kernel<M, L, CPL, FULL>;
+    const uint32_t lds = gemv_lds_bytes(M, k);
+    const uint32_t groups = (n + kRowsPerWave - 1) / kRowsPerWave;
+    const uint32_t need = (groups + kGemvWaves - 1) / kGemvWaves;
+    const uint32_t cap = cus * resident_blocks(kernel, lds);
+    const uint32_t blocks = need < cap ? need : cap;
+    hipLaunchKernelGGL(kernel, dim3(blocks), dim3(kGemvThreads), lds, stream, x, x_ld, wq, s, b, n,
+                       k, y, y_ld, y_is_f32);
+}
+
+template <int M, int L, int CPL>
+static void launch_gemv_mlc(hipStream_t stream, uint32_t cus, const uint16_t *x, uint32_t x_ld,
+                            const uint32_t *wq, const uint16_t *s, const uint16_t *b, uint32_t n,
+                            uint32_t k, void *y, uint32_t y_ld, int y_is_f32) {
+    const uint32_t chunks = k / 32;
+    if (chunks > 0 && chunks % (CPL * L) == 0)
+        launch_gemv_full<M, L, CPL, true>(stream, cus, x, x_ld, wq, s, b, n, k, y, y_ld, y_is_f32);
+    else
+        launch_gemv_full<M, L, CPL, false>(stream, cus, x, x_ld, wq, s, b, n, k, y, y_ld, y_is_f32);
+}
+
+template <int L, int CPL>
+static void launch_gemv_lc(int m, hipStream_t stream, uint32_t cus, const uint16_t *x,
+                           uint32_t x_ld, const uint32_t *wq, const uint16_t *s,
+                           const uint16_t *b, uint32_t n, uint32_t k, void *y, uint32_t y_ld,
+                           int y_is_f32) {
+#define FH_GEMV_CASE(MM) \
+    case MM: launch_gemv_mlc<MM, L, CPL>(stream, cus, x, x_ld, wq, s, b, n, k, y, y_ld, y_is_f32); break;
     switch (m) {
-        case 1: launch_gemv_ml<1, L>(stream, x, x_ld, wq, s, b, n, k, y, y_ld, y_is_f32); break;
-        case 2: launch_gemv_ml<2, L>(stream, x, x_ld, wq, s, b, n, k, y, y_ld, y_is_f32); break;
-        case 3: launch_gemv_ml<3, L>(stream, x, x_ld, wq, s, b, n, k, y, y_ld, y_is_f32); break;
-        case 4: launch_gemv_ml<4, L>(stream, x, x_ld, wq, s, b, n, k, y, y_ld, y_is_f32); break;
-        case 5: launch_gemv_ml<5, L>(stream, x, x_ld, wq, s, b, n, k, y, y_ld, y_is_f32); break;
-        case 6: launch_gemv_ml<6, L>(stream, x, x_ld, wq, s, b, n, k, y, y_ld, y_is_f32); break;
-        case 7: launch_gemv_ml<7, L>(stream, x, x_ld, wq, s, b, n, k, y, y_ld, y_is_f32); break;
-        default: launch_gemv_ml<8, L>(stream, x, x_ld, wq, s, b, n, k, y, y_ld, y_is_f32); break;
+        FH_GEMV_CASE(1)
+        FH_GEMV_CASE(2)
+        FH_GEMV_CASE(3)
+        FH_GEMV_CASE(4)
+        FH_GEMV_CASE(5)
+        FH_GEMV_CASE(6)
+        FH_GEMV_CASE(7)
+        default: launch_gemv_mlc<8, L, CPL>(stream, cus, x, x_ld, wq, s, b, n, k, y, y_ld, y_is_f32);
     }
+#undef FH_GEMV_CASE
 }
 
 // Largest count of x rows whose staged copy fits the LDS budget at this k.
@@ -209,17 +255,25 @@ uint32_t gemv_rows_per_launch(uint32_t k) {
 }
 
 // Launches the GEMV for m in [1, 8] rows of x whose staged copy fits LDS;
-// the caller splits larger m (see gemv_rows_per_launch).
-void launch_q4_gemv(hipStream_t stream, int m, const uint16_t *x, uint32_t x_ld,
+// the caller splits larger m (see gemv_rows_per_launch). Lanes per row L and
+// chunks per lane CPL follow k: a row group's loads cover K in as few
+// segments as possible with at most 8 chunks (128 bytes) per lane.
+void launch_q4_gemv(hipStream_t stream, uint32_t cus, int m, const uint16_t *x, uint32_t x_ld,
                     const uint32_t *wq, const uint16_t *s, const uint16_t *b, uint32_t n,
                     uint32_t k, void *y, uint32_t y_ld, int y_is_f32) {
     const uint32_t chunks = k / 32;
-    if (chunks <= 128)
-        launch_gemv_l<16>(m, stream, x, x_ld, wq, s, b, n, k, y, y_ld, y_is_f32);
-    else if (chunks <= 256)
-        launch_gemv_l<32>(m, stream, x, x_ld, wq, s, b, n, k, y, y_ld, y_is_f32);
+    if (chunks <= 16 * 2)
+        launch_gemv_lc<16, 2>(m, stream, cus, x, x_ld, wq, s, b, n, k, y, y_ld, y_is_f32);
+    else if (chunks <= 16 * 4)
+        launch_gemv_lc<16, 4>(m, stream, cus, x, x_ld, wq, s, b, n, k, y, y_ld, y_is_f32);
+    else if (chunks <= 16 * 6)
+        launch_gemv_lc<16, 6>(m, stream, cus, x, x_ld, wq, s, b, n, k, y, y_ld, y_is_f32);
+    else if (chunks <= 16 * 8)
+        launch_gemv_lc<16, 8>(m, stream, cus, x, x_ld, wq, s, b, n, k, y, y_ld, y_is_f32);
+    else if (chunks <= 32 * 8)
+        launch_gemv_lc<32, 8>(m, stream, cus, x, x_ld, wq, s, b, n, k, y, y_ld, y_is_f32);
     else
-        launch_gemv_l<64>(m, stream, x, x_ld, wq, s, b, n, k, y, y_ld, y_is_f32);
+        launch_gemv_lc<64, 8>(m, stream, cus, x, x_ld, wq, s, b, n, k, y, y_ld, y_is_f32);
 }
 
 }  // namespace fh

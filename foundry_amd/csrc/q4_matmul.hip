@@ -12,7 +12,7 @@ namespace fh {
 int check_q4_table(const fh_device *dev, const char *fn, const uint32_t *wq,
                    const uint16_t *scales, const uint16_t *biases, int64_t rows, int64_t k,
                    int64_t group);
-void launch_q4_gemv(hipStream_t stream, int m, const uint16_t *x, uint32_t x_ld,
+void launch_q4_gemv(hipStream_t stream, uint32_t cus, int m, const uint16_t *x, uint32_t x_ld,
                     const uint32_t *wq, const uint16_t *s, const uint16_t *b, uint32_t n,
                     uint32_t k, void *y, uint32_t y_ld, int y_is_f32);
 uint32_t gemv_rows_per_launch(uint32_t k);
@@ -69,7 +69,7 @@ extern "C" int fh_q4_matmul(fh_device *dev, const uint16_t *x, int64_t m, int64_
             void *yr = y_is_f32 ? static_cast<void *>(static_cast<float *>(y) + r0 * n)
                                 : static_cast<void *>(static_cast<uint16_t *>(y) + r0 * n);
             int rc = dispatch(dev, fn, [&] {
-                launch_q4_gemv(dev->stream, rows, xr, ld32, wq, scales, biases, n32, k32, yr, n32,
+                launch_q4_gemv(dev->stream, dev->compute_units, rows, xr, ld32, wq, scales, biases, n32, k32, yr, n32,
                                y_is_f32);
             });
             if (rc) return rc;
