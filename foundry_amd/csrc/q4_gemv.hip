@@ -1,250 +1,9 @@
-// q4 decode GEMV: y[m, r] = sum_j x[m, j] * (s[r, j/64] * q[r, j] + b[r, j/64])
-// for m < 8 rows of x. Replaces the M=1..8 use of matmul_tiled
-// (src/metal/kernels/matmul.metal:29-65) behind Linear::forward
-// (src/nn/linear.rs:22-35), where 15 of 16 thread rows idle at M=1.
-//
-// HBM-bound: per weight 0.5 byte of nibbles plus 4 bytes of scale+bias per 64.
-// Design for CDNA4:
-// - A lane owns 16-byte chunks (32 weights, half a group) of one weight row;
-//   L lanes share a row, chunk c = sub + L*i, so each load instruction of an
-//   L-lane row group reads 16*L contiguous bytes. A wavefront covers 64/L
-//   rows at once (a "row group").
-// - Blocks are persistent: the grid is sized to the chip (8 blocks of 4
-//   wavefronts per CU), each block stages x once and its wavefronts walk row
-//   groups with a stride. A lane issues all CPL chunk loads of a row group at
-//   once, and the next row group's loads before the current one's reduction;
-//   latency is hidden by occupancy (one register buffer keeps VGPRs low).
-// - x is staged into LDS, permuted so that the bf16 pair for nibbles
-//   (e, e+4) of a word is one dword, and laid out [m][word-in-chunk][chunk]
-//   so neighbouring lanes read neighbouring 16 bytes (no bank conflicts).
-//   Per-chunk sums of x are staged beside it.
-// - Dequantisation in registers without conversions: (w >> 4t) & 0x000F000F
-//   | 0x43004300 is a bf16 pair (128 + q_t, 128 + q_{t+4}), exact since q < 16;
-//   v_dot2_f32_bf16 multiplies it with the x pair and accumulates in fp32.
-//   Per chunk: sum_j x_j (s q_j + b) = s * d + (b - 128 s) * X, with
-//   d = sum_j x_j (128 + q_j) and X = sum_j x_j.
-// - Partial sums are reduced across the L lanes of a row with cross-lane
-//   shuffles; one lane writes each output (bf16 RNE or fp32).
-#include "device.hpp"
-#include "q4_common.hpp"
+// Shape selection and dispatch of the q4 decode GEMV (kernel in q4_gemv.hpp;
+// one translation unit per row count, q4_gemv_m<M>.hip, so they build in
+// parallel).
+#include "q4_gemv.hpp"
 
 namespace fh {
-
-constexpr int kGemvThreads = 256;
-constexpr int kGemvWaves = kGemvThreads / 64;
-// Dynamic LDS one block may use for staged x (bytes).
-constexpr uint32_t kGemvLdsLimit = 64 * 1024;
-// Persistent blocks per CU.
-constexpr uint32_t kGemvBlocksPerCu = 8;
-
-typedef __attribute__((ext_vector_type(2))) __bf16 bf16x2_t;
-
-__device__ __forceinline__ float dot2_bf16(uint32_t a, uint32_t b, float c) {
-    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, a),
-                                           __builtin_bit_cast(bf16x2_t, b), c, false);
-}
-
-// Bytes of LDS the kernel needs for `m` rows of x with k columns.
-__host__ __device__ constexpr uint32_t gemv_lds_bytes(uint32_t m, uint32_t k) {
-    return m * (k / 32) * (4 * 16 + 4);
-}
-
-// One lane's chunks of one row group: packed words and the group scale/bias.
-template <int CPL>
-struct GemvChunks {
-    uint4 w[CPL];
-    uint32_t s[CPL], b[CPL];
-};
-
-// FULL: every lane's CPL chunks exist (k is a multiple of 32*CPL*L), so the
-// loads need no per-chunk guard and share one address with immediate offsets.
-template <int M, int L, int CPL, bool FULL>
-__global__ __launch_bounds__(kGemvThreads) void q4_gemv_kernel(
-    const uint16_t *__restrict__ x, uint32_t x_ld, const uint32_t *__restrict__ wq,
-    const uint16_t *__restrict__ scales, const uint16_t *__restrict__ biases, uint32_t n,
-    uint32_t k, void *__restrict__ y, uint32_t y_ld, int y_is_f32) {
-    constexpr uint32_t kRowsPerWave = 64 / L;
-    extern __shared__ uint4 lds[];
-    const uint32_t chunks = k / 32;
-    uint4 *xs = lds;                                                // [M][4][chunks]
-    float *xsum = reinterpret_cast<float *>(lds + M * 4 * chunks);  // [M][chunks]
-
-    const uint32_t lane = threadIdx.x & 63;
-    const uint32_t wave = threadIdx.x >> 6;
-    const uint32_t sub = lane % L;
-    const uint32_t seg_chunks = CPL * L;
-    const uint32_t segs = FULL ? chunks / seg_chunks : (chunks == 0 ? 1 : (chunks + seg_chunks - 1) / seg_chunks);
-    const uint32_t groups_total = (n + kRowsPerWave - 1) / kRowsPerWave;
-    const uint32_t group_first = blockIdx.x * kGemvWaves + wave;
-    const uint32_t group_stride = gridDim.x * kGemvWaves;
-
-    auto load = [&](uint32_t group, uint32_t seg, GemvChunks<CPL> &buf) {
-        const uint32_t row = group * kRowsPerWave + lane / L;
-        const uint64_t row_c = row < n ? row : n - 1;  // clamped rows load, never store
-        const uint32_t c0 = seg * seg_chunks + sub;
-        const uint4 *wrow = reinterpret_cast<const uint4 *>(wq + row_c * (k / 8)) + c0;
-        const uint16_t *srow = scales + row_c * (k / kGroup);
-        const uint16_t *brow = biases + row_c * (k / kGroup);
-#pragma unroll
-        for (int u = 0; u < CPL; ++u) {
-            const uint32_t c = c0 + u * L;
-            if (FULL || c < chunks) {
-                buf.w[u] = wrow[u * L];
-                buf.s[u] = srow[c / 2];
-                buf.b[u] = brow[c / 2];
-            }
-        }
-    };
-
-    GemvChunks<CPL> buf;
-    if (group_first < groups_total) load(group_first, 0, buf);  // in flight while x is staged
-
-    // stage x: one thread per (m, chunk): four 16-byte loads, permute, sum
-    for (uint32_t t = threadIdx.x; t < M * chunks; t += kGemvThreads) {
-        const uint32_t m = t / chunks, c = t % chunks;
-        const uint4 *src = reinterpret_cast<const uint4 *>(x + static_cast<uint64_t>(m) * x_ld + c * 32);
-        float sum = 0.f;
-#pragma unroll
-        for (int wi = 0; wi < 4; ++wi) {
-            const uint4 v = src[wi];  // (x0,x1) (x2,x3) (x4,x5) (x6,x7)
-            uint4 p;
-            p.x = (v.x & 0xFFFFu) | (v.z << 16);      // (x0, x4)
-            p.y = (v.x >> 16) | (v.z & 0xFFFF0000u);  // (x1, x5)
-            p.z = (v.y & 0xFFFFu) | (v.w << 16);      // (x2, x6)
-            p.w = (v.y >> 16) | (v.w & 0xFFFF0000u);  // (x3, x7)
-            xs[(m * 4 + wi) * chunks + c] = p;
-            sum += bf16_to_f32(v.x & 0xFFFFu) + bf16_to_f32(v.x >> 16);
-            sum += bf16_to_f32(v.y & 0xFFFFu) + bf16_to_f32(v.y >> 16);
-            sum += bf16_to_f32(v.z & 0xFFFFu) + bf16_to_f32(v.z >> 16);
-            sum += bf16_to_f32(v.w & 0xFFFFu) + bf16_to_f32(v.w >> 16);
-        }
-        xsum[m * chunks + c] = sum;
-    }
-    __syncthreads();
-
-    // The bf16 exponent constant lives in a VGPR so that mask-and-or is one
-    // v_and_or_b32 (a VOP3 on gfx9 takes no literal and at most one SGPR).
-    uint32_t magic = 0x43004300u;
-    asm volatile("" : "+v"(magic));
-
-    for (uint32_t group = group_first; group < groups_total; group += group_stride) {
-        float acc[M];
-#pragma unroll
-        for (int m = 0; m < M; ++m) acc[m] = 0.f;
-        for (uint32_t seg = 0; seg < segs; ++seg) {
-            if (seg > 0) load(group, seg, buf);
-            const uint32_t c0 = seg * seg_chunks + sub;
-#pragma unroll
-            for (int u = 0; u < CPL; ++u) {
-                const uint32_t c = c0 + u * L;
-                if (FULL || c < chunks) {
-                    const float s = bf16_to_f32(buf.s[u]);
-                    const float bc = fmaf(-128.f, s, bf16_to_f32(buf.b[u]));
-                    const uint32_t words[4] = {buf.w[u].x, buf.w[u].y, buf.w[u].z, buf.w[u].w};
-                    uint32_t pr[4][4];
-#pragma unroll
-                    for (int wi = 0; wi < 4; ++wi)
-#pragma unroll
-                        for (int t = 0; t < 4; ++t)
-                            pr[wi][t] = ((words[wi] >> (4 * t)) & 0x000F000Fu) | magic;
-#pragma unroll
-                    for (int m = 0; m < M; ++m) {
-                        float d0 = 0.f, d1 = 0.f;
-#pragma unroll
-                        for (int wi = 0; wi < 4; ++wi) {
-                            const uint4 xp = xs[(m * 4 + wi) * chunks + c];
-                            d0 = dot2_bf16(pr[wi][0], xp.x, d0);
-                            d1 = dot2_bf16(pr[wi][1], xp.y, d1);
-                            d0 = dot2_bf16(pr[wi][2], xp.z, d0);
-                            d1 = dot2_bf16(pr[wi][3], xp.w, d1);
-                        }
-                        acc[m] = fmaf(s, d0 + d1, acc[m]);
-                        acc[m] = fmaf(bc, xsum[m * chunks + c], acc[m]);
-                    }
-                }
-            }
-        }
-        // next row group's loads go out before this one's reduction
-        const uint32_t next = group + group_stride;
-        if (next < groups_total) load(next, 0, buf);
-#pragma unroll
-        for (int m = 0; m < M; ++m) {
-            float v = acc[m];
-#pragma unroll
-            for (int off = L / 2; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
-            acc[m] = v;
-        }
-        const uint32_t row = group * kRowsPerWave + lane / L;
-        if (row < n && sub == 0) {
-#pragma unroll
-            for (int m = 0; m < M; ++m) {
-                const uint64_t o = static_cast<uint64_t>(m) * y_ld + row;
-                if (y_is_f32)
-                    static_cast<float *>(y)[o] = acc[m];
-                else
-                    static_cast<uint16_t *>(y)[o] = static_cast<uint16_t>(f32_to_bf16_rne(acc[m]));
-            }
-        }
-    }
-}
-
-// Blocks of `kernel` that stay resident on one CU with `lds` bytes each,
-// capped at kGemvBlocksPerCu; a persistent grid larger than this would leave
-// the excess blocks to run after the others, as a tail.
-template <typename Kernel>
-static uint32_t resident_blocks(Kernel kernel, uint32_t lds) {
-    int per_cu = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, kGemvThreads, lds) != hipSuccess ||
-        per_cu < 1)
-        per_cu = 1;
-    return per_cu < static_cast<int>(kGemvBlocksPerCu) ? per_cu : kGemvBlocksPerCu;
-}
-
-template <int M, int L, int CPL, bool FULL>
-static void launch_gemv_full(hipStream_t stream, uint32_t cus, const uint16_t *x, uint32_t x_ld,
-                             const uint32_t *wq, const uint16_t *s, const uint16_t *b, uint32_t n,
-                             uint32_t k, void *y, uint32_t y_ld, int y_is_f32) {
-    constexpr uint32_t kRowsPerWave = 64 / L;
-    auto kernel = q4_gemv_kernel<M, L, CPL, FULL>;
-    const uint32_t lds = gemv_lds_bytes(M, k);
-    const uint32_t groups = (n + kRowsPerWave - 1) / kRowsPerWave;
-    const uint32_t need = (groups + kGemvWaves - 1) / kGemvWaves;
-    const uint32_t cap = cus * resident_blocks(kernel, lds);
-    const uint32_t blocks = need < cap ? need : cap;
-    hipLaunchKernelGGL(kernel, dim3(blocks), dim3(kGemvThreads), lds, stream, x, x_ld, wq, s, b, n,
-                       k, y, y_ld, y_is_f32);
-}
-
-template <int M, int L, int CPL>
-static void launch_gemv_mlc(hipStream_t stream, uint32_t cus, const uint16_t *x, uint32_t x_ld,
-                            const uint32_t *wq, const uint16_t *s, const uint16_t *b, uint32_t n,
-                            uint32_t k, void *y, uint32_t y_ld, int y_is_f32) {
-    const uint32_t chunks = k / 32;
-    if (chunks > 0 && chunks % (CPL * L) == 0)
-        launch_gemv_full<M, L, CPL, true>(stream, cus, x, x_ld, wq, s, b, n, k, y, y_ld, y_is_f32);
-    else
-        launch_gemv_full<M, L, CPL, false>(stream, cus, x, x_ld, wq, s, b, n, k, y, y_ld, y_is_f32);
-}
-
-template <int L, int CPL>
-static void launch_gemv_lc(int m, hipStream_t stream, uint32_t cus, const uint16_t *x,
-                           uint32_t x_ld, const uint32_t *wq, const uint16_t *s,
-                           const uint16_t *b, uint32_t n, uint32_t k, void *y, uint32_t y_ld,
-                           int y_is_f32) {
-#define FH_GEMV_CASE(MM) \
-    case MM: launch_gemv_mlc<MM, L, CPL>(stream, cus, x, x_ld, wq, s, b, n, k, y, y_ld, y_is_f32); break;
-    switch (m) {
-        FH_GEMV_CASE(1)
-        FH_GEMV_CASE(2)
-        FH_GEMV_CASE(3)
-        FH_GEMV_CASE(4)
-        FH_GEMV_CASE(5)
-        FH_GEMV_CASE(6)
-        FH_GEMV_CASE(7)
-        default: launch_gemv_mlc<8, L, CPL>(stream, cus, x, x_ld, wq, s, b, n, k, y, y_ld, y_is_f32);
-    }
-#undef FH_GEMV_CASE
-}
 
 // Largest count of x rows whose staged copy fits the LDS budget at this k.
 uint32_t gemv_rows_per_launch(uint32_t k) {
@@ -254,26 +13,59 @@ uint32_t gemv_rows_per_launch(uint32_t k) {
     return r > 8 ? 8 : r;
 }
 
+struct GemvShape {
+    uint32_t lanes, cpl;
+};
+#define FH_GEMV_SHAPE_ENTRY(LL, CC) {LL, CC},
+constexpr GemvShape kGemvShapes[] = {FH_GEMV_SHAPES(FH_GEMV_SHAPE_ENTRY)};
+#undef FH_GEMV_SHAPE_ENTRY
+
+// Picks the shape for k and n. Preferred: one segment covers K exactly (no
+// guards, one pass). Among those, the fewest lanes per row that still gives
+// at least 16 wavefronts per CU (less reduction work per output); for small n,
+// the most lanes per row (more, shorter wavefronts: a shorter compute tail).
+// Otherwise 64 lanes x 8 chunks, walking K in segments.
+static GemvShape pick_gemv_shape(uint32_t n, uint32_t k, uint32_t cus) {
+    const uint32_t chunks = k / 32;
+    const GemvShape *best = nullptr;
+    for (const GemvShape &sh : kGemvShapes) {
+        if (chunks == 0 || chunks != sh.lanes * sh.cpl) continue;
+        const uint64_t waves = (static_cast<uint64_t>(n) * sh.lanes + 63) / 64;
+        if (best == nullptr) {
+            best = &sh;
+            continue;
+        }
+        const uint64_t best_waves = (static_cast<uint64_t>(n) * best->lanes + 63) / 64;
+        const bool enough = waves >= 16ull * cus, best_enough = best_waves >= 16ull * cus;
+        if (enough && (!best_enough || sh.lanes < best->lanes)) best = &sh;
+        else if (!enough && !best_enough && sh.lanes > best->lanes) best = &sh;
+    }
+    if (best) return *best;
+    if (chunks <= 32) return {16, 2};
+    return {64, 8};
+}
+
 // Launches the GEMV for m in [1, 8] rows of x whose staged copy fits LDS;
-// the caller splits larger m (see gemv_rows_per_launch). Lanes per row L and
-// chunks per lane CPL follow k: a row group's loads cover K in as few
-// segments as possible with at most 8 chunks (128 bytes) per lane.
+// the caller splits larger m (see gemv_rows_per_launch).
 void launch_q4_gemv(hipStream_t stream, uint32_t cus, int m, const uint16_t *x, uint32_t x_ld,
                     const uint32_t *wq, const uint16_t *s, const uint16_t *b, uint32_t n,
                     uint32_t k, void *y, uint32_t y_ld, int y_is_f32) {
-    const uint32_t chunks = k / 32;
-    if (chunks <= 16 * 2)
-        launch_gemv_lc<16, 2>(m, stream, cus, x, x_ld, wq, s, b, n, k, y, y_ld, y_is_f32);
-    else if (chunks <= 16 * 4)
-        launch_gemv_lc<16, 4>(m, stream, cus, x, x_ld, wq, s, b, n, k, y, y_ld, y_is_f32);
-    else if (chunks <= 16 * 6)
-        launch_gemv_lc<16, 6>(m, stream, cus, x, x_ld, wq, s, b, n, k, y, y_ld, y_is_f32);
-    else if (chunks <= 16 * 8)
-        launch_gemv_lc<16, 8>(m, stream, cus, x, x_ld, wq, s, b, n, k, y, y_ld, y_is_f32);
-    else if (chunks <= 32 * 8)
-        launch_gemv_lc<32, 8>(m, stream, cus, x, x_ld, wq, s, b, n, k, y, y_ld, y_is_f32);
-    else
-        launch_gemv_lc<64, 8>(m, stream, cus, x, x_ld, wq, s, b, n, k, y, y_ld, y_is_f32);
+    const GemvShape sh = pick_gemv_shape(n, k, cus);
+#define FH_GEMV_M(MM)                                                                             \
+    case MM:                                                                                      \
+        launch_gemv_m<MM>(sh.lanes, sh.cpl, stream, cus, x, x_ld, wq, s, b, n, k, y, y_ld, y_is_f32); \
+        break;
+    switch (m) {
+        FH_GEMV_M(1)
+        FH_GEMV_M(2)
+        FH_GEMV_M(3)
+        FH_GEMV_M(4)
+        FH_GEMV_M(5)
+        FH_GEMV_M(6)
+        FH_GEMV_M(7)
+        default: launch_gemv_m<8>(sh.lanes, sh.cpl, stream, cus, x, x_ld, wq, s, b, n, k, y, y_ld, y_is_f32);
+    }
+#undef FH_GEMV_M
 }
 
 }  // namespace fh

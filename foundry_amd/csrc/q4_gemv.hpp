@@ -1,0 +1,258 @@
+// q4 decode GEMV: y[m, r] = sum_j x[m, j] * (s[r, j/64] * q[r, j] + b[r, j/64])
+// for m < 8 rows of x. Replaces the M=1..8 use of matmul_tiled
+// (src/metal/kernels/matmul.metal:29-65) behind Linear::forward
+// (src/nn/linear.rs:22-35), where 15 of 16 thread rows idle at M=1.
+//
+// HBM-bound: per weight 0.5 byte of nibbles plus 4 bytes of scale+bias per 64.
+// Design for CDNA4:
+// - A lane owns 16-byte chunks (32 weights, half a group) of one weight row;
+//   L lanes share a row, chunk c = sub + L*i, so each load instruction of an
+//   L-lane row group reads 16*L contiguous bytes. A wavefront covers 64/L
+//   rows at once (a "row group").
+// - Blocks are persistent: the grid is sized to the chip (8 blocks of 4
+//   wavefronts per CU), each block stages x once and its wavefronts walk row
+//   groups with a stride. A lane issues all CPL chunk loads of a row group at
+//   once, and the next row group's loads before the current one's reduction;
+//   latency is hidden by occupancy (one register buffer keeps VGPRs low).
+// - x is staged into LDS, permuted so that the bf16 pair for nibbles
+//   (e, e+4) of a word is one dword, and laid out [m][word-in-chunk][chunk]
+//   so neighbouring lanes read neighbouring 16 bytes (no bank conflicts).
+//   Per-chunk sums of x are staged beside it.
+// - Dequantisation in registers without conversions: (w >> 4t) & 0x000F000F
+//   | 0x43004300 is a bf16 pair (128 + q_t, 128 + q_{t+4}), exact since q < 16;
+//   v_dot2_f32_bf16 multiplies it with the x pair and accumulates in fp32.
+//   Per chunk: sum_j x_j (s q_j + b) = s * d + (b - 128 s) * X, with
+//   d = sum_j x_j (128 + q_j) and X = sum_j x_j.
+// - Partial sums are reduced across the L lanes of a row with cross-lane
+//   shuffles; one lane writes each output (bf16 RNE or fp32).
+#pragma once
+
+#include "device.hpp"
+#include "q4_common.hpp"
+
+namespace fh {
+
+constexpr int kGemvThreads = 256;
+constexpr int kGemvWaves = kGemvThreads / 64;
+// Dynamic LDS one block may use for staged x (bytes).
+constexpr uint32_t kGemvLdsLimit = 64 * 1024;
+// Persistent blocks per CU.
+constexpr uint32_t kGemvBlocksPerCu = 8;
+
+typedef __attribute__((ext_vector_type(2))) __bf16 bf16x2_t;
+
+__device__ __forceinline__ float dot2_bf16(uint32_t a, uint32_t b, float c) {
+    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, a),
+                                           __builtin_bit_cast(bf16x2_t, b), c, false);
+}
+
+// Bytes of LDS the kernel needs for `m` rows of x with k columns.
+__host__ __device__ constexpr uint32_t gemv_lds_bytes(uint32_t m, uint32_t k) {
+    return m * (k / 32) * (4 * 16 + 4);
+}
+
+// One lane's chunks of one row group: packed words and the group scale/bias.
+template <int CPL>
+struct GemvChunks {
+    uint4 w[CPL];
+    uint32_t s[CPL], b[CPL];
+};
+
+// FULL: every lane's CPL chunks exist (k is a multiple of 32*CPL*L), so the
+// loads need no per-chunk guard and share one address with immediate offsets.
+template <int M, int L, int CPL, bool FULL>
+__global__ __launch_bounds__(kGemvThreads) void q4_gemv_kernel(
+    const uint16_t *__restrict__ x, uint32_t x_ld, const uint32_t *__restrict__ wq,
+    const uint16_t *__restrict__ scales, const uint16_t *__restrict__ biases, uint32_t n,
+    uint32_t k, void *__restrict__ y, uint32_t y_ld, int y_is_f32) {
+    constexpr uint32_t kRowsPerWave = 64 / L;
+    extern __shared__ uint4 lds[];
+    const uint32_t chunks = k / 32;
+    uint4 *xs = lds;                                                // [M][4][chunks]
+    float *xsum = reinterpret_cast<float *>(lds + M * 4 * chunks);  // [M][chunks]
+
+    const uint32_t lane = threadIdx.x & 63;
+    const uint32_t wave = threadIdx.x >> 6;
+    const uint32_t sub = lane % L;
+    const uint32_t seg_chunks = CPL * L;
+    const uint32_t segs = FULL ? chunks / seg_chunks : (chunks == 0 ? 1 : (chunks + seg_chunks - 1) / seg_chunks);
+    const uint32_t groups_total = (n + kRowsPerWave - 1) / kRowsPerWave;
+    const uint32_t group_first = blockIdx.x * kGemvWaves + wave;
+    const uint32_t group_stride = gridDim.x * kGemvWaves;
+
+    auto load = [&](uint32_t group, uint32_t seg, GemvChunks<CPL> &buf) {
+        const uint32_t row = group * kRowsPerWave + lane / L;
+        const uint64_t row_c = row < n ? row : n - 1;  // clamped rows load, never store
+        const uint32_t c0 = seg * seg_chunks + sub;
+        const uint4 *wrow = reinterpret_cast<const uint4 *>(wq + row_c * (k / 8)) + c0;
+        const uint16_t *srow = scales + row_c * (k / kGroup);
+        const uint16_t *brow = biases + row_c * (k / kGroup);
+#pragma unroll
+        for (int u = 0; u < CPL; ++u) {
+            const uint32_t c = c0 + u * L;
+            if (FULL || c < chunks) {
+                buf.w[u] = wrow[u * L];
+                buf.s[u] = srow[c / 2];
+                buf.b[u] = brow[c / 2];
+            }
+        }
+    };
+
+    // Stage x: one thread per (m, chunk): four 16-byte loads, permute, sum.
+    // The first item's x loads go out before the weight loads so that waiting
+    // for x (in-order load counters) does not wait for the weights; chunk 0 of
+    // the weights is then computed while later chunks are still arriving.
+    auto stage = [&](uint32_t t, const uint4 (&v)[4]) {
+        const uint32_t m = t / chunks, c = t % chunks;
+        float sum = 0.f;
+#pragma unroll
+        for (int wi = 0; wi < 4; ++wi) {  // v[wi] = (x0,x1) (x2,x3) (x4,x5) (x6,x7)
+            uint4 p;
+            p.x = (v[wi].x & 0xFFFFu) | (v[wi].z << 16);      // (x0, x4)
+            p.y = (v[wi].x >> 16) | (v[wi].z & 0xFFFF0000u);  // (x1, x5)
+            p.z = (v[wi].y & 0xFFFFu) | (v[wi].w << 16);      // (x2, x6)
+            p.w = (v[wi].y >> 16) | (v[wi].w & 0xFFFF0000u);  // (x3, x7)
+            xs[(m * 4 + wi) * chunks + c] = p;
+            sum += bf16_to_f32(v[wi].x & 0xFFFFu) + bf16_to_f32(v[wi].x >> 16);
+            sum += bf16_to_f32(v[wi].y & 0xFFFFu) + bf16_to_f32(v[wi].y >> 16);
+            sum += bf16_to_f32(v[wi].z & 0xFFFFu) + bf16_to_f32(v[wi].z >> 16);
+            sum += bf16_to_f32(v[wi].w & 0xFFFFu) + bf16_to_f32(v[wi].w >> 16);
+        }
+        xsum[m * chunks + c] = sum;
+    };
+    auto load_x = [&](uint32_t t, uint4 (&v)[4]) {
+        const uint32_t m = t / chunks, c = t % chunks;
+        const uint4 *src = reinterpret_cast<const uint4 *>(x + static_cast<uint64_t>(m) * x_ld + c * 32);
+#pragma unroll
+        for (int wi = 0; wi < 4; ++wi) v[wi] = src[wi];
+    };
+
+    const uint32_t items_x = M * chunks;
+    uint4 xv[4];
+    if (threadIdx.x < items_x) load_x(threadIdx.x, xv);
+    GemvChunks<CPL> buf;
+    if (group_first < groups_total) load(group_first, 0, buf);
+    if (threadIdx.x < items_x) stage(threadIdx.x, xv);
+    for (uint32_t t = threadIdx.x + kGemvThreads; t < items_x; t += kGemvThreads) {
+        load_x(t, xv);
+        stage(t, xv);
+    }
+    __syncthreads();
+
+    // The bf16 exponent constant lives in a VGPR so that mask-and-or is one
+    // v_and_or_b32 (a VOP3 on gfx9 takes no literal and at most one SGPR).
+    uint32_t magic = 0x43004300u;
+    asm volatile("" : "+v"(magic));
+
+    for (uint32_t group = group_first; group < groups_total; group += group_stride) {
+        float acc[M];
+#pragma unroll
+        for (int m = 0; m < M; ++m) acc[m] = 0.f;
+        for (uint32_t seg = 0; seg < segs; ++seg) {
+            if (seg > 0) load(group, seg, buf);
+            const uint32_t c0 = seg * seg_chunks + sub;
+#pragma unroll
+            for (int u = 0; u < CPL; ++u) {
+                const uint32_t c = c0 + u * L;
+                if (FULL || c < chunks) {
+                    const float s = bf16_to_f32(buf.s[u]);
+                    const float bc = fmaf(-128.f, s, bf16_to_f32(buf.b[u]));
+                    const uint32_t words[4] = {buf.w[u].x, buf.w[u].y, buf.w[u].z, buf.w[u].w};
+                    uint32_t pr[4][4];
+#pragma unroll
+                    for (int wi = 0; wi < 4; ++wi)
+#pragma unroll
+                        for (int t = 0; t < 4; ++t)
+                            pr[wi][t] = ((words[wi] >> (4 * t)) & 0x000F000Fu) | magic;
+#pragma unroll
+                    for (int m = 0; m < M; ++m) {
+                        float d0 = 0.f, d1 = 0.f;
+#pragma unroll
+                        for (int wi = 0; wi < 4; ++wi) {
+                            const uint4 xp = xs[(m * 4 + wi) * chunks + c];
+                            d0 = dot2_bf16(pr[wi][0], xp.x, d0);
+                            d1 = dot2_bf16(pr[wi][1], xp.y, d1);
+                            d0 = dot2_bf16(pr[wi][2], xp.z, d0);
+                            d1 = dot2_bf16(pr[wi][3], xp.w, d1);
+                        }
+                        acc[m] = fmaf(s, d0 + d1, acc[m]);
+                        acc[m] = fmaf(bc, xsum[m * chunks + c], acc[m]);
+                    }
+                }
+            }
+        }
+        // next row group's loads go out before this one's reduction
+        const uint32_t next = group + group_stride;
+        if (next < groups_total) load(next, 0, buf);
+#pragma unroll
+        for (int m = 0; m < M; ++m) {
+            float v = acc[m];
+#pragma unroll
+            for (int off = L / 2; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
+            acc[m] = v;
+        }
+        const uint32_t row = group * kRowsPerWave + lane / L;
+        if (row < n && sub == 0) {
+#pragma unroll
+            for (int m = 0; m < M; ++m) {
+                const uint64_t o = static_cast<uint64_t>(m) * y_ld + row;
+                if (y_is_f32)
+                    static_cast<float *>(y)[o] = acc[m];
+                else
+                    static_cast<uint16_t *>(y)[o] = static_cast<uint16_t>(f32_to_bf16_rne(acc[m]));
+            }
+        }
+    }
+}
+
+// Blocks of `kernel` that stay resident on one CU with `lds` bytes each,
+// capped at kGemvBlocksPerCu; a persistent grid larger than this would leave
+// the excess blocks to run after the others, as a tail.
+template <typename Kernel>
+inline uint32_t resident_blocks(Kernel kernel, uint32_t lds) {
+    int per_cu = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, kGemvThreads, lds) != hipSuccess ||
+        per_cu < 1)
+        per_cu = 1;
+    return per_cu < static_cast<int>(kGemvBlocksPerCu) ? per_cu : kGemvBlocksPerCu;
+}
+
+template <int M, int L, int CPL, bool FULL>
+inline void launch_gemv_full(hipStream_t stream, uint32_t cus, const uint16_t *x, uint32_t x_ld,
+                             const uint32_t *wq, const uint16_t *s, const uint16_t *b, uint32_t n,
+                             uint32_t k, void *y, uint32_t y_ld, int y_is_f32) {
+    constexpr uint32_t kRowsPerWave = 64 / L;
+    auto kernel = q4_gemv_kernel<M, L, CPL, FULL>;
+    const uint32_t lds = gemv_lds_bytes(M, k);
+    const uint32_t groups = (n + kRowsPerWave - 1) / kRowsPerWave;
+    const uint32_t need = (groups + kGemvWaves - 1) / kGemvWaves;
+    const uint32_t cap = cus * resident_blocks(kernel, lds);
+    const uint32_t blocks = need < cap ? need : cap;
+    hipLaunchKernelGGL(kernel, dim3(blocks), dim3(kGemvThreads), lds, stream, x, x_ld, wq, s, b, n,
+                       k, y, y_ld, y_is_f32);
+}
+
+template <int M, int L, int CPL>
+inline void launch_gemv_mlc(hipStream_t stream, uint32_t cus, const uint16_t *x, uint32_t x_ld,
+                            const uint32_t *wq, const uint16_t *s, const uint16_t *b, uint32_t n,
+                            uint32_t k, void *y, uint32_t y_ld, int y_is_f32) {
+    const uint32_t chunks = k / 32;
+    if (chunks > 0 && chunks % (CPL * L) == 0)
+        launch_gemv_full<M, L, CPL, true>(stream, cus, x, x_ld, wq, s, b, n, k, y, y_ld, y_is_f32);
+    else
+        launch_gemv_full<M, L, CPL, false>(stream, cus, x, x_ld, wq, s, b, n, k, y, y_ld, y_is_f32);
+}
+
+// (lanes per row, chunks per lane) shapes the kernels are built for; X lists
+// them for the per-row-count translation units and the dispatcher.
+#define FH_GEMV_SHAPES(X) \
+    X(16, 2) X(16, 4) X(16, 6) X(16, 8) X(32, 3) X(32, 4) X(32, 8) X(64, 2) X(64, 4) X(64, 7) X(64, 8)
+
+// Defined in q4_gemv_m<M>.hip: launches the M-row GEMV with the given shape.
+template <int M>
+void launch_gemv_m(uint32_t lanes, uint32_t cpl, hipStream_t stream, uint32_t cus,
+                   const uint16_t *x, uint32_t x_ld, const uint32_t *wq, const uint16_t *s,
+                   const uint16_t *b, uint32_t n, uint32_t k, void *y, uint32_t y_ld,
+                   int y_is_f32);
+
+}  // namespace fh
