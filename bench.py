@@ -172,6 +172,43 @@ def cpu_baseline(seconds: float = 12.0):
     return out, cpu
 
 
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "q4_gemv_8192x3072_traffic.md")
+
+
+def measured_traffic():
+    """HBM bytes per launch of the headline GEMV, from the committed
+    rocprofv3 FETCH_SIZE + WRITE_SIZE summary (copy-calibrated), or None."""
+    try:
+        with open(TRAFFIC_FILE) as f:
+            for line in f:
+                if line.strip().startswith("traffic_bytes_per_dispatch="):
+                    return int(float(line.split("=", 1)[1].split()[0]))
+    except OSError:
+        return None
+    return None
+
+
+def calibrate_copy() -> int:
+    """One device-to-device copy of a known size on the device's stream: the
+    plain copy kernel that scales the FETCH_SIZE / WRITE_SIZE counters."""
+    from foundry_amd.profiling import CALIBRATION_BYTES
+
+    dev = HipDevice(0)
+    src = dev.zeros(CALIBRATION_BYTES)
+    dst = dev.empty(CALIBRATION_BYTES)
+    hip = ctypes.CDLL("libamdhip64.so")
+    stream = ctypes.c_void_p()
+    _lib.call("fh_device_stream", dev.handle, ctypes.byref(stream))
+    hip.hipMemcpyDtoDAsync.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p]
+    rc = hip.hipMemcpyDtoDAsync(ctypes.c_void_p(dst.ptr), ctypes.c_void_p(src.ptr), CALIBRATION_BYTES, stream)
+    if rc != 0:
+        raise RuntimeError(f"hipMemcpyDtoDAsync failed: {rc}")
+    dev.synchronize()
+    dev.close()
+    print(f"[bench] copied {CALIBRATION_BYTES} bytes device to device", flush=True)
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -180,12 +217,16 @@ def main() -> int:
     ap.add_argument("--copies", type=int, default=48)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--quick", action="store_true", help="headline only, no secondary lines")
+    ap.add_argument("--calibrate-copy", action="store_true",
+                    help="also run one device copy of known size (counter calibration)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not supported "
               "(the q4 path has no multi-GPU form here)", file=sys.stderr)
         return 2
 
+    if args.calibrate_copy:
+        calibrate_copy()
     dev = HipDevice(0)
     head = bench_gemv(dev, 8192, 3072, args.copies, args.steps, args.warmup, seed=1)
     print(f"[bench] gemv 8192x3072: {head['us_per_launch']:.2f} us/launch, {head['GB_per_s']:.0f} GB/s", flush=True)
@@ -227,7 +268,8 @@ def main() -> int:
         "config": {"workload": f"q4 decode GEMV x[1,3072].W[8192,3072]^T over {args.copies} weight copies per step",
                    "m": 1, "n": 8192, "k": 3072, "group": 64, "copies": args.copies},
         "roofline": {"bound": "hbm", "achieved": round(head["GB_per_s"], 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(head["GB_per_s"] / HBM_PEAK_GBS, 4), "traffic": None,
+                     "frac": round(head["GB_per_s"] / HBM_PEAK_GBS, 4), "traffic": measured_traffic(),
+                     "traffic_source": os.path.relpath(TRAFFIC_FILE, ROOT),
                      "algorithmic_bytes_per_launch": per_launch_bytes,
                      "us_per_launch": head["us_per_launch"]},
         "cpu_baseline": cpu,

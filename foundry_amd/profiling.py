@@ -1,0 +1,72 @@
+"""Readers for rocprofv3 output, used to build the summaries under profiles/.
+
+    python -m foundry_amd.profiling stats <dir>        # kernel-trace --stats CSV
+    python -m foundry_amd.profiling traffic <fetch_dir> <write_dir> <kernel-substring>
+
+``traffic`` takes two ``rocprofv3 --pmc`` runs of the same command, one with
+FETCH_SIZE and one with WRITE_SIZE (KiB per dispatch), each of which also ran
+``bench.py --calibrate-copy`` (a device-to-device copy of a known byte count).
+Each counter is scaled by known bytes / what the counter read for the copy
+kernel, then averaged over the dispatches of the named kernel.
+"""
+from __future__ import annotations
+
+import csv
+import glob
+import os
+import statistics
+import sys
+
+COPY_KERNEL = "copyBuffer"
+CALIBRATION_BYTES = 256 << 20  # bench.py --calibrate-copy copies this many bytes
+
+
+def _rows(pattern: str):
+    for path in glob.glob(pattern, recursive=True):
+        with open(path, newline="") as f:
+            yield from csv.DictReader(f)
+
+
+def kernel_stats(directory: str):
+    """[(name, calls, avg_ns, total_ns)] from a *_kernel_stats.csv."""
+    out = []
+    for r in _rows(os.path.join(directory, "**", "*kernel_stats.csv")):
+        out.append((r["Name"], int(r["Calls"]), float(r["AverageNs"]), float(r["TotalDurationNs"])))
+    return sorted(out, key=lambda t: -t[3])
+
+
+def counter_per_dispatch(directory: str, counter: str, kernel_substring: str):
+    vals = [float(r["Counter_Value"]) for r in _rows(os.path.join(directory, "**", "*counter_collection.csv"))
+            if r["Counter_Name"] == counter and kernel_substring in r["Kernel_Name"]]
+    return vals
+
+
+def scaled_bytes(directory: str, counter: str, kernel_substring: str):
+    """Mean bytes per dispatch of the kernel, scaled by the copy calibration."""
+    kernel = counter_per_dispatch(directory, counter, kernel_substring)
+    copy = counter_per_dispatch(directory, counter, COPY_KERNEL)
+    if not kernel or not copy:
+        raise RuntimeError(f"{counter}: no dispatches of {kernel_substring!r} or of the copy kernel in {directory}")
+    # the copy reads and writes CALIBRATION_BYTES each
+    scale = CALIBRATION_BYTES / (max(copy) * 1024.0)
+    return statistics.mean(kernel) * 1024.0 * scale, scale, len(kernel)
+
+
+def main(argv):
+    if len(argv) >= 2 and argv[0] == "stats":
+        for name, calls, avg, total in kernel_stats(argv[1]):
+            print(f"| {name[:90]} | {calls} | {avg / 1e3:.2f} | {total / 1e6:.3f} |")
+        return 0
+    if len(argv) >= 4 and argv[0] == "traffic":
+        fetch, fscale, n1 = scaled_bytes(argv[1], "FETCH_SIZE", argv[3])
+        write, wscale, n2 = scaled_bytes(argv[2], "WRITE_SIZE", argv[3])
+        print(f"fetch_bytes_per_dispatch={fetch:.0f} (scale {fscale:.4f}, {n1} dispatches)")
+        print(f"write_bytes_per_dispatch={write:.0f} (scale {wscale:.4f}, {n2} dispatches)")
+        print(f"traffic_bytes_per_dispatch={fetch + write:.0f}")
+        return 0
+    print(__doc__)
+    return 2
+
+
+if __name__ == "__main__":
+    sys.exit(main(sys.argv[1:]))
