@@ -105,6 +105,13 @@ SIGNATURES = {
     "fh_q4_embed": [_vp, _vp, _vp, _vp, _i64, _i64, _i64, _vp, _i64, _vp],
     "fh_q4_matmul": [_vp, _vp, _i64, _i64, _i64, _vp, _vp, _vp, _i64, _i64, _vp, _int],
     "fh_q4_dequant": [_vp, _vp, _vp, _vp, _i64, _i64, _i64, _vp],
+    "fh_rms_norm": [_vp, _vp, _vp, _vp, _vp, _i64, _i64, ctypes.c_float, _vp],
+    "fh_rope_kv": [_vp, _vp, _i64, _i64, _i64, _i64, _vp, _vp, _i64, _vp, _vp, _vp, _i64, _vp],
+    "fh_attention": [_vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, ctypes.c_float, _vp],
+    "fh_silu_mul": [_vp, _vp, _i64, _i64, _vp],
+    "fh_argmax": [_vp, _vp, _i64, _i64, _vp],
+    "fh_advance_positions": [_vp, _vp, _i64, _i64],
+    "fh_append_token": [_vp, _vp, _vp, _vp, _i64, _i64],
 }
 
 _lib = None

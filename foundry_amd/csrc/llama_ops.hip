@@ -1,0 +1,416 @@
+// Decoder-step ops around the q4 linears: residual add + RMSNorm, RoPE with
+// the KV-cache write, attention, SiLU-and-multiply, argmax and the device-side
+// position counter. They are the HIP counterparts of the reference's
+// RmsNorm (src/nn/norm.rs:32-50), apply_rotary_pos_emb
+// (src/models/llama/rotary_emb.rs:62-85), StaticCache::update
+// (src/nn/kv_cache.rs:41-80), scaled_dot_product_attention
+// (src/nn/attention.rs:23-60), Silu (src/nn/activation.rs:19-28) and the
+// greedy argmax (src/generate/mod.rs:192-204; src/metal/kernels/reduce.metal:42-78).
+//
+// Each keeps the reference's bf16 rounding points (its tensors are bf16, and
+// every op rounds its output): e.g. RMSNorm rounds x*scale to bf16 before the
+// weight multiply, RoPE rounds x*cos and rot*sin before adding, attention
+// rounds the scores and the probabilities to bf16. Where the reference runs
+// several dispatches (about ten for RMSNorm, six for SiLU, twelve for SDPA)
+// these are one kernel each.
+//
+// The decode step is captured once as a HIP graph and replayed: the token id
+// and position live in device memory (argmax writes the next id that the
+// embedding gather reads; fh_advance_positions bumps the position), so no
+// kernel argument changes between steps.
+#include <initializer_list>
+
+#include "device.hpp"
+#include "q4_common.hpp"
+
+namespace fh {
+
+__device__ __forceinline__ uint16_t rne(float v) { return static_cast<uint16_t>(f32_to_bf16_rne(v)); }
+__device__ __forceinline__ float bf(uint16_t b) { return bf16_to_f32(b); }
+
+// Sum across a 256-thread block (every thread gets the result).
+__device__ __forceinline__ float block_sum(float v, float *red) {
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    __syncthreads();
+    if (lane == 0) red[wave] = v;
+    __syncthreads();
+    float t = 0.f;
+    for (int w = 0; w < static_cast<int>(blockDim.x >> 6); ++w) t += red[w];
+    return t;
+}
+
+__device__ __forceinline__ float block_max(float v, float *red) {
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    __syncthreads();
+    if (lane == 0) red[wave] = v;
+    __syncthreads();
+    float t = -INFINITY;
+    for (int w = 0; w < static_cast<int>(blockDim.x >> 6); ++w) t = fmaxf(t, red[w]);
+    return t;
+}
+
+// One block per row. With `res`, h = RNE(x + res) is formed first (the
+// residual add, src/models/llama/model.rs:254-279) and written to res_out.
+// y = RNE(RNE(h * scale) * w), scale = 1 / sqrt(sum(h^2) * (1/dim) + eps).
+__global__ __launch_bounds__(256) void rms_norm_kernel(const uint16_t *__restrict__ x,
+                                                       const uint16_t *__restrict__ res,
+                                                       uint16_t *__restrict__ res_out,
+                                                       const uint16_t *__restrict__ w,
+                                                       uint32_t dim, float eps, float dim_inv,
+                                                       uint16_t *__restrict__ y) {
+    __shared__ float red[4];
+    const uint64_t base = static_cast<uint64_t>(blockIdx.x) * dim;
+    float ss = 0.f;
+    for (uint32_t i = threadIdx.x; i < dim; i += blockDim.x) {
+        float h = bf(x[base + i]);
+        if (res) {
+            const uint16_t hb = rne(h + bf(res[base + i]));
+            res_out[base + i] = hb;
+            h = bf(hb);
+        }
+        ss += h * h;
+    }
+    ss = block_sum(ss, red);
+    const float scale = 1.0f / sqrtf(ss * dim_inv + eps);
+    for (uint32_t i = threadIdx.x; i < dim; i += blockDim.x) {
+        const float h = bf(res ? res_out[base + i] : x[base + i]);
+        y[base + i] = rne(bf(rne(h * scale)) * bf(w[i]));
+    }
+}
+
+// RoPE on q and k of one token (block), then k and v into the cache at the
+// token's position. qkv row: [q heads | k heads | v heads] * head_dim.
+// x' = RNE(RNE(x * cos) + RNE(rot * sin)), rot = cat(-x2, x1).
+__global__ __launch_bounds__(256) void rope_kv_kernel(
+    const uint16_t *__restrict__ qkv, uint32_t n_heads, uint32_t n_kv, uint32_t head_dim,
+    const uint16_t *__restrict__ cos_tab, const uint16_t *__restrict__ sin_tab, uint32_t table_len,
+    const uint32_t *__restrict__ positions, uint16_t *__restrict__ k_cache,
+    uint16_t *__restrict__ v_cache, uint32_t max_len, uint16_t *__restrict__ q_out) {
+    const uint32_t t = blockIdx.x;
+    const uint32_t pos = positions[t];
+    // positions are device data the host cannot check: a position outside the
+    // cache or the tables writes nothing
+    if (pos >= max_len || pos >= table_len) return;
+    const uint32_t width = (n_heads + 2 * n_kv) * head_dim;
+    const uint16_t *row = qkv + static_cast<uint64_t>(t) * width;
+    const uint16_t *c = cos_tab + static_cast<uint64_t>(pos) * head_dim;
+    const uint16_t *s = sin_tab + static_cast<uint64_t>(pos) * head_dim;
+    const uint32_t half = head_dim / 2;
+    const uint32_t rot_elems = (n_heads + n_kv) * head_dim;
+    for (uint32_t i = threadIdx.x; i < rot_elems; i += blockDim.x) {
+        const uint32_t h = i / head_dim, d = i % head_dim;
+        const uint16_t *xh = row + h * head_dim;
+        const float xv = bf(xh[d]);
+        const float rv = d < half ? -bf(xh[d + half]) : bf(xh[d - half]);
+        const uint16_t out = rne(bf(rne(xv * bf(c[d]))) + bf(rne(rv * bf(s[d]))));
+        if (h < n_heads) {
+            q_out[(static_cast<uint64_t>(t) * n_heads + h) * head_dim + d] = out;
+        } else {
+            const uint32_t kh = h - n_heads;
+            k_cache[(static_cast<uint64_t>(kh) * max_len + pos) * head_dim + d] = out;
+        }
+    }
+    const uint16_t *vrow = row + rot_elems;
+    for (uint32_t i = threadIdx.x; i < n_kv * head_dim; i += blockDim.x) {
+        const uint32_t kh = i / head_dim, d = i % head_dim;
+        v_cache[(static_cast<uint64_t>(kh) * max_len + pos) * head_dim + d] = vrow[i];
+    }
+}
+
+// Attention for one (token, query head) per block over keys 0..pos of its KV
+// head (causal; decode uses pos = current position). Scores: RNE(q . k) with
+// fp32 accumulation, then s * scale in fp32; softmax in fp32; probabilities
+// rounded to bf16; out = RNE(sum_j p_j v_j) in fp32. Scores go through LDS
+// (max_len floats); head_dim <= 256.
+__global__ __launch_bounds__(256) void attention_kernel(
+    const uint16_t *__restrict__ q, const uint16_t *__restrict__ k_cache,
+    const uint16_t *__restrict__ v_cache, const uint32_t *__restrict__ positions,
+    uint32_t n_heads, uint32_t n_kv, uint32_t head_dim, uint32_t max_len, float scale,
+    uint16_t *__restrict__ out) {
+    extern __shared__ float sh[];
+    float *qs = sh;                 // head_dim
+    float *scores = sh + head_dim;  // max_len
+    __shared__ float red[4];
+    const uint32_t t = blockIdx.y, h = blockIdx.x;
+    const uint32_t kvh = h / (n_heads / n_kv);
+    // keys 0..pos, never past the cache (positions are unchecked device data)
+    const uint32_t ctx = positions[t] < max_len ? positions[t] + 1 : max_len;
+    const uint16_t *qrow = q + (static_cast<uint64_t>(t) * n_heads + h) * head_dim;
+    for (uint32_t d = threadIdx.x; d < head_dim; d += blockDim.x) qs[d] = bf(qrow[d]);
+    __syncthreads();
+    const uint16_t *kb = k_cache + static_cast<uint64_t>(kvh) * max_len * head_dim;
+    const uint16_t *vb = v_cache + static_cast<uint64_t>(kvh) * max_len * head_dim;
+    float mx = -INFINITY;
+    for (uint32_t j = threadIdx.x; j < ctx; j += blockDim.x) {
+        const uint16_t *kr = kb + static_cast<uint64_t>(j) * head_dim;
+        float acc = 0.f;
+        for (uint32_t d = 0; d < head_dim; d += 8) {
+            const uint4 kv = *reinterpret_cast<const uint4 *>(kr + d);
+            const uint32_t w[4] = {kv.x, kv.y, kv.z, kv.w};
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                acc += qs[d + 2 * e] * bf(static_cast<uint16_t>(w[e] & 0xFFFFu));
+                acc += qs[d + 2 * e + 1] * bf(static_cast<uint16_t>(w[e] >> 16));
+            }
+        }
+        const float sc = bf(rne(acc)) * scale;
+        scores[j] = sc;
+        mx = fmaxf(mx, sc);
+    }
+    mx = block_max(mx, red);
+    float sum = 0.f;
+    for (uint32_t j = threadIdx.x; j < ctx; j += blockDim.x) {
+        const float e = expf(scores[j] - mx);
+        scores[j] = e;
+        sum += e;
+    }
+    sum = block_sum(sum, red);
+    for (uint32_t j = threadIdx.x; j < ctx; j += blockDim.x) scores[j] = bf(rne(scores[j] / sum));
+    __syncthreads();
+    // out[d]: threads split (dim, key half); keys ascending within each half
+    const uint32_t halves = blockDim.x / head_dim;  // >= 1 when head_dim <= 256
+    const uint32_t d = threadIdx.x % head_dim, part = threadIdx.x / head_dim;
+    float acc = 0.f;
+    if (part < halves) {
+        const uint32_t per = (ctx + halves - 1) / halves;
+        const uint32_t j0 = part * per, j1 = j0 + per < ctx ? j0 + per : ctx;
+        for (uint32_t j = j0; j < j1; ++j) acc += scores[j] * bf(vb[static_cast<uint64_t>(j) * head_dim + d]);
+    }
+    __syncthreads();
+    float *partial = scores;  // reuse
+    if (part < halves) partial[part * head_dim + d] = acc;
+    __syncthreads();
+    if (threadIdx.x < head_dim) {
+        float o = 0.f;
+        for (uint32_t p = 0; p < halves; ++p) o += partial[p * head_dim + threadIdx.x];
+        out[(static_cast<uint64_t>(t) * n_heads + h) * head_dim + threadIdx.x] = rne(o);
+    }
+}
+
+// out = RNE(RNE(g / (1 + exp(-g))) * u), gu row = [g (F) | u (F)].
+__global__ __launch_bounds__(256) void silu_mul_kernel(const uint16_t *__restrict__ gu, uint32_t f,
+                                                       uint64_t total, uint16_t *__restrict__ out) {
+    const uint64_t i = static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (i >= total) return;
+    const uint64_t r = i / f, c = i % f;
+    const float g = bf(gu[r * 2 * f + c]);
+    const float u = bf(gu[r * 2 * f + f + c]);
+    const float den = expf(-g) + 1.0f;
+    out[i] = rne(bf(rne(g / den)) * u);
+}
+
+// Row argmax of bf16 values; ties go to the lowest index.
+__global__ __launch_bounds__(256) void argmax_kernel(const uint16_t *__restrict__ x, uint32_t n,
+                                                     uint32_t *__restrict__ out) {
+    __shared__ float bv[256];
+    __shared__ uint32_t bi[256];
+    const uint16_t *row = x + static_cast<uint64_t>(blockIdx.x) * n;
+    float best = -INFINITY;
+    uint32_t idx = 0xFFFFFFFFu;
+    // indices ascend per thread, so the first maximum seen is the lowest
+    for (uint32_t i = threadIdx.x; i < n; i += blockDim.x) {
+        const float v = bf(row[i]);
+        if (v > best || idx == 0xFFFFFFFFu) {
+            best = v;
+            idx = i;
+        }
+    }
+    bv[threadIdx.x] = best;
+    bi[threadIdx.x] = idx;
+    __syncthreads();
+    for (uint32_t off = blockDim.x / 2; off > 0; off >>= 1) {
+        if (threadIdx.x < off) {
+            const float ov = bv[threadIdx.x + off];
+            const uint32_t oi = bi[threadIdx.x + off];
+            if (ov > bv[threadIdx.x] || (ov == bv[threadIdx.x] && oi < bi[threadIdx.x])) {
+                bv[threadIdx.x] = ov;
+                bi[threadIdx.x] = oi;
+            }
+        }
+        __syncthreads();
+    }
+    if (threadIdx.x == 0) out[blockIdx.x] = bi[0] == 0xFFFFFFFFu ? 0u : bi[0];
+}
+
+// log[position - base] = token when that index is below capacity.
+__global__ void append_token_kernel(const uint32_t *__restrict__ token, uint32_t *__restrict__ log,
+                                    const uint32_t *__restrict__ position, uint32_t base,
+                                    uint32_t capacity) {
+    const uint32_t idx = position[0] - base;
+    if (position[0] >= base && idx < capacity) log[idx] = token[0];
+}
+
+__global__ void advance_kernel(uint32_t *__restrict__ p, uint32_t n, uint32_t by) {
+    const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) p[i] += by;
+}
+
+}  // namespace fh
+
+using namespace fh;
+
+namespace {
+
+int check_dims(const char *fn, std::initializer_list<int64_t> dims) {
+    for (int64_t d : dims)
+        if (d < 0 || d > 0x7FFFFFFFll)
+            return fail(FH_ERR_INVALID_ARGUMENT, "%s: dimension %lld out of range", fn, (long long)d);
+    return FH_OK;
+}
+
+}  // namespace
+
+extern "C" int fh_rms_norm(fh_device *dev, const uint16_t *x, const uint16_t *residual,
+                           uint16_t *residual_out, const uint16_t *weight, int64_t rows,
+                           int64_t dim, float eps, uint16_t *y) {
+    const char *fn = "fh_rms_norm";
+    if (int rc = check_usable(dev, fn)) return rc;
+    if (int rc = check_dims(fn, {rows, dim})) return rc;
+    if (rows == 0 || dim == 0) return FH_OK;
+    if ((residual == nullptr) != (residual_out == nullptr))
+        return fail(FH_ERR_INVALID_ARGUMENT, "%s: residual and residual_out go together", fn);
+    const uint64_t bytes = static_cast<uint64_t>(rows) * dim * 2;
+    if (int rc = check_range(dev, x, bytes, fn, "x")) return rc;
+    if (residual) {
+        if (int rc = check_range(dev, residual, bytes, fn, "residual")) return rc;
+        if (int rc = check_range(dev, residual_out, bytes, fn, "residual_out")) return rc;
+    }
+    if (int rc = check_range(dev, weight, static_cast<uint64_t>(dim) * 2, fn, "weight")) return rc;
+    if (int rc = check_range(dev, y, bytes, fn, "y")) return rc;
+    if (int rc = set_current(dev, fn)) return rc;
+    const float dim_inv = 1.0f / static_cast<float>(dim);
+    return dispatch(dev, fn, [&] {
+        hipLaunchKernelGGL(rms_norm_kernel, dim3(static_cast<uint32_t>(rows)), dim3(256), 0,
+                           dev->stream, x, residual, residual_out, weight,
+                           static_cast<uint32_t>(dim), eps, dim_inv, y);
+    });
+}
+
+extern "C" int fh_rope_kv(fh_device *dev, const uint16_t *qkv, int64_t tokens, int64_t n_heads,
+                          int64_t n_kv, int64_t head_dim, const uint16_t *cos_tab,
+                          const uint16_t *sin_tab, int64_t table_len, const uint32_t *positions,
+                          uint16_t *k_cache, uint16_t *v_cache, int64_t max_len,
+                          uint16_t *q_out) {
+    const char *fn = "fh_rope_kv";
+    if (int rc = check_usable(dev, fn)) return rc;
+    if (int rc = check_dims(fn, {tokens, n_heads, n_kv, head_dim, table_len, max_len})) return rc;
+    if (tokens == 0) return FH_OK;
+    if (n_kv == 0 || n_heads % n_kv != 0 || head_dim % 8 != 0 || head_dim == 0)
+        return fail(FH_ERR_INVALID_ARGUMENT, "%s: heads %lld/%lld, head_dim %lld", fn,
+                    (long long)n_heads, (long long)n_kv, (long long)head_dim);
+    const uint64_t width = static_cast<uint64_t>(n_heads + 2 * n_kv) * head_dim;
+    if (int rc = check_range(dev, qkv, tokens * width * 2, fn, "qkv")) return rc;
+    if (int rc = check_range(dev, cos_tab, static_cast<uint64_t>(table_len) * head_dim * 2, fn, "cos")) return rc;
+    if (int rc = check_range(dev, sin_tab, static_cast<uint64_t>(table_len) * head_dim * 2, fn, "sin")) return rc;
+    if (int rc = check_range(dev, positions, static_cast<uint64_t>(tokens) * 4, fn, "positions")) return rc;
+    const uint64_t cache = static_cast<uint64_t>(n_kv) * max_len * head_dim * 2;
+    if (int rc = check_range(dev, k_cache, cache, fn, "k_cache")) return rc;
+    if (int rc = check_range(dev, v_cache, cache, fn, "v_cache")) return rc;
+    if (int rc = check_range(dev, q_out, static_cast<uint64_t>(tokens) * n_heads * head_dim * 2, fn, "q_out")) return rc;
+    if (int rc = set_current(dev, fn)) return rc;
+    return dispatch(dev, fn, [&] {
+        hipLaunchKernelGGL(rope_kv_kernel, dim3(static_cast<uint32_t>(tokens)), dim3(256), 0,
+                           dev->stream, qkv, static_cast<uint32_t>(n_heads),
+                           static_cast<uint32_t>(n_kv), static_cast<uint32_t>(head_dim), cos_tab,
+                           sin_tab, static_cast<uint32_t>(table_len), positions, k_cache, v_cache,
+                           static_cast<uint32_t>(max_len), q_out);
+    });
+}
+
+extern "C" int fh_attention(fh_device *dev, const uint16_t *q, const uint16_t *k_cache,
+                            const uint16_t *v_cache, const uint32_t *positions, int64_t tokens,
+                            int64_t n_heads, int64_t n_kv, int64_t head_dim, int64_t max_len,
+                            float scale, uint16_t *out) {
+    const char *fn = "fh_attention";
+    if (int rc = check_usable(dev, fn)) return rc;
+    if (int rc = check_dims(fn, {tokens, n_heads, n_kv, head_dim, max_len})) return rc;
+    if (tokens == 0) return FH_OK;
+    if (n_kv == 0 || n_heads % n_kv != 0 || head_dim == 0 || head_dim > 256 || head_dim % 8 != 0)
+        return fail(FH_ERR_UNSUPPORTED, "%s: heads %lld/%lld, head_dim %lld", fn, (long long)n_heads,
+                    (long long)n_kv, (long long)head_dim);
+    const uint64_t lds = (static_cast<uint64_t>(head_dim) + (max_len > 256 ? max_len : 256)) * 4;
+    if (lds > 64 * 1024)
+        return fail(FH_ERR_UNSUPPORTED, "%s: max_len %lld too long for the LDS score buffer", fn,
+                    (long long)max_len);
+    const uint64_t cache = static_cast<uint64_t>(n_kv) * max_len * head_dim * 2;
+    if (int rc = check_range(dev, q, static_cast<uint64_t>(tokens) * n_heads * head_dim * 2, fn, "q")) return rc;
+    if (int rc = check_range(dev, k_cache, cache, fn, "k_cache")) return rc;
+    if (int rc = check_range(dev, v_cache, cache, fn, "v_cache")) return rc;
+    if (int rc = check_range(dev, positions, static_cast<uint64_t>(tokens) * 4, fn, "positions")) return rc;
+    if (int rc = check_range(dev, out, static_cast<uint64_t>(tokens) * n_heads * head_dim * 2, fn, "out")) return rc;
+    if (int rc = set_current(dev, fn)) return rc;
+    return dispatch(dev, fn, [&] {
+        hipLaunchKernelGGL(attention_kernel,
+                           dim3(static_cast<uint32_t>(n_heads), static_cast<uint32_t>(tokens)),
+                           dim3(256), static_cast<uint32_t>(lds), dev->stream, q, k_cache, v_cache,
+                           positions, static_cast<uint32_t>(n_heads), static_cast<uint32_t>(n_kv),
+                           static_cast<uint32_t>(head_dim), static_cast<uint32_t>(max_len), scale,
+                           out);
+    });
+}
+
+extern "C" int fh_silu_mul(fh_device *dev, const uint16_t *gate_up, int64_t rows, int64_t f,
+                           uint16_t *out) {
+    const char *fn = "fh_silu_mul";
+    if (int rc = check_usable(dev, fn)) return rc;
+    if (int rc = check_dims(fn, {rows, f})) return rc;
+    if (rows == 0 || f == 0) return FH_OK;
+    const uint64_t total = static_cast<uint64_t>(rows) * f;
+    if (int rc = check_range(dev, gate_up, total * 4, fn, "gate_up")) return rc;
+    if (int rc = check_range(dev, out, total * 2, fn, "out")) return rc;
+    if (int rc = set_current(dev, fn)) return rc;
+    const uint32_t blocks = static_cast<uint32_t>((total + 255) / 256);
+    return dispatch(dev, fn, [&] {
+        hipLaunchKernelGGL(silu_mul_kernel, dim3(blocks), dim3(256), 0, dev->stream, gate_up,
+                           static_cast<uint32_t>(f), total, out);
+    });
+}
+
+extern "C" int fh_argmax(fh_device *dev, const uint16_t *x, int64_t rows, int64_t n, uint32_t *out) {
+    const char *fn = "fh_argmax";
+    if (int rc = check_usable(dev, fn)) return rc;
+    if (int rc = check_dims(fn, {rows, n})) return rc;
+    if (rows == 0) return FH_OK;
+    if (n == 0) return fail(FH_ERR_INVALID_ARGUMENT, "%s: argmax over an empty row", fn);
+    if (int rc = check_range(dev, x, static_cast<uint64_t>(rows) * n * 2, fn, "x")) return rc;
+    if (int rc = check_range(dev, out, static_cast<uint64_t>(rows) * 4, fn, "out")) return rc;
+    if (int rc = set_current(dev, fn)) return rc;
+    return dispatch(dev, fn, [&] {
+        hipLaunchKernelGGL(argmax_kernel, dim3(static_cast<uint32_t>(rows)), dim3(256), 0,
+                           dev->stream, x, static_cast<uint32_t>(n), out);
+    });
+}
+
+extern "C" int fh_advance_positions(fh_device *dev, uint32_t *positions, int64_t n, int64_t by) {
+    const char *fn = "fh_advance_positions";
+    if (int rc = check_usable(dev, fn)) return rc;
+    if (int rc = check_dims(fn, {n, by})) return rc;
+    if (n == 0) return FH_OK;
+    if (int rc = check_range(dev, positions, static_cast<uint64_t>(n) * 4, fn, "positions")) return rc;
+    if (int rc = set_current(dev, fn)) return rc;
+    return dispatch(dev, fn, [&] {
+        hipLaunchKernelGGL(advance_kernel, dim3(static_cast<uint32_t>((n + 255) / 256)), dim3(256),
+                           0, dev->stream, positions, static_cast<uint32_t>(n),
+                           static_cast<uint32_t>(by));
+    });
+}
+
+extern "C" int fh_append_token(fh_device *dev, const uint32_t *token, uint32_t *log,
+                               const uint32_t *position, int64_t base, int64_t capacity) {
+    const char *fn = "fh_append_token";
+    if (int rc = check_usable(dev, fn)) return rc;
+    if (int rc = check_dims(fn, {base, capacity})) return rc;
+    if (capacity == 0) return FH_OK;
+    if (int rc = check_range(dev, token, 4, fn, "token")) return rc;
+    if (int rc = check_range(dev, position, 4, fn, "position")) return rc;
+    if (int rc = check_range(dev, log, static_cast<uint64_t>(capacity) * 4, fn, "log")) return rc;
+    if (int rc = set_current(dev, fn)) return rc;
+    return dispatch(dev, fn, [&] {
+        hipLaunchKernelGGL(append_token_kernel, dim3(1), dim3(1), 0, dev->stream, token, log, position,
+                           static_cast<uint32_t>(base), static_cast<uint32_t>(capacity));
+    });
+}

@@ -1,0 +1,305 @@
+"""Llama decoder with q4 weights on the HIP backend: the caller of the q4 path.
+
+Mirrors the reference's model call sites (src/models/llama/model.rs:92-194,
+src/models/llama/attention.rs:72-132, src/models/llama/mlp.rs:49-58) and its
+greedy driver (src/generate/mod.rs:45-204):
+
+    h = embed(ids)                                  (q4 gather, tied table)
+    for each layer:
+        x = rms_norm(h);  q,k,v = x Wq, x Wk, x Wv  (one GEMV/GEMM on [Wq;Wk;Wv])
+        q,k = rope(q,k); cache k,v; a = attention(q, cache) Wo
+        h = h + a; x = rms_norm(h)
+        m = (silu(x Wgate) * (x Wup)) Wdown          (one GEMV/GEMM on [Wgate;Wup])
+        h = h + m
+    logits = rms_norm(h)[last] Wembed^T;  next = argmax(logits)
+
+Fusions that keep each output row's arithmetic unchanged:
+- q/k/v and gate/up weights are concatenated along N (each output row of a
+  linear depends only on its own weight row);
+- each residual add is fused into the RMSNorm that follows it.
+
+The decode step reads its token id and position from device memory, so it is
+captured once as a HIP graph and replayed for every generated token. Weights
+are random-init (SplitMix64-seeded); no checkpoint is read.
+"""
+from __future__ import annotations
+
+import ctypes
+from dataclasses import dataclass, field
+
+import numpy as np
+
+from . import _lib, synth
+from .device import HipDevice, HipStorage
+
+GROUP = 64
+
+
+@dataclass(frozen=True)
+class RopeScaling:
+    """Llama3RopeScaling (src/models/llama/config.rs:31-36)."""
+
+    factor: float = 32.0
+    low_freq_factor: float = 1.0
+    high_freq_factor: float = 4.0
+    original_max_position_embeddings: int = 8192
+
+
+@dataclass(frozen=True)
+class LlamaConfig:
+    n_layers: int
+    hidden: int
+    n_heads: int
+    n_kv_heads: int
+    head_dim: int
+    ffn: int
+    vocab: int
+    rms_norm_eps: float = 1e-5
+    rope_theta: float = 500000.0
+    rope_scaling: RopeScaling | None = field(default_factory=RopeScaling)
+    max_position_embeddings: int = 131072
+
+    @staticmethod
+    def llama_3_2_3b() -> "LlamaConfig":
+        return LlamaConfig(28, 3072, 24, 8, 128, 8192, 128256)
+
+    @staticmethod
+    def llama_3_1_8b() -> "LlamaConfig":
+        return LlamaConfig(32, 4096, 32, 8, 128, 14336, 128256)
+
+    @property
+    def qkv_rows(self) -> int:
+        return (self.n_heads + 2 * self.n_kv_heads) * self.head_dim
+
+
+def inv_freq(cfg: LlamaConfig) -> np.ndarray:
+    """src/models/llama/rotary_emb.rs:135-186, in float32."""
+    d = cfg.head_dim
+    theta = np.float32(cfg.rope_theta)
+    out = []
+    for i in range(0, d, 2):
+        f = np.float32(1.0) / np.power(theta, np.float32(i) / np.float32(d), dtype=np.float32)
+        sc = cfg.rope_scaling
+        if sc is not None:
+            ctx = np.float32(sc.original_max_position_embeddings)
+            low, high = np.float32(sc.low_freq_factor), np.float32(sc.high_freq_factor)
+            factor = np.float32(sc.factor)
+            wl_low, wl_high = ctx / low, ctx / high
+            wl = np.float32(2 * np.pi) / f
+            fs = f / factor if wl > wl_low else f
+            smooth = (ctx / wl - low) / (high - low)
+            if wl_high <= wl <= wl_low:
+                fs = (np.float32(1) - smooth) * fs / factor + smooth * fs
+            f = np.float32(fs)
+        out.append(f)
+    return np.array(out, dtype=np.float32)
+
+
+def rope_tables(cfg: LlamaConfig, length: int):
+    """cos/sin tables [length, head_dim] in bf16 (src/models/llama/rotary_emb.rs:87-131):
+    angle = position * inv_freq in float32, duplicated over both halves."""
+    f = inv_freq(cfg)
+    f2 = np.concatenate([f, f])
+    pos = np.arange(length, dtype=np.float32)[:, None]
+    ang = (pos * f2[None, :]).astype(np.float32)
+    return synth.bf16_rne(np.cos(ang).astype(np.float32)), synth.bf16_rne(np.sin(ang).astype(np.float32))
+
+
+class _Q4:
+    """A q4 weight triplet on the device."""
+
+    def __init__(self, dev: HipDevice, wq: np.ndarray, s: np.ndarray, b: np.ndarray):
+        self.n, self.k = wq.shape[0], wq.shape[1] * 8
+        self.wq = dev.storage_from_bytes(np.ascontiguousarray(wq).tobytes())
+        self.s = dev.storage_from_bytes(np.ascontiguousarray(s).tobytes())
+        self.b = dev.storage_from_bytes(np.ascontiguousarray(b).tobytes())
+
+
+def layer_weights(cfg: LlamaConfig, seed: int, layer: int):
+    """Host-side random-init q4 weights of one layer: dict of (wq, s, b)
+    triplets and bf16 norm weights. Layer l's packed words are layer 0's xor a
+    per-layer constant (uniform nibbles stay uniform), so building a
+    28-layer model costs one layer's draws."""
+    key = np.uint32((0x9E3779B9 * (layer + 1)) & 0xFFFFFFFF)
+    out = {}
+    for name, (n, k, s_off) in {
+        "qkv": (cfg.qkv_rows, cfg.hidden, 1),
+        "o": (cfg.hidden, cfg.n_heads * cfg.head_dim, 2),
+        "gate_up": (2 * cfg.ffn, cfg.hidden, 3),
+        "down": (cfg.hidden, cfg.ffn, 4),
+    }.items():
+        wq, s, b = _cached_q4(seed * 16 + s_off, n, k)
+        out[name] = (wq ^ key if layer else wq, s, b)
+    for name, s_off in (("input_norm", 5), ("post_norm", 6)):
+        out[name] = _norm_weight(seed * 16 + s_off + 97 * layer, cfg.hidden)
+    return out
+
+
+_CACHE: dict = {}
+
+
+def _cached_q4(seed: int, n: int, k: int):
+    key = (seed, n, k)
+    if key not in _CACHE:
+        _CACHE[key] = synth.q4_weights(seed, n, k, GROUP)
+    return _CACHE[key]
+
+
+def _norm_weight(seed: int, n: int) -> np.ndarray:
+    z = synth.bf16_to_f32(synth.bf16_normal(seed, (n,))).astype(np.float64)
+    return synth.bf16_rne((1.0 + 0.1 * z).astype(np.float32))
+
+
+def embed_weights(cfg: LlamaConfig, seed: int):
+    return _cached_q4(seed * 16 + 7, cfg.vocab, cfg.hidden)
+
+
+def final_norm_weight(cfg: LlamaConfig, seed: int):
+    return _norm_weight(seed * 16 + 8, cfg.hidden)
+
+
+class Q4Llama:
+    """Random-init q4 Llama on one device, with a static KV cache of
+    `max_len` positions per layer (StaticCache, src/nn/kv_cache.rs:13-39)."""
+
+    def __init__(self, dev: HipDevice, cfg: LlamaConfig, seed: int, max_len: int, max_tokens: int):
+        self.dev, self.cfg, self.max_len = dev, cfg, max_len
+        if max_len > cfg.max_position_embeddings:
+            raise ValueError("max_len exceeds max_position_embeddings")
+        self.max_tokens = max(1, max_tokens)
+        self.embed = _Q4(dev, *embed_weights(cfg, seed))
+        self.layers = []
+        for layer in range(cfg.n_layers):
+            w = layer_weights(cfg, seed, layer)
+            self.layers.append({
+                "qkv": _Q4(dev, *w["qkv"]), "o": _Q4(dev, *w["o"]),
+                "gate_up": _Q4(dev, *w["gate_up"]), "down": _Q4(dev, *w["down"]),
+                "input_norm": dev.storage_from_bytes(w["input_norm"].tobytes()),
+                "post_norm": dev.storage_from_bytes(w["post_norm"].tobytes()),
+                "k_cache": dev.zeros(cfg.n_kv_heads * max_len * cfg.head_dim * 2),
+                "v_cache": dev.zeros(cfg.n_kv_heads * max_len * cfg.head_dim * 2),
+            })
+        self.final_norm = dev.storage_from_bytes(final_norm_weight(cfg, seed).tobytes())
+        cos, sin = rope_tables(cfg, max_len)
+        self.cos = dev.storage_from_bytes(cos.tobytes())
+        self.sin = dev.storage_from_bytes(sin.tobytes())
+        self.scale = float(np.float32(1.0) / np.sqrt(np.float32(cfg.head_dim), dtype=np.float32))
+        t, c = self.max_tokens, cfg
+        self.buf = {
+            "h": dev.empty(t * c.hidden * 2),
+            "x": dev.empty(t * c.hidden * 2),
+            "qkv": dev.empty(t * c.qkv_rows * 2),
+            "q": dev.empty(t * c.n_heads * c.head_dim * 2),
+            "attn": dev.empty(t * c.n_heads * c.head_dim * 2),
+            "o": dev.empty(t * c.hidden * 2),
+            "gu": dev.empty(t * 2 * c.ffn * 2),
+            "act": dev.empty(t * c.ffn * 2),
+            "logits": dev.empty(c.vocab * 2),
+            "ids": dev.empty(t * 4),
+            "positions": dev.empty(t * 4),
+            "next": dev.zeros(4),
+            "pos1": dev.zeros(4),
+        }
+
+    # ---- thin wrappers over the C-ABI ----
+    def _p(self, st: HipStorage, byte_offset: int = 0):
+        return ctypes.c_void_p(st.ptr + byte_offset)
+
+    def _linear(self, x: HipStorage, rows: int, w: _Q4, y: HipStorage, x_off: int = 0):
+        _lib.call("fh_q4_matmul", self.dev.handle, self._p(x, x_off), rows, w.k, w.k, self._p(w.wq),
+                  self._p(w.s), self._p(w.b), w.n, GROUP, self._p(y), _lib.BF16)
+
+    def _forward(self, tokens: int, ids: HipStorage, positions: HipStorage):
+        """One forward over `tokens` rows; leaves the next id in buf['next']."""
+        c, d, b = self.cfg, self.dev.handle, self.buf
+        _lib.call("fh_q4_embed", d, self._p(self.embed.wq), self._p(self.embed.s), self._p(self.embed.b),
+                  c.vocab, c.hidden, GROUP, self._p(ids), tokens, self._p(b["h"]))
+        pending = None  # output of the previous block still to be added to h
+        for L in self.layers:
+            self._norm(tokens, pending, L["input_norm"])
+            self._linear(b["x"], tokens, L["qkv"], b["qkv"])
+            _lib.call("fh_rope_kv", d, self._p(b["qkv"]), tokens, c.n_heads, c.n_kv_heads, c.head_dim,
+                      self._p(self.cos), self._p(self.sin), self.max_len, self._p(positions),
+                      self._p(L["k_cache"]), self._p(L["v_cache"]), self.max_len, self._p(b["q"]))
+            _lib.call("fh_attention", d, self._p(b["q"]), self._p(L["k_cache"]), self._p(L["v_cache"]),
+                      self._p(positions), tokens, c.n_heads, c.n_kv_heads, c.head_dim, self.max_len,
+                      ctypes.c_float(self.scale), self._p(b["attn"]))
+            self._linear(b["attn"], tokens, L["o"], b["o"])
+            self._norm(tokens, b["o"], L["post_norm"])
+            self._linear(b["x"], tokens, L["gate_up"], b["gu"])
+            _lib.call("fh_silu_mul", d, self._p(b["gu"]), tokens, c.ffn, self._p(b["act"]))
+            self._linear(b["act"], tokens, L["down"], b["o"])
+            pending = b["o"]
+        self._norm(tokens, pending, self.final_norm)
+        last = (tokens - 1) * c.hidden * 2
+        self._linear(b["x"], 1, self.embed, b["logits"], x_off=last)
+        _lib.call("fh_argmax", d, self._p(b["logits"]), 1, c.vocab, self._p(b["next"]))
+
+    def _norm(self, tokens: int, pending, weight: HipStorage):
+        """x = rms_norm(h [+ pending]); h updated in place when pending."""
+        c, b = self.cfg, self.buf
+        if pending is None:
+            _lib.call("fh_rms_norm", self.dev.handle, self._p(b["h"]), None, None, self._p(weight), tokens,
+                      c.hidden, ctypes.c_float(c.rms_norm_eps), self._p(b["x"]))
+        else:
+            _lib.call("fh_rms_norm", self.dev.handle, self._p(pending), self._p(b["h"]), self._p(b["h"]),
+                      self._p(weight), tokens, c.hidden, ctypes.c_float(c.rms_norm_eps), self._p(b["x"]))
+
+    # ---- prefill and decode ----
+    def prefill(self, prompt: np.ndarray) -> None:
+        """Runs the prompt (positions 0..T-1); the first generated id is left
+        on the device."""
+        t = int(prompt.size)
+        if t == 0 or t > self.max_tokens or t >= self.max_len:
+            raise ValueError(f"prompt of {t} tokens does not fit (max_tokens {self.max_tokens}, max_len {self.max_len})")
+        d = self.dev.handle
+        ids = np.ascontiguousarray(prompt, dtype=np.uint32)
+        _lib.call("fh_upload", d, self._p(self.buf["ids"]), ids.ctypes.data_as(ctypes.c_void_p), ids.nbytes)
+        pos = np.arange(t, dtype=np.uint32)
+        _lib.call("fh_upload", d, self._p(self.buf["positions"]), pos.ctypes.data_as(ctypes.c_void_p), pos.nbytes)
+        self._forward(t, self.buf["ids"], self.buf["positions"])
+        p1 = np.array([t], dtype=np.uint32)
+        _lib.call("fh_upload", d, self._p(self.buf["pos1"]), p1.ctypes.data_as(ctypes.c_void_p), 4)
+        self.prompt_len = t
+
+    def capture_decode(self, log: HipStorage, capacity: int):
+        """Captures one decode step: the token in buf['next'] at position
+        buf['pos1'] -> next token, logged at log[pos - prompt_len + 1] (index 0
+        is the prefill's token), then position + 1."""
+        d = self.dev.handle
+        self.dev.capture_begin()
+        try:
+            self._forward(1, self.buf["next"], self.buf["pos1"])
+            _lib.call("fh_append_token", d, self._p(self.buf["next"]), self._p(log), self._p(self.buf["pos1"]),
+                      self.prompt_len - 1, capacity)
+            _lib.call("fh_advance_positions", d, self._p(self.buf["pos1"]), 1, 1)
+        except Exception:
+            self.dev.capture_end()
+            raise
+        return self.dev.capture_end()
+
+    def generate(self, prompt: np.ndarray, new_tokens: int):
+        """Greedy generation (src/generate/mod.rs:45-90): returns the new ids
+        (the first is the prefill's argmax)."""
+        self.prefill(prompt)
+        if self.prompt_len + new_tokens > self.max_len:
+            raise ValueError("generation would run past the KV cache")
+        log = self.dev.zeros(4 * max(new_tokens, 1))
+        first = np.empty(1, dtype=np.uint32)
+        _lib.call("fh_download", self.dev.handle, first.ctypes.data_as(ctypes.c_void_p), self._p(self.buf["next"]), 4)
+        if new_tokens <= 1:
+            return first[:new_tokens]
+        graph = self.capture_decode(log, new_tokens)
+        for _ in range(new_tokens - 1):
+            graph.launch()
+        out = np.empty(new_tokens, dtype=np.uint32)
+        _lib.call("fh_download", self.dev.handle, out.ctypes.data_as(ctypes.c_void_p), self._p(log), 4 * new_tokens)
+        out[0] = first[0]
+        return out
+
+    def logits(self) -> np.ndarray:
+        """Last computed logits (bf16 bits) of the final position."""
+        out = np.empty(self.cfg.vocab, dtype=np.uint16)
+        _lib.call("fh_download", self.dev.handle, out.ctypes.data_as(ctypes.c_void_p), self._p(self.buf["logits"]),
+                  out.nbytes)
+        return out

@@ -178,6 +178,66 @@ int fh_q4_dequant(fh_device *dev, const uint32_t *wq, const uint16_t *scales,
                   const uint16_t *biases, int64_t rows, int64_t k, int64_t group,
                   uint16_t *out);
 
+/* ======================================================================
+ * Decoder-step ops: the plumbing around the q4 linears that a Llama decode
+ * step needs, each one kernel where the reference runs several dispatches.
+ * All tensors are bf16 (uint16_t bits) unless stated; every op rounds where
+ * the reference's op sequence rounds (its tensors are bf16).
+ * `positions` are device u32 arrays, so a captured decode step can be
+ * replayed with the position advanced on the device (fh_advance_positions).
+ * ====================================================================== */
+
+/* RmsNorm::forward (src/nn/norm.rs:32-50), optionally fused with the
+ * residual add before it (src/models/llama/model.rs:254-279):
+ *   h = residual ? RNE(x + residual) : x   (h written to residual_out)
+ *   y = RNE(RNE(h * 1/sqrt(sum(h^2)/dim + eps)) * weight)
+ * x, residual, residual_out, y: [rows, dim]; weight: [dim]. */
+int fh_rms_norm(fh_device *dev, const uint16_t *x, const uint16_t *residual,
+                uint16_t *residual_out, const uint16_t *weight, int64_t rows, int64_t dim,
+                float eps, uint16_t *y);
+
+/* apply_rotary_pos_emb (src/models/llama/rotary_emb.rs:62-85) on q and k of
+ * each token, then StaticCache::update (src/nn/kv_cache.rs:41-80) of k and v
+ * at the token's position. qkv: [tokens, (n_heads + 2 n_kv) * head_dim] (q
+ * heads, then k heads, then v heads); cos_tab/sin_tab: [table_len, head_dim];
+ * positions: device u32 [tokens]; k_cache/v_cache: [n_kv, max_len, head_dim];
+ * q_out: [tokens, n_heads, head_dim]. A position >= max_len or >= table_len
+ * writes nothing. */
+int fh_rope_kv(fh_device *dev, const uint16_t *qkv, int64_t tokens, int64_t n_heads,
+               int64_t n_kv, int64_t head_dim, const uint16_t *cos_tab, const uint16_t *sin_tab,
+               int64_t table_len, const uint32_t *positions, uint16_t *k_cache,
+               uint16_t *v_cache, int64_t max_len, uint16_t *q_out);
+
+/* scaled_dot_product_attention (src/nn/attention.rs:23-60) with the causal
+ * mask (src/nn/masking.rs:11-32): query token t attends keys 0..positions[t]
+ * of its KV head (grouped-query: head h uses KV head h / (n_heads/n_kv)).
+ * Scores RNE(q.k) (fp32 sums), times scale in fp32, softmax in fp32,
+ * probabilities RNE to bf16, out = RNE(sum p v). out: [tokens, n_heads *
+ * head_dim]. head_dim <= 256; max_len * 4 bytes must fit 64 KiB of LDS. */
+int fh_attention(fh_device *dev, const uint16_t *q, const uint16_t *k_cache,
+                 const uint16_t *v_cache, const uint32_t *positions, int64_t tokens,
+                 int64_t n_heads, int64_t n_kv, int64_t head_dim, int64_t max_len, float scale,
+                 uint16_t *out);
+
+/* LlamaMlp's act_fn(gate) * up (src/models/llama/mlp.rs:49-58, Silu at
+ * src/nn/activation.rs:19-28): gate_up row = [gate (f) | up (f)],
+ * out = RNE(RNE(g / (1 + exp(-g))) * u), out: [rows, f]. */
+int fh_silu_mul(fh_device *dev, const uint16_t *gate_up, int64_t rows, int64_t f, uint16_t *out);
+
+/* Greedy next token (src/generate/mod.rs:192-204): row argmax of bf16
+ * values, ties to the lowest index (src/metal/kernels/reduce.metal:42-78).
+ * x: [rows, n]; out: u32 [rows]. */
+int fh_argmax(fh_device *dev, const uint16_t *x, int64_t rows, int64_t n, uint32_t *out);
+
+/* log[*position - base] = *token when 0 <= *position - base < capacity: the
+ * greedy loop's token record, kept on the device so a captured step can be
+ * replayed without reading back each token. */
+int fh_append_token(fh_device *dev, const uint32_t *token, uint32_t *log, const uint32_t *position,
+                    int64_t base, int64_t capacity);
+
+/* positions[i] += by for i < n, on the device's stream. */
+int fh_advance_positions(fh_device *dev, uint32_t *positions, int64_t n, int64_t by);
+
 #ifdef __cplusplus
 }
 #endif

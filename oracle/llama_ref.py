@@ -1,0 +1,197 @@
+"""CPU restatement of the reference's Llama forward pass: TEST INFRASTRUCTURE ONLY.
+
+Used by tests/ and bench.py's agreement check as the checker of the HIP
+decoder (foundry_amd/llama.py). It follows the reference's op sequence and its
+bf16 rounding points (every reference tensor op rounds its output to the
+tensor dtype, bf16):
+
+- RmsNorm (src/nn/norm.rs:32-50): fp32 sum of squares, scale =
+  1/sqrt(ss * (1/dim) + eps), y = RNE(RNE(x * scale) * w).
+- Linear (src/nn/linear.rs:22-35 -> matmul_tiled): fp32 accumulation of
+  x . (s*q + b), RNE output. (numpy's sgemm sums in a different order than
+  matmul_tiled's sequential k; within fp32 accumulation error.)
+- RoPE (src/models/llama/rotary_emb.rs:62-85): rot = cat(-x2, x1),
+  RNE(RNE(x*cos) + RNE(rot*sin)); tables RNE(cos/sin(pos * inv_freq)) with
+  the llama3 frequency scaling (:135-186).
+- SDPA (src/nn/attention.rs:23-60): scores RNE(q.k), fp32 scale + causal
+  mask, fp32 softmax, RNE probabilities, RNE(p . v).
+- Silu * up (src/nn/activation.rs:19-28, src/models/llama/mlp.rs:49-58):
+  RNE(RNE(g / (exp(-g) + 1)) * u).
+- residual adds RNE(a + b); argmax with ties to the lowest index
+  (src/metal/kernels/reduce.metal:42-78).
+- generation comparison (src/eval/generation.rs:132-176).
+
+Weights are inputs (the same seeded q4 triplets the GPU model uses).
+"""
+from __future__ import annotations
+
+import numpy as np
+
+
+def rne(x) -> np.ndarray:
+    """float32 -> nearest bf16 (ties to even), returned as float32 values."""
+    f = np.ascontiguousarray(x, dtype=np.float32)
+    bits = f.view(np.uint32).astype(np.uint64)
+    r = (((bits + 0x7FFF + ((bits >> 16) & 1)) >> 16) << 16).astype(np.uint32)
+    nan = np.isnan(f)
+    if nan.any():
+        r[nan] = ((bits[nan] >> 16) | 0x40).astype(np.uint32) << 16
+    return r.view(np.float32)
+
+
+def from_bf16(bits) -> np.ndarray:
+    return (np.asarray(bits, dtype=np.uint16).astype(np.uint32) << 16).view(np.float32)
+
+
+def dequant_f32(wq, s, b, group: int = 64) -> np.ndarray:
+    """w = f32(s) * q + f32(b) (one rounding; s*q is exact)."""
+    n, kw = wq.shape
+    q = ((wq[:, :, None] >> (4 * np.arange(8, dtype=np.uint32))[None, None, :]) & 0xF).reshape(n, kw * 8)
+    sf = np.repeat(from_bf16(s), group, axis=1)
+    bf = np.repeat(from_bf16(b), group, axis=1)
+    return (sf * q.astype(np.float32)).astype(np.float32) + bf
+
+
+def inv_freq(head_dim, theta, scaling) -> np.ndarray:
+    out = []
+    for i in range(0, head_dim, 2):
+        f = np.float32(1.0) / np.power(np.float32(theta), np.float32(i) / np.float32(head_dim), dtype=np.float32)
+        if scaling is not None:
+            factor, low, high, orig = (np.float32(scaling[0]), np.float32(scaling[1]), np.float32(scaling[2]),
+                                       np.float32(scaling[3]))
+            wl = np.float32(2 * np.pi) / f
+            fs = f / factor if wl > orig / low else f
+            smooth = (orig / wl - low) / (high - low)
+            if orig / high <= wl <= orig / low:
+                fs = (np.float32(1) - smooth) * fs / factor + smooth * fs
+            f = np.float32(fs)
+        out.append(f)
+    return np.array(out, dtype=np.float32)
+
+
+def rope_tables(head_dim, theta, scaling, length):
+    f = inv_freq(head_dim, theta, scaling)
+    ang = (np.arange(length, dtype=np.float32)[:, None] * np.concatenate([f, f])[None, :]).astype(np.float32)
+    return rne(np.cos(ang)), rne(np.sin(ang))
+
+
+class RefLlama:
+    """Reference-arithmetic model. `weights` supplies, per layer, dicts with
+    q4 triplets 'qkv' ([q;k;v] rows), 'o', 'gate_up' ([gate;up] rows), 'down'
+    and bf16 'input_norm', 'post_norm'; plus 'embed' and 'final_norm'."""
+
+    def __init__(self, cfg, embed, layers, final_norm, max_len):
+        self.cfg, self.max_len = cfg, max_len
+        self.embed_q4 = embed
+        self.embed_f = dequant_f32(*embed)
+        self.layers = []
+        for L in layers:
+            self.layers.append({k: dequant_f32(*L[k]) for k in ("qkv", "o", "gate_up", "down")}
+                               | {k: from_bf16(L[k]) for k in ("input_norm", "post_norm")})
+        self.final_norm = from_bf16(final_norm)
+        sc = cfg.rope_scaling
+        scaling = None if sc is None else (sc.factor, sc.low_freq_factor, sc.high_freq_factor,
+                                           sc.original_max_position_embeddings)
+        self.cos, self.sin = rope_tables(cfg.head_dim, cfg.rope_theta, scaling, max_len)
+        self.reset()
+
+    def reset(self):
+        c = self.cfg
+        self.k = [np.zeros((c.n_kv_heads, self.max_len, c.head_dim), np.float32) for _ in self.layers]
+        self.v = [np.zeros((c.n_kv_heads, self.max_len, c.head_dim), np.float32) for _ in self.layers]
+
+    def rms_norm(self, h, w):
+        ss = np.sum(h * h, axis=-1, dtype=np.float32, keepdims=True)
+        scale = np.float32(1.0) / np.sqrt(ss * np.float32(1.0 / h.shape[-1]) + np.float32(self.cfg.rms_norm_eps))
+        return rne(rne(h * scale) * w)
+
+    @staticmethod
+    def linear(x, w):
+        return rne(x @ w.T)
+
+    def rope(self, x, pos):
+        d = x.shape[-1] // 2
+        rot = np.concatenate([-x[..., d:], x[..., :d]], axis=-1)
+        c, s = self.cos[pos][:, None, :], self.sin[pos][:, None, :]
+        return rne(rne(x * c) + rne(rot * s))
+
+    def forward(self, ids, positions):
+        """Returns the last position's logits (float32 of bf16 values)."""
+        c = self.cfg
+        t = len(ids)
+        pos = np.asarray(positions)
+        h = rne(self.embed_f[np.asarray(ids)])
+        group = c.n_heads // c.n_kv_heads
+        scale = np.float32(1.0) / np.sqrt(np.float32(c.head_dim), dtype=np.float32)
+        for li, L in enumerate(self.layers):
+            x = self.rms_norm(h, L["input_norm"])
+            qkv = self.linear(x, L["qkv"])
+            hq, hk = c.n_heads * c.head_dim, c.n_kv_heads * c.head_dim
+            q = qkv[:, :hq].reshape(t, c.n_heads, c.head_dim)
+            k = qkv[:, hq:hq + hk].reshape(t, c.n_kv_heads, c.head_dim)
+            v = qkv[:, hq + hk:].reshape(t, c.n_kv_heads, c.head_dim)
+            q, k = self.rope(q, pos), self.rope(k, pos)
+            self.k[li][:, pos, :] = k.transpose(1, 0, 2)
+            self.v[li][:, pos, :] = v.transpose(1, 0, 2)
+            ctx = int(pos.max()) + 1
+            out = np.empty((t, c.n_heads, c.head_dim), np.float32)
+            for hh in range(c.n_heads):
+                kv = hh // group
+                sc = rne(q[:, hh, :] @ self.k[li][kv, :ctx, :].T) * scale
+                mask = np.arange(ctx)[None, :] > pos[:, None]
+                sc = np.where(mask, np.float32(-np.inf), sc).astype(np.float32)
+                m = sc.max(axis=-1, keepdims=True)
+                e = np.exp(sc - m).astype(np.float32)
+                p = rne(e / e.sum(axis=-1, dtype=np.float32, keepdims=True))
+                out[:, hh, :] = rne(p @ self.v[li][kv, :ctx, :])
+            a = self.linear(out.reshape(t, -1), L["o"])
+            h = rne(h + a)
+            x = self.rms_norm(h, L["post_norm"])
+            gu = self.linear(x, L["gate_up"])
+            g, u = gu[:, :c.ffn], gu[:, c.ffn:]
+            act = rne(rne(g / (np.exp(-g).astype(np.float32) + np.float32(1.0))) * u)
+            h = rne(h + self.linear(act, L["down"]))
+        x = self.rms_norm(h, self.final_norm)
+        return self.linear(x[-1:], self.embed_f)[0]
+
+    def generate(self, prompt, new_tokens, top_k=5):
+        """Greedy tokens and, per step, the top-k ids (ranked by logit, then
+        by the lowest id)."""
+        self.reset()
+        ids = list(int(i) for i in prompt)
+        logits = self.forward(ids, np.arange(len(ids)))
+        tokens, tops = [], []
+        for step in range(new_tokens):
+            tokens.append(argmax(logits))
+            tops.append(top_ids(logits, top_k))
+            if step + 1 == new_tokens:
+                break
+            p = len(prompt) + step
+            logits = self.forward([tokens[-1]], np.array([p]))
+        return np.array(tokens, dtype=np.uint32), tops
+
+
+def argmax(values) -> int:
+    v = np.asarray(values, dtype=np.float32)
+    return int(np.flatnonzero(v == v.max())[0])
+
+
+def top_ids(values, k):
+    v = np.asarray(values, dtype=np.float32)
+    order = np.lexsort((np.arange(v.size), -v))
+    return [int(i) for i in order[:k]]
+
+
+def compare_generation(actual_tokens, actual_tops, expected_tokens, expected_tops):
+    """src/eval/generation.rs:132-176: close when the tokens match, or when at
+    the first divergence each token is in the other run's top-k."""
+    n = min(len(actual_tokens), len(expected_tokens))
+    first = next((i for i in range(n) if actual_tokens[i] != expected_tokens[i]), None)
+
+    def in_top(tops, step, tok):
+        return step < len(tops) and tok in tops[step]
+
+    close = n > 0 and (first is None or (in_top(expected_tops, first, int(actual_tokens[first]))
+                                         and in_top(actual_tops, first, int(expected_tokens[first]))))
+    return {"compared_tokens": n, "matched_tokens": n if first is None else first,
+            "first_divergence": first, "close": bool(close)}
