@@ -172,6 +172,93 @@ def cpu_baseline(seconds: float = 12.0):
     return out, cpu
 
 
+def decode_step_bytes(cfg, context: int) -> int:
+    """HBM bytes one decode step must read at a given context: every q4 linear
+    (weights + scales/biases), the LM head (tied table), the norm weights and
+    the K/V cache rows attended to."""
+    def q4(n, k):
+        return n * k // 2 + 4 * n * (k // 64)
+
+    per_layer = (q4(cfg.qkv_rows, cfg.hidden) + q4(cfg.hidden, cfg.n_heads * cfg.head_dim)
+                 + q4(2 * cfg.ffn, cfg.hidden) + q4(cfg.hidden, cfg.ffn) + 2 * 2 * cfg.hidden
+                 + 2 * cfg.n_kv_heads * cfg.head_dim * 2 * context)
+    return cfg.n_layers * per_layer + q4(cfg.vocab, cfg.hidden) + 2 * cfg.hidden
+
+
+def bench_decode(dev, new_tokens: int, agreement: int, seed: int = 0):
+    """Config 4: Llama-3.2-3B-shaped random-init q4 decoder, the reference's
+    512 seeded prompt ids (SplitMix64 seed 0, vocab 128256), greedy decode
+    through the captured step."""
+    from foundry_amd.llama import LlamaConfig, Q4Llama
+
+    cfg = LlamaConfig.llama_3_2_3b()
+    prompt = synth.token_ids(0, 512, cfg.vocab)
+    max_len = len(prompt) + max(new_tokens, agreement)
+    t0 = time.perf_counter()
+    model = Q4Llama(dev, cfg, seed, max_len, max_tokens=len(prompt) + agreement)
+    build_s = time.perf_counter() - t0
+    model.generate(prompt[:64], 4)  # warm the kernels once
+    dev.timer_begin()
+    model.prefill(prompt)
+    prefill_ms = dev.timer_end()
+    log = dev.zeros(4 * new_tokens)
+    first = np.empty(1, dtype=np.uint32)
+    _lib.call("fh_download", dev.handle, first.ctypes.data_as(ctypes.c_void_p), ctypes.c_void_p(model.buf["next"].ptr), 4)
+    graph = model.capture_decode(log, new_tokens)
+    dev.timer_begin()
+    for _ in range(new_tokens - 1):
+        graph.launch()
+    decode_ms = dev.timer_end()
+    tokens = np.empty(new_tokens, dtype=np.uint32)
+    _lib.call("fh_download", dev.handle, tokens.ctypes.data_as(ctypes.c_void_p), ctypes.c_void_p(log.ptr), tokens.nbytes)
+    tokens[0] = first[0]
+    steps = new_tokens - 1
+    step_ms = decode_ms / steps
+    mean_ctx = len(prompt) + steps / 2
+    step_bytes = decode_step_bytes(cfg, int(mean_ctx))
+    out = {
+        "config": "Llama-3.2-3B shape (28 layers, hidden 3072, 24/8 heads, head_dim 128, FFN 8192, vocab 128256), "
+                  "q4 group 64, tied embedding/LM head, random init",
+        "prompt_tokens": len(prompt), "new_tokens": new_tokens,
+        "prefill_ms": prefill_ms, "prefill_tok_s": len(prompt) / (prefill_ms * 1e-3),
+        "decode_ms_per_step": step_ms, "decode_tok_s": 1e3 / step_ms,
+        "decode_bytes_per_step": step_bytes,
+        "decode_GB_per_s": step_bytes / (step_ms * 1e-3) / 1e9,
+        "decode_frac_hbm_peak": step_bytes / (step_ms * 1e-3) / 1e9 / HBM_PEAK_GBS,
+        "decode_ceiling_tok_s_at_peak": HBM_PEAK_GBS * 1e9 / step_bytes,
+        "model_build_s": build_s,
+        "first_tokens": tokens[:8].tolist(),
+    }
+    if agreement:
+        out["agreement"] = greedy_agreement(model, cfg, seed, prompt, tokens, agreement)
+    return out
+
+
+def greedy_agreement(model, cfg, seed, prompt, tokens, n):
+    """Greedy agreement with the CPU restatement of the reference's forward
+    (oracle/llama_ref.py) over the first n new tokens, by the reference's rule
+    (src/eval/generation.rs:132-176) with top-k 5."""
+    from foundry_amd.llama import embed_weights, final_norm_weight, layer_weights
+    from oracle import llama_ref as R  # checker only
+
+    t0 = time.perf_counter()
+    layers = [layer_weights(cfg, seed, l) for l in range(cfg.n_layers)]
+    ref = R.RefLlama(cfg, embed_weights(cfg, seed), layers, final_norm_weight(cfg, seed), len(prompt) + n)
+    exp_tokens, exp_tops = ref.generate(prompt, n)
+    got = tokens[:n]
+    report = R.compare_generation(got, [[]] * n, exp_tokens, exp_tops)
+    if report["first_divergence"] is not None:
+        d = report["first_divergence"]
+        model.prefill(np.concatenate([prompt, got[:d]]).astype(np.uint32))
+        gpu_tops = [[]] * n
+        gpu_tops[d] = R.top_ids(R.from_bf16(model.logits()), 5)
+        report = R.compare_generation(got, gpu_tops, exp_tokens, exp_tops)
+    report["cpu_s"] = time.perf_counter() - t0
+    report["gpu_tokens"] = got.tolist()
+    report["reference_arithmetic_tokens"] = exp_tokens.tolist()
+    return report
+
+
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "q4_gemv_8192x3072_traffic.md")
 
 
@@ -219,6 +306,9 @@ def main() -> int:
     ap.add_argument("--quick", action="store_true", help="headline only, no secondary lines")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="also run one device copy of known size (counter calibration)")
+    ap.add_argument("--decode-tokens", type=int, default=256, help="config-4 greedy steps (0 skips)")
+    ap.add_argument("--agreement", type=int, default=0,
+                    help="compare the first N config-4 tokens with the CPU reference arithmetic")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not supported "
@@ -240,6 +330,11 @@ def main() -> int:
         secondary["gemm_gate_up"] = bench_gemm(dev, 2048, 8192, 3072, max(5, args.steps // 5), 2, seed=7)
         secondary["gemm_down"] = bench_gemm(dev, 2048, 3072, 8192, max(5, args.steps // 5), 2, seed=9)
         print(f"[bench] gemm: {secondary['gemm_gate_up']['TFLOP_per_s']:.0f} TFLOP/s", flush=True)
+    if not args.quick and args.decode_tokens > 1:
+        secondary["decode_llama_3_2_3b"] = bench_decode(dev, args.decode_tokens, args.agreement)
+        d = secondary["decode_llama_3_2_3b"]
+        print(f"[bench] decode: {d['decode_tok_s']:.0f} tok/s ({d['decode_frac_hbm_peak']*100:.1f}% of HBM roofline), "
+              f"prefill {d['prefill_tok_s']:.0f} tok/s", flush=True)
     dev.close()
 
     cpu = None
@@ -273,6 +368,7 @@ def main() -> int:
                      "algorithmic_bytes_per_launch": per_launch_bytes,
                      "us_per_launch": head["us_per_launch"]},
         "cpu_baseline": cpu,
+        "decode_tok_s": secondary.get("decode_llama_3_2_3b", {}).get("decode_tok_s"),
         "secondary": secondary,
     }
     print(json.dumps(line), flush=True)

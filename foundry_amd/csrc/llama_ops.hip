@@ -53,38 +53,88 @@ __device__ __forceinline__ float block_max(float v, float *red) {
     return t;
 }
 
-// One block per row. With `res`, h = RNE(x + res) is formed first (the
-// residual add, src/models/llama/model.rs:254-279) and written to res_out.
-// y = RNE(RNE(h * scale) * w), scale = 1 / sqrt(sum(h^2) * (1/dim) + eps).
-__global__ __launch_bounds__(256) void rms_norm_kernel(const uint16_t *__restrict__ x,
-                                                       const uint16_t *__restrict__ res,
-                                                       uint16_t *__restrict__ res_out,
-                                                       const uint16_t *__restrict__ w,
-                                                       uint32_t dim, float eps, float dim_inv,
-                                                       uint16_t *__restrict__ y) {
-    __shared__ float red[4];
+// One block per row, the row held in registers (16-byte loads, up to
+// kNormChunks pieces of 8 per thread). With `res`, h = RNE(x + res) is formed
+// first (the residual add, src/models/llama/model.rs:254-279) and written to
+// res_out. y = RNE(RNE(h * scale) * w), scale = 1 / sqrt(sum(h^2) * (1/dim) + eps).
+constexpr int kNormThreads = 256;
+constexpr int kNormChunks = 4;  // dim <= 256 * 8 * 4 = 8192
+
+__global__ __launch_bounds__(kNormThreads) void rms_norm_kernel(const uint16_t *__restrict__ x,
+                                                                const uint16_t *__restrict__ res,
+                                                                uint16_t *__restrict__ res_out,
+                                                                const uint16_t *__restrict__ w,
+                                                                uint32_t dim, float eps, float dim_inv,
+                                                                uint16_t *__restrict__ y) {
+    __shared__ float red[kNormThreads / 64];
     const uint64_t base = static_cast<uint64_t>(blockIdx.x) * dim;
+    const uint32_t pieces = dim / 8;
+    float h[kNormChunks][8];
     float ss = 0.f;
-    for (uint32_t i = threadIdx.x; i < dim; i += blockDim.x) {
-        float h = bf(x[base + i]);
-        if (res) {
-            const uint16_t hb = rne(h + bf(res[base + i]));
-            res_out[base + i] = hb;
-            h = bf(hb);
+#pragma unroll
+    for (int c = 0; c < kNormChunks; ++c) {
+        const uint32_t piece = threadIdx.x + c * kNormThreads;
+        if (piece < pieces) {
+            const uint4 xv = *reinterpret_cast<const uint4 *>(x + base + piece * 8);
+            const uint32_t xw[4] = {xv.x, xv.y, xv.z, xv.w};
+            uint32_t hw[4];
+            if (res) {
+                const uint4 rv = *reinterpret_cast<const uint4 *>(res + base + piece * 8);
+                const uint32_t rw[4] = {rv.x, rv.y, rv.z, rv.w};
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const uint32_t lo = rne(bf(xw[e] & 0xFFFFu) + bf(rw[e] & 0xFFFFu));
+                    const uint32_t hi = rne(bf(xw[e] >> 16) + bf(rw[e] >> 16));
+                    hw[e] = lo | (hi << 16);
+                }
+                *reinterpret_cast<uint4 *>(res_out + base + piece * 8) = make_uint4(hw[0], hw[1], hw[2], hw[3]);
+            } else {
+#pragma unroll
+                for (int e = 0; e < 4; ++e) hw[e] = xw[e];
+            }
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                h[c][2 * e] = bf(hw[e] & 0xFFFFu);
+                h[c][2 * e + 1] = bf(hw[e] >> 16);
+            }
+#pragma unroll
+            for (int e = 0; e < 8; ++e) ss += h[c][e] * h[c][e];
         }
-        ss += h * h;
     }
     ss = block_sum(ss, red);
     const float scale = 1.0f / sqrtf(ss * dim_inv + eps);
-    for (uint32_t i = threadIdx.x; i < dim; i += blockDim.x) {
-        const float h = bf(res ? res_out[base + i] : x[base + i]);
-        y[base + i] = rne(bf(rne(h * scale)) * bf(w[i]));
+#pragma unroll
+    for (int c = 0; c < kNormChunks; ++c) {
+        const uint32_t piece = threadIdx.x + c * kNormThreads;
+        if (piece < pieces) {
+            const uint4 wv = *reinterpret_cast<const uint4 *>(w + piece * 8);
+            const uint32_t ww[4] = {wv.x, wv.y, wv.z, wv.w};
+            uint32_t o[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const uint32_t lo = rne(bf(rne(h[c][2 * e] * scale)) * bf(ww[e] & 0xFFFFu));
+                const uint32_t hi = rne(bf(rne(h[c][2 * e + 1] * scale)) * bf(ww[e] >> 16));
+                o[e] = lo | (hi << 16);
+            }
+            *reinterpret_cast<uint4 *>(y + base + piece * 8) = make_uint4(o[0], o[1], o[2], o[3]);
+        }
     }
 }
 
 // RoPE on q and k of one token (block), then k and v into the cache at the
 // token's position. qkv row: [q heads | k heads | v heads] * head_dim.
-// x' = RNE(RNE(x * cos) + RNE(rot * sin)), rot = cat(-x2, x1).
+// x' = RNE(RNE(x * cos) + RNE(rot * sin)), rot = cat(-x2, x1). A thread
+// handles 8 consecutive dims (16-byte loads); its rotation partner is the
+// matching 8 dims of the other half (head_dim is a multiple of 16).
+__device__ __forceinline__ void unpack8(const uint4 v, float (&f)[8]) {
+    const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        f[2 * e] = bf(w[e] & 0xFFFFu);
+        f[2 * e + 1] = bf(w[e] >> 16);
+    }
+}
+
 __global__ __launch_bounds__(256) void rope_kv_kernel(
     const uint16_t *__restrict__ qkv, uint32_t n_heads, uint32_t n_kv, uint32_t head_dim,
     const uint16_t *__restrict__ cos_tab, const uint16_t *__restrict__ sin_tab, uint32_t table_len,
@@ -99,25 +149,36 @@ __global__ __launch_bounds__(256) void rope_kv_kernel(
     const uint16_t *row = qkv + static_cast<uint64_t>(t) * width;
     const uint16_t *c = cos_tab + static_cast<uint64_t>(pos) * head_dim;
     const uint16_t *s = sin_tab + static_cast<uint64_t>(pos) * head_dim;
-    const uint32_t half = head_dim / 2;
-    const uint32_t rot_elems = (n_heads + n_kv) * head_dim;
-    for (uint32_t i = threadIdx.x; i < rot_elems; i += blockDim.x) {
-        const uint32_t h = i / head_dim, d = i % head_dim;
-        const uint16_t *xh = row + h * head_dim;
-        const float xv = bf(xh[d]);
-        const float rv = d < half ? -bf(xh[d + half]) : bf(xh[d - half]);
-        const uint16_t out = rne(bf(rne(xv * bf(c[d]))) + bf(rne(rv * bf(s[d]))));
-        if (h < n_heads) {
-            q_out[(static_cast<uint64_t>(t) * n_heads + h) * head_dim + d] = out;
-        } else {
-            const uint32_t kh = h - n_heads;
-            k_cache[(static_cast<uint64_t>(kh) * max_len + pos) * head_dim + d] = out;
+    const uint32_t ppw = head_dim / 8, hp = ppw / 2;  // pieces per head, per half
+    const uint32_t rot_pieces = (n_heads + n_kv) * ppw;
+    for (uint32_t i = threadIdx.x; i < rot_pieces; i += blockDim.x) {
+        const uint32_t h = i / ppw, p = i % ppw;
+        const uint32_t partner = p < hp ? p + hp : p - hp;
+        const float sign = p < hp ? -1.0f : 1.0f;
+        float xv[8], rv[8], cv[8], sv[8];
+        unpack8(*reinterpret_cast<const uint4 *>(row + h * head_dim + p * 8), xv);
+        unpack8(*reinterpret_cast<const uint4 *>(row + h * head_dim + partner * 8), rv);
+        unpack8(*reinterpret_cast<const uint4 *>(c + p * 8), cv);
+        unpack8(*reinterpret_cast<const uint4 *>(s + p * 8), sv);
+        uint32_t o[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const uint32_t lo = rne(bf(rne(xv[2 * e] * cv[2 * e])) + bf(rne(sign * rv[2 * e] * sv[2 * e])));
+            const uint32_t hi =
+                rne(bf(rne(xv[2 * e + 1] * cv[2 * e + 1])) + bf(rne(sign * rv[2 * e + 1] * sv[2 * e + 1])));
+            o[e] = lo | (hi << 16);
         }
+        const uint4 ov = make_uint4(o[0], o[1], o[2], o[3]);
+        if (h < n_heads)
+            *reinterpret_cast<uint4 *>(q_out + (static_cast<uint64_t>(t) * n_heads + h) * head_dim + p * 8) = ov;
+        else
+            *reinterpret_cast<uint4 *>(k_cache + (static_cast<uint64_t>(h - n_heads) * max_len + pos) * head_dim + p * 8) = ov;
     }
-    const uint16_t *vrow = row + rot_elems;
-    for (uint32_t i = threadIdx.x; i < n_kv * head_dim; i += blockDim.x) {
-        const uint32_t kh = i / head_dim, d = i % head_dim;
-        v_cache[(static_cast<uint64_t>(kh) * max_len + pos) * head_dim + d] = vrow[i];
+    const uint16_t *vrow = row + rot_pieces * 8;
+    for (uint32_t i = threadIdx.x; i < n_kv * ppw; i += blockDim.x) {
+        const uint32_t kh = i / ppw, p = i % ppw;
+        *reinterpret_cast<uint4 *>(v_cache + (static_cast<uint64_t>(kh) * max_len + pos) * head_dim + p * 8) =
+            *reinterpret_cast<const uint4 *>(vrow + i * 8);
     }
 }
 
@@ -125,7 +186,7 @@ __global__ __launch_bounds__(256) void rope_kv_kernel(
 // head (causal; decode uses pos = current position). Scores: RNE(q . k) with
 // fp32 accumulation, then s * scale in fp32; softmax in fp32; probabilities
 // rounded to bf16; out = RNE(sum_j p_j v_j) in fp32. Scores go through LDS
-// (max_len floats); head_dim <= 256.
+// (max_len floats); head_dim is 64, 128 or 256.
 __global__ __launch_bounds__(256) void attention_kernel(
     const uint16_t *__restrict__ q, const uint16_t *__restrict__ k_cache,
     const uint16_t *__restrict__ v_cache, const uint32_t *__restrict__ positions,
@@ -171,22 +232,46 @@ __global__ __launch_bounds__(256) void attention_kernel(
     sum = block_sum(sum, red);
     for (uint32_t j = threadIdx.x; j < ctx; j += blockDim.x) scores[j] = bf(rne(scores[j] / sum));
     __syncthreads();
-    // out[d]: threads split (dim, key half); keys ascending within each half
-    const uint32_t halves = blockDim.x / head_dim;  // >= 1 when head_dim <= 256
-    const uint32_t d = threadIdx.x % head_dim, part = threadIdx.x / head_dim;
-    float acc = 0.f;
-    if (part < halves) {
-        const uint32_t per = (ctx + halves - 1) / halves;
-        const uint32_t j0 = part * per, j1 = j0 + per < ctx ? j0 + per : ctx;
-        for (uint32_t j = j0; j < j1; ++j) acc += scores[j] * bf(vb[static_cast<uint64_t>(j) * head_dim + d]);
+    // out[d] = sum_j p_j v_j[d]: wavefront w takes keys j = w, w+4, ...; lane
+    // l takes dims l*DPL .. +DPL, so each key's V row is one coalesced read.
+    // The four partial vectors are summed through LDS (in wavefront order).
+    const uint32_t wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const uint32_t dpl = head_dim / 64;  // 1, 2 or 4
+    float acc[4] = {0.f, 0.f, 0.f, 0.f};
+    // batches of kBatchKeys keys: all loads of a batch are issued before any
+    // is used, so the wavefront waits for memory once per batch, not per key
+    constexpr int kBatchKeys = 8;
+    for (uint32_t j0 = wave; j0 < ctx; j0 += 4 * kBatchKeys) {
+        uint2 v[kBatchKeys];
+        float p[kBatchKeys];
+#pragma unroll
+        for (int u = 0; u < kBatchKeys; ++u) {
+            const uint32_t j = j0 + 4 * u;
+            const bool ok = j < ctx;
+            const uint16_t *vr = vb + static_cast<uint64_t>(ok ? j : 0) * head_dim + lane * dpl;
+            if (dpl == 4)
+                v[u] = *reinterpret_cast<const uint2 *>(vr);
+            else if (dpl == 2)
+                v[u] = make_uint2(*reinterpret_cast<const uint32_t *>(vr), 0u);
+            else
+                v[u] = make_uint2(vr[0], 0u);
+            p[u] = ok ? scores[j] : 0.f;
+        }
+#pragma unroll
+        for (int u = 0; u < kBatchKeys; ++u) {
+            acc[0] += p[u] * bf(v[u].x & 0xFFFFu);
+            acc[1] += p[u] * bf(v[u].x >> 16);
+            acc[2] += p[u] * bf(v[u].y & 0xFFFFu);
+            acc[3] += p[u] * bf(v[u].y >> 16);
+        }
     }
     __syncthreads();
-    float *partial = scores;  // reuse
-    if (part < halves) partial[part * head_dim + d] = acc;
+    float *partial = scores;  // reuse: [4][head_dim]
+    for (uint32_t e = 0; e < dpl; ++e) partial[wave * head_dim + lane * dpl + e] = acc[e];
     __syncthreads();
     if (threadIdx.x < head_dim) {
-        float o = 0.f;
-        for (uint32_t p = 0; p < halves; ++p) o += partial[p * head_dim + threadIdx.x];
+        const float o = partial[threadIdx.x] + partial[head_dim + threadIdx.x] + partial[2 * head_dim + threadIdx.x] +
+                        partial[3 * head_dim + threadIdx.x];
         out[(static_cast<uint64_t>(t) * n_heads + h) * head_dim + threadIdx.x] = rne(o);
     }
 }
@@ -203,26 +288,44 @@ __global__ __launch_bounds__(256) void silu_mul_kernel(const uint16_t *__restric
     out[i] = rne(bf(rne(g / den)) * u);
 }
 
-// Row argmax of bf16 values; ties go to the lowest index.
-__global__ __launch_bounds__(256) void argmax_kernel(const uint16_t *__restrict__ x, uint32_t n,
-                                                     uint32_t *__restrict__ out) {
-    __shared__ float bv[256];
-    __shared__ uint32_t bi[256];
+// Row argmax of bf16 values; ties go to the lowest index. One block of 1024
+// threads per row, 16-byte loads (8 values) per thread per step.
+constexpr int kArgmaxThreads = 1024;
+
+__device__ __forceinline__ void take_max(float &best, uint32_t &idx, float v, uint32_t i) {
+    if (v > best || (v == best && i < idx)) {
+        best = v;
+        idx = i;
+    }
+}
+
+__global__ __launch_bounds__(kArgmaxThreads) void argmax_kernel(const uint16_t *__restrict__ x, uint32_t n,
+                                                                uint32_t *__restrict__ out) {
+    __shared__ float bv[kArgmaxThreads];
+    __shared__ uint32_t bi[kArgmaxThreads];
     const uint16_t *row = x + static_cast<uint64_t>(blockIdx.x) * n;
     float best = -INFINITY;
     uint32_t idx = 0xFFFFFFFFu;
-    // indices ascend per thread, so the first maximum seen is the lowest
-    for (uint32_t i = threadIdx.x; i < n; i += blockDim.x) {
-        const float v = bf(row[i]);
-        if (v > best || idx == 0xFFFFFFFFu) {
-            best = v;
-            idx = i;
+    const uint32_t pieces = n / 8;
+    const bool aligned = (reinterpret_cast<uintptr_t>(row) & 15u) == 0;
+    if (aligned) {
+        for (uint32_t p = threadIdx.x; p < pieces; p += kArgmaxThreads) {
+            const uint4 v = *reinterpret_cast<const uint4 *>(row + p * 8);
+            const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                take_max(best, idx, bf(w[e] & 0xFFFFu), p * 8 + 2 * e);
+                take_max(best, idx, bf(w[e] >> 16), p * 8 + 2 * e + 1);
+            }
         }
     }
+    for (uint32_t i = (aligned ? pieces * 8 : 0) + threadIdx.x; i < n; i += kArgmaxThreads)
+        take_max(best, idx, bf(row[i]), i);
+    if (idx == 0xFFFFFFFFu) best = -INFINITY;
     bv[threadIdx.x] = best;
     bi[threadIdx.x] = idx;
     __syncthreads();
-    for (uint32_t off = blockDim.x / 2; off > 0; off >>= 1) {
+    for (uint32_t off = kArgmaxThreads / 2; off > 0; off >>= 1) {
         if (threadIdx.x < off) {
             const float ov = bv[threadIdx.x + off];
             const uint32_t oi = bi[threadIdx.x + off];
@@ -273,6 +376,14 @@ extern "C" int fh_rms_norm(fh_device *dev, const uint16_t *x, const uint16_t *re
     if (rows == 0 || dim == 0) return FH_OK;
     if ((residual == nullptr) != (residual_out == nullptr))
         return fail(FH_ERR_INVALID_ARGUMENT, "%s: residual and residual_out go together", fn);
+    if (dim % 8 != 0 || dim > 8 * kNormThreads * kNormChunks)
+        return fail(FH_ERR_UNSUPPORTED, "%s: dim %lld must be a multiple of 8 and at most %d", fn,
+                    (long long)dim, 8 * kNormThreads * kNormChunks);
+    for (const void *p : {static_cast<const void *>(x), static_cast<const void *>(residual),
+                          static_cast<const void *>(residual_out), static_cast<const void *>(weight),
+                          static_cast<const void *>(y)})
+        if (reinterpret_cast<uintptr_t>(p) % 16 != 0)
+            return fail(FH_ERR_INVALID_ARGUMENT, "%s: operands must be 16-byte aligned", fn);
     const uint64_t bytes = static_cast<uint64_t>(rows) * dim * 2;
     if (int rc = check_range(dev, x, bytes, fn, "x")) return rc;
     if (residual) {
@@ -284,7 +395,7 @@ extern "C" int fh_rms_norm(fh_device *dev, const uint16_t *x, const uint16_t *re
     if (int rc = set_current(dev, fn)) return rc;
     const float dim_inv = 1.0f / static_cast<float>(dim);
     return dispatch(dev, fn, [&] {
-        hipLaunchKernelGGL(rms_norm_kernel, dim3(static_cast<uint32_t>(rows)), dim3(256), 0,
+        hipLaunchKernelGGL(rms_norm_kernel, dim3(static_cast<uint32_t>(rows)), dim3(kNormThreads), 0,
                            dev->stream, x, residual, residual_out, weight,
                            static_cast<uint32_t>(dim), eps, dim_inv, y);
     });
@@ -299,9 +410,14 @@ extern "C" int fh_rope_kv(fh_device *dev, const uint16_t *qkv, int64_t tokens, i
     if (int rc = check_usable(dev, fn)) return rc;
     if (int rc = check_dims(fn, {tokens, n_heads, n_kv, head_dim, table_len, max_len})) return rc;
     if (tokens == 0) return FH_OK;
-    if (n_kv == 0 || n_heads % n_kv != 0 || head_dim % 8 != 0 || head_dim == 0)
+    if (n_kv == 0 || n_heads % n_kv != 0 || head_dim % 16 != 0 || head_dim == 0)
         return fail(FH_ERR_INVALID_ARGUMENT, "%s: heads %lld/%lld, head_dim %lld", fn,
                     (long long)n_heads, (long long)n_kv, (long long)head_dim);
+    for (const void *p : {static_cast<const void *>(qkv), static_cast<const void *>(cos_tab),
+                          static_cast<const void *>(sin_tab), static_cast<const void *>(k_cache),
+                          static_cast<const void *>(v_cache), static_cast<const void *>(q_out)})
+        if (reinterpret_cast<uintptr_t>(p) % 16 != 0)
+            return fail(FH_ERR_INVALID_ARGUMENT, "%s: operands must be 16-byte aligned", fn);
     const uint64_t width = static_cast<uint64_t>(n_heads + 2 * n_kv) * head_dim;
     if (int rc = check_range(dev, qkv, tokens * width * 2, fn, "qkv")) return rc;
     if (int rc = check_range(dev, cos_tab, static_cast<uint64_t>(table_len) * head_dim * 2, fn, "cos")) return rc;
@@ -329,10 +445,11 @@ extern "C" int fh_attention(fh_device *dev, const uint16_t *q, const uint16_t *k
     if (int rc = check_usable(dev, fn)) return rc;
     if (int rc = check_dims(fn, {tokens, n_heads, n_kv, head_dim, max_len})) return rc;
     if (tokens == 0) return FH_OK;
-    if (n_kv == 0 || n_heads % n_kv != 0 || head_dim == 0 || head_dim > 256 || head_dim % 8 != 0)
+    if (n_kv == 0 || n_heads % n_kv != 0 || (head_dim != 64 && head_dim != 128 && head_dim != 256))
         return fail(FH_ERR_UNSUPPORTED, "%s: heads %lld/%lld, head_dim %lld", fn, (long long)n_heads,
                     (long long)n_kv, (long long)head_dim);
-    const uint64_t lds = (static_cast<uint64_t>(head_dim) + (max_len > 256 ? max_len : 256)) * 4;
+    const uint64_t score_floats = max_len > 4 * head_dim ? max_len : 4 * head_dim;  // scores, then partials
+    const uint64_t lds = (static_cast<uint64_t>(head_dim) + score_floats) * 4;
     if (lds > 64 * 1024)
         return fail(FH_ERR_UNSUPPORTED, "%s: max_len %lld too long for the LDS score buffer", fn,
                     (long long)max_len);
@@ -380,7 +497,7 @@ extern "C" int fh_argmax(fh_device *dev, const uint16_t *x, int64_t rows, int64_
     if (int rc = check_range(dev, out, static_cast<uint64_t>(rows) * 4, fn, "out")) return rc;
     if (int rc = set_current(dev, fn)) return rc;
     return dispatch(dev, fn, [&] {
-        hipLaunchKernelGGL(argmax_kernel, dim3(static_cast<uint32_t>(rows)), dim3(256), 0,
+        hipLaunchKernelGGL(argmax_kernel, dim3(static_cast<uint32_t>(rows)), dim3(kArgmaxThreads), 0,
                            dev->stream, x, static_cast<uint32_t>(n), out);
     });
 }

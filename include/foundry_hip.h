@@ -191,7 +191,9 @@ int fh_q4_dequant(fh_device *dev, const uint32_t *wq, const uint16_t *scales,
  * residual add before it (src/models/llama/model.rs:254-279):
  *   h = residual ? RNE(x + residual) : x   (h written to residual_out)
  *   y = RNE(RNE(h * 1/sqrt(sum(h^2)/dim + eps)) * weight)
- * x, residual, residual_out, y: [rows, dim]; weight: [dim]. */
+ * x, residual, residual_out, y: [rows, dim]; weight: [dim]. dim is a multiple
+ * of 8, at most 8192; operands are 16-byte aligned. residual_out may alias
+ * residual (an in-place residual stream). */
 int fh_rms_norm(fh_device *dev, const uint16_t *x, const uint16_t *residual,
                 uint16_t *residual_out, const uint16_t *weight, int64_t rows, int64_t dim,
                 float eps, uint16_t *y);
@@ -201,8 +203,9 @@ int fh_rms_norm(fh_device *dev, const uint16_t *x, const uint16_t *residual,
  * at the token's position. qkv: [tokens, (n_heads + 2 n_kv) * head_dim] (q
  * heads, then k heads, then v heads); cos_tab/sin_tab: [table_len, head_dim];
  * positions: device u32 [tokens]; k_cache/v_cache: [n_kv, max_len, head_dim];
- * q_out: [tokens, n_heads, head_dim]. A position >= max_len or >= table_len
- * writes nothing. */
+ * q_out: [tokens, n_heads, head_dim]. head_dim is a multiple of 16 and every
+ * operand 16-byte aligned. A position >= max_len or >= table_len writes
+ * nothing. */
 int fh_rope_kv(fh_device *dev, const uint16_t *qkv, int64_t tokens, int64_t n_heads,
                int64_t n_kv, int64_t head_dim, const uint16_t *cos_tab, const uint16_t *sin_tab,
                int64_t table_len, const uint32_t *positions, uint16_t *k_cache,
@@ -213,7 +216,8 @@ int fh_rope_kv(fh_device *dev, const uint16_t *qkv, int64_t tokens, int64_t n_he
  * of its KV head (grouped-query: head h uses KV head h / (n_heads/n_kv)).
  * Scores RNE(q.k) (fp32 sums), times scale in fp32, softmax in fp32,
  * probabilities RNE to bf16, out = RNE(sum p v). out: [tokens, n_heads *
- * head_dim]. head_dim <= 256; max_len * 4 bytes must fit 64 KiB of LDS. */
+ * head_dim]. head_dim is 64, 128 or 256; (head_dim + max(max_len, 4 head_dim)) * 4
+ * bytes must fit 64 KiB of LDS. */
 int fh_attention(fh_device *dev, const uint16_t *q, const uint16_t *k_cache,
                  const uint16_t *v_cache, const uint32_t *positions, int64_t tokens,
                  int64_t n_heads, int64_t n_kv, int64_t head_dim, int64_t max_len, float scale,
