@@ -107,7 +107,9 @@ SIGNATURES = {
     "fh_q4_dequant": [_vp, _vp, _vp, _vp, _i64, _i64, _i64, _vp],
     "fh_rms_norm": [_vp, _vp, _vp, _vp, _vp, _i64, _i64, ctypes.c_float, _vp],
     "fh_rope_kv": [_vp, _vp, _i64, _i64, _i64, _i64, _vp, _vp, _i64, _vp, _vp, _vp, _i64, _vp],
-    "fh_attention": [_vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, ctypes.c_float, _vp],
+    "fh_attention_workspace": [_i64, _i64, _i64, _i64, _i64, ctypes.POINTER(ctypes.c_uint64)],
+    "fh_attention": [_vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, ctypes.c_float, _vp,
+                     ctypes.c_uint64, _vp],
     "fh_silu_mul": [_vp, _vp, _i64, _i64, _vp],
     "fh_argmax": [_vp, _vp, _i64, _i64, _vp],
     "fh_advance_positions": [_vp, _vp, _i64, _i64],
@@ -146,6 +148,12 @@ def last_error() -> str:
 def check(status: int) -> None:
     if status != OK:
         raise HipError(status, last_error())
+
+
+def attention_workspace_bytes(tokens: int, n_heads: int, n_kv: int, head_dim: int, max_len: int) -> int:
+    out = ctypes.c_uint64()
+    call("fh_attention_workspace", tokens, n_heads, n_kv, head_dim, max_len, ctypes.byref(out))
+    return out.value
 
 
 def call(name: str, *args) -> None:

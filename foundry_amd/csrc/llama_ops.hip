@@ -182,98 +182,249 @@ __global__ __launch_bounds__(256) void rope_kv_kernel(
     }
 }
 
-// Attention for one (token, query head) per block over keys 0..pos of its KV
-// head (causal; decode uses pos = current position). Scores: RNE(q . k) with
-// fp32 accumulation, then s * scale in fp32; softmax in fp32; probabilities
-// rounded to bf16; out = RNE(sum_j p_j v_j) in fp32. Scores go through LDS
-// (max_len floats); head_dim is 64, 128 or 256.
-__global__ __launch_bounds__(256) void attention_kernel(
+// Split-context attention. The keys 0..ctx-1 of a (token, KV head) are cut
+// into chunks of kAttnChunk keys, dealt round-robin to `splits` blocks; block
+// (KV head, split, token) serves all G = n_heads / n_kv query heads of its KV
+// head, so a K or V row is read once per chunk for the whole group. splits
+// is chosen so that tokens * n_kv * splits is about kAttnTargetBlocks: decode
+// (one token) spreads its context over many blocks, prefill (many tokens)
+// keeps one block per (token, KV head) and needs no cross-block combine.
+// Two kernels, because the reference rounds each probability to bf16 from
+// the GLOBAL max and sum of its row:
+//   attn_scores_kernel: s_j = RNE(q.k_j) * scale, written to the workspace
+//     with each chunk's (m_c = max s_j, l_c = sum exp(s_j - m_c)).
+//   attn_pv_kernel: M = max m_c, S = sum l_c exp(m_c - M), p_j =
+//     RNE(exp(s_j - M) / S) as the reference forms them, and the block's
+//     partial sum_j p_j v_j over its chunks. With one active split the block
+//     writes RNE of it; otherwise the last block of the (token, KV head) to
+//     finish (a completion counter in the workspace) adds the partials in
+//     split order, writes RNE(sum) and re-arms the counter at zero, so the
+//     result does not depend on block timing.
+// A key row of HD bf16 is read by HD/8 lanes with 16-byte loads: one
+// wavefront load covers 64/(HD/8) whole keys.
+constexpr int kAttnChunk = 128;
+constexpr int kAttnMaxGroup = 8;
+constexpr int kAttnThreads = 256;
+constexpr uint64_t kAttnTargetBlocks = 512;
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
+    return v;
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
+    return v;
+}
+
+struct AttnLayout {
+    uint64_t nck, splits, stats, scores, partial, total;  // byte offsets; counters at 0
+};
+
+static AttnLayout attn_layout(uint64_t tokens, uint64_t n_heads, uint64_t n_kv, uint64_t head_dim,
+                              uint64_t max_len) {
+    auto round_up = [](uint64_t b) { return (b + 255) & ~static_cast<uint64_t>(255); };
+    AttnLayout a;
+    a.nck = (max_len + kAttnChunk - 1) / kAttnChunk;
+    const uint64_t rows = tokens * n_kv;
+    const uint64_t want = rows ? (kAttnTargetBlocks + rows - 1) / rows : 1;
+    a.splits = want < a.nck ? want : a.nck;
+    if (a.splits == 0) a.splits = 1;
+    a.stats = round_up(tokens * n_kv * 4);
+    a.scores = a.stats + round_up(tokens * n_heads * a.nck * 8);
+    a.partial = a.scores + round_up(tokens * n_heads * max_len * 4);
+    a.total = a.partial + (a.splits > 1 ? round_up(tokens * n_heads * a.splits * head_dim * 4) : 0);
+    return a;
+}
+
+template <int HD>
+__global__ __launch_bounds__(kAttnThreads) void attn_scores_kernel(
     const uint16_t *__restrict__ q, const uint16_t *__restrict__ k_cache,
-    const uint16_t *__restrict__ v_cache, const uint32_t *__restrict__ positions,
-    uint32_t n_heads, uint32_t n_kv, uint32_t head_dim, uint32_t max_len, float scale,
-    uint16_t *__restrict__ out) {
-    extern __shared__ float sh[];
-    float *qs = sh;                 // head_dim
-    float *scores = sh + head_dim;  // max_len
-    __shared__ float red[4];
-    const uint32_t t = blockIdx.y, h = blockIdx.x;
-    const uint32_t kvh = h / (n_heads / n_kv);
+    const uint32_t *__restrict__ positions, uint32_t n_heads, uint32_t n_kv, uint32_t max_len,
+    uint32_t nck, uint32_t splits, float scale, float *__restrict__ scores, float2 *__restrict__ stats) {
+    constexpr int LPK = HD / 8, KPI = 64 / LPK, IT = kAttnChunk / 4 / KPI;
+    __shared__ float sc[kAttnMaxGroup][kAttnChunk];
+    const uint32_t t = blockIdx.y, kvh = blockIdx.x / splits, split = blockIdx.x % splits;
     // keys 0..pos, never past the cache (positions are unchecked device data)
     const uint32_t ctx = positions[t] < max_len ? positions[t] + 1 : max_len;
-    const uint16_t *qrow = q + (static_cast<uint64_t>(t) * n_heads + h) * head_dim;
-    for (uint32_t d = threadIdx.x; d < head_dim; d += blockDim.x) qs[d] = bf(qrow[d]);
-    __syncthreads();
-    const uint16_t *kb = k_cache + static_cast<uint64_t>(kvh) * max_len * head_dim;
-    const uint16_t *vb = v_cache + static_cast<uint64_t>(kvh) * max_len * head_dim;
-    float mx = -INFINITY;
-    for (uint32_t j = threadIdx.x; j < ctx; j += blockDim.x) {
-        const uint16_t *kr = kb + static_cast<uint64_t>(j) * head_dim;
-        float acc = 0.f;
-        for (uint32_t d = 0; d < head_dim; d += 8) {
-            const uint4 kv = *reinterpret_cast<const uint4 *>(kr + d);
-            const uint32_t w[4] = {kv.x, kv.y, kv.z, kv.w};
+    const uint32_t nact = (ctx + kAttnChunk - 1) / kAttnChunk;
+    if (split >= nact) return;
+    const uint32_t G = n_heads / n_kv, h0 = kvh * G;
+    const uint32_t wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const uint32_t ks = lane / LPK, li = lane % LPK;
+    const uint16_t *kb = k_cache + static_cast<uint64_t>(kvh) * max_len * HD + li * 8;
+    float qf[kAttnMaxGroup][8];
 #pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                acc += qs[d + 2 * e] * bf(static_cast<uint16_t>(w[e] & 0xFFFFu));
-                acc += qs[d + 2 * e + 1] * bf(static_cast<uint16_t>(w[e] >> 16));
+    for (int g = 0; g < kAttnMaxGroup; ++g)
+        if (g < static_cast<int>(G))
+            unpack8(*reinterpret_cast<const uint4 *>(q + (static_cast<uint64_t>(t) * n_heads + h0 + g) * HD + li * 8),
+                    qf[g]);
+    for (uint32_t c = split; c < nact; c += splits) {
+        const uint32_t j0 = c * kAttnChunk;
+        const uint32_t jw = j0 + wave * (kAttnChunk / 4) + ks;
+        uint4 kr[IT];
+#pragma unroll
+        for (int it = 0; it < IT; ++it) {
+            const uint32_t j = jw + it * KPI;
+            kr[it] = j < ctx ? *reinterpret_cast<const uint4 *>(kb + static_cast<uint64_t>(j) * HD)
+                             : make_uint4(0u, 0u, 0u, 0u);
+        }
+#pragma unroll
+        for (int it = 0; it < IT; ++it) {
+            float kf[8];
+            unpack8(kr[it], kf);
+            const uint32_t j = jw + it * KPI;
+#pragma unroll
+            for (int g = 0; g < kAttnMaxGroup; ++g) {
+                if (g < static_cast<int>(G)) {
+                    float d = 0.f;
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) d += qf[g][e] * kf[e];
+#pragma unroll
+                    for (int off = 1; off < LPK; off <<= 1) d += __shfl_xor(d, off, 64);
+                    if (li == 0) sc[g][j - j0] = j < ctx ? bf(rne(d)) * scale : -INFINITY;
+                }
             }
         }
-        const float sc = bf(rne(acc)) * scale;
-        scores[j] = sc;
-        mx = fmaxf(mx, sc);
+        __syncthreads();
+        static_assert(kAttnChunk == 128, "statistics pass assumes two scores per lane");
+        for (uint32_t g = wave; g < G; g += 4) {
+            const float a = sc[g][lane], b = sc[g][lane + 64];
+            const float m = wave_max(fmaxf(a, b));
+            const float l = wave_sum(expf(a - m) + expf(b - m));
+            if (lane == 0) stats[(static_cast<uint64_t>(t) * n_heads + h0 + g) * nck + c] = make_float2(m, l);
+        }
+        const uint32_t valid = min(ctx - j0, static_cast<uint32_t>(kAttnChunk));
+        for (uint32_t i = threadIdx.x; i < G * kAttnChunk; i += kAttnThreads) {
+            const uint32_t g = i / kAttnChunk, jj = i % kAttnChunk;
+            if (jj < valid) scores[(static_cast<uint64_t>(t) * n_heads + h0 + g) * max_len + j0 + jj] = sc[g][jj];
+        }
+        __syncthreads();  // sc is rewritten by the next chunk
     }
-    mx = block_max(mx, red);
-    float sum = 0.f;
-    for (uint32_t j = threadIdx.x; j < ctx; j += blockDim.x) {
-        const float e = expf(scores[j] - mx);
-        scores[j] = e;
-        sum += e;
-    }
-    sum = block_sum(sum, red);
-    for (uint32_t j = threadIdx.x; j < ctx; j += blockDim.x) scores[j] = bf(rne(scores[j] / sum));
-    __syncthreads();
-    // out[d] = sum_j p_j v_j[d]: wavefront w takes keys j = w, w+4, ...; lane
-    // l takes dims l*DPL .. +DPL, so each key's V row is one coalesced read.
-    // The four partial vectors are summed through LDS (in wavefront order).
+}
+
+template <int HD>
+__global__ __launch_bounds__(kAttnThreads) void attn_pv_kernel(
+    const uint16_t *__restrict__ v_cache, const uint32_t *__restrict__ positions, uint32_t n_heads,
+    uint32_t n_kv, uint32_t max_len, uint32_t nck, uint32_t splits, const float *__restrict__ scores,
+    const float2 *__restrict__ stats, float *__restrict__ partial, uint32_t *__restrict__ counters,
+    uint16_t *__restrict__ out) {
+    constexpr int LPK = HD / 8, KPI = 64 / LPK, IT = kAttnChunk / 4 / KPI;
+    __shared__ float p[kAttnMaxGroup][kAttnChunk];
+    __shared__ float wsum[4][kAttnMaxGroup * HD];
+    __shared__ float mg[kAttnMaxGroup], sg[kAttnMaxGroup];
+    __shared__ uint32_t is_last;
+    const uint32_t t = blockIdx.y, kvh = blockIdx.x / splits, split = blockIdx.x % splits;
+    const uint32_t ctx = positions[t] < max_len ? positions[t] + 1 : max_len;
+    const uint32_t nact = (ctx + kAttnChunk - 1) / kAttnChunk;
+    if (split >= nact) return;
+    const uint32_t nsp = min(splits, nact);  // splits holding at least one chunk
+    const uint32_t G = n_heads / n_kv, h0 = kvh * G;
     const uint32_t wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    const uint32_t dpl = head_dim / 64;  // 1, 2 or 4
-    float acc[4] = {0.f, 0.f, 0.f, 0.f};
-    // batches of kBatchKeys keys: all loads of a batch are issued before any
-    // is used, so the wavefront waits for memory once per batch, not per key
-    constexpr int kBatchKeys = 8;
-    for (uint32_t j0 = wave; j0 < ctx; j0 += 4 * kBatchKeys) {
-        uint2 v[kBatchKeys];
-        float p[kBatchKeys];
-#pragma unroll
-        for (int u = 0; u < kBatchKeys; ++u) {
-            const uint32_t j = j0 + 4 * u;
-            const bool ok = j < ctx;
-            const uint16_t *vr = vb + static_cast<uint64_t>(ok ? j : 0) * head_dim + lane * dpl;
-            if (dpl == 4)
-                v[u] = *reinterpret_cast<const uint2 *>(vr);
-            else if (dpl == 2)
-                v[u] = make_uint2(*reinterpret_cast<const uint32_t *>(vr), 0u);
-            else
-                v[u] = make_uint2(vr[0], 0u);
-            p[u] = ok ? scores[j] : 0.f;
+    const uint32_t ks = lane / LPK, li = lane % LPK;
+    const uint16_t *vb = v_cache + static_cast<uint64_t>(kvh) * max_len * HD + li * 8;
+    for (uint32_t g = wave; g < G; g += 4) {
+        const float2 *st = stats + (static_cast<uint64_t>(t) * n_heads + h0 + g) * nck;
+        float m = -INFINITY;
+        for (uint32_t cc = lane; cc < nact; cc += 64) m = fmaxf(m, st[cc].x);
+        m = wave_max(m);
+        float s = 0.f;
+        for (uint32_t cc = lane; cc < nact; cc += 64) {
+            const float2 v = st[cc];
+            s += v.y * expf(v.x - m);
         }
-#pragma unroll
-        for (int u = 0; u < kBatchKeys; ++u) {
-            acc[0] += p[u] * bf(v[u].x & 0xFFFFu);
-            acc[1] += p[u] * bf(v[u].x >> 16);
-            acc[2] += p[u] * bf(v[u].y & 0xFFFFu);
-            acc[3] += p[u] * bf(v[u].y >> 16);
+        s = wave_sum(s);
+        if (lane == 0) {
+            mg[g] = m;
+            sg[g] = s;
         }
     }
-    __syncthreads();
-    float *partial = scores;  // reuse: [4][head_dim]
-    for (uint32_t e = 0; e < dpl; ++e) partial[wave * head_dim + lane * dpl + e] = acc[e];
-    __syncthreads();
-    if (threadIdx.x < head_dim) {
-        const float o = partial[threadIdx.x] + partial[head_dim + threadIdx.x] + partial[2 * head_dim + threadIdx.x] +
-                        partial[3 * head_dim + threadIdx.x];
-        out[(static_cast<uint64_t>(t) * n_heads + h) * head_dim + threadIdx.x] = rne(o);
+    float acc[kAttnMaxGroup][8];
+#pragma unroll
+    for (int g = 0; g < kAttnMaxGroup; ++g)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) acc[g][e] = 0.f;
+    for (uint32_t c = split; c < nact; c += splits) {
+        const uint32_t j0 = c * kAttnChunk;
+        // V rows first: they do not depend on the probabilities
+        const uint32_t jw = j0 + wave * (kAttnChunk / 4) + ks;
+        uint4 vr[IT];
+#pragma unroll
+        for (int it = 0; it < IT; ++it) {
+            const uint32_t j = jw + it * KPI;
+            vr[it] = j < ctx ? *reinterpret_cast<const uint4 *>(vb + static_cast<uint64_t>(j) * HD)
+                             : make_uint4(0u, 0u, 0u, 0u);
+        }
+        __syncthreads();  // mg/sg written; p free from the previous chunk
+        const uint32_t valid = min(ctx - j0, static_cast<uint32_t>(kAttnChunk));
+        for (uint32_t i = threadIdx.x; i < G * kAttnChunk; i += kAttnThreads) {
+            const uint32_t g = i / kAttnChunk, jj = i % kAttnChunk;
+            float v = 0.f;
+            if (jj < valid)
+                v = bf(rne(expf(scores[(static_cast<uint64_t>(t) * n_heads + h0 + g) * max_len + j0 + jj] - mg[g]) /
+                           sg[g]));
+            p[g][jj] = v;
+        }
+        __syncthreads();
+#pragma unroll
+        for (int it = 0; it < IT; ++it) {
+            float vf[8];
+            unpack8(vr[it], vf);
+            const uint32_t jj = wave * (kAttnChunk / 4) + it * KPI + ks;
+#pragma unroll
+            for (int g = 0; g < kAttnMaxGroup; ++g) {
+                if (g < static_cast<int>(G)) {
+                    const float pg = p[g][jj];
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) acc[g][e] += pg * vf[e];
+                }
+            }
+        }
     }
+    // sum over the key slots of the wavefront, then over the four wavefronts
+#pragma unroll
+    for (int off = LPK; off < 64; off <<= 1)
+#pragma unroll
+        for (int g = 0; g < kAttnMaxGroup; ++g)
+            if (g < static_cast<int>(G))
+#pragma unroll
+                for (int e = 0; e < 8; ++e) acc[g][e] += __shfl_xor(acc[g][e], off, 64);
+    if (ks == 0) {
+#pragma unroll
+        for (int g = 0; g < kAttnMaxGroup; ++g)
+            if (g < static_cast<int>(G))
+#pragma unroll
+                for (int e = 0; e < 8; ++e) wsum[wave][g * HD + li * 8 + e] = acc[g][e];
+    }
+    __syncthreads();
+    uint16_t *orow = out + (static_cast<uint64_t>(t) * n_heads + h0) * HD;
+    float *part = partial + (static_cast<uint64_t>(t) * n_kv + kvh) * splits * G * HD;
+    for (uint32_t i = threadIdx.x; i < G * HD; i += kAttnThreads) {
+        const float v = wsum[0][i] + wsum[1][i] + wsum[2][i] + wsum[3][i];
+        if (nsp == 1)
+            orow[i] = rne(v);
+        else
+            part[static_cast<uint64_t>(split) * G * HD + i] = v;
+    }
+    if (nsp == 1) return;
+    // publish this split's partial, then count it; the last split to arrive
+    // combines
+    __threadfence();
+    __syncthreads();
+    uint32_t *counter = counters + static_cast<uint64_t>(t) * n_kv + kvh;
+    if (threadIdx.x == 0)
+        is_last = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT) == nsp - 1;
+    __syncthreads();
+    if (!is_last) return;
+    __threadfence();
+    for (uint32_t i = threadIdx.x; i < G * HD; i += kAttnThreads) {
+        float s = 0.f;
+        for (uint32_t sp = 0; sp < nsp; ++sp) s += part[static_cast<uint64_t>(sp) * G * HD + i];
+        orow[i] = rne(s);
+    }
+    if (threadIdx.x == 0) __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // out = RNE(RNE(g / (1 + exp(-g))) * u), gu row = [g (F) | u (F)].
@@ -365,6 +516,17 @@ int check_dims(const char *fn, std::initializer_list<int64_t> dims) {
     return FH_OK;
 }
 
+// The workspace holds at most tokens * n_heads * (3 max_len + head_dim)
+// floats (scores, chunk partials); refuse sizes whose byte counts would not
+// fit comfortably in 64 bits.
+int check_attn_size(const char *fn, int64_t tokens, int64_t n_heads, int64_t head_dim, int64_t max_len) {
+    const long double floats = static_cast<long double>(tokens) * n_heads * (3.0L * max_len + head_dim);
+    if (floats > 0x1p56L)
+        return fail(FH_ERR_INDEX_TOO_LARGE, "%s: attention workspace for %lld tokens x %lld heads x %lld "
+                    "keys is too large", fn, (long long)tokens, (long long)n_heads, (long long)max_len);
+    return FH_OK;
+}
+
 }  // namespace
 
 extern "C" int fh_rms_norm(fh_device *dev, const uint16_t *x, const uint16_t *residual,
@@ -437,36 +599,75 @@ extern "C" int fh_rope_kv(fh_device *dev, const uint16_t *qkv, int64_t tokens, i
     });
 }
 
+extern "C" int fh_attention_workspace(int64_t tokens, int64_t n_heads, int64_t n_kv, int64_t head_dim,
+                                      int64_t max_len, uint64_t *bytes) {
+    const char *fn = "fh_attention_workspace";
+    if (!bytes) return fail(FH_ERR_INVALID_ARGUMENT, "%s: null output", fn);
+    if (int rc = check_dims(fn, {tokens, n_heads, n_kv, head_dim, max_len})) return rc;
+    if (int rc = check_attn_size(fn, tokens, n_heads, head_dim, max_len)) return rc;
+    *bytes = attn_layout(tokens, n_heads, n_kv, head_dim, max_len).total;
+    return FH_OK;
+}
+
+template <int HD>
+static void launch_attention(hipStream_t stream, dim3 grid, const uint16_t *q, const uint16_t *k_cache,
+                             const uint16_t *v_cache, const uint32_t *positions, uint32_t n_heads,
+                             uint32_t n_kv, uint32_t max_len, uint32_t nck, float scale, char *ws,
+                             const AttnLayout &a, uint16_t *out) {
+    auto *counters = reinterpret_cast<uint32_t *>(ws);
+    auto *stats = reinterpret_cast<float2 *>(ws + a.stats);
+    auto *scores = reinterpret_cast<float *>(ws + a.scores);
+    auto *partial = reinterpret_cast<float *>(ws + a.partial);
+    const uint32_t splits = static_cast<uint32_t>(a.splits);
+    hipLaunchKernelGGL(attn_scores_kernel<HD>, grid, dim3(kAttnThreads), 0, stream, q, k_cache, positions,
+                       n_heads, n_kv, max_len, nck, splits, scale, scores, stats);
+    hipLaunchKernelGGL(attn_pv_kernel<HD>, grid, dim3(kAttnThreads), 0, stream, v_cache, positions, n_heads,
+                       n_kv, max_len, nck, splits, scores, stats, partial, counters, out);
+}
+
 extern "C" int fh_attention(fh_device *dev, const uint16_t *q, const uint16_t *k_cache,
                             const uint16_t *v_cache, const uint32_t *positions, int64_t tokens,
                             int64_t n_heads, int64_t n_kv, int64_t head_dim, int64_t max_len,
-                            float scale, uint16_t *out) {
+                            float scale, void *workspace, uint64_t workspace_bytes, uint16_t *out) {
     const char *fn = "fh_attention";
     if (int rc = check_usable(dev, fn)) return rc;
     if (int rc = check_dims(fn, {tokens, n_heads, n_kv, head_dim, max_len})) return rc;
     if (tokens == 0) return FH_OK;
-    if (n_kv == 0 || n_heads % n_kv != 0 || (head_dim != 64 && head_dim != 128 && head_dim != 256))
+    if (n_kv == 0 || n_heads % n_kv != 0 || n_heads / n_kv > kAttnMaxGroup ||
+        (head_dim != 64 && head_dim != 128 && head_dim != 256))
         return fail(FH_ERR_UNSUPPORTED, "%s: heads %lld/%lld, head_dim %lld", fn, (long long)n_heads,
                     (long long)n_kv, (long long)head_dim);
-    const uint64_t score_floats = max_len > 4 * head_dim ? max_len : 4 * head_dim;  // scores, then partials
-    const uint64_t lds = (static_cast<uint64_t>(head_dim) + score_floats) * 4;
-    if (lds > 64 * 1024)
-        return fail(FH_ERR_UNSUPPORTED, "%s: max_len %lld too long for the LDS score buffer", fn,
-                    (long long)max_len);
+    if (max_len == 0) return fail(FH_ERR_INVALID_ARGUMENT, "%s: empty KV cache", fn);
+    if (int rc = check_attn_size(fn, tokens, n_heads, head_dim, max_len)) return rc;
+    const AttnLayout a = attn_layout(tokens, n_heads, n_kv, head_dim, max_len);
+    if (tokens > 65535 || static_cast<uint64_t>(n_kv) * a.splits > 0x7FFFFFFFu)
+        return fail(FH_ERR_INDEX_TOO_LARGE, "%s: %lld tokens x %llu splits exceed the grid", fn,
+                    (long long)tokens, (unsigned long long)(n_kv * a.splits));
+    if (workspace_bytes < a.total)
+        return fail(FH_ERR_INVALID_ARGUMENT, "%s: workspace of %llu bytes, %llu needed", fn,
+                    (unsigned long long)workspace_bytes, (unsigned long long)a.total);
+    if ((reinterpret_cast<uintptr_t>(q) | reinterpret_cast<uintptr_t>(k_cache) |
+         reinterpret_cast<uintptr_t>(v_cache) | reinterpret_cast<uintptr_t>(workspace)) & 15u)
+        return fail(FH_ERR_INVALID_ARGUMENT, "%s: q, caches and workspace must be 16-byte aligned", fn);
     const uint64_t cache = static_cast<uint64_t>(n_kv) * max_len * head_dim * 2;
     if (int rc = check_range(dev, q, static_cast<uint64_t>(tokens) * n_heads * head_dim * 2, fn, "q")) return rc;
     if (int rc = check_range(dev, k_cache, cache, fn, "k_cache")) return rc;
     if (int rc = check_range(dev, v_cache, cache, fn, "v_cache")) return rc;
     if (int rc = check_range(dev, positions, static_cast<uint64_t>(tokens) * 4, fn, "positions")) return rc;
+    if (int rc = check_range(dev, workspace, a.total, fn, "workspace")) return rc;
     if (int rc = check_range(dev, out, static_cast<uint64_t>(tokens) * n_heads * head_dim * 2, fn, "out")) return rc;
     if (int rc = set_current(dev, fn)) return rc;
+    const dim3 grid(static_cast<uint32_t>(n_kv * a.splits), static_cast<uint32_t>(tokens));
+    const uint32_t nh = static_cast<uint32_t>(n_heads), nk = static_cast<uint32_t>(n_kv),
+                   ml = static_cast<uint32_t>(max_len), nck = static_cast<uint32_t>(a.nck);
+    char *ws = static_cast<char *>(workspace);
     return dispatch(dev, fn, [&] {
-        hipLaunchKernelGGL(attention_kernel,
-                           dim3(static_cast<uint32_t>(n_heads), static_cast<uint32_t>(tokens)),
-                           dim3(256), static_cast<uint32_t>(lds), dev->stream, q, k_cache, v_cache,
-                           positions, static_cast<uint32_t>(n_heads), static_cast<uint32_t>(n_kv),
-                           static_cast<uint32_t>(head_dim), static_cast<uint32_t>(max_len), scale,
-                           out);
+        if (head_dim == 64)
+            launch_attention<64>(dev->stream, grid, q, k_cache, v_cache, positions, nh, nk, ml, nck, scale, ws, a, out);
+        else if (head_dim == 128)
+            launch_attention<128>(dev->stream, grid, q, k_cache, v_cache, positions, nh, nk, ml, nck, scale, ws, a, out);
+        else
+            launch_attention<256>(dev->stream, grid, q, k_cache, v_cache, positions, nh, nk, ml, nck, scale, ws, a, out);
     });
 }
 

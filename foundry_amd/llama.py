@@ -200,6 +200,8 @@ class Q4Llama:
             "next": dev.zeros(4),
             "pos1": dev.zeros(4),
         }
+        self.attn_ws_bytes = _lib.attention_workspace_bytes(t, c.n_heads, c.n_kv_heads, c.head_dim, max_len)
+        self.attn_ws = dev.zeros(self.attn_ws_bytes)
 
     # ---- thin wrappers over the C-ABI ----
     def _p(self, st: HipStorage, byte_offset: int = 0):
@@ -223,7 +225,7 @@ class Q4Llama:
                       self._p(L["k_cache"]), self._p(L["v_cache"]), self.max_len, self._p(b["q"]))
             _lib.call("fh_attention", d, self._p(b["q"]), self._p(L["k_cache"]), self._p(L["v_cache"]),
                       self._p(positions), tokens, c.n_heads, c.n_kv_heads, c.head_dim, self.max_len,
-                      ctypes.c_float(self.scale), self._p(b["attn"]))
+                      ctypes.c_float(self.scale), self._p(self.attn_ws), self.attn_ws_bytes, self._p(b["attn"]))
             self._linear(b["attn"], tokens, L["o"], b["o"])
             self._norm(tokens, b["o"], L["post_norm"])
             self._linear(b["x"], tokens, L["gate_up"], b["gu"])

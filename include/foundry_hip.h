@@ -211,17 +211,29 @@ int fh_rope_kv(fh_device *dev, const uint16_t *qkv, int64_t tokens, int64_t n_he
                int64_t table_len, const uint32_t *positions, uint16_t *k_cache,
                uint16_t *v_cache, int64_t max_len, uint16_t *q_out);
 
+/* Bytes of device workspace fh_attention needs for these sizes (scores,
+ * per-chunk softmax statistics and partial outputs, completion counters). */
+int fh_attention_workspace(int64_t tokens, int64_t n_heads, int64_t n_kv, int64_t head_dim,
+                           int64_t max_len, uint64_t *bytes);
+
 /* scaled_dot_product_attention (src/nn/attention.rs:23-60) with the causal
  * mask (src/nn/masking.rs:11-32): query token t attends keys 0..positions[t]
  * of its KV head (grouped-query: head h uses KV head h / (n_heads/n_kv)).
  * Scores RNE(q.k) (fp32 sums), times scale in fp32, softmax in fp32,
- * probabilities RNE to bf16, out = RNE(sum p v). out: [tokens, n_heads *
- * head_dim]. head_dim is 64, 128 or 256; (head_dim + max(max_len, 4 head_dim)) * 4
- * bytes must fit 64 KiB of LDS. */
+ * probabilities RNE to bf16 from the row's global max and sum, out =
+ * RNE(sum p v). q, out: [tokens, n_heads * head_dim]; caches [n_kv, max_len,
+ * head_dim]. head_dim is 64, 128 or 256 and n_heads/n_kv at most 8; tokens at
+ * most 65535. The context is split into chunks of 128 keys processed in
+ * parallel, so long contexts fill the device.
+ * workspace: at least fh_attention_workspace() bytes of device memory, 16-byte
+ * aligned, ZERO-FILLED before its first use (fh_alloc with zero_fill); every
+ * call leaves its counters at zero again, so the workspace can be reused by
+ * later calls and by calls captured in a graph. Calls that share a workspace
+ * must not run concurrently. */
 int fh_attention(fh_device *dev, const uint16_t *q, const uint16_t *k_cache,
                  const uint16_t *v_cache, const uint32_t *positions, int64_t tokens,
                  int64_t n_heads, int64_t n_kv, int64_t head_dim, int64_t max_len, float scale,
-                 uint16_t *out);
+                 void *workspace, uint64_t workspace_bytes, uint16_t *out);
 
 /* LlamaMlp's act_fn(gate) * up (src/models/llama/mlp.rs:49-58, Silu at
  * src/nn/activation.rs:19-28): gate_up row = [gate (f) | up (f)],

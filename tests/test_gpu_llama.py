@@ -6,7 +6,8 @@ Bars:
 - RMSNorm, SiLU*up, attention: within 2 bf16 ulps of the restatement (the
   fp32 sums run in another order and exp comes from another library; each op
   then rounds to bf16, so a 1-ulp difference in an fp32 intermediate can move
-  the output by one bf16 ulp).
+  the output by one bf16 ulp). Attention also allows the absolute shift of
+  two bf16 probabilities rounding the other way (assert_attention_close).
 - Generation: "close" by the reference's rule (src/eval/generation.rs:132-176),
   top-k 5, and the first-step logits within 3% of max|logit|.
 """
@@ -114,31 +115,103 @@ def test_rope_out_of_range_position_writes_nothing(device):
     assert not down(device, vc, np.uint16, c.n_kv_heads * max_len * c.head_dim).any()
 
 
-@pytest.mark.parametrize("t,max_len", [(1, 40), (7, 40), (64, 512)])
-def test_attention(device, t, max_len):
-    c = TINY
-    q = synth.bf16_normal(6, (t, c.n_heads, c.head_dim))
-    kc = synth.bf16_normal(7, (c.n_kv_heads, max_len, c.head_dim))
-    vc = synth.bf16_normal(8, (c.n_kv_heads, max_len, c.head_dim))
-    pos = np.sort(np.random.default_rng(t).choice(max_len, size=t, replace=False)).astype(np.uint32)
-    s = [up(device, a) for a in (q, kc, vc, pos)]
-    out = device.empty(t * c.n_heads * c.head_dim * 2)
-    scale = float(np.float32(1) / np.sqrt(np.float32(c.head_dim), dtype=np.float32))
-    _lib.call("fh_attention", device.handle, ctypes.c_void_p(s[0].ptr), ctypes.c_void_p(s[1].ptr),
-              ctypes.c_void_p(s[2].ptr), ctypes.c_void_p(s[3].ptr), t, c.n_heads, c.n_kv_heads, c.head_dim,
-              max_len, ctypes.c_float(scale), ctypes.c_void_p(out.ptr))
-    got = down(device, out, np.uint16, t * c.n_heads * c.head_dim).reshape(t, c.n_heads, c.head_dim)
+def attention_ref(q, kc, vc, pos, scale):
+    """Per (token, head) restatement of the reference SDPA rounding points.
+    Also returns, per (token, head), the output shift one probability
+    rounding the other way can cause: ulp(max p) * max|v|."""
+    t, n_heads, _ = q.shape
+    group = n_heads // kc.shape[0]
     qf, kf, vf = R.from_bf16(q), R.from_bf16(kc), R.from_bf16(vc)
-    group = c.n_heads // c.n_kv_heads
+    out = np.empty(q.shape, np.float32)
+    flip = np.empty((t, n_heads), np.float32)
     for i in range(t):
-        ctx = int(pos[i]) + 1
-        for h in range(c.n_heads):
+        ctx = min(int(pos[i]) + 1, kc.shape[1])
+        for h in range(n_heads):
             kv = h // group
             sc = R.rne(qf[i, h] @ kf[kv, :ctx].T) * np.float32(scale)
             e = np.exp(sc - sc.max()).astype(np.float32)
             p = R.rne(e / e.sum(dtype=np.float32))
-            ref = R.rne(p @ vf[kv, :ctx])
-            assert ulps(got[i, h], ref).max() <= 2, (i, h)
+            out[i, h] = R.rne(p @ vf[kv, :ctx])
+            flip[i, h] = p.max() * 2.0 ** -8 * np.abs(vf[kv, :ctx]).max()
+    return out, flip
+
+
+def assert_attention_close(got, ref, flip, what):
+    """Within 2 bf16 ulps, or within the shift of two probability roundings.
+    p_j = RNE(e_j / S): the device sums S in another order than numpy's
+    pairwise sum (both fp32), so a p_j whose e_j / S lies within fp32 noise of
+    a bf16 rounding boundary may round the other way. Each such p_j moves
+    every output of its row by at most ulp(p_max) * max|v| (an absolute
+    amount, many ulps for outputs near zero); they are rare (about one per
+    10^4 probabilities)."""
+    u = ulps(got, ref)
+    diff = np.abs(R.from_bf16(got) - ref)
+    ok = (u <= 2) | (diff <= 2 * flip[..., None])
+    assert ok.all(), (what, np.argwhere(~ok)[:4].tolist(), int(u.max()))
+
+
+def run_attention(device, q, kc, vc, pos, ws=None):
+    t, n_heads, hd = q.shape
+    n_kv, max_len, _ = kc.shape
+    s = [up(device, a) for a in (q, kc, vc, np.ascontiguousarray(pos, dtype=np.uint32))]
+    nbytes = _lib.attention_workspace_bytes(t, n_heads, n_kv, hd, max_len)
+    if ws is None:
+        ws = device.zeros(nbytes)
+    out = device.empty(t * n_heads * hd * 2)
+    scale = float(np.float32(1) / np.sqrt(np.float32(hd), dtype=np.float32))
+    _lib.call("fh_attention", device.handle, ctypes.c_void_p(s[0].ptr), ctypes.c_void_p(s[1].ptr),
+              ctypes.c_void_p(s[2].ptr), ctypes.c_void_p(s[3].ptr), t, n_heads, n_kv, hd, max_len,
+              ctypes.c_float(scale), ctypes.c_void_p(ws.ptr), nbytes, ctypes.c_void_p(out.ptr))
+    got = down(device, out, np.uint16, t * n_heads * hd).reshape(t, n_heads, hd)
+    return got, scale, ws
+
+
+# (n_heads, n_kv, head_dim, tokens, max_len): group sizes 2, 1, 3 (Llama-3.2-3B),
+# 4 (Llama-3.1-8B) and 8; contexts of one chunk (128 keys) and of many, split
+# over one block per chunk (decode), several chunks per block with a combine
+# (64 tokens x 4096 keys: 4 splits of 8 chunks), or one block per row
+# (300 tokens: prefill, no combine).
+ATTN_CASES = [(4, 2, 64, 1, 40), (4, 2, 64, 7, 40), (4, 2, 64, 64, 512), (2, 2, 128, 3, 300),
+              (24, 8, 128, 1, 4096), (32, 8, 128, 2, 1000), (8, 1, 256, 3, 700),
+              (4, 2, 64, 64, 4096), (4, 2, 64, 300, 700)]
+
+
+@pytest.mark.parametrize("n_heads,n_kv,hd,t,max_len", ATTN_CASES)
+def test_attention(device, n_heads, n_kv, hd, t, max_len):
+    rng = np.random.default_rng(t * 131 + max_len)
+    q = synth.bf16_normal(6, (t, n_heads, hd))
+    kc = synth.bf16_normal(7, (n_kv, max_len, hd))
+    vc = synth.bf16_normal(8, (n_kv, max_len, hd))
+    pos = np.sort(rng.choice(max_len, size=t, replace=False)).astype(np.uint32)
+    pos[-1] = max_len - 1  # the full cache, every chunk active
+    got, scale, _ = run_attention(device, q, kc, vc, pos)
+    ref, flip = attention_ref(q, kc, vc, pos, scale)
+    assert_attention_close(got, ref, flip, pos.tolist())
+
+
+def test_attention_workspace_reuse(device):
+    """The completion counters return to zero: a second call on the same
+    workspace, with other positions (fewer active chunks), is still exact."""
+    n_heads, n_kv, hd, max_len = 24, 8, 128, 1024
+    q = synth.bf16_normal(16, (2, n_heads, hd))
+    kc = synth.bf16_normal(17, (n_kv, max_len, hd))
+    vc = synth.bf16_normal(18, (n_kv, max_len, hd))
+    ws = None
+    for pos in (np.array([700, 1023]), np.array([5, 300]), np.array([1023, 129])):
+        got, scale, ws = run_attention(device, q, kc, vc, pos, ws)
+        ref, flip = attention_ref(q, kc, vc, pos, scale)
+        assert_attention_close(got, ref, flip, pos.tolist())
+
+
+def test_attention_rejects_small_workspace(device):
+    n_heads, n_kv, hd, max_len = 4, 2, 64, 256
+    nbytes = _lib.attention_workspace_bytes(1, n_heads, n_kv, hd, max_len)
+    ws = device.zeros(nbytes)
+    buf = device.zeros(n_kv * max_len * hd * 2)
+    with pytest.raises(_lib.HipError, match="workspace"):
+        _lib.call("fh_attention", device.handle, ctypes.c_void_p(buf.ptr), ctypes.c_void_p(buf.ptr),
+                  ctypes.c_void_p(buf.ptr), ctypes.c_void_p(buf.ptr), 1, n_heads, n_kv, hd, max_len,
+                  ctypes.c_float(0.125), ctypes.c_void_p(ws.ptr), nbytes - 8, ctypes.c_void_p(buf.ptr))
 
 
 def test_silu_mul(device):
