@@ -1,0 +1,92 @@
+// Device helpers shared by the decoder-step kernels: bf16 rounding in the
+// reference's convention, 8-value bf16 unpacking, wavefront reductions and
+// the RoPE rotation of an 8-dim piece.
+#pragma once
+
+#include <initializer_list>
+
+#include "device.hpp"
+#include "q4_common.hpp"
+
+namespace fh {
+
+__device__ __forceinline__ uint16_t rne(float v) { return static_cast<uint16_t>(f32_to_bf16_rne(v)); }
+__device__ __forceinline__ float bf(uint16_t b) { return bf16_to_f32(b); }
+
+__device__ __forceinline__ void unpack8(const uint4 v, float (&f)[8]) {
+    const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        f[2 * e] = bf(w[e] & 0xFFFFu);
+        f[2 * e + 1] = bf(w[e] >> 16);
+    }
+}
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
+    return v;
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
+    return v;
+}
+
+// Lane value of a DPP permutation within 16-lane rows (CDNA DPP controls:
+// 0xB1 quad_perm [1,0,3,2], 0x4E quad_perm [2,3,0,1], 0x141 row_half_mirror,
+// 0x140 row_mirror).
+template <int CTRL>
+__device__ __forceinline__ float dpp_mov(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+}
+
+// Sum over aligned groups of N lanes (N = 8, 16 or 32), the total in every
+// lane of the group. Within a row the steps are DPP moves (no LDS traffic);
+// every lane of a group computes the same additions in the same order, so
+// all hold bit-identical totals.
+template <int N>
+__device__ __forceinline__ float group_sum(float v) {
+    static_assert(N == 8 || N == 16 || N == 32, "group of 8, 16 or 32 lanes");
+    v += dpp_mov<0xB1>(v);
+    v += dpp_mov<0x4E>(v);
+    v += dpp_mov<0x141>(v);
+    if constexpr (N >= 16) v += dpp_mov<0x140>(v);
+    if constexpr (N == 32) v += __shfl_xor(v, 16, 64);
+    return v;
+}
+
+// RoPE (src/models/llama/rotary_emb.rs:62-85) of dims p*8 .. p*8+7 of one
+// head: x' = RNE(RNE(x * cos) + RNE(rot * sin)), rot = cat(-x2, x1); the
+// partner piece is the matching 8 dims of the other half (hp pieces per
+// half). head: the head's row; c, s: the position's table rows.
+__device__ __forceinline__ uint4 rope_piece(const uint16_t *head, const uint16_t *c, const uint16_t *s,
+                                            uint32_t p, uint32_t hp) {
+    const uint32_t partner = p < hp ? p + hp : p - hp;
+    const float sign = p < hp ? -1.0f : 1.0f;
+    float xv[8], rv[8], cv[8], sv[8];
+    unpack8(*reinterpret_cast<const uint4 *>(head + p * 8), xv);
+    unpack8(*reinterpret_cast<const uint4 *>(head + partner * 8), rv);
+    unpack8(*reinterpret_cast<const uint4 *>(c + p * 8), cv);
+    unpack8(*reinterpret_cast<const uint4 *>(s + p * 8), sv);
+    uint32_t o[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        const uint32_t lo = rne(bf(rne(xv[2 * e] * cv[2 * e])) + bf(rne(sign * rv[2 * e] * sv[2 * e])));
+        const uint32_t hi = rne(bf(rne(xv[2 * e + 1] * cv[2 * e + 1])) + bf(rne(sign * rv[2 * e + 1] * sv[2 * e + 1])));
+        o[e] = lo | (hi << 16);
+    }
+    return make_uint4(o[0], o[1], o[2], o[3]);
+}
+
+}  // namespace fh
+
+// Host-side check shared by the decoder entry points: sizes are
+// non-negative and fit 32-bit kernel arguments.
+inline int fh_check_dims(const char *fn, std::initializer_list<int64_t> dims) {
+    for (int64_t d : dims)
+        if (d < 0 || d > 0x7FFFFFFFll)
+            return fh::fail(FH_ERR_INVALID_ARGUMENT, "%s: dimension %lld out of range", fn, (long long)d);
+    return FH_OK;
+}

@@ -18,15 +18,9 @@
 // and position live in device memory (argmax writes the next id that the
 // embedding gather reads; fh_advance_positions bumps the position), so no
 // kernel argument changes between steps.
-#include <initializer_list>
-
-#include "device.hpp"
-#include "q4_common.hpp"
+#include "decoder_common.hpp"
 
 namespace fh {
-
-__device__ __forceinline__ uint16_t rne(float v) { return static_cast<uint16_t>(f32_to_bf16_rne(v)); }
-__device__ __forceinline__ float bf(uint16_t b) { return bf16_to_f32(b); }
 
 // Sum across a 256-thread block (every thread gets the result).
 __device__ __forceinline__ float block_sum(float v, float *red) {
@@ -126,15 +120,6 @@ __global__ __launch_bounds__(kNormThreads) void rms_norm_kernel(const uint16_t *
 // x' = RNE(RNE(x * cos) + RNE(rot * sin)), rot = cat(-x2, x1). A thread
 // handles 8 consecutive dims (16-byte loads); its rotation partner is the
 // matching 8 dims of the other half (head_dim is a multiple of 16).
-__device__ __forceinline__ void unpack8(const uint4 v, float (&f)[8]) {
-    const uint32_t w[4] = {v.x, v.y, v.z, v.w};
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-        f[2 * e] = bf(w[e] & 0xFFFFu);
-        f[2 * e + 1] = bf(w[e] >> 16);
-    }
-}
-
 __global__ __launch_bounds__(256) void rope_kv_kernel(
     const uint16_t *__restrict__ qkv, uint32_t n_heads, uint32_t n_kv, uint32_t head_dim,
     const uint16_t *__restrict__ cos_tab, const uint16_t *__restrict__ sin_tab, uint32_t table_len,
@@ -153,22 +138,7 @@ __global__ __launch_bounds__(256) void rope_kv_kernel(
     const uint32_t rot_pieces = (n_heads + n_kv) * ppw;
     for (uint32_t i = threadIdx.x; i < rot_pieces; i += blockDim.x) {
         const uint32_t h = i / ppw, p = i % ppw;
-        const uint32_t partner = p < hp ? p + hp : p - hp;
-        const float sign = p < hp ? -1.0f : 1.0f;
-        float xv[8], rv[8], cv[8], sv[8];
-        unpack8(*reinterpret_cast<const uint4 *>(row + h * head_dim + p * 8), xv);
-        unpack8(*reinterpret_cast<const uint4 *>(row + h * head_dim + partner * 8), rv);
-        unpack8(*reinterpret_cast<const uint4 *>(c + p * 8), cv);
-        unpack8(*reinterpret_cast<const uint4 *>(s + p * 8), sv);
-        uint32_t o[4];
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            const uint32_t lo = rne(bf(rne(xv[2 * e] * cv[2 * e])) + bf(rne(sign * rv[2 * e] * sv[2 * e])));
-            const uint32_t hi =
-                rne(bf(rne(xv[2 * e + 1] * cv[2 * e + 1])) + bf(rne(sign * rv[2 * e + 1] * sv[2 * e + 1])));
-            o[e] = lo | (hi << 16);
-        }
-        const uint4 ov = make_uint4(o[0], o[1], o[2], o[3]);
+        const uint4 ov = rope_piece(row + h * head_dim, c, s, p, hp);
         if (h < n_heads)
             *reinterpret_cast<uint4 *>(q_out + (static_cast<uint64_t>(t) * n_heads + h) * head_dim + p * 8) = ov;
         else
@@ -206,18 +176,6 @@ constexpr int kAttnChunk = 128;
 constexpr int kAttnMaxGroup = 8;
 constexpr int kAttnThreads = 256;
 constexpr uint64_t kAttnTargetBlocks = 512;
-
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
-    return v;
-}
-
-__device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
-    return v;
-}
 
 struct AttnLayout {
     uint64_t nck, splits, stats, scores, partial, total;  // byte offsets; counters at 0
@@ -509,13 +467,6 @@ using namespace fh;
 
 namespace {
 
-int check_dims(const char *fn, std::initializer_list<int64_t> dims) {
-    for (int64_t d : dims)
-        if (d < 0 || d > 0x7FFFFFFFll)
-            return fail(FH_ERR_INVALID_ARGUMENT, "%s: dimension %lld out of range", fn, (long long)d);
-    return FH_OK;
-}
-
 // The workspace holds at most tokens * n_heads * (3 max_len + head_dim)
 // floats (scores, chunk partials); refuse sizes whose byte counts would not
 // fit comfortably in 64 bits.
@@ -534,7 +485,7 @@ extern "C" int fh_rms_norm(fh_device *dev, const uint16_t *x, const uint16_t *re
                            int64_t dim, float eps, uint16_t *y) {
     const char *fn = "fh_rms_norm";
     if (int rc = check_usable(dev, fn)) return rc;
-    if (int rc = check_dims(fn, {rows, dim})) return rc;
+    if (int rc = fh_check_dims(fn, {rows, dim})) return rc;
     if (rows == 0 || dim == 0) return FH_OK;
     if ((residual == nullptr) != (residual_out == nullptr))
         return fail(FH_ERR_INVALID_ARGUMENT, "%s: residual and residual_out go together", fn);
@@ -570,7 +521,7 @@ extern "C" int fh_rope_kv(fh_device *dev, const uint16_t *qkv, int64_t tokens, i
                           uint16_t *q_out) {
     const char *fn = "fh_rope_kv";
     if (int rc = check_usable(dev, fn)) return rc;
-    if (int rc = check_dims(fn, {tokens, n_heads, n_kv, head_dim, table_len, max_len})) return rc;
+    if (int rc = fh_check_dims(fn, {tokens, n_heads, n_kv, head_dim, table_len, max_len})) return rc;
     if (tokens == 0) return FH_OK;
     if (n_kv == 0 || n_heads % n_kv != 0 || head_dim % 16 != 0 || head_dim == 0)
         return fail(FH_ERR_INVALID_ARGUMENT, "%s: heads %lld/%lld, head_dim %lld", fn,
@@ -603,7 +554,7 @@ extern "C" int fh_attention_workspace(int64_t tokens, int64_t n_heads, int64_t n
                                       int64_t max_len, uint64_t *bytes) {
     const char *fn = "fh_attention_workspace";
     if (!bytes) return fail(FH_ERR_INVALID_ARGUMENT, "%s: null output", fn);
-    if (int rc = check_dims(fn, {tokens, n_heads, n_kv, head_dim, max_len})) return rc;
+    if (int rc = fh_check_dims(fn, {tokens, n_heads, n_kv, head_dim, max_len})) return rc;
     if (int rc = check_attn_size(fn, tokens, n_heads, head_dim, max_len)) return rc;
     *bytes = attn_layout(tokens, n_heads, n_kv, head_dim, max_len).total;
     return FH_OK;
@@ -631,7 +582,7 @@ extern "C" int fh_attention(fh_device *dev, const uint16_t *q, const uint16_t *k
                             float scale, void *workspace, uint64_t workspace_bytes, uint16_t *out) {
     const char *fn = "fh_attention";
     if (int rc = check_usable(dev, fn)) return rc;
-    if (int rc = check_dims(fn, {tokens, n_heads, n_kv, head_dim, max_len})) return rc;
+    if (int rc = fh_check_dims(fn, {tokens, n_heads, n_kv, head_dim, max_len})) return rc;
     if (tokens == 0) return FH_OK;
     if (n_kv == 0 || n_heads % n_kv != 0 || n_heads / n_kv > kAttnMaxGroup ||
         (head_dim != 64 && head_dim != 128 && head_dim != 256))
@@ -675,7 +626,7 @@ extern "C" int fh_silu_mul(fh_device *dev, const uint16_t *gate_up, int64_t rows
                            uint16_t *out) {
     const char *fn = "fh_silu_mul";
     if (int rc = check_usable(dev, fn)) return rc;
-    if (int rc = check_dims(fn, {rows, f})) return rc;
+    if (int rc = fh_check_dims(fn, {rows, f})) return rc;
     if (rows == 0 || f == 0) return FH_OK;
     const uint64_t total = static_cast<uint64_t>(rows) * f;
     if (int rc = check_range(dev, gate_up, total * 4, fn, "gate_up")) return rc;
@@ -691,7 +642,7 @@ extern "C" int fh_silu_mul(fh_device *dev, const uint16_t *gate_up, int64_t rows
 extern "C" int fh_argmax(fh_device *dev, const uint16_t *x, int64_t rows, int64_t n, uint32_t *out) {
     const char *fn = "fh_argmax";
     if (int rc = check_usable(dev, fn)) return rc;
-    if (int rc = check_dims(fn, {rows, n})) return rc;
+    if (int rc = fh_check_dims(fn, {rows, n})) return rc;
     if (rows == 0) return FH_OK;
     if (n == 0) return fail(FH_ERR_INVALID_ARGUMENT, "%s: argmax over an empty row", fn);
     if (int rc = check_range(dev, x, static_cast<uint64_t>(rows) * n * 2, fn, "x")) return rc;
@@ -706,7 +657,7 @@ extern "C" int fh_argmax(fh_device *dev, const uint16_t *x, int64_t rows, int64_
 extern "C" int fh_advance_positions(fh_device *dev, uint32_t *positions, int64_t n, int64_t by) {
     const char *fn = "fh_advance_positions";
     if (int rc = check_usable(dev, fn)) return rc;
-    if (int rc = check_dims(fn, {n, by})) return rc;
+    if (int rc = fh_check_dims(fn, {n, by})) return rc;
     if (n == 0) return FH_OK;
     if (int rc = check_range(dev, positions, static_cast<uint64_t>(n) * 4, fn, "positions")) return rc;
     if (int rc = set_current(dev, fn)) return rc;
@@ -721,7 +672,7 @@ extern "C" int fh_append_token(fh_device *dev, const uint32_t *token, uint32_t *
                                const uint32_t *position, int64_t base, int64_t capacity) {
     const char *fn = "fh_append_token";
     if (int rc = check_usable(dev, fn)) return rc;
-    if (int rc = check_dims(fn, {base, capacity})) return rc;
+    if (int rc = fh_check_dims(fn, {base, capacity})) return rc;
     if (capacity == 0) return FH_OK;
     if (int rc = check_range(dev, token, 4, fn, "token")) return rc;
     if (int rc = check_range(dev, position, 4, fn, "position")) return rc;

@@ -202,6 +202,7 @@ class Q4Llama:
         }
         self.attn_ws_bytes = _lib.attention_workspace_bytes(t, c.n_heads, c.n_kv_heads, c.head_dim, max_len)
         self.attn_ws = dev.zeros(self.attn_ws_bytes)
+        self.fused_decode = max_len <= _lib.decode_attention_max_len(c.n_heads, c.n_kv_heads, c.head_dim)
 
     # ---- thin wrappers over the C-ABI ----
     def _p(self, st: HipStorage, byte_offset: int = 0):
@@ -220,12 +221,20 @@ class Q4Llama:
         for L in self.layers:
             self._norm(tokens, pending, L["input_norm"])
             self._linear(b["x"], tokens, L["qkv"], b["qkv"])
-            _lib.call("fh_rope_kv", d, self._p(b["qkv"]), tokens, c.n_heads, c.n_kv_heads, c.head_dim,
-                      self._p(self.cos), self._p(self.sin), self.max_len, self._p(positions),
-                      self._p(L["k_cache"]), self._p(L["v_cache"]), self.max_len, self._p(b["q"]))
-            _lib.call("fh_attention", d, self._p(b["q"]), self._p(L["k_cache"]), self._p(L["v_cache"]),
-                      self._p(positions), tokens, c.n_heads, c.n_kv_heads, c.head_dim, self.max_len,
-                      ctypes.c_float(self.scale), self._p(self.attn_ws), self.attn_ws_bytes, self._p(b["attn"]))
+            if tokens == 1 and self.fused_decode:
+                # one new token: RoPE, cache write and attention in one kernel
+                _lib.call("fh_decode_attention", d, self._p(b["qkv"]), 1, c.n_heads, c.n_kv_heads, c.head_dim,
+                          self._p(self.cos), self._p(self.sin), self.max_len, self._p(positions),
+                          self._p(L["k_cache"]), self._p(L["v_cache"]), self.max_len, ctypes.c_float(self.scale),
+                          self._p(b["attn"]))
+            else:
+                _lib.call("fh_rope_kv", d, self._p(b["qkv"]), tokens, c.n_heads, c.n_kv_heads, c.head_dim,
+                          self._p(self.cos), self._p(self.sin), self.max_len, self._p(positions),
+                          self._p(L["k_cache"]), self._p(L["v_cache"]), self.max_len, self._p(b["q"]))
+                _lib.call("fh_attention", d, self._p(b["q"]), self._p(L["k_cache"]), self._p(L["v_cache"]),
+                          self._p(positions), tokens, c.n_heads, c.n_kv_heads, c.head_dim, self.max_len,
+                          ctypes.c_float(self.scale), self._p(self.attn_ws), self.attn_ws_bytes,
+                          self._p(b["attn"]))
             self._linear(b["attn"], tokens, L["o"], b["o"])
             self._norm(tokens, b["o"], L["post_norm"])
             self._linear(b["x"], tokens, L["gate_up"], b["gu"])

@@ -235,6 +235,26 @@ int fh_attention(fh_device *dev, const uint16_t *q, const uint16_t *k_cache,
                  int64_t n_heads, int64_t n_kv, int64_t head_dim, int64_t max_len, float scale,
                  void *workspace, uint64_t workspace_bytes, uint16_t *out);
 
+/* The decode step's attention for a batch of sequences that each add one
+ * token, fused: fh_rope_kv's RoPE and cache write, then fh_attention over keys
+ * 0..positions[b] of sequence b, in one kernel with the scores in LDS (same
+ * rounding points as the two ops). qkv: [batch, (n_heads + 2 n_kv) *
+ * head_dim]; cos_tab/sin_tab: [table_len, head_dim]; positions: device u32
+ * [batch]; k_cache/v_cache: [batch, n_kv, max_len, head_dim] (one cache per
+ * sequence); out: [batch, n_heads * head_dim]. A position >= max_len or >=
+ * table_len writes nothing to the caches and zeros to out. head_dim is 64,
+ * 128 or 256, n_heads/n_kv at most 8, batch at most 65535, operands 16-byte
+ * aligned, and max_len at most fh_decode_attention_max_len() (the scores of
+ * a row live in LDS; longer caches use fh_rope_kv + fh_attention). */
+int fh_decode_attention(fh_device *dev, const uint16_t *qkv, int64_t batch, int64_t n_heads,
+                        int64_t n_kv, int64_t head_dim, const uint16_t *cos_tab,
+                        const uint16_t *sin_tab, int64_t table_len, const uint32_t *positions,
+                        uint16_t *k_cache, uint16_t *v_cache, int64_t max_len, float scale,
+                        uint16_t *out);
+
+/* Largest max_len fh_decode_attention accepts for these head counts. */
+int fh_decode_attention_max_len(int64_t n_heads, int64_t n_kv, int64_t head_dim, int64_t *max_len);
+
 /* LlamaMlp's act_fn(gate) * up (src/models/llama/mlp.rs:49-58, Silu at
  * src/nn/activation.rs:19-28): gate_up row = [gate (f) | up (f)],
  * out = RNE(RNE(g / (1 + exp(-g))) * u), out: [rows, f]. */

@@ -214,6 +214,90 @@ def test_attention_rejects_small_workspace(device):
                   ctypes.c_float(0.125), ctypes.c_void_p(ws.ptr), nbytes - 8, ctypes.c_void_p(buf.ptr))
 
 
+def rope_ref(x, pos, cos, sin):
+    """RoPE restatement on [t, heads, hd] at positions pos (tables as floats)."""
+    ref = type("M", (), {})()
+    ref.cos, ref.sin = cos, sin
+    return R.RefLlama.rope(ref, x, pos)
+
+
+# (n_heads, n_kv, head_dim, batch, max_len): group sizes 3 (Llama-3.2-3B), 4
+# (Llama-3.1-8B, batched decode at context 4096), 2, 1, 7.
+DECODE_CASES = [(24, 8, 128, 1, 768), (32, 8, 128, 8, 4096), (4, 2, 64, 3, 40), (8, 8, 256, 2, 300),
+                (28, 4, 128, 2, 1100)]
+
+
+@pytest.mark.parametrize("n_heads,n_kv,hd,batch,max_len", DECODE_CASES)
+def test_decode_attention(device, n_heads, n_kv, hd, batch, max_len):
+    """Fused RoPE + cache write + attention for a batch of sequences: caches
+    bit-exact to the restatement's RoPE, output as the restated SDPA."""
+    c = LlamaConfig(n_layers=1, hidden=n_heads * hd, n_heads=n_heads, n_kv_heads=n_kv, head_dim=hd, ffn=64,
+                    vocab=16)
+    rng = np.random.default_rng(batch * 7 + max_len)
+    qkv = synth.bf16_normal(20, (batch, (n_heads + 2 * n_kv) * hd))
+    kc = synth.bf16_normal(21, (batch, n_kv, max_len, hd))
+    vc = synth.bf16_normal(22, (batch, n_kv, max_len, hd))
+    pos = rng.integers(0, max_len, size=batch).astype(np.uint32)
+    pos[0] = max_len - 1
+    if batch > 1:
+        pos[1] = 0
+    cos, sin = rope_tables(c, max_len)
+    rc, rs = R.rope_tables(hd, c.rope_theta, (32.0, 1.0, 4.0, 8192), max_len)
+    s = [up(device, a) for a in (qkv, cos, sin, pos, kc, vc)]
+    out = device.empty(batch * n_heads * hd * 2)
+    scale = float(np.float32(1) / np.sqrt(np.float32(hd), dtype=np.float32))
+    _lib.call("fh_decode_attention", device.handle, ctypes.c_void_p(s[0].ptr), batch, n_heads, n_kv, hd,
+              ctypes.c_void_p(s[1].ptr), ctypes.c_void_p(s[2].ptr), max_len, ctypes.c_void_p(s[3].ptr),
+              ctypes.c_void_p(s[4].ptr), ctypes.c_void_p(s[5].ptr), max_len, ctypes.c_float(scale),
+              ctypes.c_void_p(out.ptr))
+    got = down(device, out, np.uint16, batch * n_heads * hd).reshape(batch, n_heads, hd)
+    kgot = down(device, s[4], np.uint16, kc.size).reshape(kc.shape)
+    vgot = down(device, s[5], np.uint16, vc.size).reshape(vc.shape)
+    xf = R.from_bf16(qkv)
+    hq, hk = n_heads * hd, n_kv * hd
+    bits = lambda a: (a.view(np.uint32) >> 16).astype(np.uint16)
+    for b in range(batch):
+        p = int(pos[b])
+        q = rope_ref(xf[b:b + 1, :hq].reshape(1, n_heads, hd), np.array([p]), rc, rs)
+        k = rope_ref(xf[b:b + 1, hq:hq + hk].reshape(1, n_kv, hd), np.array([p]), rc, rs)
+        kexp, vexp = kc[b].copy(), vc[b].copy()
+        kexp[:, p, :] = bits(k[0])
+        vexp[:, p, :] = qkv[b, hq + hk:].reshape(n_kv, hd)
+        assert np.array_equal(kgot[b], kexp) and np.array_equal(vgot[b], vexp), b
+        ref, flip = attention_ref(bits(q), kexp, vexp, np.array([p]), scale)
+        assert_attention_close(got[b:b + 1], ref, flip, (b, p))
+
+
+def test_decode_attention_out_of_range_position(device):
+    n_heads, n_kv, hd, max_len = 4, 2, 64, 32
+    c = LlamaConfig(n_layers=1, hidden=256, n_heads=n_heads, n_kv_heads=n_kv, head_dim=hd, ffn=64, vocab=16)
+    qkv = synth.bf16_normal(23, (2, (n_heads + 2 * n_kv) * hd))
+    cos, sin = rope_tables(c, max_len)
+    pos = np.array([max_len, max_len + 9], dtype=np.uint32)
+    s = [up(device, a) for a in (qkv, cos, sin, pos)]
+    kc, vc = device.zeros(2 * n_kv * max_len * hd * 2), device.zeros(2 * n_kv * max_len * hd * 2)
+    out = up(device, np.full(2 * n_heads * hd, 0x3F80, np.uint16))
+    _lib.call("fh_decode_attention", device.handle, ctypes.c_void_p(s[0].ptr), 2, n_heads, n_kv, hd,
+              ctypes.c_void_p(s[1].ptr), ctypes.c_void_p(s[2].ptr), max_len, ctypes.c_void_p(s[3].ptr),
+              ctypes.c_void_p(kc.ptr), ctypes.c_void_p(vc.ptr), max_len, ctypes.c_float(0.125),
+              ctypes.c_void_p(out.ptr))
+    assert not down(device, out, np.uint16, 2 * n_heads * hd).any()
+    assert not down(device, kc, np.uint16, 2 * n_kv * max_len * hd).any()
+    assert not down(device, vc, np.uint16, 2 * n_kv * max_len * hd).any()
+
+
+def test_decode_attention_max_len_limit(device):
+    limit = _lib.decode_attention_max_len(24, 8, 128)
+    assert 8192 <= limit < 16384  # 3 x max_len fp32 scores in 159 KiB of LDS
+    assert _lib.decode_attention_max_len(32, 8, 128) >= 8192
+    buf = device.zeros(64)
+    with pytest.raises(_lib.HipError, match="LDS"):
+        _lib.call("fh_decode_attention", device.handle, ctypes.c_void_p(buf.ptr), 1, 24, 8, 128,
+                  ctypes.c_void_p(buf.ptr), ctypes.c_void_p(buf.ptr), 1, ctypes.c_void_p(buf.ptr),
+                  ctypes.c_void_p(buf.ptr), ctypes.c_void_p(buf.ptr), limit + 4, ctypes.c_float(0.1),
+                  ctypes.c_void_p(buf.ptr))
+
+
 def test_silu_mul(device):
     rows, f = 3, 8192
     gu = synth.bf16_normal(9, (rows, 2 * f))
