@@ -110,9 +110,9 @@ SIGNATURES = {
     "fh_attention_workspace": [_i64, _i64, _i64, _i64, _i64, ctypes.POINTER(ctypes.c_uint64)],
     "fh_attention": [_vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, ctypes.c_float, _vp,
                      ctypes.c_uint64, _vp],
+    "fh_decode_attention_workspace": [_i64, _i64, _i64, _i64, _i64, ctypes.POINTER(ctypes.c_uint64)],
     "fh_decode_attention": [_vp, _vp, _i64, _i64, _i64, _i64, _vp, _vp, _i64, _vp, _vp, _vp, _i64,
-                            ctypes.c_float, _vp],
-    "fh_decode_attention_max_len": [_i64, _i64, _i64, ctypes.POINTER(_i64)],
+                            ctypes.c_float, _vp, ctypes.c_uint64, _vp],
     "fh_silu_mul": [_vp, _vp, _i64, _i64, _vp],
     "fh_argmax": [_vp, _vp, _i64, _i64, _vp],
     "fh_advance_positions": [_vp, _vp, _i64, _i64],
@@ -159,9 +159,9 @@ def attention_workspace_bytes(tokens: int, n_heads: int, n_kv: int, head_dim: in
     return out.value
 
 
-def decode_attention_max_len(n_heads: int, n_kv: int, head_dim: int) -> int:
-    out = _i64()
-    call("fh_decode_attention_max_len", n_heads, n_kv, head_dim, ctypes.byref(out))
+def decode_attention_workspace_bytes(batch: int, n_heads: int, n_kv: int, head_dim: int, max_len: int) -> int:
+    out = ctypes.c_uint64()
+    call("fh_decode_attention_workspace", batch, n_heads, n_kv, head_dim, max_len, ctypes.byref(out))
     return out.value
 
 

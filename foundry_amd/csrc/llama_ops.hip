@@ -1,17 +1,15 @@
-// Decoder-step ops around the q4 linears: residual add + RMSNorm, RoPE with
-// the KV-cache write, attention, SiLU-and-multiply, argmax and the device-side
-// position counter. They are the HIP counterparts of the reference's
-// RmsNorm (src/nn/norm.rs:32-50), apply_rotary_pos_emb
+// Decoder-step ops around the q4 linears (attention is in attention.hip):
+// residual add + RMSNorm, RoPE with the KV-cache write, SiLU-and-multiply,
+// argmax and the device-side position counter. They are the HIP counterparts
+// of the reference's RmsNorm (src/nn/norm.rs:32-50), apply_rotary_pos_emb
 // (src/models/llama/rotary_emb.rs:62-85), StaticCache::update
-// (src/nn/kv_cache.rs:41-80), scaled_dot_product_attention
-// (src/nn/attention.rs:23-60), Silu (src/nn/activation.rs:19-28) and the
+// (src/nn/kv_cache.rs:41-80), Silu (src/nn/activation.rs:19-28) and the
 // greedy argmax (src/generate/mod.rs:192-204; src/metal/kernels/reduce.metal:42-78).
 //
 // Each keeps the reference's bf16 rounding points (its tensors are bf16, and
 // every op rounds its output): e.g. RMSNorm rounds x*scale to bf16 before the
-// weight multiply, RoPE rounds x*cos and rot*sin before adding, attention
-// rounds the scores and the probabilities to bf16. Where the reference runs
-// several dispatches (about ten for RMSNorm, six for SiLU, twelve for SDPA)
+// weight multiply, RoPE rounds x*cos and rot*sin before adding. Where the
+// reference runs several dispatches (about ten for RMSNorm, six for SiLU)
 // these are one kernel each.
 //
 // The decode step is captured once as a HIP graph and replayed: the token id
@@ -152,239 +150,6 @@ __global__ __launch_bounds__(256) void rope_kv_kernel(
     }
 }
 
-// Split-context attention. The keys 0..ctx-1 of a (token, KV head) are cut
-// into chunks of kAttnChunk keys, dealt round-robin to `splits` blocks; block
-// (KV head, split, token) serves all G = n_heads / n_kv query heads of its KV
-// head, so a K or V row is read once per chunk for the whole group. splits
-// is chosen so that tokens * n_kv * splits is about kAttnTargetBlocks: decode
-// (one token) spreads its context over many blocks, prefill (many tokens)
-// keeps one block per (token, KV head) and needs no cross-block combine.
-// Two kernels, because the reference rounds each probability to bf16 from
-// the GLOBAL max and sum of its row:
-//   attn_scores_kernel: s_j = RNE(q.k_j) * scale, written to the workspace
-//     with each chunk's (m_c = max s_j, l_c = sum exp(s_j - m_c)).
-//   attn_pv_kernel: M = max m_c, S = sum l_c exp(m_c - M), p_j =
-//     RNE(exp(s_j - M) / S) as the reference forms them, and the block's
-//     partial sum_j p_j v_j over its chunks. With one active split the block
-//     writes RNE of it; otherwise the last block of the (token, KV head) to
-//     finish (a completion counter in the workspace) adds the partials in
-//     split order, writes RNE(sum) and re-arms the counter at zero, so the
-//     result does not depend on block timing.
-// A key row of HD bf16 is read by HD/8 lanes with 16-byte loads: one
-// wavefront load covers 64/(HD/8) whole keys.
-constexpr int kAttnChunk = 128;
-constexpr int kAttnMaxGroup = 8;
-constexpr int kAttnThreads = 256;
-constexpr uint64_t kAttnTargetBlocks = 512;
-
-struct AttnLayout {
-    uint64_t nck, splits, stats, scores, partial, total;  // byte offsets; counters at 0
-};
-
-static AttnLayout attn_layout(uint64_t tokens, uint64_t n_heads, uint64_t n_kv, uint64_t head_dim,
-                              uint64_t max_len) {
-    auto round_up = [](uint64_t b) { return (b + 255) & ~static_cast<uint64_t>(255); };
-    AttnLayout a;
-    a.nck = (max_len + kAttnChunk - 1) / kAttnChunk;
-    const uint64_t rows = tokens * n_kv;
-    const uint64_t want = rows ? (kAttnTargetBlocks + rows - 1) / rows : 1;
-    a.splits = want < a.nck ? want : a.nck;
-    if (a.splits == 0) a.splits = 1;
-    a.stats = round_up(tokens * n_kv * 4);
-    a.scores = a.stats + round_up(tokens * n_heads * a.nck * 8);
-    a.partial = a.scores + round_up(tokens * n_heads * max_len * 4);
-    a.total = a.partial + (a.splits > 1 ? round_up(tokens * n_heads * a.splits * head_dim * 4) : 0);
-    return a;
-}
-
-template <int HD>
-__global__ __launch_bounds__(kAttnThreads) void attn_scores_kernel(
-    const uint16_t *__restrict__ q, const uint16_t *__restrict__ k_cache,
-    const uint32_t *__restrict__ positions, uint32_t n_heads, uint32_t n_kv, uint32_t max_len,
-    uint32_t nck, uint32_t splits, float scale, float *__restrict__ scores, float2 *__restrict__ stats) {
-    constexpr int LPK = HD / 8, KPI = 64 / LPK, IT = kAttnChunk / 4 / KPI;
-    __shared__ float sc[kAttnMaxGroup][kAttnChunk];
-    const uint32_t t = blockIdx.y, kvh = blockIdx.x / splits, split = blockIdx.x % splits;
-    // keys 0..pos, never past the cache (positions are unchecked device data)
-    const uint32_t ctx = positions[t] < max_len ? positions[t] + 1 : max_len;
-    const uint32_t nact = (ctx + kAttnChunk - 1) / kAttnChunk;
-    if (split >= nact) return;
-    const uint32_t G = n_heads / n_kv, h0 = kvh * G;
-    const uint32_t wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    const uint32_t ks = lane / LPK, li = lane % LPK;
-    const uint16_t *kb = k_cache + static_cast<uint64_t>(kvh) * max_len * HD + li * 8;
-    float qf[kAttnMaxGroup][8];
-#pragma unroll
-    for (int g = 0; g < kAttnMaxGroup; ++g)
-        if (g < static_cast<int>(G))
-            unpack8(*reinterpret_cast<const uint4 *>(q + (static_cast<uint64_t>(t) * n_heads + h0 + g) * HD + li * 8),
-                    qf[g]);
-    for (uint32_t c = split; c < nact; c += splits) {
-        const uint32_t j0 = c * kAttnChunk;
-        const uint32_t jw = j0 + wave * (kAttnChunk / 4) + ks;
-        uint4 kr[IT];
-#pragma unroll
-        for (int it = 0; it < IT; ++it) {
-            const uint32_t j = jw + it * KPI;
-            kr[it] = j < ctx ? *reinterpret_cast<const uint4 *>(kb + static_cast<uint64_t>(j) * HD)
-                             : make_uint4(0u, 0u, 0u, 0u);
-        }
-#pragma unroll
-        for (int it = 0; it < IT; ++it) {
-            float kf[8];
-            unpack8(kr[it], kf);
-            const uint32_t j = jw + it * KPI;
-#pragma unroll
-            for (int g = 0; g < kAttnMaxGroup; ++g) {
-                if (g < static_cast<int>(G)) {
-                    float d = 0.f;
-#pragma unroll
-                    for (int e = 0; e < 8; ++e) d += qf[g][e] * kf[e];
-#pragma unroll
-                    for (int off = 1; off < LPK; off <<= 1) d += __shfl_xor(d, off, 64);
-                    if (li == 0) sc[g][j - j0] = j < ctx ? bf(rne(d)) * scale : -INFINITY;
-                }
-            }
-        }
-        __syncthreads();
-        static_assert(kAttnChunk == 128, "statistics pass assumes two scores per lane");
-        for (uint32_t g = wave; g < G; g += 4) {
-            const float a = sc[g][lane], b = sc[g][lane + 64];
-            const float m = wave_max(fmaxf(a, b));
-            const float l = wave_sum(expf(a - m) + expf(b - m));
-            if (lane == 0) stats[(static_cast<uint64_t>(t) * n_heads + h0 + g) * nck + c] = make_float2(m, l);
-        }
-        const uint32_t valid = min(ctx - j0, static_cast<uint32_t>(kAttnChunk));
-        for (uint32_t i = threadIdx.x; i < G * kAttnChunk; i += kAttnThreads) {
-            const uint32_t g = i / kAttnChunk, jj = i % kAttnChunk;
-            if (jj < valid) scores[(static_cast<uint64_t>(t) * n_heads + h0 + g) * max_len + j0 + jj] = sc[g][jj];
-        }
-        __syncthreads();  // sc is rewritten by the next chunk
-    }
-}
-
-template <int HD>
-__global__ __launch_bounds__(kAttnThreads) void attn_pv_kernel(
-    const uint16_t *__restrict__ v_cache, const uint32_t *__restrict__ positions, uint32_t n_heads,
-    uint32_t n_kv, uint32_t max_len, uint32_t nck, uint32_t splits, const float *__restrict__ scores,
-    const float2 *__restrict__ stats, float *__restrict__ partial, uint32_t *__restrict__ counters,
-    uint16_t *__restrict__ out) {
-    constexpr int LPK = HD / 8, KPI = 64 / LPK, IT = kAttnChunk / 4 / KPI;
-    __shared__ float p[kAttnMaxGroup][kAttnChunk];
-    __shared__ float wsum[4][kAttnMaxGroup * HD];
-    __shared__ float mg[kAttnMaxGroup], sg[kAttnMaxGroup];
-    __shared__ uint32_t is_last;
-    const uint32_t t = blockIdx.y, kvh = blockIdx.x / splits, split = blockIdx.x % splits;
-    const uint32_t ctx = positions[t] < max_len ? positions[t] + 1 : max_len;
-    const uint32_t nact = (ctx + kAttnChunk - 1) / kAttnChunk;
-    if (split >= nact) return;
-    const uint32_t nsp = min(splits, nact);  // splits holding at least one chunk
-    const uint32_t G = n_heads / n_kv, h0 = kvh * G;
-    const uint32_t wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    const uint32_t ks = lane / LPK, li = lane % LPK;
-    const uint16_t *vb = v_cache + static_cast<uint64_t>(kvh) * max_len * HD + li * 8;
-    for (uint32_t g = wave; g < G; g += 4) {
-        const float2 *st = stats + (static_cast<uint64_t>(t) * n_heads + h0 + g) * nck;
-        float m = -INFINITY;
-        for (uint32_t cc = lane; cc < nact; cc += 64) m = fmaxf(m, st[cc].x);
-        m = wave_max(m);
-        float s = 0.f;
-        for (uint32_t cc = lane; cc < nact; cc += 64) {
-            const float2 v = st[cc];
-            s += v.y * expf(v.x - m);
-        }
-        s = wave_sum(s);
-        if (lane == 0) {
-            mg[g] = m;
-            sg[g] = s;
-        }
-    }
-    float acc[kAttnMaxGroup][8];
-#pragma unroll
-    for (int g = 0; g < kAttnMaxGroup; ++g)
-#pragma unroll
-        for (int e = 0; e < 8; ++e) acc[g][e] = 0.f;
-    for (uint32_t c = split; c < nact; c += splits) {
-        const uint32_t j0 = c * kAttnChunk;
-        // V rows first: they do not depend on the probabilities
-        const uint32_t jw = j0 + wave * (kAttnChunk / 4) + ks;
-        uint4 vr[IT];
-#pragma unroll
-        for (int it = 0; it < IT; ++it) {
-            const uint32_t j = jw + it * KPI;
-            vr[it] = j < ctx ? *reinterpret_cast<const uint4 *>(vb + static_cast<uint64_t>(j) * HD)
-                             : make_uint4(0u, 0u, 0u, 0u);
-        }
-        __syncthreads();  // mg/sg written; p free from the previous chunk
-        const uint32_t valid = min(ctx - j0, static_cast<uint32_t>(kAttnChunk));
-        for (uint32_t i = threadIdx.x; i < G * kAttnChunk; i += kAttnThreads) {
-            const uint32_t g = i / kAttnChunk, jj = i % kAttnChunk;
-            float v = 0.f;
-            if (jj < valid)
-                v = bf(rne(expf(scores[(static_cast<uint64_t>(t) * n_heads + h0 + g) * max_len + j0 + jj] - mg[g]) /
-                           sg[g]));
-            p[g][jj] = v;
-        }
-        __syncthreads();
-#pragma unroll
-        for (int it = 0; it < IT; ++it) {
-            float vf[8];
-            unpack8(vr[it], vf);
-            const uint32_t jj = wave * (kAttnChunk / 4) + it * KPI + ks;
-#pragma unroll
-            for (int g = 0; g < kAttnMaxGroup; ++g) {
-                if (g < static_cast<int>(G)) {
-                    const float pg = p[g][jj];
-#pragma unroll
-                    for (int e = 0; e < 8; ++e) acc[g][e] += pg * vf[e];
-                }
-            }
-        }
-    }
-    // sum over the key slots of the wavefront, then over the four wavefronts
-#pragma unroll
-    for (int off = LPK; off < 64; off <<= 1)
-#pragma unroll
-        for (int g = 0; g < kAttnMaxGroup; ++g)
-            if (g < static_cast<int>(G))
-#pragma unroll
-                for (int e = 0; e < 8; ++e) acc[g][e] += __shfl_xor(acc[g][e], off, 64);
-    if (ks == 0) {
-#pragma unroll
-        for (int g = 0; g < kAttnMaxGroup; ++g)
-            if (g < static_cast<int>(G))
-#pragma unroll
-                for (int e = 0; e < 8; ++e) wsum[wave][g * HD + li * 8 + e] = acc[g][e];
-    }
-    __syncthreads();
-    uint16_t *orow = out + (static_cast<uint64_t>(t) * n_heads + h0) * HD;
-    float *part = partial + (static_cast<uint64_t>(t) * n_kv + kvh) * splits * G * HD;
-    for (uint32_t i = threadIdx.x; i < G * HD; i += kAttnThreads) {
-        const float v = wsum[0][i] + wsum[1][i] + wsum[2][i] + wsum[3][i];
-        if (nsp == 1)
-            orow[i] = rne(v);
-        else
-            part[static_cast<uint64_t>(split) * G * HD + i] = v;
-    }
-    if (nsp == 1) return;
-    // publish this split's partial, then count it; the last split to arrive
-    // combines
-    __threadfence();
-    __syncthreads();
-    uint32_t *counter = counters + static_cast<uint64_t>(t) * n_kv + kvh;
-    if (threadIdx.x == 0)
-        is_last = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT) == nsp - 1;
-    __syncthreads();
-    if (!is_last) return;
-    __threadfence();
-    for (uint32_t i = threadIdx.x; i < G * HD; i += kAttnThreads) {
-        float s = 0.f;
-        for (uint32_t sp = 0; sp < nsp; ++sp) s += part[static_cast<uint64_t>(sp) * G * HD + i];
-        orow[i] = rne(s);
-    }
-    if (threadIdx.x == 0) __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
 // out = RNE(RNE(g / (1 + exp(-g))) * u), gu row = [g (F) | u (F)].
 __global__ __launch_bounds__(256) void silu_mul_kernel(const uint16_t *__restrict__ gu, uint32_t f,
                                                        uint64_t total, uint16_t *__restrict__ out) {
@@ -465,21 +230,6 @@ __global__ void advance_kernel(uint32_t *__restrict__ p, uint32_t n, uint32_t by
 
 using namespace fh;
 
-namespace {
-
-// The workspace holds at most tokens * n_heads * (3 max_len + head_dim)
-// floats (scores, chunk partials); refuse sizes whose byte counts would not
-// fit comfortably in 64 bits.
-int check_attn_size(const char *fn, int64_t tokens, int64_t n_heads, int64_t head_dim, int64_t max_len) {
-    const long double floats = static_cast<long double>(tokens) * n_heads * (3.0L * max_len + head_dim);
-    if (floats > 0x1p56L)
-        return fail(FH_ERR_INDEX_TOO_LARGE, "%s: attention workspace for %lld tokens x %lld heads x %lld "
-                    "keys is too large", fn, (long long)tokens, (long long)n_heads, (long long)max_len);
-    return FH_OK;
-}
-
-}  // namespace
-
 extern "C" int fh_rms_norm(fh_device *dev, const uint16_t *x, const uint16_t *residual,
                            uint16_t *residual_out, const uint16_t *weight, int64_t rows,
                            int64_t dim, float eps, uint16_t *y) {
@@ -547,78 +297,6 @@ extern "C" int fh_rope_kv(fh_device *dev, const uint16_t *qkv, int64_t tokens, i
                            static_cast<uint32_t>(n_kv), static_cast<uint32_t>(head_dim), cos_tab,
                            sin_tab, static_cast<uint32_t>(table_len), positions, k_cache, v_cache,
                            static_cast<uint32_t>(max_len), q_out);
-    });
-}
-
-extern "C" int fh_attention_workspace(int64_t tokens, int64_t n_heads, int64_t n_kv, int64_t head_dim,
-                                      int64_t max_len, uint64_t *bytes) {
-    const char *fn = "fh_attention_workspace";
-    if (!bytes) return fail(FH_ERR_INVALID_ARGUMENT, "%s: null output", fn);
-    if (int rc = fh_check_dims(fn, {tokens, n_heads, n_kv, head_dim, max_len})) return rc;
-    if (int rc = check_attn_size(fn, tokens, n_heads, head_dim, max_len)) return rc;
-    *bytes = attn_layout(tokens, n_heads, n_kv, head_dim, max_len).total;
-    return FH_OK;
-}
-
-template <int HD>
-static void launch_attention(hipStream_t stream, dim3 grid, const uint16_t *q, const uint16_t *k_cache,
-                             const uint16_t *v_cache, const uint32_t *positions, uint32_t n_heads,
-                             uint32_t n_kv, uint32_t max_len, uint32_t nck, float scale, char *ws,
-                             const AttnLayout &a, uint16_t *out) {
-    auto *counters = reinterpret_cast<uint32_t *>(ws);
-    auto *stats = reinterpret_cast<float2 *>(ws + a.stats);
-    auto *scores = reinterpret_cast<float *>(ws + a.scores);
-    auto *partial = reinterpret_cast<float *>(ws + a.partial);
-    const uint32_t splits = static_cast<uint32_t>(a.splits);
-    hipLaunchKernelGGL(attn_scores_kernel<HD>, grid, dim3(kAttnThreads), 0, stream, q, k_cache, positions,
-                       n_heads, n_kv, max_len, nck, splits, scale, scores, stats);
-    hipLaunchKernelGGL(attn_pv_kernel<HD>, grid, dim3(kAttnThreads), 0, stream, v_cache, positions, n_heads,
-                       n_kv, max_len, nck, splits, scores, stats, partial, counters, out);
-}
-
-extern "C" int fh_attention(fh_device *dev, const uint16_t *q, const uint16_t *k_cache,
-                            const uint16_t *v_cache, const uint32_t *positions, int64_t tokens,
-                            int64_t n_heads, int64_t n_kv, int64_t head_dim, int64_t max_len,
-                            float scale, void *workspace, uint64_t workspace_bytes, uint16_t *out) {
-    const char *fn = "fh_attention";
-    if (int rc = check_usable(dev, fn)) return rc;
-    if (int rc = fh_check_dims(fn, {tokens, n_heads, n_kv, head_dim, max_len})) return rc;
-    if (tokens == 0) return FH_OK;
-    if (n_kv == 0 || n_heads % n_kv != 0 || n_heads / n_kv > kAttnMaxGroup ||
-        (head_dim != 64 && head_dim != 128 && head_dim != 256))
-        return fail(FH_ERR_UNSUPPORTED, "%s: heads %lld/%lld, head_dim %lld", fn, (long long)n_heads,
-                    (long long)n_kv, (long long)head_dim);
-    if (max_len == 0) return fail(FH_ERR_INVALID_ARGUMENT, "%s: empty KV cache", fn);
-    if (int rc = check_attn_size(fn, tokens, n_heads, head_dim, max_len)) return rc;
-    const AttnLayout a = attn_layout(tokens, n_heads, n_kv, head_dim, max_len);
-    if (tokens > 65535 || static_cast<uint64_t>(n_kv) * a.splits > 0x7FFFFFFFu)
-        return fail(FH_ERR_INDEX_TOO_LARGE, "%s: %lld tokens x %llu splits exceed the grid", fn,
-                    (long long)tokens, (unsigned long long)(n_kv * a.splits));
-    if (workspace_bytes < a.total)
-        return fail(FH_ERR_INVALID_ARGUMENT, "%s: workspace of %llu bytes, %llu needed", fn,
-                    (unsigned long long)workspace_bytes, (unsigned long long)a.total);
-    if ((reinterpret_cast<uintptr_t>(q) | reinterpret_cast<uintptr_t>(k_cache) |
-         reinterpret_cast<uintptr_t>(v_cache) | reinterpret_cast<uintptr_t>(workspace)) & 15u)
-        return fail(FH_ERR_INVALID_ARGUMENT, "%s: q, caches and workspace must be 16-byte aligned", fn);
-    const uint64_t cache = static_cast<uint64_t>(n_kv) * max_len * head_dim * 2;
-    if (int rc = check_range(dev, q, static_cast<uint64_t>(tokens) * n_heads * head_dim * 2, fn, "q")) return rc;
-    if (int rc = check_range(dev, k_cache, cache, fn, "k_cache")) return rc;
-    if (int rc = check_range(dev, v_cache, cache, fn, "v_cache")) return rc;
-    if (int rc = check_range(dev, positions, static_cast<uint64_t>(tokens) * 4, fn, "positions")) return rc;
-    if (int rc = check_range(dev, workspace, a.total, fn, "workspace")) return rc;
-    if (int rc = check_range(dev, out, static_cast<uint64_t>(tokens) * n_heads * head_dim * 2, fn, "out")) return rc;
-    if (int rc = set_current(dev, fn)) return rc;
-    const dim3 grid(static_cast<uint32_t>(n_kv * a.splits), static_cast<uint32_t>(tokens));
-    const uint32_t nh = static_cast<uint32_t>(n_heads), nk = static_cast<uint32_t>(n_kv),
-                   ml = static_cast<uint32_t>(max_len), nck = static_cast<uint32_t>(a.nck);
-    char *ws = static_cast<char *>(workspace);
-    return dispatch(dev, fn, [&] {
-        if (head_dim == 64)
-            launch_attention<64>(dev->stream, grid, q, k_cache, v_cache, positions, nh, nk, ml, nck, scale, ws, a, out);
-        else if (head_dim == 128)
-            launch_attention<128>(dev->stream, grid, q, k_cache, v_cache, positions, nh, nk, ml, nck, scale, ws, a, out);
-        else
-            launch_attention<256>(dev->stream, grid, q, k_cache, v_cache, positions, nh, nk, ml, nck, scale, ws, a, out);
     });
 }
 

@@ -202,7 +202,8 @@ class Q4Llama:
         }
         self.attn_ws_bytes = _lib.attention_workspace_bytes(t, c.n_heads, c.n_kv_heads, c.head_dim, max_len)
         self.attn_ws = dev.zeros(self.attn_ws_bytes)
-        self.fused_decode = max_len <= _lib.decode_attention_max_len(c.n_heads, c.n_kv_heads, c.head_dim)
+        self.dec_ws_bytes = _lib.decode_attention_workspace_bytes(1, c.n_heads, c.n_kv_heads, c.head_dim, max_len)
+        self.dec_ws = dev.zeros(self.dec_ws_bytes)
 
     # ---- thin wrappers over the C-ABI ----
     def _p(self, st: HipStorage, byte_offset: int = 0):
@@ -221,12 +222,12 @@ class Q4Llama:
         for L in self.layers:
             self._norm(tokens, pending, L["input_norm"])
             self._linear(b["x"], tokens, L["qkv"], b["qkv"])
-            if tokens == 1 and self.fused_decode:
-                # one new token: RoPE, cache write and attention in one kernel
+            if tokens == 1:
+                # one new token: RoPE and the cache write fused into attention
                 _lib.call("fh_decode_attention", d, self._p(b["qkv"]), 1, c.n_heads, c.n_kv_heads, c.head_dim,
                           self._p(self.cos), self._p(self.sin), self.max_len, self._p(positions),
                           self._p(L["k_cache"]), self._p(L["v_cache"]), self.max_len, ctypes.c_float(self.scale),
-                          self._p(b["attn"]))
+                          self._p(self.dec_ws), self.dec_ws_bytes, self._p(b["attn"]))
             else:
                 _lib.call("fh_rope_kv", d, self._p(b["qkv"]), tokens, c.n_heads, c.n_kv_heads, c.head_dim,
                           self._p(self.cos), self._p(self.sin), self.max_len, self._p(positions),

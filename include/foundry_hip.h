@@ -211,8 +211,8 @@ int fh_rope_kv(fh_device *dev, const uint16_t *qkv, int64_t tokens, int64_t n_he
                int64_t table_len, const uint32_t *positions, uint16_t *k_cache,
                uint16_t *v_cache, int64_t max_len, uint16_t *q_out);
 
-/* Bytes of device workspace fh_attention needs for these sizes (scores,
- * per-chunk softmax statistics and partial outputs, completion counters). */
+/* Bytes of device workspace fh_attention needs for these sizes (the scores
+ * and per-chunk softmax statistics of every row). */
 int fh_attention_workspace(int64_t tokens, int64_t n_heads, int64_t n_kv, int64_t head_dim,
                            int64_t max_len, uint64_t *bytes);
 
@@ -223,37 +223,36 @@ int fh_attention_workspace(int64_t tokens, int64_t n_heads, int64_t n_kv, int64_
  * probabilities RNE to bf16 from the row's global max and sum, out =
  * RNE(sum p v). q, out: [tokens, n_heads * head_dim]; caches [n_kv, max_len,
  * head_dim]. head_dim is 64, 128 or 256 and n_heads/n_kv at most 8; tokens at
- * most 65535. The context is split into chunks of 128 keys processed in
- * parallel, so long contexts fill the device.
- * workspace: at least fh_attention_workspace() bytes of device memory, 16-byte
- * aligned, ZERO-FILLED before its first use (fh_alloc with zero_fill); every
- * call leaves its counters at zero again, so the workspace can be reused by
- * later calls and by calls captured in a graph. Calls that share a workspace
+ * most 65535. The context is split into chunks of 64 keys scored in
+ * parallel, and P.V is split over head_dim, so a long context fills the
+ * device. workspace: at least fh_attention_workspace() bytes of device
+ * memory, 16-byte aligned, no initial contents; calls that share a workspace
  * must not run concurrently. */
 int fh_attention(fh_device *dev, const uint16_t *q, const uint16_t *k_cache,
                  const uint16_t *v_cache, const uint32_t *positions, int64_t tokens,
                  int64_t n_heads, int64_t n_kv, int64_t head_dim, int64_t max_len, float scale,
                  void *workspace, uint64_t workspace_bytes, uint16_t *out);
 
+/* Bytes of device workspace fh_decode_attention needs for these sizes. */
+int fh_decode_attention_workspace(int64_t batch, int64_t n_heads, int64_t n_kv, int64_t head_dim,
+                                  int64_t max_len, uint64_t *bytes);
+
 /* The decode step's attention for a batch of sequences that each add one
- * token, fused: fh_rope_kv's RoPE and cache write, then fh_attention over keys
- * 0..positions[b] of sequence b, in one kernel with the scores in LDS (same
- * rounding points as the two ops). qkv: [batch, (n_heads + 2 n_kv) *
- * head_dim]; cos_tab/sin_tab: [table_len, head_dim]; positions: device u32
- * [batch]; k_cache/v_cache: [batch, n_kv, max_len, head_dim] (one cache per
- * sequence); out: [batch, n_heads * head_dim]. A position >= max_len or >=
- * table_len writes nothing to the caches and zeros to out. head_dim is 64,
- * 128 or 256, n_heads/n_kv at most 8, batch at most 65535, operands 16-byte
- * aligned, and max_len at most fh_decode_attention_max_len() (the scores of
- * a row live in LDS; longer caches use fh_rope_kv + fh_attention). */
+ * token: fh_rope_kv's RoPE of the token's q and k and its cache write at
+ * positions[b], then fh_attention over keys 0..positions[b] of sequence b --
+ * the same rounding points, in two kernel launches instead of three. qkv:
+ * [batch, (n_heads + 2 n_kv) * head_dim]; cos_tab/sin_tab: [table_len,
+ * head_dim]; positions: device u32 [batch]; k_cache/v_cache: [batch, n_kv,
+ * max_len, head_dim] (one cache per sequence); out: [batch, n_heads *
+ * head_dim]. A position >= max_len or >= table_len writes nothing to the
+ * caches and zeros to out. head_dim is 64, 128 or 256, n_heads/n_kv at most
+ * 8, batch at most 65535, operands 16-byte aligned. workspace: as for
+ * fh_attention, at least fh_decode_attention_workspace() bytes. */
 int fh_decode_attention(fh_device *dev, const uint16_t *qkv, int64_t batch, int64_t n_heads,
                         int64_t n_kv, int64_t head_dim, const uint16_t *cos_tab,
                         const uint16_t *sin_tab, int64_t table_len, const uint32_t *positions,
                         uint16_t *k_cache, uint16_t *v_cache, int64_t max_len, float scale,
-                        uint16_t *out);
-
-/* Largest max_len fh_decode_attention accepts for these head counts. */
-int fh_decode_attention_max_len(int64_t n_heads, int64_t n_kv, int64_t head_dim, int64_t *max_len);
+                        void *workspace, uint64_t workspace_bytes, uint16_t *out);
 
 /* LlamaMlp's act_fn(gate) * up (src/models/llama/mlp.rs:49-58, Silu at
  * src/nn/activation.rs:19-28): gate_up row = [gate (f) | up (f)],
