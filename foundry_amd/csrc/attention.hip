@@ -87,6 +87,21 @@ __global__ __launch_bounds__(kAttnThreads) void attn_scores_kernel(
     const uint32_t h0 = kvh * G;
     const uint32_t wave = tid >> 6, lane = tid & 63, ks = lane / LPK, li = lane % LPK;
     const uint64_t cache = static_cast<uint64_t>(r) * row_stride + static_cast<uint64_t>(kvh) * max_len * HD;
+    // keys below kmax come from the cache; with ROPE key pos is the new one
+    // (from LDS, substituted when the chunk is scored)
+    const uint32_t kmax = ROPE ? pos : ctx;
+    const uint16_t *kb = k_cache + cache + li * 8;
+    auto load_chunk = [&](uint32_t c, uint4 (&kr)[IT]) {
+        const uint32_t jw = c * kAttnChunk + wave * (kAttnChunk / kAttnWaves) + ks;
+#pragma unroll
+        for (int it = 0; it < IT; ++it) {
+            const uint32_t j = jw + it * KPI;
+            kr[it] = j < kmax ? *reinterpret_cast<const uint4 *>(kb + static_cast<uint64_t>(j) * HD)
+                              : make_uint4(0u, 0u, 0u, 0u);
+        }
+    };
+    uint4 kr[IT];
+    load_chunk(split, kr);  // in flight during the q set-up
     float qf[G][8];
     uint4 kn = make_uint4(0u, 0u, 0u, 0u);
     if constexpr (ROPE) {
@@ -124,24 +139,17 @@ __global__ __launch_bounds__(kAttnThreads) void attn_scores_kernel(
             unpack8(*reinterpret_cast<const uint4 *>(q_src + (static_cast<uint64_t>(r) * n_heads + h0 + g) * HD + li * 8),
                     qf[g]);
     }
-    // keys below kmax come from the cache; with ROPE key pos comes from LDS
-    const uint32_t kmax = ROPE ? pos : ctx;
-    const uint16_t *kb = k_cache + cache + li * 8;
     for (uint32_t c = split; c < nact; c += splits) {
         const uint32_t j0 = c * kAttnChunk;
         const uint32_t jw = j0 + wave * (kAttnChunk / kAttnWaves) + ks;
-        uint4 kr[IT];
+        uint4 next[IT];
+        const bool more = c + splits < nact;
+        if (more) load_chunk(c + splits, next);  // the next chunk's keys load while this one is scored
 #pragma unroll
         for (int it = 0; it < IT; ++it) {
             const uint32_t j = jw + it * KPI;
-            kr[it] = j < kmax ? *reinterpret_cast<const uint4 *>(kb + static_cast<uint64_t>(j) * HD)
-                              : (ROPE && j == pos ? kn : make_uint4(0u, 0u, 0u, 0u));
-        }
-#pragma unroll
-        for (int it = 0; it < IT; ++it) {
             float kf[8];
-            unpack8(kr[it], kf);
-            const uint32_t j = jw + it * KPI;
+            unpack8(ROPE && j == pos ? kn : kr[it], kf);
 #pragma unroll
             for (int g = 0; g < G; ++g) {
                 float d = 0.f;
@@ -165,6 +173,9 @@ __global__ __launch_bounds__(kAttnThreads) void attn_scores_kernel(
             if (jj < valid) scores[(static_cast<uint64_t>(r) * n_heads + h0 + g) * max_len + j0 + jj] = sc[g][jj];
         }
         __syncthreads();  // sc is rewritten by the next chunk
+        if (more)
+#pragma unroll
+            for (int it = 0; it < IT; ++it) kr[it] = next[it];
     }
 }
 
@@ -202,13 +213,25 @@ __global__ __launch_bounds__(kAttnThreads) void attn_pv_kernel(
     const uint32_t wave = tid >> 6, lane = tid & 63, q = tid % P, s = tid / P;
     const uint16_t *vb = v_cache + static_cast<uint64_t>(r) * row_stride + static_cast<uint64_t>(kvh) * max_len * head_dim +
                          d0 + 2 * q;
-    uint32_t vr[S::kLoads];
-    // the first tile's V rows do not depend on the softmax statistics
+    const float *srow = scores + (static_cast<uint64_t>(r) * n_heads + h0) * max_len;
+    // A tile: V of keys t0 + s + k * slots (this thread's dims) and the raw
+    // scores of entries i = tid + n * 256 of the tile's [G][kTile] block.
+    constexpr int NS = (G * S::kTile + kAttnThreads - 1) / kAttnThreads;
+    auto load_tile = [&](uint32_t t0, uint32_t (&vr)[S::kLoads], float (&sr)[NS]) {
 #pragma unroll
-    for (int k = 0; k < S::kLoads; ++k) {
-        const uint32_t j = s + k * S::kSlots;
-        vr[k] = j < ctx ? *reinterpret_cast<const uint32_t *>(vb + static_cast<uint64_t>(j) * head_dim) : 0u;
-    }
+        for (int k = 0; k < S::kLoads; ++k) {
+            const uint32_t j = t0 + s + k * S::kSlots;
+            vr[k] = j < ctx ? *reinterpret_cast<const uint32_t *>(vb + static_cast<uint64_t>(j) * head_dim) : 0u;
+        }
+#pragma unroll
+        for (int n = 0; n < NS; ++n) {
+            const uint32_t i = tid + n * kAttnThreads, g = i / S::kTile, j = t0 + i % S::kTile;
+            sr[n] = i < G * S::kTile && j < ctx ? srow[static_cast<uint64_t>(g) * max_len + j] : 0.f;
+        }
+    };
+    uint32_t vr[S::kLoads];
+    float sr[NS];
+    load_tile(0, vr, sr);  // independent of the softmax statistics
     for (uint32_t g = wave; g < G; g += kAttnWaves) {
         const float2 *st = stats + (static_cast<uint64_t>(r) * n_heads + h0 + g) * nck;
         float m = -INFINITY;
@@ -228,19 +251,16 @@ __global__ __launch_bounds__(kAttnThreads) void attn_pv_kernel(
     float acc[G][2];
 #pragma unroll
     for (int g = 0; g < G; ++g) acc[g][0] = acc[g][1] = 0.f;
-    const float *srow = scores + (static_cast<uint64_t>(r) * n_heads + h0) * max_len;
     for (uint32_t t0 = 0; t0 < ctx; t0 += S::kTile) {
-        if (t0 != 0) {
-#pragma unroll
-            for (int k = 0; k < S::kLoads; ++k) {
-                const uint32_t j = t0 + s + k * S::kSlots;
-                vr[k] = j < ctx ? *reinterpret_cast<const uint32_t *>(vb + static_cast<uint64_t>(j) * head_dim) : 0u;
-            }
-        }
+        uint32_t vnext[S::kLoads];
+        float snext[NS];
+        const bool more = t0 + S::kTile < ctx;
+        if (more) load_tile(t0 + S::kTile, vnext, snext);  // in flight while this tile is used
         __syncthreads();  // mg/sg written; p free from the previous tile
-        for (uint32_t i = tid; i < G * S::kTile; i += kAttnThreads) {
-            const uint32_t g = i / S::kTile, jj = i % S::kTile, j = t0 + jj;
-            p[g][jj] = j < ctx ? bf(rne(expf(srow[static_cast<uint64_t>(g) * max_len + j] - mg[g]) / sg[g])) : 0.f;
+#pragma unroll
+        for (int n = 0; n < NS; ++n) {
+            const uint32_t i = tid + n * kAttnThreads, g = i / S::kTile, jj = i % S::kTile;
+            if (i < G * S::kTile) p[g][jj] = t0 + jj < ctx ? bf(rne(expf(sr[n] - mg[g]) / sg[g])) : 0.f;
         }
         __syncthreads();
 #pragma unroll
@@ -252,6 +272,12 @@ __global__ __launch_bounds__(kAttnThreads) void attn_pv_kernel(
                 acc[g][0] += p[g][jj] * v0;
                 acc[g][1] += p[g][jj] * v1;
             }
+        }
+        if (more) {
+#pragma unroll
+            for (int k = 0; k < S::kLoads; ++k) vr[k] = vnext[k];
+#pragma unroll
+            for (int n = 0; n < NS; ++n) sr[n] = snext[n];
         }
     }
 #pragma unroll
