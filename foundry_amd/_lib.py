@@ -113,6 +113,9 @@ SIGNATURES = {
     "fh_decode_attention_workspace": [_i64, _i64, _i64, _i64, _i64, ctypes.POINTER(ctypes.c_uint64)],
     "fh_decode_attention": [_vp, _vp, _i64, _i64, _i64, _i64, _vp, _vp, _i64, _vp, _vp, _vp, _i64,
                             ctypes.c_float, _vp, ctypes.c_uint64, _vp],
+    "fh_q4_matmul_rmsnorm": [_vp, _vp, _vp, _vp, _vp, ctypes.c_float, _i64, _i64, _vp, _vp, _vp, _i64, _i64,
+                             _vp, _int],
+    "fh_q4_gate_up_silu": [_vp, _vp, _vp, _vp, _vp, ctypes.c_float, _i64, _i64, _vp, _vp, _vp, _i64, _i64, _vp],
     "fh_silu_mul": [_vp, _vp, _i64, _i64, _vp],
     "fh_argmax": [_vp, _vp, _i64, _i64, _vp],
     "fh_advance_positions": [_vp, _vp, _i64, _i64],

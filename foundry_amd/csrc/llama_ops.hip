@@ -62,6 +62,12 @@ __global__ __launch_bounds__(kNormThreads) void rms_norm_kernel(const uint16_t *
     const uint64_t base = static_cast<uint64_t>(blockIdx.x) * dim;
     const uint32_t pieces = dim / 8;
     float h[kNormChunks][8];
+    uint4 wv[kNormChunks];  // the weight loads go out with x's, before the reduction
+#pragma unroll
+    for (int c = 0; c < kNormChunks; ++c) {
+        const uint32_t piece = threadIdx.x + c * kNormThreads;
+        if (piece < pieces) wv[c] = *reinterpret_cast<const uint4 *>(w + piece * 8);
+    }
     float ss = 0.f;
 #pragma unroll
     for (int c = 0; c < kNormChunks; ++c) {
@@ -99,8 +105,7 @@ __global__ __launch_bounds__(kNormThreads) void rms_norm_kernel(const uint16_t *
     for (int c = 0; c < kNormChunks; ++c) {
         const uint32_t piece = threadIdx.x + c * kNormThreads;
         if (piece < pieces) {
-            const uint4 wv = *reinterpret_cast<const uint4 *>(w + piece * 8);
-            const uint32_t ww[4] = {wv.x, wv.y, wv.z, wv.w};
+            const uint32_t ww[4] = {wv[c].x, wv[c].y, wv[c].z, wv[c].w};
             uint32_t o[4];
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
@@ -173,44 +178,68 @@ __device__ __forceinline__ void take_max(float &best, uint32_t &idx, float v, ui
     }
 }
 
+// Per thread, kArgmaxBatch 16-byte loads are issued together before any is
+// compared, so a row costs one or two memory round trips instead of one per
+// load. The loads are unconditional (indices past the row are clamped to its
+// last piece and ignored): a guarded load sits in its own basic block, where
+// the compiler drains every outstanding load before issuing it. Lanes then
+// wavefronts reduce with the same (max, lowest index) rule.
+constexpr int kArgmaxBatch = 16;
+
 __global__ __launch_bounds__(kArgmaxThreads) void argmax_kernel(const uint16_t *__restrict__ x, uint32_t n,
                                                                 uint32_t *__restrict__ out) {
-    __shared__ float bv[kArgmaxThreads];
-    __shared__ uint32_t bi[kArgmaxThreads];
+    __shared__ float bv[kArgmaxThreads / 64];
+    __shared__ uint32_t bi[kArgmaxThreads / 64];
     const uint16_t *row = x + static_cast<uint64_t>(blockIdx.x) * n;
     float best = -INFINITY;
     uint32_t idx = 0xFFFFFFFFu;
-    const uint32_t pieces = n / 8;
     const bool aligned = (reinterpret_cast<uintptr_t>(row) & 15u) == 0;
-    if (aligned) {
-        for (uint32_t p = threadIdx.x; p < pieces; p += kArgmaxThreads) {
-            const uint4 v = *reinterpret_cast<const uint4 *>(row + p * 8);
-            const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+    const uint32_t pieces = aligned ? n / 8 : 0;
+    for (uint32_t p0 = 0; p0 < pieces; p0 += kArgmaxThreads * kArgmaxBatch) {
+        uint4 v[kArgmaxBatch];
 #pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                take_max(best, idx, bf(w[e] & 0xFFFFu), p * 8 + 2 * e);
-                take_max(best, idx, bf(w[e] >> 16), p * 8 + 2 * e + 1);
+        for (int u = 0; u < kArgmaxBatch; ++u) {
+            const uint32_t p = min(p0 + u * kArgmaxThreads + threadIdx.x, pieces - 1);
+            v[u] = *reinterpret_cast<const uint4 *>(row + static_cast<uint64_t>(p) * 8);
+        }
+#pragma unroll
+        for (int u = 0; u < kArgmaxBatch; ++u) {
+            const uint32_t p = p0 + u * kArgmaxThreads + threadIdx.x;
+            if (p < pieces) {
+                const uint32_t w[4] = {v[u].x, v[u].y, v[u].z, v[u].w};
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    take_max(best, idx, bf(w[e] & 0xFFFFu), p * 8 + 2 * e);
+                    take_max(best, idx, bf(w[e] >> 16), p * 8 + 2 * e + 1);
+                }
             }
         }
     }
-    for (uint32_t i = (aligned ? pieces * 8 : 0) + threadIdx.x; i < n; i += kArgmaxThreads)
-        take_max(best, idx, bf(row[i]), i);
+    for (uint32_t i = pieces * 8 + threadIdx.x; i < n; i += kArgmaxThreads) take_max(best, idx, bf(row[i]), i);
     if (idx == 0xFFFFFFFFu) best = -INFINITY;
-    bv[threadIdx.x] = best;
-    bi[threadIdx.x] = idx;
-    __syncthreads();
-    for (uint32_t off = kArgmaxThreads / 2; off > 0; off >>= 1) {
-        if (threadIdx.x < off) {
-            const float ov = bv[threadIdx.x + off];
-            const uint32_t oi = bi[threadIdx.x + off];
-            if (ov > bv[threadIdx.x] || (ov == bv[threadIdx.x] && oi < bi[threadIdx.x])) {
-                bv[threadIdx.x] = ov;
-                bi[threadIdx.x] = oi;
-            }
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) {
+        const float ov = __shfl_xor(best, off, 64);
+        const uint32_t oi = __shfl_xor(idx, off, 64);
+        if (ov > best || (ov == best && oi < idx)) {
+            best = ov;
+            idx = oi;
         }
-        __syncthreads();
     }
-    if (threadIdx.x == 0) out[blockIdx.x] = bi[0] == 0xFFFFFFFFu ? 0u : bi[0];
+    const uint32_t wave = threadIdx.x >> 6;
+    if ((threadIdx.x & 63) == 0) {
+        bv[wave] = best;
+        bi[wave] = idx;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        for (int w = 1; w < kArgmaxThreads / 64; ++w)
+            if (bv[w] > best || (bv[w] == best && bi[w] < idx)) {
+                best = bv[w];
+                idx = bi[w];
+            }
+        out[blockIdx.x] = idx == 0xFFFFFFFFu ? 0u : idx;
+    }
 }
 
 // log[position - base] = token when that index is below capacity.

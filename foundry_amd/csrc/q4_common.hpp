@@ -20,10 +20,21 @@ __device__ __forceinline__ float bf16_to_f32(uint32_t bits16) {
 // f32 -> bf16, round to nearest with ties to even; a NaN keeps its top bits
 // and is made quiet (src/metal/kernels/common.metal:37-43). The same rule as
 // the reference so every materialised value, NaN included, is bit-identical.
+// gfx950's v_cvt_pk_bf16_f32 implements exactly this rule (checked on the
+// GPU against (b + 0x7FFF + ((b >> 16) & 1)) >> 16, with NaN -> (b >> 16) |
+// 0x40, for 4.2M inputs: every tie pattern of every upper half, denormals,
+// the largest finite values, infinities and NaN payloads), so the conversion
+// is one instruction.
+typedef __attribute__((ext_vector_type(2))) __bf16 fh_bf16x2_t;
+
 __device__ __forceinline__ uint32_t f32_to_bf16_rne(float v) {
-    const uint32_t b = __float_as_uint(v);
-    if (v != v) return (b >> 16) | 0x0040u;
-    return (b + 0x7FFFu + ((b >> 16) & 1u)) >> 16;
+    return __builtin_bit_cast(uint16_t, static_cast<__bf16>(v));
+}
+
+// Two values in one conversion: lo in bits 0..15, hi in 16..31.
+__device__ __forceinline__ uint32_t f32x2_to_bf16x2_rne(float lo, float hi) {
+    const fh_bf16x2_t v = {static_cast<__bf16>(lo), static_cast<__bf16>(hi)};
+    return __builtin_bit_cast(uint32_t, v);
 }
 
 // Dequantised weight in fp32: the product, rounded, then the sum, rounded.

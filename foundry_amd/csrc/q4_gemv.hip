@@ -5,11 +5,14 @@
 
 namespace fh {
 
-// Largest count of x rows whose staged copy fits the LDS budget at this k.
-uint32_t gemv_rows_per_launch(uint32_t k) {
+// Largest count of x rows whose staged copy fits the LDS budget at this k
+// (norm: the RMSNorm prologue also stages the k-wide norm weight).
+uint32_t gemv_rows_per_launch(uint32_t k, bool norm) {
     const uint32_t per_row = gemv_lds_bytes(1, k);
+    const uint32_t fixed = norm ? k * 2 : 0;
     if (per_row == 0) return 8;
-    uint32_t r = kGemvLdsLimit / per_row;
+    if (fixed >= kGemvLdsLimit) return 0;
+    uint32_t r = (kGemvLdsLimit - fixed) / per_row;
     return r > 8 ? 8 : r;
 }
 
@@ -25,11 +28,13 @@ constexpr GemvShape kGemvShapes[] = {FH_GEMV_SHAPES(FH_GEMV_SHAPE_ENTRY)};
 // at least 16 wavefronts per CU (less reduction work per output); for small n,
 // the most lanes per row (more, shorter wavefronts: a shorter compute tail).
 // Otherwise 64 lanes x 8 chunks, walking K in segments.
-static GemvShape pick_gemv_shape(uint32_t n, uint32_t k, uint32_t cus) {
+// max_lanes: the SiLU epilogue pairs rows inside a wavefront (at most 32
+// lanes per row).
+static GemvShape pick_gemv_shape(uint32_t n, uint32_t k, uint32_t cus, uint32_t max_lanes) {
     const uint32_t chunks = k / 32;
     const GemvShape *best = nullptr;
     for (const GemvShape &sh : kGemvShapes) {
-        if (chunks == 0 || chunks != sh.lanes * sh.cpl) continue;
+        if (chunks == 0 || chunks != sh.lanes * sh.cpl || sh.lanes > max_lanes) continue;
         const uint64_t waves = (static_cast<uint64_t>(n) * sh.lanes + 63) / 64;
         if (best == nullptr) {
             best = &sh;
@@ -42,30 +47,23 @@ static GemvShape pick_gemv_shape(uint32_t n, uint32_t k, uint32_t cus) {
     }
     if (best) return *best;
     if (chunks <= 32) return {16, 2};
-    return {64, 8};
+    return max_lanes >= 64 ? GemvShape{64, 8} : GemvShape{32, 8};
 }
 
 // Launches the GEMV for m in [1, 8] rows of x whose staged copy fits LDS;
 // the caller splits larger m (see gemv_rows_per_launch).
-void launch_q4_gemv(hipStream_t stream, uint32_t cus, int m, const uint16_t *x, uint32_t x_ld,
-                    const uint32_t *wq, const uint16_t *s, const uint16_t *b, uint32_t n,
-                    uint32_t k, void *y, uint32_t y_ld, int y_is_f32) {
-    const GemvShape sh = pick_gemv_shape(n, k, cus);
-#define FH_GEMV_M(MM)                                                                             \
-    case MM:                                                                                      \
-        launch_gemv_m<MM>(sh.lanes, sh.cpl, stream, cus, x, x_ld, wq, s, b, n, k, y, y_ld, y_is_f32); \
-        break;
+void launch_q4_gemv(hipStream_t stream, uint32_t cus, int m, const GemvArgs &a) {
+    const GemvShape sh = pick_gemv_shape(a.n, a.k, cus, a.epi == kEpiSiluMul ? 32 : 64);
     switch (m) {
-        FH_GEMV_M(1)
-        FH_GEMV_M(2)
-        FH_GEMV_M(3)
-        FH_GEMV_M(4)
-        FH_GEMV_M(5)
-        FH_GEMV_M(6)
-        FH_GEMV_M(7)
-        default: launch_gemv_m<8>(sh.lanes, sh.cpl, stream, cus, x, x_ld, wq, s, b, n, k, y, y_ld, y_is_f32);
+        case 1: launch_gemv_m<1>(sh.lanes, sh.cpl, stream, cus, a); break;
+        case 2: launch_gemv_m<2>(sh.lanes, sh.cpl, stream, cus, a); break;
+        case 3: launch_gemv_m<3>(sh.lanes, sh.cpl, stream, cus, a); break;
+        case 4: launch_gemv_m<4>(sh.lanes, sh.cpl, stream, cus, a); break;
+        case 5: launch_gemv_m<5>(sh.lanes, sh.cpl, stream, cus, a); break;
+        case 6: launch_gemv_m<6>(sh.lanes, sh.cpl, stream, cus, a); break;
+        case 7: launch_gemv_m<7>(sh.lanes, sh.cpl, stream, cus, a); break;
+        default: launch_gemv_m<8>(sh.lanes, sh.cpl, stream, cus, a);
     }
-#undef FH_GEMV_M
 }
 
 }  // namespace fh

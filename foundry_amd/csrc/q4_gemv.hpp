@@ -46,9 +46,56 @@ __device__ __forceinline__ float dot2_bf16(uint32_t a, uint32_t b, float c) {
                                            __builtin_bit_cast(bf16x2_t, b), c, false);
 }
 
-// Bytes of LDS the kernel needs for `m` rows of x with k columns.
-__host__ __device__ constexpr uint32_t gemv_lds_bytes(uint32_t m, uint32_t k) {
-    return m * (k / 32) * (4 * 16 + 4);
+// Bytes of LDS the kernel needs for `m` rows of x with k columns (plus the
+// staged norm weight with the RMSNorm prologue).
+__host__ __device__ constexpr uint32_t gemv_lds_bytes(uint32_t m, uint32_t k, bool norm = false) {
+    return m * (k / 32) * (4 * 16 + 4) + (norm ? k * 2 : 0);
+}
+
+// Decode-step fusions (the reference runs these as separate ops):
+//   PRO kProRmsNorm: the product's input is RmsNorm (src/nn/norm.rs:32-50) of
+//     h = x (+ res): h_j = RNE(x_j + res_j), x'_j = RNE(RNE(h_j * scale) *
+//     w_j), scale = 1 / sqrt(sum h^2 * (1/k) + eps); block 0 writes h to
+//     res_out. Work items are 8-value pieces spread over the whole block, and
+//     x, res and w are requested before the weights, so the prologue costs
+//     one block reduction on the block's critical path.
+//   EPI kEpiSiluMul: act(gate) * up of LlamaMlp (src/models/llama/mlp.rs:
+//     49-58) on the rows [gate (f) | up (f)] of the weight: a wavefront's row
+//     group holds gate rows in its first half and the matching up rows in its
+//     second, so after the reduction one shuffle brings u to g's lane, which
+//     writes RNE(RNE(g / (exp(-g) + 1)) * u) with g, u the bf16 outputs. The
+//     output has f columns (bf16).
+enum GemvPro { kProNone = 0, kProRmsNorm = 1 };
+enum GemvEpi { kEpiNone = 0, kEpiSiluMul = 1 };
+
+struct GemvFusion {
+    const uint16_t *res;  // kProRmsNorm: residual rows (stride k), or null
+    uint16_t *res_out;    // kProRmsNorm: h rows (stride k), or null; no overlap with x or res
+    const uint16_t *w;    // kProRmsNorm: norm weight [k]
+    float eps, dim_inv;
+};
+
+// A 16-byte piece (x0..x7) as the staged layout holds it: dwords (x0,x4)
+// (x1,x5) (x2,x6) (x3,x7), the bf16 pairs that nibbles (e, e+4) of a word meet.
+__device__ __forceinline__ uint4 gemv_permute(const uint4 v) {
+    uint4 p;
+    p.x = (v.x & 0xFFFFu) | (v.z << 16);
+    p.y = (v.x >> 16) | (v.z & 0xFFFF0000u);
+    p.z = (v.y & 0xFFFFu) | (v.w << 16);
+    p.w = (v.y >> 16) | (v.w & 0xFFFF0000u);
+    return p;
+}
+
+// f applied to matching bf16 values of two pieces, RNE'd back into a.
+template <typename F>
+__device__ __forceinline__ uint4 gemv_pairwise(const uint4 a, const uint4 b, F f) {
+    const uint32_t av[4] = {a.x, a.y, a.z, a.w}, bv[4] = {b.x, b.y, b.z, b.w};
+    uint32_t o[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+        o[e] = f32x2_to_bf16x2_rne(f(bf16_to_f32(av[e] & 0xFFFFu), bf16_to_f32(bv[e] & 0xFFFFu)),
+                                   f(bf16_to_f32(av[e] >> 16), bf16_to_f32(bv[e] >> 16)));
+    return make_uint4(o[0], o[1], o[2], o[3]);
 }
 
 // One lane's chunks of one row group: packed words and the group scale/bias.
@@ -60,12 +107,16 @@ struct GemvChunks {
 
 // FULL: every lane's CPL chunks exist (k is a multiple of 32*CPL*L), so the
 // loads need no per-chunk guard and share one address with immediate offsets.
-template <int M, int L, int CPL, bool FULL>
+template <int M, int L, int CPL, bool FULL, int PRO, int EPI>
 __global__ __launch_bounds__(kGemvThreads) void q4_gemv_kernel(
     const uint16_t *__restrict__ x, uint32_t x_ld, const uint32_t *__restrict__ wq,
     const uint16_t *__restrict__ scales, const uint16_t *__restrict__ biases, uint32_t n,
-    uint32_t k, void *__restrict__ y, uint32_t y_ld, int y_is_f32) {
+    uint32_t k, void *__restrict__ y, uint32_t y_ld, int y_is_f32, GemvFusion fu) {
     constexpr uint32_t kRowsPerWave = 64 / L;
+    static_assert(EPI == kEpiNone || kRowsPerWave >= 2, "the SiLU epilogue pairs rows within a wavefront");
+    // rows of one wavefront that produce outputs: with kEpiSiluMul, gate rows
+    // (the other half are their up rows)
+    constexpr uint32_t kOutRowsPerWave = EPI == kEpiSiluMul ? kRowsPerWave / 2 : kRowsPerWave;
     extern __shared__ uint4 lds[];
     const uint32_t chunks = k / 32;
     uint4 *xs = lds;                                                // [M][4][chunks]
@@ -76,13 +127,25 @@ __global__ __launch_bounds__(kGemvThreads) void q4_gemv_kernel(
     const uint32_t sub = lane % L;
     const uint32_t seg_chunks = CPL * L;
     const uint32_t segs = FULL ? chunks / seg_chunks : (chunks == 0 ? 1 : (chunks + seg_chunks - 1) / seg_chunks);
-    const uint32_t groups_total = (n + kRowsPerWave - 1) / kRowsPerWave;
+    const uint32_t n_out = EPI == kEpiSiluMul ? n / 2 : n;  // output columns
+    const uint32_t groups_total = (n_out + kOutRowsPerWave - 1) / kOutRowsPerWave;
     const uint32_t group_first = blockIdx.x * kGemvWaves + wave;
     const uint32_t group_stride = gridDim.x * kGemvWaves;
+    // output column of this lane's row in a row group, and its weight row
+    const uint32_t rl = lane / L;
+    auto out_col = [&](uint32_t group) {
+        return group * kOutRowsPerWave + (EPI == kEpiSiluMul ? rl % kOutRowsPerWave : rl);
+    };
+    auto weight_row = [&](uint32_t group) {
+        const uint32_t col = out_col(group);
+        return EPI == kEpiSiluMul && rl >= kOutRowsPerWave ? col + n_out : col;
+    };
+    const bool out_lane = EPI == kEpiSiluMul ? rl < kOutRowsPerWave : true;
 
     auto load = [&](uint32_t group, uint32_t seg, GemvChunks<CPL> &buf) {
-        const uint32_t row = group * kRowsPerWave + lane / L;
-        const uint64_t row_c = row < n ? row : n - 1;  // clamped rows load, never store
+        const uint32_t row = weight_row(group);
+        const bool in = out_col(group) < n_out;
+        const uint64_t row_c = in ? row : n - 1;  // clamped rows load, never store
         const uint32_t c0 = seg * seg_chunks + sub;
         const uint4 *wrow = reinterpret_cast<const uint4 *>(wq + row_c * (k / 8)) + c0;
         const uint16_t *srow = scales + row_c * (k / kGroup);
@@ -127,15 +190,114 @@ __global__ __launch_bounds__(kGemvThreads) void q4_gemv_kernel(
         for (int wi = 0; wi < 4; ++wi) v[wi] = src[wi];
     };
 
-    const uint32_t items_x = M * chunks;
-    uint4 xv[4];
-    if (threadIdx.x < items_x) load_x(threadIdx.x, xv);
     GemvChunks<CPL> buf;
-    if (group_first < groups_total) load(group_first, 0, buf);
-    if (threadIdx.x < items_x) stage(threadIdx.x, xv);
-    for (uint32_t t = threadIdx.x + kGemvThreads; t < items_x; t += kGemvThreads) {
-        load_x(t, xv);
-        stage(t, xv);
+    if constexpr (PRO == kProRmsNorm) {
+        // Pieces of 8 values, piece t = (m * chunks + c) * 4 + wi: 4 adjacent
+        // lanes hold a chunk. Pass 1: h = x (+ res) staged (permuted) and sum
+        // of squares per row; the norm weight staged beside it. Reduction.
+        // Pass 2 in LDS: x' = RNE(RNE(h * scale) * w) and the chunk sums.
+        uint4 *wsh = reinterpret_cast<uint4 *>(xsum + M * chunks);  // [4][chunks] norm weight
+        __shared__ float red[kGemvWaves][M];
+        const uint32_t pieces = M * chunks * 4;
+        auto xoff = [&](uint32_t t) {
+            const uint32_t m = t / (chunks * 4), r = t % (chunks * 4);
+            return static_cast<uint64_t>(m) * k + r * 8;
+        };
+        float ss[M];
+#pragma unroll
+        for (int m = 0; m < M; ++m) ss[m] = 0.f;
+        // a round's pieces load while the previous round is processed; past
+        // the end, addresses are clamped to piece 0 and the values unused
+        auto load_round = [&](uint32_t t0, uint4 &xv, uint4 &rv, uint4 &wv) {
+            const uint32_t t = t0 + threadIdx.x;
+            const uint64_t o = xoff(t < pieces ? t : 0);
+            xv = *reinterpret_cast<const uint4 *>(x + o);
+            rv = fu.res ? *reinterpret_cast<const uint4 *>(fu.res + o) : make_uint4(0u, 0u, 0u, 0u);
+            wv = *reinterpret_cast<const uint4 *>(fu.w + (t < chunks * 4 ? t : 0) * 8);
+        };
+        uint4 xv, rv, wv;
+        load_round(0, xv, rv, wv);
+        if (group_first < groups_total) load(group_first, 0, buf);
+        for (uint32_t t0 = 0; t0 < pieces; t0 += kGemvThreads) {
+            const uint32_t t = t0 + threadIdx.x;
+            const bool live = t < pieces;
+            const uint64_t o = xoff(live ? t : 0);
+            const bool wpiece = t < chunks * 4;
+            const bool more = t0 + kGemvThreads < pieces;
+            uint4 xn, rn, wn;
+            if (more) load_round(t0 + kGemvThreads, xn, rn, wn);
+            if (fu.res) {
+                xv = gemv_pairwise(xv, rv, [](float a, float b) { return a + b; });
+                if (blockIdx.x == 0 && fu.res_out && live) *reinterpret_cast<uint4 *>(fu.res_out + o) = xv;
+            }
+            if (live) {
+                const uint32_t hv[4] = {xv.x, xv.y, xv.z, xv.w};
+                float sq = 0.f;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const float lo = bf16_to_f32(hv[e] & 0xFFFFu), hi = bf16_to_f32(hv[e] >> 16);
+                    sq += lo * lo;
+                    sq += hi * hi;
+                }
+                const uint32_t m = t / (chunks * 4), c = (t / 4) % chunks, wi = t % 4;
+#pragma unroll
+                for (int mm = 0; mm < M; ++mm)
+                    if (mm == static_cast<int>(m)) ss[mm] += sq;
+                xs[(m * 4 + wi) * chunks + c] = gemv_permute(xv);
+                if (wpiece) wsh[wi * chunks + c] = gemv_permute(wv);
+            }
+            if (more) {
+                xv = xn;
+                rv = rn;
+                wv = wn;
+            }
+        }
+        {
+            const uint32_t lane_x = threadIdx.x & 63, wave_x = threadIdx.x >> 6;
+#pragma unroll
+            for (int m = 0; m < M; ++m) {
+                float v = ss[m];
+#pragma unroll
+                for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
+                if (lane_x == 0) red[wave_x][m] = v;
+            }
+        }
+        __syncthreads();
+        for (uint32_t t0 = 0; t0 < pieces; t0 += kGemvThreads) {
+            const uint32_t t = t0 + threadIdx.x;
+            const bool live = t < pieces;
+            const uint32_t m = live ? t / (chunks * 4) : 0, c = (t / 4) % chunks, wi = t % 4;
+            float tot = 0.f;
+#pragma unroll
+            for (int w = 0; w < kGemvWaves; ++w) tot += red[w][m];
+            const float scale = 1.0f / sqrtf(tot * fu.dim_inv + fu.eps);
+            float psum = 0.f;
+            if (live) {
+                const uint4 p = gemv_pairwise(xs[(m * 4 + wi) * chunks + c], wsh[wi * chunks + c],
+                                              [scale](float h, float g) {
+                                                  return bf16_to_f32(f32_to_bf16_rne(h * scale)) * g;
+                                              });
+                xs[(m * 4 + wi) * chunks + c] = p;
+                // (x0+x1) + (x2+x3) + (x4+x5) + (x6+x7) of the piece
+                psum = ((bf16_to_f32(p.x & 0xFFFFu) + bf16_to_f32(p.y & 0xFFFFu)) +
+                        (bf16_to_f32(p.z & 0xFFFFu) + bf16_to_f32(p.w & 0xFFFFu))) +
+                       ((bf16_to_f32(p.x >> 16) + bf16_to_f32(p.y >> 16)) +
+                        (bf16_to_f32(p.z >> 16) + bf16_to_f32(p.w >> 16)));
+            }
+            psum += __shfl_xor(psum, 1, 64);
+            psum += __shfl_xor(psum, 2, 64);
+            if (live && wi == 0) xsum[m * chunks + c] = psum;
+        }
+    } else {
+        const uint32_t items_x = M * chunks;
+        uint4 xv[4];
+        if (threadIdx.x < items_x) load_x(threadIdx.x, xv);
+        if (group_first < groups_total) load(group_first, 0, buf);
+        if (threadIdx.x < items_x) stage(threadIdx.x, xv);
+        for (uint32_t t = threadIdx.x + kGemvThreads; t < items_x; t += kGemvThreads) {
+            load_x(t, xv);
+            stage(t, xv);
+        }
     }
     __syncthreads();
 
@@ -191,11 +353,21 @@ __global__ __launch_bounds__(kGemvThreads) void q4_gemv_kernel(
             for (int off = L / 2; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
             acc[m] = v;
         }
-        const uint32_t row = group * kRowsPerWave + lane / L;
-        if (row < n && sub == 0) {
+        if constexpr (EPI == kEpiSiluMul) {
+            // the up row's sum, from the lane kOutRowsPerWave rows further on
 #pragma unroll
             for (int m = 0; m < M; ++m) {
-                const uint64_t o = static_cast<uint64_t>(m) * y_ld + row;
+                const float u = __shfl_down(acc[m], kOutRowsPerWave * L, 64);
+                const float g = bf16_to_f32(f32_to_bf16_rne(acc[m]));
+                const float ub = bf16_to_f32(f32_to_bf16_rne(u));
+                acc[m] = bf16_to_f32(f32_to_bf16_rne(g / (expf(-g) + 1.0f))) * ub;
+            }
+        }
+        const uint32_t col = out_col(group);
+        if (out_lane && col < n_out && sub == 0) {
+#pragma unroll
+            for (int m = 0; m < M; ++m) {
+                const uint64_t o = static_cast<uint64_t>(m) * y_ld + col;
                 if (y_is_f32)
                     static_cast<float *>(y)[o] = acc[m];
                 else
@@ -217,30 +389,59 @@ inline uint32_t resident_blocks(Kernel kernel, uint32_t lds) {
     return per_cu < static_cast<int>(kGemvBlocksPerCu) ? per_cu : kGemvBlocksPerCu;
 }
 
-template <int M, int L, int CPL, bool FULL>
-inline void launch_gemv_full(hipStream_t stream, uint32_t cus, const uint16_t *x, uint32_t x_ld,
-                             const uint32_t *wq, const uint16_t *s, const uint16_t *b, uint32_t n,
-                             uint32_t k, void *y, uint32_t y_ld, int y_is_f32) {
+// Everything one GEMV launch needs besides its template shape.
+struct GemvArgs {
+    const uint16_t *x;
+    uint32_t x_ld;
+    const uint32_t *wq;
+    const uint16_t *s, *b;
+    uint32_t n, k;  // weight rows (with kEpiSiluMul: 2f), columns
+    void *y;
+    uint32_t y_ld;
+    int y_is_f32;
+    int pro, epi;
+    GemvFusion fu;
+};
+
+template <int M, int L, int CPL, bool FULL, int PRO, int EPI>
+inline void launch_gemv_full(hipStream_t stream, uint32_t cus, const GemvArgs &a) {
     constexpr uint32_t kRowsPerWave = 64 / L;
-    auto kernel = q4_gemv_kernel<M, L, CPL, FULL>;
-    const uint32_t lds = gemv_lds_bytes(M, k);
-    const uint32_t groups = (n + kRowsPerWave - 1) / kRowsPerWave;
+    constexpr uint32_t kOutRows = EPI == kEpiSiluMul ? kRowsPerWave / 2 : kRowsPerWave;
+    auto kernel = q4_gemv_kernel<M, L, CPL, FULL, PRO, EPI>;
+    const uint32_t lds = gemv_lds_bytes(M, a.k, PRO == kProRmsNorm);
+    const uint32_t n_out = EPI == kEpiSiluMul ? a.n / 2 : a.n;
+    const uint32_t groups = (n_out + kOutRows - 1) / kOutRows;
     const uint32_t need = (groups + kGemvWaves - 1) / kGemvWaves;
     const uint32_t cap = cus * resident_blocks(kernel, lds);
     const uint32_t blocks = need < cap ? need : cap;
-    hipLaunchKernelGGL(kernel, dim3(blocks), dim3(kGemvThreads), lds, stream, x, x_ld, wq, s, b, n,
-                       k, y, y_ld, y_is_f32);
+    hipLaunchKernelGGL(kernel, dim3(blocks), dim3(kGemvThreads), lds, stream, a.x, a.x_ld, a.wq, a.s, a.b, a.n,
+                       a.k, a.y, a.y_ld, a.y_is_f32, a.fu);
+}
+
+template <int M, int L, int CPL, int PRO, int EPI>
+inline void launch_gemv_fused(hipStream_t stream, uint32_t cus, const GemvArgs &a) {
+    const uint32_t chunks = a.k / 32;
+    if (chunks > 0 && chunks % (CPL * L) == 0)
+        launch_gemv_full<M, L, CPL, true, PRO, EPI>(stream, cus, a);
+    else
+        launch_gemv_full<M, L, CPL, false, PRO, EPI>(stream, cus, a);
 }
 
 template <int M, int L, int CPL>
-inline void launch_gemv_mlc(hipStream_t stream, uint32_t cus, const uint16_t *x, uint32_t x_ld,
-                            const uint32_t *wq, const uint16_t *s, const uint16_t *b, uint32_t n,
-                            uint32_t k, void *y, uint32_t y_ld, int y_is_f32) {
-    const uint32_t chunks = k / 32;
-    if (chunks > 0 && chunks % (CPL * L) == 0)
-        launch_gemv_full<M, L, CPL, true>(stream, cus, x, x_ld, wq, s, b, n, k, y, y_ld, y_is_f32);
+inline void launch_gemv_mlc(hipStream_t stream, uint32_t cus, const GemvArgs &a) {
+    if constexpr (L <= 32) {  // the SiLU epilogue needs two rows per wavefront
+        if (a.epi == kEpiSiluMul) {
+            if (a.pro == kProRmsNorm)
+                launch_gemv_fused<M, L, CPL, kProRmsNorm, kEpiSiluMul>(stream, cus, a);
+            else
+                launch_gemv_fused<M, L, CPL, kProNone, kEpiSiluMul>(stream, cus, a);
+            return;
+        }
+    }
+    if (a.pro == kProRmsNorm)
+        launch_gemv_fused<M, L, CPL, kProRmsNorm, kEpiNone>(stream, cus, a);
     else
-        launch_gemv_full<M, L, CPL, false>(stream, cus, x, x_ld, wq, s, b, n, k, y, y_ld, y_is_f32);
+        launch_gemv_fused<M, L, CPL, kProNone, kEpiNone>(stream, cus, a);
 }
 
 // (lanes per row, chunks per lane) shapes the kernels are built for; X lists
@@ -250,9 +451,6 @@ inline void launch_gemv_mlc(hipStream_t stream, uint32_t cus, const uint16_t *x,
 
 // Defined in q4_gemv_m<M>.hip: launches the M-row GEMV with the given shape.
 template <int M>
-void launch_gemv_m(uint32_t lanes, uint32_t cpl, hipStream_t stream, uint32_t cus,
-                   const uint16_t *x, uint32_t x_ld, const uint32_t *wq, const uint16_t *s,
-                   const uint16_t *b, uint32_t n, uint32_t k, void *y, uint32_t y_ld,
-                   int y_is_f32);
+void launch_gemv_m(uint32_t lanes, uint32_t cpl, hipStream_t stream, uint32_t cus, const GemvArgs &a);
 
 }  // namespace fh

@@ -4,24 +4,40 @@
 // (src/nn/primitive.rs:234-256 for the shape rule), then pick the kernel. The
 // reference has one tiled kernel for every shape; here m <= 8 goes to the
 // decode GEMV and larger m to the MFMA GEMM.
-#include "device.hpp"
-#include "q4_common.hpp"
+#include "q4_gemv.hpp"
 
 namespace fh {
 
 int check_q4_table(const fh_device *dev, const char *fn, const uint32_t *wq,
                    const uint16_t *scales, const uint16_t *biases, int64_t rows, int64_t k,
                    int64_t group);
-void launch_q4_gemv(hipStream_t stream, uint32_t cus, int m, const uint16_t *x, uint32_t x_ld,
-                    const uint32_t *wq, const uint16_t *s, const uint16_t *b, uint32_t n,
-                    uint32_t k, void *y, uint32_t y_ld, int y_is_f32);
-uint32_t gemv_rows_per_launch(uint32_t k);
+void launch_q4_gemv(hipStream_t stream, uint32_t cus, int m, const GemvArgs &a);
+uint32_t gemv_rows_per_launch(uint32_t k, bool norm);
 void launch_q4_gemm(hipStream_t stream, const uint16_t *x, uint32_t x_ld, const uint32_t *wq,
                     const uint16_t *s, const uint16_t *b, uint32_t m, uint32_t n, uint32_t k,
                     void *y, int y_is_f32);
 
 // Row counts up to this go to the GEMV.
 constexpr int64_t kGemvMaxRows = 8;
+
+// Launches the GEMV over m rows in groups whose staged x fits LDS (every
+// prologue and epilogue is row-independent); x, res, res_out and y advance
+// by their row strides. y_cols: columns of y per row.
+int launch_gemv_rows(fh_device *dev, const char *fn, int64_t m, const GemvArgs &base, int64_t y_cols) {
+    const int64_t per = gemv_rows_per_launch(base.k, base.pro == kProRmsNorm);
+    for (int64_t r0 = 0; r0 < m; r0 += per) {
+        const int rows = static_cast<int>(m - r0 < per ? m - r0 : per);
+        GemvArgs a = base;
+        a.x += r0 * base.x_ld;
+        if (a.fu.res) a.fu.res += r0 * base.k;
+        if (a.fu.res_out) a.fu.res_out += r0 * base.k;
+        a.y = base.y_is_f32 ? static_cast<void *>(static_cast<float *>(base.y) + r0 * y_cols)
+                            : static_cast<void *>(static_cast<uint16_t *>(base.y) + r0 * y_cols);
+        int rc = dispatch(dev, fn, [&] { launch_q4_gemv(dev->stream, dev->compute_units, rows, a); });
+        if (rc) return rc;
+    }
+    return FH_OK;
+}
 
 }  // namespace fh
 
@@ -58,26 +74,110 @@ extern "C" int fh_q4_matmul(fh_device *dev, const uint16_t *x, int64_t m, int64_
     const uint32_t k32 = static_cast<uint32_t>(k), n32 = static_cast<uint32_t>(n);
     const uint32_t ld32 = static_cast<uint32_t>(x_ld);
     if (m <= kGemvMaxRows) {
-        // x rows whose staged copy fits LDS go in one launch; the rest follow
-        const int64_t per = gemv_rows_per_launch(k32);
-        if (per < 1)
+        if (gemv_rows_per_launch(k32, false) < 1)
             return fail(FH_ERR_UNSUPPORTED, "%s: k=%lld is too large for the GEMV's LDS stage", fn,
                         (long long)k);
-        for (int64_t r0 = 0; r0 < m; r0 += per) {
-            const int rows = static_cast<int>(m - r0 < per ? m - r0 : per);
-            const uint16_t *xr = x + r0 * x_ld;
-            void *yr = y_is_f32 ? static_cast<void *>(static_cast<float *>(y) + r0 * n)
-                                : static_cast<void *>(static_cast<uint16_t *>(y) + r0 * n);
-            int rc = dispatch(dev, fn, [&] {
-                launch_q4_gemv(dev->stream, dev->compute_units, rows, xr, ld32, wq, scales, biases, n32, k32, yr, n32,
-                               y_is_f32);
-            });
-            if (rc) return rc;
-        }
-        return FH_OK;
+        GemvArgs a{x, ld32, wq, scales, biases, n32, k32, y, n32, y_is_f32, kProNone, kEpiNone, GemvFusion{}};
+        return launch_gemv_rows(dev, fn, m, a, n);
     }
     return dispatch(dev, fn, [&] {
         launch_q4_gemm(dev->stream, x, ld32, wq, scales, biases, static_cast<uint32_t>(m), n32,
                        k32, y, y_is_f32);
     });
+}
+
+namespace {
+
+// Checks shared by the fused decode entry points: the q4 table, at most
+// kGemvMaxRows rows, y's dtype, alignment and range (y_cols columns).
+int check_fused(fh_device *dev, const char *fn, int64_t m, int64_t k, const uint32_t *wq, const uint16_t *scales,
+                const uint16_t *biases, int64_t n, int64_t group, void *y, int y_dtype, int64_t y_cols, bool norm) {
+    if (int rc = check_usable(dev, fn)) return rc;
+    if (int rc = check_q4_table(dev, fn, wq, scales, biases, n, k, group)) return rc;
+    if (m < 0) return fail(FH_ERR_INVALID_ARGUMENT, "%s: m=%lld", fn, (long long)m);
+    if (m > kGemvMaxRows)
+        return fail(FH_ERR_UNSUPPORTED, "%s: %lld rows; the fused GEMV takes at most %lld, use the unfused ops", fn,
+                    (long long)m, (long long)kGemvMaxRows);
+    if (gemv_rows_per_launch(static_cast<uint32_t>(k), norm) < 1)
+        return fail(FH_ERR_UNSUPPORTED, "%s: k=%lld is too large for the GEMV's LDS stage", fn, (long long)k);
+    if (y_dtype != FH_BF16 && y_dtype != FH_F32)
+        return fail(FH_ERR_DTYPE, "%s: y_dtype must be FH_BF16 or FH_F32", fn);
+    if (reinterpret_cast<uintptr_t>(y) % (y_dtype == FH_F32 ? 4 : 2) != 0)
+        return fail(FH_ERR_INVALID_ARGUMENT, "%s: y is misaligned for its dtype", fn);
+    if (m == 0 || y_cols == 0) return FH_OK;
+    return check_range(dev, y, static_cast<uint64_t>(m) * y_cols * (y_dtype == FH_F32 ? 4 : 2), fn, "y");
+}
+
+bool overlaps(const void *a, uint64_t na, const void *b, uint64_t nb) {
+    const auto pa = reinterpret_cast<uintptr_t>(a), pb = reinterpret_cast<uintptr_t>(b);
+    return a && b && pa < pb + nb && pb < pa + na;
+}
+
+}  // namespace
+
+namespace {
+
+// Validates the RMSNorm prologue's operands (norm_weight null: no norm).
+int check_norm_operands(fh_device *dev, const char *fn, const uint16_t *x, const uint16_t *residual,
+                        const uint16_t *residual_out, const uint16_t *norm_weight, int64_t m, int64_t k) {
+    if (!norm_weight && (residual || residual_out))
+        return fail(FH_ERR_INVALID_ARGUMENT, "%s: a residual without a norm weight", fn);
+    if (residual_out && !residual)
+        return fail(FH_ERR_INVALID_ARGUMENT, "%s: residual_out without residual", fn);
+    for (const void *p : {static_cast<const void *>(x), static_cast<const void *>(residual),
+                          static_cast<const void *>(residual_out), static_cast<const void *>(norm_weight)})
+        if (reinterpret_cast<uintptr_t>(p) % 16 != 0)
+            return fail(FH_ERR_INVALID_ARGUMENT, "%s: x, residual, residual_out and the weight must be 16-byte aligned",
+                        fn);
+    if (m == 0) return FH_OK;
+    const uint64_t rows_bytes = static_cast<uint64_t>(m) * k * 2;
+    if (int rc = check_range(dev, x, rows_bytes, fn, "x")) return rc;
+    if (norm_weight) {
+        if (int rc = check_range(dev, norm_weight, static_cast<uint64_t>(k) * 2, fn, "norm_weight")) return rc;
+    }
+    if (residual) {
+        if (int rc = check_range(dev, residual, rows_bytes, fn, "residual")) return rc;
+    }
+    if (residual_out) {
+        if (int rc = check_range(dev, residual_out, rows_bytes, fn, "residual_out")) return rc;
+        // block 0 writes h while every block reads x and the residual
+        if (overlaps(residual_out, rows_bytes, x, rows_bytes) || overlaps(residual_out, rows_bytes, residual, rows_bytes))
+            return fail(FH_ERR_INVALID_ARGUMENT, "%s: residual_out overlaps x or residual", fn);
+    }
+    return FH_OK;
+}
+
+}  // namespace
+
+extern "C" int fh_q4_matmul_rmsnorm(fh_device *dev, const uint16_t *x, const uint16_t *residual,
+                                    uint16_t *residual_out, const uint16_t *norm_weight, float eps, int64_t m,
+                                    int64_t k, const uint32_t *wq, const uint16_t *scales,
+                                    const uint16_t *biases, int64_t n, int64_t group, void *y, int y_dtype) {
+    const char *fn = "fh_q4_matmul_rmsnorm";
+    if (int rc = check_fused(dev, fn, m, k, wq, scales, biases, n, group, y, y_dtype, n, true)) return rc;
+    if (!norm_weight) return fail(FH_ERR_INVALID_ARGUMENT, "%s: null norm weight", fn);
+    if (int rc = check_norm_operands(dev, fn, x, residual, residual_out, norm_weight, m, k)) return rc;
+    if (m == 0 || n == 0) return FH_OK;
+    if (int rc = set_current(dev, fn)) return rc;
+    const uint32_t k32 = static_cast<uint32_t>(k), n32 = static_cast<uint32_t>(n);
+    const GemvArgs a{x, k32, wq, scales, biases, n32, k32, y, n32, y_dtype == FH_F32, kProRmsNorm, kEpiNone,
+                     GemvFusion{residual, residual_out, norm_weight, eps, 1.0f / static_cast<float>(k)}};
+    return launch_gemv_rows(dev, fn, m, a, n);
+}
+
+extern "C" int fh_q4_gate_up_silu(fh_device *dev, const uint16_t *x, const uint16_t *residual,
+                                  uint16_t *residual_out, const uint16_t *norm_weight, float eps, int64_t m,
+                                  int64_t k, const uint32_t *wq, const uint16_t *scales, const uint16_t *biases,
+                                  int64_t n, int64_t group, uint16_t *act) {
+    const char *fn = "fh_q4_gate_up_silu";
+    if (n % 2 != 0) return fail(FH_ERR_INVALID_ARGUMENT, "%s: n=%lld is not [gate; up] rows", fn, (long long)n);
+    const bool norm = norm_weight != nullptr;
+    if (int rc = check_fused(dev, fn, m, k, wq, scales, biases, n, group, act, FH_BF16, n / 2, norm)) return rc;
+    if (int rc = check_norm_operands(dev, fn, x, residual, residual_out, norm_weight, m, k)) return rc;
+    if (m == 0 || n == 0) return FH_OK;
+    if (int rc = set_current(dev, fn)) return rc;
+    const uint32_t k32 = static_cast<uint32_t>(k), n32 = static_cast<uint32_t>(n);
+    const GemvArgs a{x, k32, wq, scales, biases, n32, k32, act, n32 / 2, 0, norm ? kProRmsNorm : kProNone,
+                     kEpiSiluMul, GemvFusion{residual, residual_out, norm_weight, eps, 1.0f / static_cast<float>(k)}};
+    return launch_gemv_rows(dev, fn, m, a, n / 2);
 }

@@ -16,7 +16,11 @@ greedy driver (src/generate/mod.rs:45-204):
 Fusions that keep each output row's arithmetic unchanged:
 - q/k/v and gate/up weights are concatenated along N (each output row of a
   linear depends only on its own weight row);
-- each residual add is fused into the RMSNorm that follows it.
+- each residual add is fused into the RMSNorm that follows it;
+- up to 8 rows (decode), each RMSNorm is formed inside the GEMV that consumes
+  it (fh_q4_matmul_rmsnorm, the residual stream alternating between two
+  buffers), SiLU*up inside the gate/up GEMV (fh_q4_gate_up_silu), and one
+  new token's RoPE and cache write inside attention (fh_decode_attention).
 
 The decode step reads its token id and position from device memory, so it is
 captured once as a HIP graph and replayed for every generated token. Weights
@@ -187,6 +191,7 @@ class Q4Llama:
         t, c = self.max_tokens, cfg
         self.buf = {
             "h": dev.empty(t * c.hidden * 2),
+            "h2": dev.empty(t * c.hidden * 2),
             "x": dev.empty(t * c.hidden * 2),
             "qkv": dev.empty(t * c.qkv_rows * 2),
             "q": dev.empty(t * c.n_heads * c.head_dim * 2),
@@ -213,15 +218,31 @@ class Q4Llama:
         _lib.call("fh_q4_matmul", self.dev.handle, self._p(x, x_off), rows, w.k, w.k, self._p(w.wq),
                   self._p(w.s), self._p(w.b), w.n, GROUP, self._p(y), _lib.BF16)
 
+    def _linear_norm(self, x: HipStorage, res, res_out, weight: HipStorage, rows: int, w: _Q4, y: HipStorage,
+                     off: int = 0):
+        """y = rms_norm(x [+ res]) W^T in one GEMV (res_out <- x + res)."""
+        _lib.call("fh_q4_matmul_rmsnorm", self.dev.handle, self._p(x, off),
+                  None if res is None else self._p(res, off), None if res_out is None else self._p(res_out, off),
+                  self._p(weight), ctypes.c_float(self.cfg.rms_norm_eps), rows, w.k, self._p(w.wq), self._p(w.s),
+                  self._p(w.b), w.n, GROUP, self._p(y), _lib.BF16)
+
     def _forward(self, tokens: int, ids: HipStorage, positions: HipStorage):
         """One forward over `tokens` rows; leaves the next id in buf['next']."""
         c, d, b = self.cfg, self.dev.handle, self.buf
         _lib.call("fh_q4_embed", d, self._p(self.embed.wq), self._p(self.embed.s), self._p(self.embed.b),
                   c.vocab, c.hidden, GROUP, self._p(ids), tokens, self._p(b["h"]))
+        fused = tokens <= 8  # GEMV rows: the norms and SiLU go inside the linears
+        h, h_alt = b["h"], b["h2"]
         pending = None  # output of the previous block still to be added to h
         for L in self.layers:
-            self._norm(tokens, pending, L["input_norm"])
-            self._linear(b["x"], tokens, L["qkv"], b["qkv"])
+            if not fused:
+                self._norm(tokens, pending, L["input_norm"])
+                self._linear(b["x"], tokens, L["qkv"], b["qkv"])
+            elif pending is None:
+                self._linear_norm(h, None, None, L["input_norm"], tokens, L["qkv"], b["qkv"])
+            else:
+                self._linear_norm(pending, h, h_alt, L["input_norm"], tokens, L["qkv"], b["qkv"])
+                h, h_alt = h_alt, h
             if tokens == 1:
                 # one new token: RoPE and the cache write fused into attention
                 _lib.call("fh_decode_attention", d, self._p(b["qkv"]), 1, c.n_heads, c.n_kv_heads, c.head_dim,
@@ -237,14 +258,25 @@ class Q4Llama:
                           ctypes.c_float(self.scale), self._p(self.attn_ws), self.attn_ws_bytes,
                           self._p(b["attn"]))
             self._linear(b["attn"], tokens, L["o"], b["o"])
-            self._norm(tokens, b["o"], L["post_norm"])
-            self._linear(b["x"], tokens, L["gate_up"], b["gu"])
-            _lib.call("fh_silu_mul", d, self._p(b["gu"]), tokens, c.ffn, self._p(b["act"]))
+            if fused:
+                # act = silu_mul(rms_norm(o + h) [Wgate; Wup]^T) in one GEMV
+                w = L["gate_up"]
+                _lib.call("fh_q4_gate_up_silu", d, self._p(b["o"]), self._p(h), self._p(h_alt), self._p(L["post_norm"]),
+                          ctypes.c_float(c.rms_norm_eps), tokens, w.k, self._p(w.wq), self._p(w.s), self._p(w.b), w.n,
+                          GROUP, self._p(b["act"]))
+                h, h_alt = h_alt, h
+            else:
+                self._norm(tokens, b["o"], L["post_norm"])
+                self._linear(b["x"], tokens, L["gate_up"], b["gu"])
+                _lib.call("fh_silu_mul", d, self._p(b["gu"]), tokens, c.ffn, self._p(b["act"]))
             self._linear(b["act"], tokens, L["down"], b["o"])
             pending = b["o"]
-        self._norm(tokens, pending, self.final_norm)
         last = (tokens - 1) * c.hidden * 2
-        self._linear(b["x"], 1, self.embed, b["logits"], x_off=last)
+        if fused:
+            self._linear_norm(pending, h, None, self.final_norm, 1, self.embed, b["logits"], off=last)
+        else:
+            self._norm(tokens, pending, self.final_norm)
+            self._linear(b["x"], 1, self.embed, b["logits"], x_off=last)
         _lib.call("fh_argmax", d, self._p(b["logits"]), 1, c.vocab, self._p(b["next"]))
 
     def _norm(self, tokens: int, pending, weight: HipStorage):

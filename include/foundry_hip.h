@@ -254,6 +254,30 @@ int fh_decode_attention(fh_device *dev, const uint16_t *qkv, int64_t batch, int6
                         uint16_t *k_cache, uint16_t *v_cache, int64_t max_len, float scale,
                         void *workspace, uint64_t workspace_bytes, uint16_t *out);
 
+/* Decode-step fusions of the q4 Linear (m <= 8 rows, the GEMV; larger m
+ * returns FH_ERR_UNSUPPORTED -- use the unfused ops). Same arithmetic as the
+ * unfused sequence, with no intermediate tensor in memory:
+ *   fh_q4_matmul_rmsnorm: y = fh_rms_norm(x, residual, residual_out,
+ *     norm_weight, eps) @ W^T (src/nn/norm.rs:32-50 then src/nn/linear.rs:
+ *     22-35). x, residual, residual_out: [m, k] (row stride k); residual and
+ *     residual_out may be null; residual_out (the updated residual stream h)
+ *     must not overlap x or residual. The sum of squares runs in another
+ *     order than fh_rms_norm's (a normalised value can differ by one bf16 ulp).
+ *   fh_q4_gate_up_silu: act = fh_silu_mul(x' @ W^T) for W = [gate; up] rows
+ *     (n = 2f): act[:, j] = RNE(RNE(g_j / (exp(-g_j) + 1)) * u_j) with g, u
+ *     the bf16 outputs of the linear (src/models/llama/mlp.rs:49-58); act:
+ *     [m, f] bf16. x' = x, or with norm_weight, the RMSNorm above (residual
+ *     arguments as for fh_q4_matmul_rmsnorm).
+ * The q4 operands follow fh_q4_matmul (group 64); x 16-byte aligned. */
+int fh_q4_matmul_rmsnorm(fh_device *dev, const uint16_t *x, const uint16_t *residual,
+                         uint16_t *residual_out, const uint16_t *norm_weight, float eps, int64_t m,
+                         int64_t k, const uint32_t *wq, const uint16_t *scales,
+                         const uint16_t *biases, int64_t n, int64_t group, void *y, int y_dtype);
+int fh_q4_gate_up_silu(fh_device *dev, const uint16_t *x, const uint16_t *residual,
+                       uint16_t *residual_out, const uint16_t *norm_weight, float eps, int64_t m,
+                       int64_t k, const uint32_t *wq, const uint16_t *scales, const uint16_t *biases,
+                       int64_t n, int64_t group, uint16_t *act);
+
 /* LlamaMlp's act_fn(gate) * up (src/models/llama/mlp.rs:49-58, Silu at
  * src/nn/activation.rs:19-28): gate_up row = [gate (f) | up (f)],
  * out = RNE(RNE(g / (1 + exp(-g))) * u), out: [rows, f]. */

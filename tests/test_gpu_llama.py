@@ -315,6 +315,21 @@ def test_argmax_ties_and_values(device):
     assert got.tolist() == [3, R.argmax(R.from_bf16(x[1])), 0, 999]
 
 
+@pytest.mark.parametrize("n", [128256, 300001])
+def test_argmax_long_rows(device, n):
+    """A vocabulary-sized row, and an odd length (the second row starts
+    unaligned) long enough for several load batches, with the maximum tied
+    across batches."""
+    x = synth.bf16_normal(11, (2, n))
+    x[0, n - 5] = x[0, 17] = x[0, 140000 % n] = 0x4400  # 512.0, tied: lowest index wins
+    x[1, n - 1] = 0x4480
+    s = up(device, x)
+    out = device.empty(8)
+    _lib.call("fh_argmax", device.handle, ctypes.c_void_p(s.ptr), 2, n, ctypes.c_void_p(out.ptr))
+    got = down(device, out, np.uint32, 2)
+    assert got.tolist() == [R.argmax(R.from_bf16(x[0])), R.argmax(R.from_bf16(x[1]))] == [17, n - 1]
+
+
 def _ref_model(cfg, seed, max_len):
     layers = [layer_weights(cfg, seed, l) for l in range(cfg.n_layers)]
     return R.RefLlama(cfg, embed_weights(cfg, seed), layers, final_norm_weight(cfg, seed), max_len)
