@@ -215,17 +215,16 @@ __global__ __launch_bounds__(kGemvThreads) void q4_gemv_kernel(
             rv = fu.res ? *reinterpret_cast<const uint4 *>(fu.res + o) : make_uint4(0u, 0u, 0u, 0u);
             wv = *reinterpret_cast<const uint4 *>(fu.w + (t < chunks * 4 ? t : 0) * 8);
         };
-        uint4 xv, rv, wv;
-        load_round(0, xv, rv, wv);
-        if (group_first < groups_total) load(group_first, 0, buf);
-        for (uint32_t t0 = 0; t0 < pieces; t0 += kGemvThreads) {
+        // The first two rounds (every piece when M * k <= 4096) and the first
+        // row group's weights are requested in straight-line code, with
+        // clamped indices instead of guards, so each wait for a round counts
+        // exactly the loads issued after it (a guarded load makes the
+        // compiler wait for all of them, weights included).
+        auto process = [&](uint32_t t0, uint4 xv, uint4 rv, uint4 wv) {
             const uint32_t t = t0 + threadIdx.x;
             const bool live = t < pieces;
             const uint64_t o = xoff(live ? t : 0);
             const bool wpiece = t < chunks * 4;
-            const bool more = t0 + kGemvThreads < pieces;
-            uint4 xn, rn, wn;
-            if (more) load_round(t0 + kGemvThreads, xn, rn, wn);
             if (fu.res) {
                 xv = gemv_pairwise(xv, rv, [](float a, float b) { return a + b; });
                 if (blockIdx.x == 0 && fu.res_out && live) *reinterpret_cast<uint4 *>(fu.res_out + o) = xv;
@@ -246,54 +245,82 @@ __global__ __launch_bounds__(kGemvThreads) void q4_gemv_kernel(
                 xs[(m * 4 + wi) * chunks + c] = gemv_permute(xv);
                 if (wpiece) wsh[wi * chunks + c] = gemv_permute(wv);
             }
-            if (more) {
-                xv = xn;
-                rv = rn;
-                wv = wn;
+        };
+        // the sum-of-squares reduction, then pass 2 (every thread calls it)
+        auto finish = [&]() {
+            {
+                const uint32_t lane_x = threadIdx.x & 63, wave_x = threadIdx.x >> 6;
+    #pragma unroll
+                for (int m = 0; m < M; ++m) {
+                    float v = ss[m];
+    #pragma unroll
+                    for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
+                    if (lane_x == 0) red[wave_x][m] = v;
+                }
             }
-        }
-        {
-            const uint32_t lane_x = threadIdx.x & 63, wave_x = threadIdx.x >> 6;
-#pragma unroll
-            for (int m = 0; m < M; ++m) {
-                float v = ss[m];
-#pragma unroll
-                for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
-                if (lane_x == 0) red[wave_x][m] = v;
+            __syncthreads();
+            for (uint32_t t0 = 0; t0 < pieces; t0 += kGemvThreads) {
+                const uint32_t t = t0 + threadIdx.x;
+                const bool live = t < pieces;
+                const uint32_t m = live ? t / (chunks * 4) : 0, c = (t / 4) % chunks, wi = t % 4;
+                float tot = 0.f;
+    #pragma unroll
+                for (int w = 0; w < kGemvWaves; ++w) tot += red[w][m];
+                const float scale = 1.0f / sqrtf(tot * fu.dim_inv + fu.eps);
+                float psum = 0.f;
+                if (live) {
+                    const uint4 p = gemv_pairwise(xs[(m * 4 + wi) * chunks + c], wsh[wi * chunks + c],
+                                                  [scale](float h, float g) {
+                                                      return bf16_to_f32(f32_to_bf16_rne(h * scale)) * g;
+                                                  });
+                    xs[(m * 4 + wi) * chunks + c] = p;
+                    // (x0+x1) + (x2+x3) + (x4+x5) + (x6+x7) of the piece
+                    psum = ((bf16_to_f32(p.x & 0xFFFFu) + bf16_to_f32(p.y & 0xFFFFu)) +
+                            (bf16_to_f32(p.z & 0xFFFFu) + bf16_to_f32(p.w & 0xFFFFu))) +
+                           ((bf16_to_f32(p.x >> 16) + bf16_to_f32(p.y >> 16)) +
+                            (bf16_to_f32(p.z >> 16) + bf16_to_f32(p.w >> 16)));
+                }
+                psum += __shfl_xor(psum, 1, 64);
+                psum += __shfl_xor(psum, 2, 64);
+                if (live && wi == 0) xsum[m * chunks + c] = psum;
             }
-        }
-        __syncthreads();
-        for (uint32_t t0 = 0; t0 < pieces; t0 += kGemvThreads) {
-            const uint32_t t = t0 + threadIdx.x;
-            const bool live = t < pieces;
-            const uint32_t m = live ? t / (chunks * 4) : 0, c = (t / 4) % chunks, wi = t % 4;
-            float tot = 0.f;
-#pragma unroll
-            for (int w = 0; w < kGemvWaves; ++w) tot += red[w][m];
-            const float scale = 1.0f / sqrtf(tot * fu.dim_inv + fu.eps);
-            float psum = 0.f;
-            if (live) {
-                const uint4 p = gemv_pairwise(xs[(m * 4 + wi) * chunks + c], wsh[wi * chunks + c],
-                                              [scale](float h, float g) {
-                                                  return bf16_to_f32(f32_to_bf16_rne(h * scale)) * g;
-                                              });
-                xs[(m * 4 + wi) * chunks + c] = p;
-                // (x0+x1) + (x2+x3) + (x4+x5) + (x6+x7) of the piece
-                psum = ((bf16_to_f32(p.x & 0xFFFFu) + bf16_to_f32(p.y & 0xFFFFu)) +
-                        (bf16_to_f32(p.z & 0xFFFFu) + bf16_to_f32(p.w & 0xFFFFu))) +
-                       ((bf16_to_f32(p.x >> 16) + bf16_to_f32(p.y >> 16)) +
-                        (bf16_to_f32(p.z >> 16) + bf16_to_f32(p.w >> 16)));
+        };
+        // Two code paths with their own tails: a join between the weight
+        // loads and the reduction would make the compiler wait for the
+        // weights there.
+        if (pieces <= 2 * kGemvThreads) {
+            uint4 x0, r0, w0, x1, r1, w1;
+            load_round(0, x0, r0, w0);
+            load_round(kGemvThreads, x1, r1, w1);
+            __builtin_amdgcn_sched_barrier(0);  // keep these ahead of the weight loads
+            load(group_first < groups_total ? group_first : groups_total - 1, 0, buf);
+            // both rounds are processed unconditionally (dead pieces are
+            // masked inside), so their loads cannot sink below the weights'
+            process(0, x0, r0, w0);
+            process(kGemvThreads, x1, r1, w1);
+            finish();
+        } else {
+            load(group_first < groups_total ? group_first : groups_total - 1, 0, buf);
+            for (uint32_t t0 = 0; t0 < pieces; t0 += kGemvThreads) {
+                uint4 xv, rv, wv;
+                load_round(t0, xv, rv, wv);
+                process(t0, xv, rv, wv);
             }
-            psum += __shfl_xor(psum, 1, 64);
-            psum += __shfl_xor(psum, 2, 64);
-            if (live && wi == 0) xsum[m * chunks + c] = psum;
+            finish();
         }
     } else {
+        // x and the first row group's weights are requested unconditionally
+        // (clamped indices; see the RMSNorm path) so that staging x waits
+        // only for x. Threads past the last item stage a copy of item 0:
+        // the same values to the same place, and no guarded use under which
+        // the compiler could sink the x loads below the weight loads.
         const uint32_t items_x = M * chunks;
         uint4 xv[4];
-        if (threadIdx.x < items_x) load_x(threadIdx.x, xv);
-        if (group_first < groups_total) load(group_first, 0, buf);
-        if (threadIdx.x < items_x) stage(threadIdx.x, xv);
+        const uint32_t t_first = threadIdx.x < items_x ? threadIdx.x : 0;
+        load_x(t_first, xv);
+        __builtin_amdgcn_sched_barrier(0);
+        load(group_first < groups_total ? group_first : groups_total - 1, 0, buf);
+        stage(t_first, xv);
         for (uint32_t t = threadIdx.x + kGemvThreads; t < items_x; t += kGemvThreads) {
             load_x(t, xv);
             stage(t, xv);
