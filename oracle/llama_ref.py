@@ -6,7 +6,7 @@ bf16 rounding points (every reference tensor op rounds its output to the
 tensor dtype, bf16):
 
 - RmsNorm (src/nn/norm.rs:32-50): fp32 sum of squares, scale =
-  1/sqrt(ss * (1/dim) + eps), y = RNE(RNE(x * scale) * w).
+  reciprocal(sqrt(ss * (1/dim) + eps)), y = RNE(RNE(x * scale) * w).
 - Linear (src/nn/linear.rs:22-35 -> matmul_tiled): fp32 accumulation of
   x . (s*q + b), RNE output. (numpy's sgemm sums in a different order than
   matmul_tiled's sequential k; within fp32 accumulation error.)
@@ -22,6 +22,9 @@ tensor dtype, bf16):
 - generation comparison (src/eval/generation.rs:132-176).
 
 Weights are inputs (the same seeded q4 triplets the GPU model uses).
+Pinned by tests/test_llama_ref.py: the reference's own tests of inv_freq,
+angles, top-k order, argmax ties and compare_generation, and closed forms for
+RmsNorm, SiLU and SDPA.
 """
 from __future__ import annotations
 
@@ -69,10 +72,51 @@ def inv_freq(head_dim, theta, scaling) -> np.ndarray:
     return np.array(out, dtype=np.float32)
 
 
+def angles(freqs, length) -> np.ndarray:
+    """[length, 2 * len(freqs)]: position * frequency, the frequencies repeated
+    for both halves (src/models/llama/rotary_emb.rs:87-133)."""
+    f = np.asarray(freqs, dtype=np.float32)
+    return (np.arange(length, dtype=np.float32)[:, None] * np.concatenate([f, f])[None, :]).astype(np.float32)
+
+
 def rope_tables(head_dim, theta, scaling, length):
-    f = inv_freq(head_dim, theta, scaling)
-    ang = (np.arange(length, dtype=np.float32)[:, None] * np.concatenate([f, f])[None, :]).astype(np.float32)
+    ang = angles(inv_freq(head_dim, theta, scaling), length)
     return rne(np.cos(ang)), rne(np.sin(ang))
+
+
+def rms_norm(h, w, eps) -> np.ndarray:
+    """RmsNorm (src/nn/norm.rs:32-50): fp32 sum of squares, scale =
+    reciprocal(sqrt(ss * (1/dim) + eps)) as two fp32 ops, RNE(RNE(h * scale) * w)."""
+    h = np.asarray(h, dtype=np.float32)
+    ss = np.sum(h * h, axis=-1, dtype=np.float32, keepdims=True)
+    dim_inv = np.float32(1.0) / np.float32(h.shape[-1])
+    root = np.sqrt(ss * dim_inv + np.float32(eps), dtype=np.float32)
+    scale = (np.float32(1.0) / root).astype(np.float32)
+    return rne(rne(h * scale) * np.asarray(w, dtype=np.float32))
+
+
+def silu_mul(g, u) -> np.ndarray:
+    """Silu (src/nn/activation.rs:19-28) times up (src/models/llama/mlp.rs:49-58):
+    RNE(RNE(g / (exp(-g) + 1)) * u) in fp32."""
+    g = np.asarray(g, dtype=np.float32)
+    return rne(rne(g / (np.exp(-g).astype(np.float32) + np.float32(1.0))) * np.asarray(u, dtype=np.float32))
+
+
+def sdpa(q, k, v, pos, scale) -> np.ndarray:
+    """One head of scaled_dot_product_attention (src/nn/attention.rs:23-60)
+    with the causal mask (src/nn/masking.rs:11-32): q [t, d] at positions
+    pos [t], k and v [ctx, d] (ctx = max(pos) + 1). Scores RNE(q.k), times
+    scale in fp32, -inf above the diagonal, fp32 softmax, probabilities RNE,
+    out RNE(p . v)."""
+    pos = np.asarray(pos)
+    ctx = k.shape[0]
+    sc = rne(np.asarray(q, np.float32) @ np.asarray(k, np.float32).T) * np.float32(scale)
+    mask = np.arange(ctx)[None, :] > pos[:, None]
+    sc = np.where(mask, np.float32(-np.inf), sc).astype(np.float32)
+    m = sc.max(axis=-1, keepdims=True)
+    e = np.exp(sc - m).astype(np.float32)
+    p = rne(e / e.sum(axis=-1, dtype=np.float32, keepdims=True))
+    return rne(p @ np.asarray(v, np.float32))
 
 
 class RefLlama:
@@ -101,9 +145,7 @@ class RefLlama:
         self.v = [np.zeros((c.n_kv_heads, self.max_len, c.head_dim), np.float32) for _ in self.layers]
 
     def rms_norm(self, h, w):
-        ss = np.sum(h * h, axis=-1, dtype=np.float32, keepdims=True)
-        scale = np.float32(1.0) / np.sqrt(ss * np.float32(1.0 / h.shape[-1]) + np.float32(self.cfg.rms_norm_eps))
-        return rne(rne(h * scale) * w)
+        return rms_norm(h, w, self.cfg.rms_norm_eps)
 
     @staticmethod
     def linear(x, w):
@@ -137,19 +179,12 @@ class RefLlama:
             out = np.empty((t, c.n_heads, c.head_dim), np.float32)
             for hh in range(c.n_heads):
                 kv = hh // group
-                sc = rne(q[:, hh, :] @ self.k[li][kv, :ctx, :].T) * scale
-                mask = np.arange(ctx)[None, :] > pos[:, None]
-                sc = np.where(mask, np.float32(-np.inf), sc).astype(np.float32)
-                m = sc.max(axis=-1, keepdims=True)
-                e = np.exp(sc - m).astype(np.float32)
-                p = rne(e / e.sum(axis=-1, dtype=np.float32, keepdims=True))
-                out[:, hh, :] = rne(p @ self.v[li][kv, :ctx, :])
+                out[:, hh, :] = sdpa(q[:, hh, :], self.k[li][kv, :ctx, :], self.v[li][kv, :ctx, :], pos, scale)
             a = self.linear(out.reshape(t, -1), L["o"])
             h = rne(h + a)
             x = self.rms_norm(h, L["post_norm"])
             gu = self.linear(x, L["gate_up"])
-            g, u = gu[:, :c.ffn], gu[:, c.ffn:]
-            act = rne(rne(g / (np.exp(-g).astype(np.float32) + np.float32(1.0))) * u)
+            act = silu_mul(gu[:, :c.ffn], gu[:, c.ffn:])
             h = rne(h + self.linear(act, L["down"]))
         x = self.rms_norm(h, self.final_norm)
         return self.linear(x[-1:], self.embed_f)[0]

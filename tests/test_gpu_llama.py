@@ -313,6 +313,15 @@ def test_argmax_ties_and_values(device):
     _lib.call("fh_argmax", device.handle, ctypes.c_void_p(s.ptr), 4, 1000, ctypes.c_void_p(out.ptr))
     got = down(device, out, np.uint32, 4)
     assert got.tolist() == [3, R.argmax(R.from_bf16(x[1])), 0, 999]
+    # the reference's tie cases (src/metal/mod.rs:2038-2096), values exact in bf16
+    ref = np.zeros((2, 600), dtype=np.uint16)
+    ref[0, :4] = (np.array([3.0, 7.0, 7.0, 1.0], np.float32).view(np.uint32) >> 16).astype(np.uint16)
+    ref[0, 4:] = 0xFF80
+    vals = np.array([9.0 if i in (10, 300) else float(i % 7) for i in range(600)], np.float32)
+    ref[1] = (vals.view(np.uint32) >> 16).astype(np.uint16)
+    s2 = up(device, ref)
+    _lib.call("fh_argmax", device.handle, ctypes.c_void_p(s2.ptr), 2, 600, ctypes.c_void_p(out.ptr))
+    assert down(device, out, np.uint32, 2).tolist() == [1, 10]
 
 
 @pytest.mark.parametrize("n", [128256, 300001])
