@@ -20,6 +20,7 @@ host's cores, for a bounded number of calls.
 from __future__ import annotations
 
 import argparse
+import gc
 import ctypes
 import json
 import os
@@ -198,6 +199,7 @@ def bench_decode(dev, new_tokens: int, agreement: int, seed: int = 0):
     model = Q4Llama(dev, cfg, seed, max_len, max_tokens=len(prompt) + agreement)
     build_s = time.perf_counter() - t0
     model.generate(prompt[:64], 4)  # warm the kernels once
+    gc.collect()
     dev.timer_begin()
     model.prefill(prompt)
     prefill_ms = dev.timer_end()
@@ -246,6 +248,15 @@ def greedy_agreement(model, cfg, seed, prompt, tokens, n):
     ref = R.RefLlama(cfg, embed_weights(cfg, seed), layers, final_norm_weight(cfg, seed), len(prompt) + n)
     exp_tokens, exp_tops = ref.generate(prompt, n)
     got = tokens[:n]
+    # first-step logits after the prompt, beside the token rule (random-init
+    # weights whose mean is -s/2 make greedy decode repeat a few tokens)
+    model.prefill(prompt)
+    gpu_logits = R.from_bf16(model.logits()).astype(np.float64)
+    ref_logits = ref.first_logits.astype(np.float64)
+    first_step = {"logits_max_abs_err_rel": float(np.max(np.abs(gpu_logits - ref_logits)) / np.max(np.abs(ref_logits))),
+                  "top5_gpu": R.top_ids(gpu_logits.astype(np.float32), 5),
+                  "top5_reference_arithmetic": R.top_ids(ref_logits.astype(np.float32), 5),
+                  "distinct_greedy_tokens": int(len(set(got.tolist())))}
     report = R.compare_generation(got, [[]] * n, exp_tokens, exp_tops)
     if report["first_divergence"] is not None:
         d = report["first_divergence"]
@@ -253,6 +264,7 @@ def greedy_agreement(model, cfg, seed, prompt, tokens, n):
         gpu_tops = [[]] * n
         gpu_tops[d] = R.top_ids(R.from_bf16(model.logits()), 5)
         report = R.compare_generation(got, gpu_tops, exp_tokens, exp_tops)
+    report["first_step"] = first_step
     report["cpu_s"] = time.perf_counter() - t0
     report["gpu_tokens"] = got.tolist()
     report["reference_arithmetic_tokens"] = exp_tokens.tolist()
@@ -309,6 +321,8 @@ def main() -> int:
     ap.add_argument("--decode-tokens", type=int, default=256, help="config-4 greedy steps (0 skips)")
     ap.add_argument("--agreement", type=int, default=0,
                     help="compare the first N config-4 tokens with the CPU reference arithmetic")
+    ap.add_argument("--decode-only", action="store_true",
+                    help="only the config-4 decode (for a kernel trace of the step); prints its JSON")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not supported "
@@ -318,6 +332,11 @@ def main() -> int:
     if args.calibrate_copy:
         calibrate_copy()
     dev = HipDevice(0)
+    if args.decode_only:
+        d = bench_decode(dev, max(2, args.decode_tokens), args.agreement)
+        dev.close()
+        print(json.dumps(d), flush=True)
+        return 0
     head = bench_gemv(dev, 8192, 3072, args.copies, args.steps, args.warmup, seed=1)
     print(f"[bench] gemv 8192x3072: {head['us_per_launch']:.2f} us/launch, {head['GB_per_s']:.0f} GB/s", flush=True)
     secondary = {}

@@ -195,6 +195,7 @@ class RefLlama:
         self.reset()
         ids = list(int(i) for i in prompt)
         logits = self.forward(ids, np.arange(len(ids)))
+        self.first_logits = logits
         tokens, tops = [], []
         for step in range(new_tokens):
             tokens.append(argmax(logits))
