@@ -280,16 +280,29 @@ __global__ __launch_bounds__(kAttnThreads) void attn_pv_kernel(
             for (int n = 0; n < NS; ++n) sr[n] = snext[n];
         }
     }
+    // slots of one dim pair inside a wavefront are P lanes apart: add them
+    // with shuffles first, so LDS holds one partial per wavefront (and the
+    // final sums read a few values instead of kSlots)
+    constexpr int SW = P < 64 ? 64 / P : 1;  // slots per wavefront
 #pragma unroll
-    for (int g = 0; g < G; ++g) {
-        red[tid][2 * g] = acc[g][0];
-        red[tid][2 * g + 1] = acc[g][1];
+    for (int off = P; off < 64; off <<= 1)
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+            acc[g][0] += __shfl_xor(acc[g][0], off, 64);
+            acc[g][1] += __shfl_xor(acc[g][1], off, 64);
+        }
+    if (s % SW == 0) {
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+            red[tid][2 * g] = acc[g][0];
+            red[tid][2 * g + 1] = acc[g][1];
+        }
     }
     __syncthreads();
     for (uint32_t i = tid; i < G * 2 * P; i += kAttnThreads) {
         const uint32_t g = i / (2 * P), dd = i % (2 * P), qq = dd / 2, e = dd % 2;
         float o = 0.f;
-        for (int ss = 0; ss < S::kSlots; ++ss) o += red[ss * P + qq][2 * g + e];
+        for (int ss = 0; ss < S::kSlots; ss += SW) o += red[ss * P + qq][2 * g + e];
         orow[g * head_dim + dd] = rne(o);
     }
 }
