@@ -173,16 +173,17 @@ def cpu_baseline(seconds: float = 12.0):
     return out, cpu
 
 
-def decode_step_bytes(cfg, context: int) -> int:
+def decode_step_bytes(cfg, context: float, batch: int = 1) -> int:
     """HBM bytes one decode step must read at a given context: every q4 linear
-    (weights + scales/biases), the LM head (tied table), the norm weights and
-    the K/V cache rows attended to."""
+    (weights + scales/biases, read once for the whole batch), the LM head
+    (tied table), the norm weights and each sequence's K/V cache rows
+    attended to."""
     def q4(n, k):
         return n * k // 2 + 4 * n * (k // 64)
 
     per_layer = (q4(cfg.qkv_rows, cfg.hidden) + q4(cfg.hidden, cfg.n_heads * cfg.head_dim)
                  + q4(2 * cfg.ffn, cfg.hidden) + q4(cfg.hidden, cfg.ffn) + 2 * 2 * cfg.hidden
-                 + 2 * cfg.n_kv_heads * cfg.head_dim * 2 * context)
+                 + int(batch * 2 * cfg.n_kv_heads * cfg.head_dim * 2 * context))
     return cfg.n_layers * per_layer + q4(cfg.vocab, cfg.hidden) + 2 * cfg.hidden
 
 
@@ -216,8 +217,9 @@ def bench_decode(dev, new_tokens: int, agreement: int, seed: int = 0):
     tokens[0] = first[0]
     steps = new_tokens - 1
     step_ms = decode_ms / steps
-    mean_ctx = len(prompt) + steps / 2
-    step_bytes = decode_step_bytes(cfg, int(mean_ctx))
+    # step i feeds position len(prompt) + i and attends to that many keys + 1
+    mean_ctx = len(prompt) + (steps + 1) / 2
+    step_bytes = decode_step_bytes(cfg, mean_ctx)
     out = {
         "config": "Llama-3.2-3B shape (28 layers, hidden 3072, 24/8 heads, head_dim 128, FFN 8192, vocab 128256), "
                   "q4 group 64, tied embedding/LM head, random init",
@@ -234,6 +236,71 @@ def bench_decode(dev, new_tokens: int, agreement: int, seed: int = 0):
     if agreement:
         out["agreement"] = greedy_agreement(model, cfg, seed, prompt, tokens, agreement)
     return out
+
+
+def bench_decode_batched(dev, new_tokens: int, seed: int = 0, batch: int = 8, depth: int = 2048,
+                         prompt_len: int = 2048):
+    """Config 5: Llama-3.1-8B-shaped random-init q4 decoder (32 layers,
+    hidden 4096, 32/8 heads, FFN 14336, vocab 128256; the q4 table is tied as
+    the reference's model requires, src/models/llama/config.rs:177-180) over
+    `batch` sequences, run as the reference's bench runs depth rows
+    (src/bench/mod.rs:203-300): depth ids fill every cache untimed, the
+    prompt step is the timed prefill, then greedy decode steps start at
+    context depth + prompt_len. Ids come from one SplitMix64 stream, every
+    depth row then every prompt row (draw_inputs, src/bench/mod.rs:203-241).
+    Rates follow the reference's report: P / Tp with P = batch * prompt
+    tokens, and D / Td with D = decode steps * batch
+    (tools/reference/README.md:83-108)."""
+    from foundry_amd.llama import LlamaConfig, Q4Llama
+
+    cfg = LlamaConfig.llama_3_1_8b()
+    ids = synth.token_ids(seed, batch * (depth + prompt_len), cfg.vocab)
+    depth_ids = ids[:batch * depth].reshape(batch, depth)
+    prompt_ids = ids[batch * depth:].reshape(batch, prompt_len)
+    max_len = depth + prompt_len + new_tokens
+    t0 = time.perf_counter()
+    model = Q4Llama(dev, cfg, seed, max_len, max_tokens=prompt_len, batch=batch)
+    build_s = time.perf_counter() - t0
+    model.generate(prompt_ids[:, :16], 3)  # warm the prefill and decode kernels (positions later overwritten)
+    t0 = time.perf_counter()
+    for s0 in range(0, depth, prompt_len):
+        model.step(depth_ids[:, s0:s0 + prompt_len], s0)
+    dev.synchronize()
+    depth_s = time.perf_counter() - t0
+    gc.collect()
+    dev.timer_begin()
+    model.step(prompt_ids, depth)
+    prefill_ms = dev.timer_end()
+    first = np.empty(batch, dtype=np.uint32)
+    _lib.call("fh_download", dev.handle, first.ctypes.data_as(ctypes.c_void_p), ctypes.c_void_p(model.buf["next"].ptr),
+              first.nbytes)
+    log = dev.zeros(4 * batch * new_tokens)
+    graph = model.capture_decode(log, new_tokens)
+    dev.timer_begin()
+    for _ in range(new_tokens - 1):
+        graph.launch()
+    decode_ms = dev.timer_end()
+    tokens = np.empty((batch, new_tokens), dtype=np.uint32)
+    _lib.call("fh_download", dev.handle, tokens.ctypes.data_as(ctypes.c_void_p), ctypes.c_void_p(log.ptr), tokens.nbytes)
+    tokens[:, 0] = first
+    steps = new_tokens - 1
+    step_ms = decode_ms / steps
+    ctx0 = depth + prompt_len
+    step_bytes = decode_step_bytes(cfg, ctx0 + (steps + 1) / 2, batch)
+    gbs = step_bytes / (step_ms * 1e-3) / 1e9
+    return {
+        "config": "Llama-3.1-8B shape (32 layers, hidden 4096, 32/8 heads, head_dim 128, FFN 14336, vocab 128256), "
+                  "q4 group 64, tied q4 embedding/LM head, random init",
+        "batch": batch, "depth_tokens": depth, "prompt_tokens": prompt_len, "new_tokens": new_tokens,
+        "decode_context_first_step": ctx0,
+        "prefill_ms": prefill_ms, "prompt_tokens_per_s": batch * prompt_len / (prefill_ms * 1e-3),
+        "depth_s_untimed": depth_s,
+        "decode_ms_per_step": step_ms, "decode_tokens_per_s": batch * 1e3 / step_ms,
+        "decode_bytes_per_step": step_bytes, "decode_GB_per_s": gbs, "decode_frac_hbm_peak": gbs / HBM_PEAK_GBS,
+        "decode_ceiling_tokens_per_s_at_peak": batch * HBM_PEAK_GBS * 1e9 / step_bytes,
+        "model_build_s": build_s,
+        "first_tokens": tokens[:, :4].tolist(),
+    }
 
 
 def greedy_agreement(model, cfg, seed, prompt, tokens, n):
@@ -323,6 +390,9 @@ def main() -> int:
                     help="compare the first N config-4 tokens with the CPU reference arithmetic")
     ap.add_argument("--decode-only", action="store_true",
                     help="only the config-4 decode (for a kernel trace of the step); prints its JSON")
+    ap.add_argument("--batched-tokens", type=int, default=32,
+                    help="config-5 greedy steps per sequence (8B shape, batch 8, context 4096; 0 skips)")
+    ap.add_argument("--batched-only", action="store_true", help="only the config-5 run; prints its JSON")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not supported "
@@ -332,8 +402,9 @@ def main() -> int:
     if args.calibrate_copy:
         calibrate_copy()
     dev = HipDevice(0)
-    if args.decode_only:
-        d = bench_decode(dev, max(2, args.decode_tokens), args.agreement)
+    if args.decode_only or args.batched_only:
+        d = (bench_decode(dev, max(2, args.decode_tokens), args.agreement) if args.decode_only
+             else bench_decode_batched(dev, max(2, args.batched_tokens)))
         dev.close()
         print(json.dumps(d), flush=True)
         return 0
@@ -354,6 +425,12 @@ def main() -> int:
         d = secondary["decode_llama_3_2_3b"]
         print(f"[bench] decode: {d['decode_tok_s']:.0f} tok/s ({d['decode_frac_hbm_peak']*100:.1f}% of HBM roofline), "
               f"prefill {d['prefill_tok_s']:.0f} tok/s", flush=True)
+    if not args.quick and args.batched_tokens > 1:
+        secondary["decode_llama_3_1_8b_b8"] = bench_decode_batched(dev, args.batched_tokens)
+        d = secondary["decode_llama_3_1_8b_b8"]
+        print(f"[bench] 8B batch 8 at context 4096: decode {d['decode_tokens_per_s']:.0f} tok/s "
+              f"({d['decode_frac_hbm_peak']*100:.1f}% of HBM roofline), prefill {d['prompt_tokens_per_s']:.0f} tok/s",
+              flush=True)
     dev.close()
 
     cpu = None

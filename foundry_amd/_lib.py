@@ -119,7 +119,7 @@ SIGNATURES = {
     "fh_silu_mul": [_vp, _vp, _i64, _i64, _vp],
     "fh_argmax": [_vp, _vp, _i64, _i64, _vp],
     "fh_advance_positions": [_vp, _vp, _i64, _i64],
-    "fh_append_token": [_vp, _vp, _vp, _vp, _i64, _i64],
+    "fh_append_token": [_vp, _vp, _i64, _vp, _vp, _i64, _i64],
 }
 
 _lib = None

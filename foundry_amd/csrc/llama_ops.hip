@@ -243,11 +243,13 @@ __global__ __launch_bounds__(kArgmaxThreads) void argmax_kernel(const uint16_t *
 }
 
 // log[position - base] = token when that index is below capacity.
-__global__ void append_token_kernel(const uint32_t *__restrict__ token, uint32_t *__restrict__ log,
-                                    const uint32_t *__restrict__ position, uint32_t base,
-                                    uint32_t capacity) {
-    const uint32_t idx = position[0] - base;
-    if (position[0] >= base && idx < capacity) log[idx] = token[0];
+__global__ void append_token_kernel(const uint32_t *__restrict__ token, uint32_t rows,
+                                    uint32_t *__restrict__ log, const uint32_t *__restrict__ position,
+                                    uint32_t base, uint32_t capacity) {
+    const uint32_t r = blockIdx.x * blockDim.x + threadIdx.x;
+    if (r >= rows) return;
+    const uint32_t p = position[r], idx = p - base;
+    if (p >= base && idx < capacity) log[static_cast<uint64_t>(r) * capacity + idx] = token[r];
 }
 
 __global__ void advance_kernel(uint32_t *__restrict__ p, uint32_t n, uint32_t by) {
@@ -375,18 +377,21 @@ extern "C" int fh_advance_positions(fh_device *dev, uint32_t *positions, int64_t
     });
 }
 
-extern "C" int fh_append_token(fh_device *dev, const uint32_t *token, uint32_t *log,
+extern "C" int fh_append_token(fh_device *dev, const uint32_t *token, int64_t rows, uint32_t *log,
                                const uint32_t *position, int64_t base, int64_t capacity) {
     const char *fn = "fh_append_token";
     if (int rc = check_usable(dev, fn)) return rc;
-    if (int rc = fh_check_dims(fn, {base, capacity})) return rc;
-    if (capacity == 0) return FH_OK;
-    if (int rc = check_range(dev, token, 4, fn, "token")) return rc;
-    if (int rc = check_range(dev, position, 4, fn, "position")) return rc;
-    if (int rc = check_range(dev, log, static_cast<uint64_t>(capacity) * 4, fn, "log")) return rc;
+    if (int rc = fh_check_dims(fn, {rows, base, capacity})) return rc;
+    if (rows == 0 || capacity == 0) return FH_OK;
+    if (static_cast<uint64_t>(rows) * static_cast<uint64_t>(capacity) > 0xFFFFFFFFull)
+        return fail(FH_ERR_UNSUPPORTED, "%s: rows * capacity must fit in 32 bits", fn);
+    if (int rc = check_range(dev, token, static_cast<uint64_t>(rows) * 4, fn, "token")) return rc;
+    if (int rc = check_range(dev, position, static_cast<uint64_t>(rows) * 4, fn, "position")) return rc;
+    if (int rc = check_range(dev, log, static_cast<uint64_t>(rows) * capacity * 4, fn, "log")) return rc;
     if (int rc = set_current(dev, fn)) return rc;
     return dispatch(dev, fn, [&] {
-        hipLaunchKernelGGL(append_token_kernel, dim3(1), dim3(1), 0, dev->stream, token, log, position,
+        hipLaunchKernelGGL(append_token_kernel, dim3(static_cast<uint32_t>((rows + 63) / 64)), dim3(64), 0,
+                           dev->stream, token, static_cast<uint32_t>(rows), log, position,
                            static_cast<uint32_t>(base), static_cast<uint32_t>(capacity));
     });
 }

@@ -163,14 +163,22 @@ def final_norm_weight(cfg: LlamaConfig, seed: int):
 
 
 class Q4Llama:
-    """Random-init q4 Llama on one device, with a static KV cache of
-    `max_len` positions per layer (StaticCache, src/nn/kv_cache.rs:13-39)."""
+    """Random-init q4 Llama on one device. It runs `batch` sequences of equal
+    length (batch_dims, src/generate/mod.rs:207-225), each with a static KV
+    cache of `max_len` positions per layer, laid out [batch, n_kv, max_len,
+    head_dim] (StaticCache, src/nn/kv_cache.rs:13-39). `max_tokens` bounds the
+    tokens of one sequence in one forward."""
 
-    def __init__(self, dev: HipDevice, cfg: LlamaConfig, seed: int, max_len: int, max_tokens: int):
+    def __init__(self, dev: HipDevice, cfg: LlamaConfig, seed: int, max_len: int, max_tokens: int,
+                 batch: int = 1):
         self.dev, self.cfg, self.max_len = dev, cfg, max_len
         if max_len > cfg.max_position_embeddings:
             raise ValueError("max_len exceeds max_position_embeddings")
+        if not 1 <= batch <= 65535:
+            raise ValueError(f"batch {batch} must be in 1..65535")
+        self.batch = int(batch)
         self.max_tokens = max(1, max_tokens)
+        self.seq_bytes = cfg.n_kv_heads * max_len * cfg.head_dim * 2  # one sequence's cache, per layer
         self.embed = _Q4(dev, *embed_weights(cfg, seed))
         self.layers = []
         for layer in range(cfg.n_layers):
@@ -180,55 +188,83 @@ class Q4Llama:
                 "gate_up": _Q4(dev, *w["gate_up"]), "down": _Q4(dev, *w["down"]),
                 "input_norm": dev.storage_from_bytes(w["input_norm"].tobytes()),
                 "post_norm": dev.storage_from_bytes(w["post_norm"].tobytes()),
-                "k_cache": dev.zeros(cfg.n_kv_heads * max_len * cfg.head_dim * 2),
-                "v_cache": dev.zeros(cfg.n_kv_heads * max_len * cfg.head_dim * 2),
+                "k_cache": dev.zeros(self.batch * self.seq_bytes),
+                "v_cache": dev.zeros(self.batch * self.seq_bytes),
             })
         self.final_norm = dev.storage_from_bytes(final_norm_weight(cfg, seed).tobytes())
         cos, sin = rope_tables(cfg, max_len)
         self.cos = dev.storage_from_bytes(cos.tobytes())
         self.sin = dev.storage_from_bytes(sin.tobytes())
         self.scale = float(np.float32(1.0) / np.sqrt(np.float32(cfg.head_dim), dtype=np.float32))
-        t, c = self.max_tokens, cfg
+        t, c, bt = self.max_tokens, cfg, self.batch
+        r = bt * t  # rows of one forward
         self.buf = {
-            "h": dev.empty(t * c.hidden * 2),
-            "h2": dev.empty(t * c.hidden * 2),
-            "x": dev.empty(t * c.hidden * 2),
-            "qkv": dev.empty(t * c.qkv_rows * 2),
-            "q": dev.empty(t * c.n_heads * c.head_dim * 2),
-            "attn": dev.empty(t * c.n_heads * c.head_dim * 2),
-            "o": dev.empty(t * c.hidden * 2),
-            "gu": dev.empty(t * 2 * c.ffn * 2),
-            "act": dev.empty(t * c.ffn * 2),
-            "logits": dev.empty(c.vocab * 2),
-            "ids": dev.empty(t * 4),
-            "positions": dev.empty(t * 4),
-            "next": dev.zeros(4),
-            "pos1": dev.zeros(4),
+            "h": dev.empty(r * c.hidden * 2),
+            "h2": dev.empty(r * c.hidden * 2),
+            "x": dev.empty(r * c.hidden * 2),
+            "qkv": dev.empty(r * c.qkv_rows * 2),
+            "q": dev.empty(r * c.n_heads * c.head_dim * 2),
+            "attn": dev.empty(r * c.n_heads * c.head_dim * 2),
+            "o": dev.empty(r * c.hidden * 2),
+            "gu": dev.empty(r * 2 * c.ffn * 2),
+            "act": dev.empty(r * c.ffn * 2),
+            "logits": dev.empty(bt * c.vocab * 2),
+            "ids": dev.empty(r * 4),
+            "positions": dev.empty(r * 4),
+            "next": dev.zeros(bt * 4),
+            "pos1": dev.zeros(bt * 4),
         }
+        # prefill attention runs one sequence at a time, reusing one workspace
         self.attn_ws_bytes = _lib.attention_workspace_bytes(t, c.n_heads, c.n_kv_heads, c.head_dim, max_len)
         self.attn_ws = dev.zeros(self.attn_ws_bytes)
-        self.dec_ws_bytes = _lib.decode_attention_workspace_bytes(1, c.n_heads, c.n_kv_heads, c.head_dim, max_len)
+        self.dec_ws_bytes = _lib.decode_attention_workspace_bytes(bt, c.n_heads, c.n_kv_heads, c.head_dim, max_len)
         self.dec_ws = dev.zeros(self.dec_ws_bytes)
+        self.seq_len = 0
 
     # ---- thin wrappers over the C-ABI ----
     def _p(self, st: HipStorage, byte_offset: int = 0):
         return ctypes.c_void_p(st.ptr + byte_offset)
 
-    def _linear(self, x: HipStorage, rows: int, w: _Q4, y: HipStorage, x_off: int = 0):
-        _lib.call("fh_q4_matmul", self.dev.handle, self._p(x, x_off), rows, w.k, w.k, self._p(w.wq),
-                  self._p(w.s), self._p(w.b), w.n, GROUP, self._p(y), _lib.BF16)
+    def _linear(self, x: HipStorage, rows: int, w: _Q4, y: HipStorage, x_off: int = 0, x_ld: int | None = None):
+        _lib.call("fh_q4_matmul", self.dev.handle, self._p(x, x_off), rows, w.k, w.k if x_ld is None else x_ld,
+                  self._p(w.wq), self._p(w.s), self._p(w.b), w.n, GROUP, self._p(y), _lib.BF16)
 
     def _linear_norm(self, x: HipStorage, res, res_out, weight: HipStorage, rows: int, w: _Q4, y: HipStorage,
-                     off: int = 0):
+                     off: int = 0, y_off: int = 0):
         """y = rms_norm(x [+ res]) W^T in one GEMV (res_out <- x + res)."""
         _lib.call("fh_q4_matmul_rmsnorm", self.dev.handle, self._p(x, off),
                   None if res is None else self._p(res, off), None if res_out is None else self._p(res_out, off),
                   self._p(weight), ctypes.c_float(self.cfg.rms_norm_eps), rows, w.k, self._p(w.wq), self._p(w.s),
-                  self._p(w.b), w.n, GROUP, self._p(y), _lib.BF16)
+                  self._p(w.b), w.n, GROUP, self._p(y, y_off), _lib.BF16)
 
-    def _forward(self, tokens: int, ids: HipStorage, positions: HipStorage):
-        """One forward over `tokens` rows; leaves the next id in buf['next']."""
+    def _attention(self, L, seq_tokens: int, positions: HipStorage):
+        """q,k = rope(q,k); cache k,v; attn = sdpa(q, cache) for every
+        sequence (src/models/llama/attention.rs:91-131)."""
         c, d, b = self.cfg, self.dev.handle, self.buf
+        if seq_tokens == 1:
+            # one new token per sequence: RoPE and the cache write fused into attention
+            _lib.call("fh_decode_attention", d, self._p(b["qkv"]), self.batch, c.n_heads, c.n_kv_heads, c.head_dim,
+                      self._p(self.cos), self._p(self.sin), self.max_len, self._p(positions),
+                      self._p(L["k_cache"]), self._p(L["v_cache"]), self.max_len, ctypes.c_float(self.scale),
+                      self._p(self.dec_ws), self.dec_ws_bytes, self._p(b["attn"]))
+            return
+        hq = c.n_heads * c.head_dim
+        for sq in range(self.batch):
+            r0, cache = sq * seq_tokens, sq * self.seq_bytes
+            _lib.call("fh_rope_kv", d, self._p(b["qkv"], r0 * c.qkv_rows * 2), seq_tokens, c.n_heads, c.n_kv_heads,
+                      c.head_dim, self._p(self.cos), self._p(self.sin), self.max_len, self._p(positions, r0 * 4),
+                      self._p(L["k_cache"], cache), self._p(L["v_cache"], cache), self.max_len,
+                      self._p(b["q"], r0 * hq * 2))
+            _lib.call("fh_attention", d, self._p(b["q"], r0 * hq * 2), self._p(L["k_cache"], cache),
+                      self._p(L["v_cache"], cache), self._p(positions, r0 * 4), seq_tokens, c.n_heads, c.n_kv_heads,
+                      c.head_dim, self.max_len, ctypes.c_float(self.scale), self._p(self.attn_ws),
+                      self.attn_ws_bytes, self._p(b["attn"], r0 * hq * 2))
+
+    def _forward(self, seq_tokens: int, ids: HipStorage, positions: HipStorage):
+        """One forward over `seq_tokens` rows of every sequence (rows ordered
+        sequence-major); leaves each sequence's next id in buf['next']."""
+        c, d, b = self.cfg, self.dev.handle, self.buf
+        tokens = self.batch * seq_tokens
         _lib.call("fh_q4_embed", d, self._p(self.embed.wq), self._p(self.embed.s), self._p(self.embed.b),
                   c.vocab, c.hidden, GROUP, self._p(ids), tokens, self._p(b["h"]))
         fused = tokens <= 8  # GEMV rows: the norms and SiLU go inside the linears
@@ -243,20 +279,7 @@ class Q4Llama:
             else:
                 self._linear_norm(pending, h, h_alt, L["input_norm"], tokens, L["qkv"], b["qkv"])
                 h, h_alt = h_alt, h
-            if tokens == 1:
-                # one new token: RoPE and the cache write fused into attention
-                _lib.call("fh_decode_attention", d, self._p(b["qkv"]), 1, c.n_heads, c.n_kv_heads, c.head_dim,
-                          self._p(self.cos), self._p(self.sin), self.max_len, self._p(positions),
-                          self._p(L["k_cache"]), self._p(L["v_cache"]), self.max_len, ctypes.c_float(self.scale),
-                          self._p(self.dec_ws), self.dec_ws_bytes, self._p(b["attn"]))
-            else:
-                _lib.call("fh_rope_kv", d, self._p(b["qkv"]), tokens, c.n_heads, c.n_kv_heads, c.head_dim,
-                          self._p(self.cos), self._p(self.sin), self.max_len, self._p(positions),
-                          self._p(L["k_cache"]), self._p(L["v_cache"]), self.max_len, self._p(b["q"]))
-                _lib.call("fh_attention", d, self._p(b["q"]), self._p(L["k_cache"]), self._p(L["v_cache"]),
-                          self._p(positions), tokens, c.n_heads, c.n_kv_heads, c.head_dim, self.max_len,
-                          ctypes.c_float(self.scale), self._p(self.attn_ws), self.attn_ws_bytes,
-                          self._p(b["attn"]))
+            self._attention(L, seq_tokens, positions)
             self._linear(b["attn"], tokens, L["o"], b["o"])
             if fused:
                 # act = silu_mul(rms_norm(o + h) [Wgate; Wup]^T) in one GEMV
@@ -271,13 +294,18 @@ class Q4Llama:
                 _lib.call("fh_silu_mul", d, self._p(b["gu"]), tokens, c.ffn, self._p(b["act"]))
             self._linear(b["act"], tokens, L["down"], b["o"])
             pending = b["o"]
-        last = (tokens - 1) * c.hidden * 2
-        if fused:
-            self._linear_norm(pending, h, None, self.final_norm, 1, self.embed, b["logits"], off=last)
+        # logits of each sequence's last row (src/models/llama/model.rs:112-121)
+        last = (seq_tokens - 1) * c.hidden * 2
+        if fused and seq_tokens == 1:
+            self._linear_norm(pending, h, None, self.final_norm, self.batch, self.embed, b["logits"])
+        elif fused:
+            for sq in range(self.batch):
+                self._linear_norm(pending, h, None, self.final_norm, 1, self.embed, b["logits"],
+                                  off=sq * seq_tokens * c.hidden * 2 + last, y_off=sq * c.vocab * 2)
         else:
             self._norm(tokens, pending, self.final_norm)
-            self._linear(b["x"], 1, self.embed, b["logits"], x_off=last)
-        _lib.call("fh_argmax", d, self._p(b["logits"]), 1, c.vocab, self._p(b["next"]))
+            self._linear(b["x"], self.batch, self.embed, b["logits"], x_off=last, x_ld=seq_tokens * c.hidden)
+        _lib.call("fh_argmax", d, self._p(b["logits"]), self.batch, c.vocab, self._p(b["next"]))
 
     def _norm(self, tokens: int, pending, weight: HipStorage):
         """x = rms_norm(h [+ pending]); h updated in place when pending."""
@@ -289,61 +317,83 @@ class Q4Llama:
             _lib.call("fh_rms_norm", self.dev.handle, self._p(pending), self._p(b["h"]), self._p(b["h"]),
                       self._p(weight), tokens, c.hidden, ctypes.c_float(c.rms_norm_eps), self._p(b["x"]))
 
+    def _upload(self, st: HipStorage, arr: np.ndarray):
+        _lib.call("fh_upload", self.dev.handle, self._p(st), arr.ctypes.data_as(ctypes.c_void_p), arr.nbytes)
+
     # ---- prefill and decode ----
-    def prefill(self, prompt: np.ndarray) -> None:
-        """Runs the prompt (positions 0..T-1); the first generated id is left
-        on the device."""
-        t = int(prompt.size)
-        if t == 0 or t > self.max_tokens or t >= self.max_len:
-            raise ValueError(f"prompt of {t} tokens does not fit (max_tokens {self.max_tokens}, max_len {self.max_len})")
-        d = self.dev.handle
-        ids = np.ascontiguousarray(prompt, dtype=np.uint32)
-        _lib.call("fh_upload", d, self._p(self.buf["ids"]), ids.ctypes.data_as(ctypes.c_void_p), ids.nbytes)
-        pos = np.arange(t, dtype=np.uint32)
-        _lib.call("fh_upload", d, self._p(self.buf["positions"]), pos.ctypes.data_as(ctypes.c_void_p), pos.nbytes)
+    def step(self, ids: np.ndarray, past: int) -> None:
+        """One forward of ids [batch, T] at positions past..past+T-1 of every
+        sequence (Decoder::step, src/generate/mod.rs:150-204): caches those
+        positions and leaves each sequence's greedy next id on the device
+        (buf['next']) and past + T in buf['pos1']."""
+        ids = np.ascontiguousarray(np.atleast_2d(ids), dtype=np.uint32)
+        rows, t = ids.shape
+        if rows != self.batch:
+            raise ValueError(f"{rows} sequences given to a model built for batch {self.batch}")
+        if t == 0 or t > self.max_tokens or past < 0 or past + t > self.max_len:
+            raise ValueError(f"{t} tokens at position {past} do not fit (max_tokens {self.max_tokens}, "
+                             f"max_len {self.max_len})")
+        self._upload(self.buf["ids"], ids)
+        self._upload(self.buf["positions"], np.tile(np.arange(past, past + t, dtype=np.uint32), rows))
         self._forward(t, self.buf["ids"], self.buf["positions"])
-        p1 = np.array([t], dtype=np.uint32)
-        _lib.call("fh_upload", d, self._p(self.buf["pos1"]), p1.ctypes.data_as(ctypes.c_void_p), 4)
-        self.prompt_len = t
+        self._upload(self.buf["pos1"], np.full(rows, past + t, dtype=np.uint32))
+        self.seq_len = past + t
+
+    def prefill(self, prompt: np.ndarray, past: int = 0) -> None:
+        """Runs the prompt ([T] for one sequence, else [batch, T]) from
+        position `past`; the first generated ids are left on the device."""
+        self.step(prompt, past)
 
     def capture_decode(self, log: HipStorage, capacity: int):
-        """Captures one decode step: the token in buf['next'] at position
-        buf['pos1'] -> next token, logged at log[pos - prompt_len + 1] (index 0
-        is the prefill's token), then position + 1."""
+        """Captures one decode step: each sequence's token in buf['next'] at
+        position buf['pos1'] -> its next token, logged at log[seq, pos -
+        seq_len + 1] (index 0 is the prefill's token), then position + 1."""
         d = self.dev.handle
         self.dev.capture_begin()
         try:
             self._forward(1, self.buf["next"], self.buf["pos1"])
-            _lib.call("fh_append_token", d, self._p(self.buf["next"]), self._p(log), self._p(self.buf["pos1"]),
-                      self.prompt_len - 1, capacity)
-            _lib.call("fh_advance_positions", d, self._p(self.buf["pos1"]), 1, 1)
+            _lib.call("fh_append_token", d, self._p(self.buf["next"]), self.batch, self._p(log),
+                      self._p(self.buf["pos1"]), self.seq_len - 1, capacity)
+            _lib.call("fh_advance_positions", d, self._p(self.buf["pos1"]), self.batch, 1)
         except Exception:
             self.dev.capture_end()
             raise
         return self.dev.capture_end()
 
-    def generate(self, prompt: np.ndarray, new_tokens: int):
+    def generate(self, prompt: np.ndarray, new_tokens: int, depth: np.ndarray | None = None):
         """Greedy generation (src/generate/mod.rs:45-90): returns the new ids
-        (the first is the prefill's argmax)."""
-        self.prefill(prompt)
-        if self.prompt_len + new_tokens > self.max_len:
+        ([new_tokens] for a 1-D prompt, else [batch, new_tokens]; the first
+        is the prefill's argmax). `depth` ([batch, D]) is run first at
+        positions 0..D-1, as the bench's depth rows (src/bench/mod.rs:
+        250-262)."""
+        single = np.ndim(prompt) == 1
+        past = 0
+        if depth is not None and np.size(depth):
+            depth = np.atleast_2d(depth)
+            for s in range(0, depth.shape[1], self.max_tokens):
+                self.step(depth[:, s:s + self.max_tokens], s)
+            past = depth.shape[1]
+        self.step(prompt, past)
+        if self.seq_len + new_tokens - 1 > self.max_len:
             raise ValueError("generation would run past the KV cache")
-        log = self.dev.zeros(4 * max(new_tokens, 1))
-        first = np.empty(1, dtype=np.uint32)
-        _lib.call("fh_download", self.dev.handle, first.ctypes.data_as(ctypes.c_void_p), self._p(self.buf["next"]), 4)
-        if new_tokens <= 1:
-            return first[:new_tokens]
-        graph = self.capture_decode(log, new_tokens)
-        for _ in range(new_tokens - 1):
-            graph.launch()
-        out = np.empty(new_tokens, dtype=np.uint32)
-        _lib.call("fh_download", self.dev.handle, out.ctypes.data_as(ctypes.c_void_p), self._p(log), 4 * new_tokens)
-        out[0] = first[0]
-        return out
+        first = np.empty(self.batch, dtype=np.uint32)
+        _lib.call("fh_download", self.dev.handle, first.ctypes.data_as(ctypes.c_void_p), self._p(self.buf["next"]),
+                  first.nbytes)
+        out = np.zeros((self.batch, max(new_tokens, 0)), dtype=np.uint32)
+        if new_tokens > 1:
+            log = self.dev.zeros(4 * self.batch * new_tokens)
+            graph = self.capture_decode(log, new_tokens)
+            for _ in range(new_tokens - 1):
+                graph.launch()
+            _lib.call("fh_download", self.dev.handle, out.ctypes.data_as(ctypes.c_void_p), self._p(log), out.nbytes)
+        if new_tokens > 0:
+            out[:, 0] = first
+        return out[0] if single else out
 
     def logits(self) -> np.ndarray:
-        """Last computed logits (bf16 bits) of the final position."""
-        out = np.empty(self.cfg.vocab, dtype=np.uint16)
+        """Last computed logits (bf16 bits) of each sequence's final position:
+        [vocab] for batch 1, else [batch, vocab]."""
+        out = np.empty((self.batch, self.cfg.vocab), dtype=np.uint16)
         _lib.call("fh_download", self.dev.handle, out.ctypes.data_as(ctypes.c_void_p), self._p(self.buf["logits"]),
                   out.nbytes)
-        return out
+        return out[0] if self.batch == 1 else out

@@ -288,11 +288,13 @@ int fh_silu_mul(fh_device *dev, const uint16_t *gate_up, int64_t rows, int64_t f
  * x: [rows, n]; out: u32 [rows]. */
 int fh_argmax(fh_device *dev, const uint16_t *x, int64_t rows, int64_t n, uint32_t *out);
 
-/* log[*position - base] = *token when 0 <= *position - base < capacity: the
- * greedy loop's token record, kept on the device so a captured step can be
- * replayed without reading back each token. */
-int fh_append_token(fh_device *dev, const uint32_t *token, uint32_t *log, const uint32_t *position,
-                    int64_t base, int64_t capacity);
+/* For each sequence r < rows: log[r * capacity + position[r] - base] =
+ * token[r] when 0 <= position[r] - base < capacity. The greedy loop's token
+ * record (token_ids per batch row, src/bench/mod.rs:250-300), kept on the
+ * device so a captured step can be replayed without reading back each
+ * token. token, position: u32 [rows]; log: u32 [rows, capacity]. */
+int fh_append_token(fh_device *dev, const uint32_t *token, int64_t rows, uint32_t *log,
+                    const uint32_t *position, int64_t base, int64_t capacity);
 
 /* positions[i] += by for i < n, on the device's stream. */
 int fh_advance_positions(fh_device *dev, uint32_t *positions, int64_t n, int64_t by);

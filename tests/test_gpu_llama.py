@@ -382,3 +382,62 @@ def test_graph_decode_equals_eager_decode(device):
         _lib.call("fh_advance_positions", device.handle, ctypes.c_void_p(b["pos1"].ptr), 1, 1)
         eager.append(int(down(device, b["next"], np.uint32, 1)[0]))
     assert graph_tokens.tolist() == eager
+
+
+@pytest.mark.parametrize("batch", [2, 3, 8])
+def test_batched_generation_with_depth_matches_reference_arithmetic(device, batch):
+    """`batch` sequences generated together after a depth prefix (run in
+    chunks of max_tokens, as the bench's depth rows) match the reference
+    arithmetic run on each sequence alone: batch rows are independent in the
+    reference (every op is row-wise or per sequence). Decode runs the GEMVs
+    at M = batch."""
+    cfg, seed, max_len, n = TINY, 4, 64, 8
+    d_len, t_len = 7, 4
+    depth = synth.token_ids(21 + batch, batch * d_len, cfg.vocab).reshape(batch, d_len)
+    prompt = synth.token_ids(22 + batch, batch * t_len, cfg.vocab).reshape(batch, t_len)
+    model = Q4Llama(device, cfg, seed, max_len, max_tokens=4, batch=batch)
+    got = model.generate(prompt, n, depth=depth)
+    assert got.shape == (batch, n)
+    full = np.concatenate([depth, prompt], axis=1)
+    # GPU top-5 at every step, from batched prefills of the generated prefix
+    wide = Q4Llama(device, cfg, seed, max_len, max_tokens=d_len + t_len + n, batch=batch)
+    got_tops, first_logits = [[] for _ in range(batch)], None
+    for step in range(n):
+        wide.prefill(np.concatenate([full, got[:, :step]], axis=1))
+        lg = R.from_bf16(wide.logits())
+        first_logits = lg if step == 0 else first_logits
+        for s in range(batch):
+            got_tops[s].append(R.top_ids(lg[s], 5))
+    ref = _ref_model(cfg, seed, max_len)
+    for s in range(batch):
+        exp_tokens, exp_tops = ref.generate(full[s], n)
+        assert np.max(np.abs(first_logits[s] - ref.first_logits)) <= 0.03 * np.max(np.abs(ref.first_logits))
+        report = R.compare_generation(got[s], got_tops[s], exp_tokens, exp_tops)
+        print(f"[batched generation b{batch} seq {s}] gpu={got[s].tolist()} ref={exp_tokens.tolist()} {report}",
+              flush=True)
+        assert report["close"], report
+
+
+def test_batched_step_argument_errors(device):
+    model = Q4Llama(device, TINY, 1, 16, max_tokens=4, batch=2)
+    with pytest.raises(ValueError, match="batch 2"):
+        model.step(np.zeros((3, 2), np.uint32), 0)
+    with pytest.raises(ValueError, match="do not fit"):
+        model.step(np.zeros((2, 5), np.uint32), 0)
+    with pytest.raises(ValueError, match="do not fit"):
+        model.step(np.zeros((2, 4), np.uint32), 13)
+    with pytest.raises(ValueError, match="1..65535"):
+        Q4Llama(device, TINY, 1, 16, max_tokens=4, batch=0)
+
+
+def test_append_token_rows(device):
+    """fh_append_token logs each sequence's token at its own position; a
+    position before base or past capacity writes nothing."""
+    tok = up(device, np.array([11, 22, 33, 44], np.uint32))
+    pos = up(device, np.array([5, 7, 4, 9], np.uint32))
+    log = device.zeros(4 * 4 * 4)
+    _lib.call("fh_append_token", device.handle, ctypes.c_void_p(tok.ptr), 4, ctypes.c_void_p(log.ptr),
+              ctypes.c_void_p(pos.ptr), 5, 4)
+    want = np.zeros((4, 4), np.uint32)
+    want[0, 0], want[1, 2] = 11, 22  # row 2 (position 4 < base) and row 3 (index 4 = capacity) write nothing
+    assert np.array_equal(down(device, log, np.uint32, 16).reshape(4, 4), want)
