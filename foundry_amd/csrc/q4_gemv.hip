@@ -1,7 +1,7 @@
 // Shape selection and dispatch of the q4 decode GEMV (kernel in q4_gemv.hpp;
 // one translation unit per row count, q4_gemv_m<M>.hip, so they build in
 // parallel).
-#include "q4_gemv.hpp"
+#include "q4_gemv_mfma.hpp"
 
 namespace fh {
 
@@ -63,6 +63,20 @@ void launch_q4_gemv(hipStream_t stream, uint32_t cus, int m, const GemvArgs &a) 
         case 6: launch_gemv_m<6>(sh.lanes, sh.cpl, stream, cus, a); break;
         case 7: launch_gemv_m<7>(sh.lanes, sh.cpl, stream, cus, a); break;
         default: launch_gemv_m<8>(sh.lanes, sh.cpl, stream, cus, a);
+    }
+}
+
+// Launches the matrix-core GEMV for m (2..8) rows whose staged x fits its
+// LDS budget (the caller checks mf_eligible and splits rows).
+void launch_q4_gemv_mfma(hipStream_t stream, uint32_t cus, int m, const GemvArgs &a) {
+    switch (m) {
+        case 2: launch_gemv_mfma_m<2>(stream, cus, a); break;
+        case 3: launch_gemv_mfma_m<3>(stream, cus, a); break;
+        case 4: launch_gemv_mfma_m<4>(stream, cus, a); break;
+        case 5: launch_gemv_mfma_m<5>(stream, cus, a); break;
+        case 6: launch_gemv_mfma_m<6>(stream, cus, a); break;
+        case 7: launch_gemv_mfma_m<7>(stream, cus, a); break;
+        default: launch_gemv_mfma_m<8>(stream, cus, a);
     }
 }
 

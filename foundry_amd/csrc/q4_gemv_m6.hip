@@ -1,5 +1,5 @@
-// q4 decode GEMV instances for 6 rows of x.
-#include "q4_gemv.hpp"
+// q4 decode GEMV instances (dot2 and matrix-core kernels) for 6 rows of x.
+#include "q4_gemv_mfma.hpp"
 
 namespace fh {
 
@@ -12,6 +12,11 @@ void launch_gemv_m<6>(uint32_t lanes, uint32_t cpl, hipStream_t stream, uint32_t
     }
     FH_GEMV_SHAPES(FH_GEMV_SHAPE)
 #undef FH_GEMV_SHAPE
+}
+
+template <>
+void launch_gemv_mfma_m<6>(hipStream_t stream, uint32_t cus, const GemvArgs &a) {
+    launch_gemv_mfma_dispatch<6>(stream, cus, a);
 }
 
 }  // namespace fh

@@ -1,0 +1,510 @@
+// q4 decode GEMV on the matrix cores, for 2..8 rows of x: the same product
+// as q4_gemv_kernel (y[m, r] = sum_j x[m, j] * (s[r, j/64] * q[r, j] +
+// b[r, j/64]), behind Linear::forward, src/nn/linear.rs:22-35), for the
+// batched decode step (Decoder over batch rows, src/generate/mod.rs:150-204).
+//
+// With several rows the dot2 kernel spends 4 dot2 per row and weight word:
+// at 8 rows the VALU, not HBM, sets its pace. Here v_mfma_f32_16x16x32_bf16
+// does the multiply-adds:
+// - Output tile: 16 weight rows (B columns). A lane holds B column l%16 and
+//   K quarter q = l/16 and loads 16 bytes of its row per instruction: words
+//   4q..4q+3 of a 16-word span, i.e. a pair of groups (q < 2: the even
+//   group, q >= 2: the odd one). MFMA j takes word 4q + j from every quarter.
+// - Groups stay apart in the sums: A row m (< 8) holds x row m on the even
+//   quarters and zeros on the odd ones, A row 8 + m the reverse, so D rows
+//   0..7 sum the even group and rows 8..15 the odd group (no wasted rows for
+//   M <= 8). A lane's D rows then belong to its own quarter's group, so it
+//   applies that group's scale and bias itself: y += s * d + (b - 128 s) * X
+//   in fp32, d = sum x (128 + q) from the MFMAs, X = sum x staged in LDS.
+// - The mask-and-or trick turns a word into bf16 (128 + q) pairs (nibbles e,
+//   e+4) without conversions, exactly; x fragments are staged permuted to
+//   match.
+// - Scale and bias load 2*CH groups per instruction; weight loads run two
+//   chunks (CH group pairs each) ahead of the MFMAs, across task boundaries,
+//   with clamped (never guarded) addresses, so every wait counts exactly.
+// - Work: blocks of 16 wavefronts, persistent; a task is one output tile
+//   (gate and up tiles together for the SiLU epilogue) over a K slice; S
+//   wavefronts split K (S = 1..16) and add their partial tiles in LDS in a
+//   fixed order, so the result is deterministic and the same for every
+//   variant over one weight.
+#pragma once
+
+#include "q4_gemv.hpp"
+
+namespace fh {
+
+constexpr int kMfThreads = 1024;
+constexpr int kMfWaves = kMfThreads / 64;
+// LDS one block may use (gfx950 gives a workgroup up to 160 KB).
+constexpr uint32_t kMfLdsLimit = 160 * 1024;
+
+typedef __attribute__((ext_vector_type(8))) __bf16 mf_bf16x8_t;
+typedef __attribute__((ext_vector_type(4))) float mf_f32x4_t;
+
+__device__ __forceinline__ mf_f32x4_t mf_mfma(const uint4 a, const uint4 b, const mf_f32x4_t c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(mf_bf16x8_t, a),
+                                                   __builtin_bit_cast(mf_bf16x8_t, b), c, 0, 0, 0);
+}
+
+// Output tiles per task: the SiLU epilogue needs the gate tile and its up tile.
+template <int EPI>
+constexpr int mf_tiles_per_task() {
+    return EPI == kEpiSiluMul ? 2 : 1;
+}
+
+// LDS bytes: staged x fragments, a zero slot and a dummy slot, group sums X
+// [G][8], the staged norm weight (norm), the partial tiles of the K split,
+// the norm's per-wavefront sums.
+__host__ __device__ constexpr uint32_t mf_lds_bytes(uint32_t m, uint32_t k, int nt, bool norm) {
+    return m * k * 2 + 32 + (k / kGroup) * 8 * 4 + (norm ? k * 2 : 0) + kMfWaves * nt * 4 * 64 * 4 +
+           kMfWaves * 8 * 4;
+}
+
+// Largest x row count (<= 8) whose staged copy fits the LDS budget.
+inline uint32_t mf_rows_per_launch(uint32_t k, int nt, bool norm) {
+    uint32_t r = 8;
+    while (r > 0 && mf_lds_bytes(r, k, nt, norm) > kMfLdsLimit) --r;
+    return r;
+}
+
+// One chunk (CH group pairs) of operands as a lane holds them: 16 bytes of
+// packed words per pair, and scale / bias of the chunk's groups (one dword
+// per pair: even group low, odd group high).
+template <int NT, int CH>
+struct MfChunk {
+    uint4 w[CH][NT];
+    uint32_t s[CH][NT], b[CH][NT];
+};
+
+// Decodes two packed words into bf16 pairs (128 + q_t, 128 + q_{t+4}); the
+// shifts run on the 64-bit pair (bits crossing between the words land
+// outside the mask).
+__device__ __forceinline__ void mf_decode2(uint32_t w0, uint32_t w1, uint32_t magic, uint4 &b0, uint4 &b1) {
+    constexpr uint32_t kM = 0x000F000Fu;
+    const uint64_t ww = (static_cast<uint64_t>(w1) << 32) | w0;
+    const uint64_t s1 = ww >> 4, s2 = ww >> 8, s3 = ww >> 12;
+    b0 = make_uint4((w0 & kM) | magic, (static_cast<uint32_t>(s1) & kM) | magic,
+                    (static_cast<uint32_t>(s2) & kM) | magic, (static_cast<uint32_t>(s3) & kM) | magic);
+    b1 = make_uint4((w1 & kM) | magic, (static_cast<uint32_t>(s1 >> 32) & kM) | magic,
+                    (static_cast<uint32_t>(s2 >> 32) & kM) | magic, (static_cast<uint32_t>(s3 >> 32) & kM) | magic);
+}
+
+// Sum of a staged (permuted) piece's 8 values.
+__device__ __forceinline__ float mf_piece_sum(const uint4 p) {
+    return ((bf16_to_f32(p.x & 0xFFFFu) + bf16_to_f32(p.y & 0xFFFFu)) +
+            (bf16_to_f32(p.z & 0xFFFFu) + bf16_to_f32(p.w & 0xFFFFu))) +
+           ((bf16_to_f32(p.x >> 16) + bf16_to_f32(p.y >> 16)) + (bf16_to_f32(p.z >> 16) + bf16_to_f32(p.w >> 16)));
+}
+
+// Items the prologue stages in straight-line code (rounds of kMfThreads);
+// beyond, it loops (and the first weight loads wait for it).
+template <int PRO>
+constexpr uint32_t mf_straight_rounds() {
+    return PRO == kProRmsNorm ? 1 : 2;
+}
+
+// M: x rows (1..8). CH: group pairs per chunk (2 or 4). ksplit: wavefronts
+// per task (divides 16; k / 64 / ksplit is a multiple of 2 * CH).
+template <int M, int PRO, int EPI, int CH>
+__global__ __launch_bounds__(kMfThreads) void q4_gemv_mfma_kernel(
+    const uint16_t *__restrict__ x, uint32_t x_ld, const uint32_t *__restrict__ wq,
+    const uint16_t *__restrict__ scales, const uint16_t *__restrict__ biases, uint32_t n, uint32_t k,
+    void *__restrict__ y, uint32_t y_ld, int y_is_f32, GemvFusion fu, uint32_t ksplit) {
+    constexpr int NT = mf_tiles_per_task<EPI>();
+    constexpr bool kNorm = PRO == kProRmsNorm;
+    static_assert(kMfWaves / 2 * M * 16 <= kMfThreads, "a K-split round stores one output per thread at most");
+    extern __shared__ uint4 lds[];
+    const uint32_t G = k / kGroup;
+    const uint32_t wpr = k / 8;  // packed words per weight row
+    const uint32_t n_out = EPI == kEpiSiluMul ? n / 2 : n;
+    const uint32_t tiles = n_out / 16;
+    uint4 *xa = lds;                                         // [G/2][4 j][4 q][M] fragments
+    const uint32_t zero = M * wpr;                           // a zero fragment (dead A lanes)
+    const uint32_t dummy = zero + 1;                         // write-only slot for dead items
+    float *xsum = reinterpret_cast<float *>(lds + dummy + 1);  // [G][8]
+    uint4 *wsh = reinterpret_cast<uint4 *>(xsum + G * 8);    // [k/8] norm weight pieces (permuted)
+    float *red = reinterpret_cast<float *>(wsh + (kNorm ? wpr : 0));  // [16][NT][4][64]
+    float *nsum = red + kMfWaves * NT * 4 * 64;              // [16][8]
+
+    const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const uint32_t col = lane & 15, quarter = lane >> 4, hi = quarter >> 1;
+    const uint32_t slots = kMfWaves / ksplit;
+    const uint32_t slot = wave / ksplit, ks = wave % ksplit;
+    const uint32_t gs = G / ksplit;      // groups per task and wavefront
+    const uint32_t cpt = gs / (2 * CH);  // chunks per task
+    const uint32_t per_round = gridDim.x * slots;
+    const uint32_t rounds = (tiles + per_round - 1) / per_round;
+    const uint32_t total = rounds * cpt;  // chunks of this wavefront
+    auto tile_of = [&](uint32_t r) { return (r * gridDim.x + blockIdx.x) * slots + slot; };
+
+    // ---- weight operands ----
+    auto wrow = [&](uint32_t tile, int t) { return (EPI == kEpiSiluMul && t == 1 ? n_out : 0u) + tile * 16 + col; };
+    // chunk c (of this wavefront's sequence) -> operands; past the end, the
+    // last chunk again (values unused)
+    auto load = [&](uint32_t c, MfChunk<NT, CH> &cb) {
+        const uint32_t cc = c < total ? c : total - 1;
+        const uint32_t r = cc / cpt;
+        const uint32_t p0 = (ks * gs) / 2 + (cc % cpt) * CH;  // first pair
+        uint32_t tile = tile_of(r);
+        tile = tile < tiles ? tile : tiles - 1;
+#pragma unroll
+        for (int t = 0; t < NT; ++t) {
+            const uint64_t row = wrow(tile, t);
+            const uint4 *wp = reinterpret_cast<const uint4 *>(wq + row * wpr + p0 * 16 + quarter * 4);
+#pragma unroll
+            for (int c2 = 0; c2 < CH; ++c2) cb.w[c2][t] = wp[c2 * 4];
+            const uint16_t *sp = scales + row * G + p0 * 2, *bp = biases + row * G + p0 * 2;
+            if constexpr (CH == 4) {
+                const uint4 sv = *reinterpret_cast<const uint4 *>(sp), bv = *reinterpret_cast<const uint4 *>(bp);
+                cb.s[0][t] = sv.x, cb.s[1][t] = sv.y, cb.s[2][t] = sv.z, cb.s[3][t] = sv.w;
+                cb.b[0][t] = bv.x, cb.b[1][t] = bv.y, cb.b[2][t] = bv.z, cb.b[3][t] = bv.w;
+            } else {
+                const uint2 sv = *reinterpret_cast<const uint2 *>(sp), bv = *reinterpret_cast<const uint2 *>(bp);
+                cb.s[0][t] = sv.x, cb.s[1][t] = sv.y;
+                cb.b[0][t] = bv.x, cb.b[1][t] = bv.y;
+            }
+        }
+    };
+    MfChunk<NT, CH> buf[2];
+    // two chunks in flight, issued in buffer order (pinned) so the first
+    // waits count the later loads instead of draining them
+    auto prefetch = [&]() {
+        __builtin_amdgcn_sched_barrier(0);
+        load(0, buf[0]);
+        __builtin_amdgcn_sched_barrier(0);
+        load(1, buf[1]);
+        __builtin_amdgcn_sched_barrier(0);
+    };
+
+    // ---- prologue: stage x (or RMSNorm(x + res)) as fragments, and X ----
+    // Item e = (m * G + g) * 2 + h: pieces 4h..4h+3 (8 values each) of group
+    // g of row m. Word w (0..15) of pair p takes fragment ((p * 4 + w % 4) *
+    // 4 + w / 4) * M + m.
+    const uint32_t items = M * G * 2;
+    const uint32_t x_stride = kNorm ? k : x_ld;
+    const bool has_res = kNorm && fu.res != nullptr;
+    const uint16_t *res_src = has_res ? fu.res : x;  // loaded unconditionally; used only with a residual
+    auto frag = [&](uint32_t m, uint32_t g, uint32_t pc) {  // pc: piece in group (0..7)
+        const uint32_t w = (g & 1) * 8 + pc;
+        return (((g >> 1) * 4 + (w & 3)) * 4 + (w >> 2)) * M + m;
+    };
+    struct Item {
+        uint4 v[4], r[kNorm ? 4 : 1];
+    };
+    auto item_load = [&](uint32_t e, Item &it) {
+        const uint32_t ec = e < items ? e : 0;
+        const uint32_t m = ec / (2 * G), g = (ec >> 1) % G, h = ec & 1;
+        const uint64_t o = static_cast<uint64_t>(m) * x_stride + g * kGroup + h * 32;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) it.v[i] = *reinterpret_cast<const uint4 *>(x + o + i * 8);
+        if constexpr (kNorm) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) it.r[i] = *reinterpret_cast<const uint4 *>(res_src + o + i * 8);
+        }
+    };
+    float ss[M];
+#pragma unroll
+    for (int m = 0; m < M; ++m) ss[m] = 0.f;
+    // pass 1: h = x (+ res) staged; X (plain) or sum of squares (norm)
+    auto item_pass1 = [&](uint32_t e, const Item &it) {
+        const bool live = e < items;
+        const uint32_t ec = live ? e : 0;
+        const uint32_t m = ec / (2 * G), g = (ec >> 1) % G, h = ec & 1;
+        const uint64_t o = static_cast<uint64_t>(m) * x_stride + g * kGroup + h * 32;
+        float acc = 0.f;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            uint4 hv = it.v[i];
+            if constexpr (kNorm) {
+                if (has_res) {
+                    hv = gemv_pairwise(hv, it.r[i], [](float a, float b) { return a + b; });
+                    if (blockIdx.x == 0 && fu.res_out && live) *reinterpret_cast<uint4 *>(fu.res_out + o + i * 8) = hv;
+                }
+                const uint32_t w4[4] = {hv.x, hv.y, hv.z, hv.w};
+#pragma unroll
+                for (int e2 = 0; e2 < 4; ++e2) {
+                    const float lo = bf16_to_f32(w4[e2] & 0xFFFFu), up = bf16_to_f32(w4[e2] >> 16);
+                    acc += lo * lo;
+                    acc += up * up;
+                }
+                xa[live ? frag(m, g, h * 4 + i) : dummy] = gemv_permute(hv);
+            } else {
+                const uint4 p = gemv_permute(hv);
+                xa[live ? frag(m, g, h * 4 + i) : dummy] = p;
+                acc += mf_piece_sum(p);
+            }
+        }
+        if constexpr (kNorm) {
+#pragma unroll
+            for (int mm = 0; mm < M; ++mm)
+                if (live && mm == static_cast<int>(m)) ss[mm] += acc;
+        } else {
+            acc += __shfl_xor(acc, 1, 64);  // the item's other half (lanes e, e ^ 1)
+            if (live && h == 0) xsum[g * 8 + m] = acc;
+        }
+    };
+    uint4 wn = make_uint4(0u, 0u, 0u, 0u);  // this thread's norm-weight piece
+    auto wn_load = [&]() {
+        if constexpr (kNorm) wn = *reinterpret_cast<const uint4 *>(fu.w + (threadIdx.x < wpr ? threadIdx.x : 0) * 8);
+    };
+    auto wn_stage = [&]() {
+        if constexpr (kNorm) *(threadIdx.x < wpr ? wsh + threadIdx.x : xa + dummy) = gemv_permute(wn);
+    };
+    constexpr uint32_t kStraight = mf_straight_rounds<PRO>() * kMfThreads;
+    if (items <= kStraight && (!kNorm || wpr <= kMfThreads)) {
+        Item it[mf_straight_rounds<PRO>()];
+#pragma unroll
+        for (uint32_t rr = 0; rr < mf_straight_rounds<PRO>(); ++rr) item_load(threadIdx.x + rr * kMfThreads, it[rr]);
+        wn_load();
+        prefetch();
+#pragma unroll
+        for (uint32_t rr = 0; rr < mf_straight_rounds<PRO>(); ++rr) item_pass1(threadIdx.x + rr * kMfThreads, it[rr]);
+        wn_stage();
+    } else {
+        for (uint32_t e0 = 0; e0 < items; e0 += kMfThreads) {
+            Item it;
+            item_load(e0 + threadIdx.x, it);
+            item_pass1(e0 + threadIdx.x, it);
+        }
+        if constexpr (kNorm) {
+            for (uint32_t t = threadIdx.x; t < wpr; t += kMfThreads)
+                wsh[t] = gemv_permute(*reinterpret_cast<const uint4 *>(fu.w + t * 8));
+        }
+        prefetch();
+    }
+    // the zero fragment; X = 0 for rows M..7
+    if (threadIdx.x == 0) xa[zero] = make_uint4(0u, 0u, 0u, 0u);
+    for (uint32_t t = threadIdx.x; t < (8 - M) * G; t += kMfThreads) xsum[(t % G) * 8 + M + t / G] = 0.f;
+    if constexpr (kNorm) {
+#pragma unroll
+        for (int m = 0; m < M; ++m) {
+            float v = ss[m];
+#pragma unroll
+            for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
+            if (lane == 0) nsum[wave * 8 + m] = v;
+        }
+        __syncthreads();
+        // pass 2: x' = RNE(RNE(h * scale) * w) in place, and X
+        for (uint32_t e0 = 0; e0 < items; e0 += kMfThreads) {
+            const uint32_t e = e0 + threadIdx.x;
+            const bool live = e < items;
+            const uint32_t ec = live ? e : 0;
+            const uint32_t m = ec / (2 * G), g = (ec >> 1) % G, h = ec & 1;
+            float tot = 0.f;
+            for (int w = 0; w < kMfWaves; ++w) tot += nsum[w * 8 + m];
+            const float scale = 1.0f / sqrtf(tot * fu.dim_inv + fu.eps);
+            float acc = 0.f;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const uint32_t f = frag(m, g, h * 4 + i);
+                const uint4 p = gemv_pairwise(xa[f], wsh[g * 8 + h * 4 + i], [scale](float hh, float gg) {
+                    return bf16_to_f32(f32_to_bf16_rne(hh * scale)) * gg;
+                });
+                xa[live ? f : dummy] = p;
+                acc += mf_piece_sum(p);
+            }
+            acc += __shfl_xor(acc, 1, 64);
+            if (live && h == 0) xsum[g * 8 + m] = acc;
+        }
+    }
+    __syncthreads();
+
+    // ---- main loop ----
+    uint32_t magic = 0x43004300u;  // in a VGPR: v_and_or_b32 takes no literal on gfx9
+    asm volatile("" : "+v"(magic));
+    // A row of this lane: x row col % 8 on its own half's quarters, else the
+    // zero fragment (stride 0: every fragment of a dead lane reads it)
+    const uint32_t am = col & 7;
+    const bool alive = (col >> 3) == hi && am < static_cast<uint32_t>(M);
+    const uint4 *abase = alive ? xa + quarter * M + am : xa + zero;
+    const uint32_t astride = alive ? 4 * M : 0;  // per (pair, j) step
+
+    mf_f32x4_t acc[NT];
+#pragma unroll
+    for (int t = 0; t < NT; ++t) acc[t] = mf_f32x4_t{0.f, 0.f, 0.f, 0.f};
+
+    // the task of round r is complete: even + odd halves, the K slices, epilogue, store
+    auto finish = [&](uint32_t r) {
+        auto store = [&](uint32_t m, uint32_t c, uint32_t tile, float v) {
+            const uint64_t o = static_cast<uint64_t>(m) * y_ld + tile * 16 + c;
+            if (y_is_f32)
+                static_cast<float *>(y)[o] = v;
+            else
+                static_cast<uint16_t *>(y)[o] = static_cast<uint16_t>(f32_to_bf16_rne(v));
+        };
+        auto epilogue = [](float gsum, float usum) {
+            if constexpr (EPI == kEpiSiluMul) {
+                const float g = bf16_to_f32(f32_to_bf16_rne(gsum));
+                const float u = bf16_to_f32(f32_to_bf16_rne(usum));
+                return bf16_to_f32(f32_to_bf16_rne(g / (expf(-g) + 1.0f))) * u;
+            } else {
+                return gsum;
+            }
+        };
+        float v[NT][4];
+#pragma unroll
+        for (int t = 0; t < NT; ++t)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) v[t][i] = acc[t][i] + __shfl_xor(acc[t][i], 32, 64);  // lanes < 32: totals
+        if (ksplit == 1) {
+            const uint32_t tile = tile_of(r);
+            if (tile < tiles && quarter < 2) {
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const uint32_t m = quarter * 4 + i;
+                    if (m < static_cast<uint32_t>(M)) store(m, col, tile, epilogue(v[0][i], v[NT - 1][i]));
+                }
+            }
+        } else {
+#pragma unroll
+            for (int t = 0; t < NT; ++t)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) red[((wave * NT + t) * 4 + i) * 64 + lane] = v[t][i];
+            __syncthreads();
+            // slots * M * 16 <= kMfThreads: one output per thread at most, and
+            // no store loop (a store loop inside the main loop would make every
+            // weight wait drain the whole pipeline)
+            const uint32_t e = threadIdx.x;
+            if (e < slots * M * 16) {
+                const uint32_t sl = e / (M * 16), m = (e / 16) % M, c = e % 16;
+                const uint32_t tile = (r * gridDim.x + blockIdx.x) * slots + sl;
+                const uint32_t i = m & 3, ln = (m >> 2) * 16 + c;
+                float sum[NT];
+#pragma unroll
+                for (int t = 0; t < NT; ++t) {
+                    sum[t] = 0.f;
+                    for (uint32_t s = 0; s < ksplit; ++s) sum[t] += red[(((sl * ksplit + s) * NT + t) * 4 + i) * 64 + ln];
+                }
+                if (tile < tiles) store(m, c, tile, epilogue(sum[0], sum[NT - 1]));
+            }
+            __syncthreads();
+        }
+    };
+
+    uint32_t cr = 0, cc = 0;  // compute position: round, chunk in task
+    // Chunks past `total` (to an even count) compute on reloaded operands and
+    // are dropped: loads and MFMAs stay unconditional.
+    for (uint32_t c0 = 0; c0 < total; c0 += 2) {
+#pragma unroll
+        for (int d = 0; d < 2; ++d) {
+            const uint32_t p0 = (ks * gs) / 2 + cc * CH;
+#pragma unroll
+            for (int c2 = 0; c2 < CH; ++c2) {
+                const uint32_t p = p0 + c2;
+                const float4 xv = *reinterpret_cast<const float4 *>(xsum + (2 * p + hi) * 8 + 4 * (quarter & 1));
+                uint4 a[4];
+#pragma unroll
+                for (int j = 0; j < 4; ++j) a[j] = abase[(p * 4 + j) * astride];
+#pragma unroll
+                for (int t = 0; t < NT; ++t) {
+                    const uint4 wv = buf[d].w[c2][t];
+                    uint4 b0, b1, b2, b3;
+                    mf_decode2(wv.x, wv.y, magic, b0, b1);
+                    mf_decode2(wv.z, wv.w, magic, b2, b3);
+                    mf_f32x4_t dv = mf_mfma(a[0], b0, mf_f32x4_t{0.f, 0.f, 0.f, 0.f});
+                    dv = mf_mfma(a[1], b1, dv);
+                    dv = mf_mfma(a[2], b2, dv);
+                    dv = mf_mfma(a[3], b3, dv);
+                    const uint32_t sb = hi ? buf[d].s[c2][t] >> 16 : buf[d].s[c2][t] & 0xFFFFu;
+                    const uint32_t bb = hi ? buf[d].b[c2][t] >> 16 : buf[d].b[c2][t] & 0xFFFFu;
+                    const float s = bf16_to_f32(sb);
+                    const float bc = fmaf(-128.f, s, bf16_to_f32(bb));
+                    acc[t][0] = fmaf(bc, xv.x, fmaf(s, dv[0], acc[t][0]));
+                    acc[t][1] = fmaf(bc, xv.y, fmaf(s, dv[1], acc[t][1]));
+                    acc[t][2] = fmaf(bc, xv.z, fmaf(s, dv[2], acc[t][2]));
+                    acc[t][3] = fmaf(bc, xv.w, fmaf(s, dv[3], acc[t][3]));
+                }
+            }
+            load(c0 + d + 2, buf[d]);
+            if (cc == cpt - 1 && cr < rounds) {  // uniform across the block
+                finish(cr);
+#pragma unroll
+                for (int t = 0; t < NT; ++t) acc[t] = mf_f32x4_t{0.f, 0.f, 0.f, 0.f};
+            }
+            if (++cc == cpt) {
+                cc = 0;
+                ++cr;
+            }
+        }
+    }
+}
+
+// Picks the K split (wavefronts per task) from the weight's 16-row tiles, its
+// groups and the CU count only (one block per CU), so that every variant over
+// the same weight (SiLU pairs included) adds the same partial sums in the
+// same order: the fewest rounds of tiles times groups per wavefront (the
+// critical path), then the fewest rounds, then the smallest split (less
+// reduction). A split leaves each wavefront a multiple of 4 groups; 0 if none
+// does.
+inline uint32_t pick_mf_split(uint32_t weight_tiles, uint32_t groups, uint32_t cus) {
+    uint32_t best_s = 0;
+    uint64_t best_cost = ~0ull, best_rounds = ~0ull;
+    for (uint32_t s = 1; s <= static_cast<uint32_t>(kMfWaves); s *= 2) {
+        if (groups % (s * 4) != 0) continue;
+        const uint32_t slots = kMfWaves / s;
+        const uint32_t need = (weight_tiles + slots - 1) / slots;
+        const uint64_t blocks = need < cus ? need : cus;
+        const uint64_t rounds = (weight_tiles + blocks * slots - 1) / (blocks * slots);
+        const uint64_t cost = rounds * (groups / s);
+        if (cost < best_cost || (cost == best_cost && rounds < best_rounds)) {
+            best_s = s;
+            best_cost = cost;
+            best_rounds = rounds;
+        }
+    }
+    return best_s;
+}
+
+template <int M, int PRO, int EPI, int CH>
+inline void launch_gemv_mfma_t(hipStream_t stream, uint32_t cus, const GemvArgs &a, uint32_t ksplit) {
+    auto kernel = q4_gemv_mfma_kernel<M, PRO, EPI, CH>;
+    const uint32_t lds = mf_lds_bytes(M, a.k, mf_tiles_per_task<EPI>(), PRO == kProRmsNorm);
+    int per_cu = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, kMfThreads, lds) != hipSuccess || per_cu < 1)
+        per_cu = 1;
+    const uint32_t n_out = EPI == kEpiSiluMul ? a.n / 2 : a.n;
+    const uint32_t slots = kMfWaves / ksplit;
+    const uint32_t need = (n_out / 16 + slots - 1) / slots;
+    const uint32_t cap = cus * static_cast<uint32_t>(per_cu);
+    hipLaunchKernelGGL(kernel, dim3(need < cap ? need : cap), dim3(kMfThreads), lds, stream, a.x, a.x_ld, a.wq,
+                       a.s, a.b, a.n, a.k, a.y, a.y_ld, a.y_is_f32, a.fu, ksplit);
+}
+
+// Whether the matrix-core GEMV takes this launch of 2..8 rows: k a multiple of
+// 256 with a K split for it, 16-row output tiles, 16-byte aligned operands,
+// and at least 2 x rows staged per launch (the caller splits larger m).
+inline bool mf_eligible(uint32_t m, const GemvArgs &a) {
+    const uint32_t n_out = a.epi == kEpiSiluMul ? a.n / 2 : a.n;
+    if (m < 2 || m > 8 || a.k == 0 || a.k % (kGroup * 4) != 0 || n_out == 0 || n_out % 16 != 0 ||
+        a.x_ld % 8 != 0)
+        return false;
+    if ((reinterpret_cast<uintptr_t>(a.wq) | reinterpret_cast<uintptr_t>(a.s) | reinterpret_cast<uintptr_t>(a.b)) & 15u)
+        return false;
+    return mf_rows_per_launch(a.k, a.epi == kEpiSiluMul ? 2 : 1, a.pro == kProRmsNorm) >= 2;
+}
+
+// Defined in q4_gemv_m<M>.hip.
+template <int M>
+void launch_gemv_mfma_m(hipStream_t stream, uint32_t cus, const GemvArgs &a);
+
+// Chunk width: 4 group pairs when each wavefront's slice allows it (one
+// 16-byte scale and one bias load per 8 groups), else 2; the SiLU variant
+// keeps 2 (two tiles of buffers).
+template <int M>
+inline void launch_gemv_mfma_dispatch(hipStream_t stream, uint32_t cus, const GemvArgs &a) {
+    const uint32_t groups = a.k / kGroup;
+    const uint32_t ksplit = pick_mf_split(a.n / 16, groups, cus);
+    const bool wide = (groups / ksplit) % 8 == 0;
+    if (a.epi == kEpiSiluMul) {
+        if (a.pro == kProRmsNorm) launch_gemv_mfma_t<M, kProRmsNorm, kEpiSiluMul, 2>(stream, cus, a, ksplit);
+        else launch_gemv_mfma_t<M, kProNone, kEpiSiluMul, 2>(stream, cus, a, ksplit);
+    } else if (a.pro == kProRmsNorm) {
+        if (wide) launch_gemv_mfma_t<M, kProRmsNorm, kEpiNone, 4>(stream, cus, a, ksplit);
+        else launch_gemv_mfma_t<M, kProRmsNorm, kEpiNone, 2>(stream, cus, a, ksplit);
+    } else {
+        if (wide) launch_gemv_mfma_t<M, kProNone, kEpiNone, 4>(stream, cus, a, ksplit);
+        else launch_gemv_mfma_t<M, kProNone, kEpiNone, 2>(stream, cus, a, ksplit);
+    }
+}
+
+}  // namespace fh

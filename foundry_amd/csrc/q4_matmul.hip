@@ -4,7 +4,7 @@
 // (src/nn/primitive.rs:234-256 for the shape rule), then pick the kernel. The
 // reference has one tiled kernel for every shape; here m <= 8 goes to the
 // decode GEMV and larger m to the MFMA GEMM.
-#include "q4_gemv.hpp"
+#include "q4_gemv_mfma.hpp"
 
 namespace fh {
 
@@ -12,6 +12,7 @@ int check_q4_table(const fh_device *dev, const char *fn, const uint32_t *wq,
                    const uint16_t *scales, const uint16_t *biases, int64_t rows, int64_t k,
                    int64_t group);
 void launch_q4_gemv(hipStream_t stream, uint32_t cus, int m, const GemvArgs &a);
+void launch_q4_gemv_mfma(hipStream_t stream, uint32_t cus, int m, const GemvArgs &a);
 uint32_t gemv_rows_per_launch(uint32_t k, bool norm);
 void launch_q4_gemm(hipStream_t stream, const uint16_t *x, uint32_t x_ld, const uint32_t *wq,
                     const uint16_t *s, const uint16_t *b, uint32_t m, uint32_t n, uint32_t k,
@@ -21,10 +22,14 @@ void launch_q4_gemm(hipStream_t stream, const uint16_t *x, uint32_t x_ld, const 
 constexpr int64_t kGemvMaxRows = 8;
 
 // Launches the GEMV over m rows in groups whose staged x fits LDS (every
-// prologue and epilogue is row-independent); x, res, res_out and y advance
-// by their row strides. y_cols: columns of y per row.
+// prologue and epilogue is row-independent): the matrix-core kernel for
+// groups of 2..8 rows where it takes the shape, else the dot2 kernel; x,
+// res, res_out and y advance by their row strides. y_cols: columns of y per
+// row.
 int launch_gemv_rows(fh_device *dev, const char *fn, int64_t m, const GemvArgs &base, int64_t y_cols) {
-    const int64_t per = gemv_rows_per_launch(base.k, base.pro == kProRmsNorm);
+    const bool mf = m >= 2 && mf_eligible(static_cast<uint32_t>(m), base);
+    const int64_t per = mf ? mf_rows_per_launch(base.k, base.epi == kEpiSiluMul ? 2 : 1, base.pro == kProRmsNorm)
+                           : gemv_rows_per_launch(base.k, base.pro == kProRmsNorm);
     for (int64_t r0 = 0; r0 < m; r0 += per) {
         const int rows = static_cast<int>(m - r0 < per ? m - r0 : per);
         GemvArgs a = base;
@@ -33,7 +38,12 @@ int launch_gemv_rows(fh_device *dev, const char *fn, int64_t m, const GemvArgs &
         if (a.fu.res_out) a.fu.res_out += r0 * base.k;
         a.y = base.y_is_f32 ? static_cast<void *>(static_cast<float *>(base.y) + r0 * y_cols)
                             : static_cast<void *>(static_cast<uint16_t *>(base.y) + r0 * y_cols);
-        int rc = dispatch(dev, fn, [&] { launch_q4_gemv(dev->stream, dev->compute_units, rows, a); });
+        int rc = dispatch(dev, fn, [&] {
+            if (mf && rows >= 2)
+                launch_q4_gemv_mfma(dev->stream, dev->compute_units, rows, a);
+            else
+                launch_q4_gemv(dev->stream, dev->compute_units, rows, a);
+        });
         if (rc) return rc;
     }
     return FH_OK;
