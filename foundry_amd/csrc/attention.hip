@@ -30,6 +30,10 @@
 // spreads one row over many CUs, prefill keeps one block per (row, KV head).
 #include "decoder_common.hpp"
 
+#ifndef FH_PV_CHUNKED_MIN_KEYS
+#define FH_PV_CHUNKED_MIN_KEYS 16384
+#endif
+
 namespace fh {
 
 constexpr int kAttnChunk = 64;
@@ -39,12 +43,24 @@ constexpr int kAttnMaxGroup = 8;
 constexpr uint64_t kAttnTargetBlocks = 1024;
 
 // Workspace: per-chunk softmax statistics [rows][n_heads][nck] float2, then
-// the scores [rows][n_heads][max_len] f32. splits: blocks per (row, KV head)
-// of the scores kernel; slices: blocks per (row, KV head) of the P.V kernel,
-// each over head_dim / slices dims (at least 16).
+// the scores [rows][n_heads][max_len] f32, then (chunked P.V) the partial
+// outputs [rows][n_kv][chunks][G][head_dim] f32. splits: blocks per (row, KV
+// head) of the scores kernel. P.V runs one of two ways:
+//   sliced: blocks per (row, KV head) = slices, each over head_dim / slices
+//     dims (at least 16) and all keys -- few, short rows (no combine pass);
+//   chunked: blocks per (row, KV head) = chunks of chunk_keys keys over all
+//     dims (16-byte V loads), then a combine pass adds the chunks -- long or
+//     many rows.
 struct AttnLayout {
-    uint64_t nck, splits, slices, scores, total;  // stats at byte 0
+    uint64_t nck, splits, slices, scores, part, total;  // stats at byte 0
+    uint64_t chunks, chunk_keys;                         // chunks == 0: sliced P.V
 };
+
+constexpr int kPvTile = 64;  // keys per tile of the chunked P.V
+// The sliced P.V reads V in 4-byte pieces (a 16-dim slice of a key row is 32
+// bytes): below this many keys per (row, KV head) pair, summed over the
+// launch, it still wins by skipping the combine pass.
+constexpr uint64_t kPvChunkedMinKeys = FH_PV_CHUNKED_MIN_KEYS;
 
 static AttnLayout attn_layout(uint64_t rows, uint64_t n_heads, uint64_t n_kv, uint64_t head_dim,
                               uint64_t max_len) {
@@ -58,7 +74,16 @@ static AttnLayout attn_layout(uint64_t rows, uint64_t n_heads, uint64_t n_kv, ui
     a.slices = 1;
     while (a.slices * 2 <= want && head_dim / (a.slices * 2) >= 16) a.slices *= 2;
     a.scores = round_up(rows * n_heads * a.nck * 8);
-    a.total = a.scores + round_up(rows * n_heads * max_len * 4);
+    a.part = a.scores + round_up(rows * n_heads * max_len * 4);
+    a.chunks = a.chunk_keys = 0;
+    if (blocks * max_len >= kPvChunkedMinKeys) {
+        const uint64_t tiles = (max_len + kPvTile - 1) / kPvTile;
+        uint64_t chunks = want < tiles ? want : tiles;
+        if (chunks == 0) chunks = 1;
+        a.chunk_keys = (tiles + chunks - 1) / chunks * kPvTile;
+        a.chunks = (max_len + a.chunk_keys - 1) / a.chunk_keys;
+    }
+    a.total = a.part + (a.chunks > 1 ? round_up(rows * n_heads * a.chunks * head_dim * 4) : 0);
     return a;
 }
 
@@ -67,16 +92,33 @@ static AttnLayout attn_layout(uint64_t rows, uint64_t n_heads, uint64_t n_kv, ui
 // Otherwise q_src is the rotated q [rows, n_heads * HD] and the cache is
 // complete. Rows whose position is >= pos_limit are skipped (the PV kernel
 // writes their zero output).
+//
+// The dot products run on the matrix cores: v_mfma_f32_16x16x32_bf16 with
+// the G query heads as A rows (rows >= G zero, fragments held for the whole
+// block) and 16 keys as B columns; a lane loads 16 bytes of its key per
+// instruction (16 key rows x 64 bytes per wavefront load). Each wavefront
+// scores whole chunks of kAttnChunk keys on its own (chunks split +
+// splits * (wave + 4 i)) and reduces the chunk's max and sum of exp across
+// its 16-lane rows, so the loop has no block barrier.
+typedef __attribute__((ext_vector_type(8))) __bf16 attn_bf16x8_t;
+typedef __attribute__((ext_vector_type(4))) float attn_f32x4_t;
+
+__device__ __forceinline__ attn_f32x4_t attn_mfma(const uint4 a, const uint4 b, const attn_f32x4_t c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(attn_bf16x8_t, a),
+                                                   __builtin_bit_cast(attn_bf16x8_t, b), c, 0, 0, 0);
+}
+
 template <int HD, int G, bool ROPE>
 __global__ __launch_bounds__(kAttnThreads) void attn_scores_kernel(
     const uint16_t *__restrict__ q_src, const uint16_t *__restrict__ cos_tab, const uint16_t *__restrict__ sin_tab,
     const uint32_t *__restrict__ positions, uint32_t pos_limit, uint16_t *__restrict__ k_cache,
     uint16_t *__restrict__ v_cache, uint64_t row_stride, uint32_t n_heads, uint32_t n_kv, uint32_t max_len,
     uint32_t nck, uint32_t splits, float scale, float *__restrict__ scores, float2 *__restrict__ stats) {
-    constexpr int LPK = HD / 8, KPI = 64 / LPK, IT = kAttnChunk / kAttnWaves / KPI;
+    constexpr int KS = HD / 32;       // MFMA k steps per key group
     constexpr uint32_t PPH = HD / 8;  // 8-dim pieces per head
-    __shared__ float sc[G][kAttnChunk];
-    __shared__ float qs[ROPE ? G : 1][ROPE ? HD : 1];
+    static_assert(kAttnChunk == 64, "a chunk is 4 groups of 16 keys");
+    static_assert(G <= 16, "query heads fit the MFMA rows");
+    __shared__ __align__(16) uint16_t qb[ROPE ? G : 1][ROPE ? HD : 8];
     __shared__ __align__(16) uint16_t knew[ROPE ? HD : 8];
     const uint32_t tid = threadIdx.x, r = blockIdx.y, kvh = blockIdx.x / splits, split = blockIdx.x % splits;
     const uint32_t pos = positions[r];
@@ -85,97 +127,110 @@ __global__ __launch_bounds__(kAttnThreads) void attn_scores_kernel(
     const uint32_t nact = (ctx + kAttnChunk - 1) / kAttnChunk;
     if (split >= nact) return;
     const uint32_t h0 = kvh * G;
-    const uint32_t wave = tid >> 6, lane = tid & 63, ks = lane / LPK, li = lane % LPK;
+    const uint32_t wave = tid >> 6, lane = tid & 63, col = lane & 15, quad = lane >> 4;
     const uint64_t cache = static_cast<uint64_t>(r) * row_stride + static_cast<uint64_t>(kvh) * max_len * HD;
-    // keys below kmax come from the cache; with ROPE key pos is the new one
-    // (from LDS, substituted when the chunk is scored)
+    // keys below kmax come from the cache; with ROPE key pos is the new one (from LDS)
     const uint32_t kmax = ROPE ? pos : ctx;
-    const uint16_t *kb = k_cache + cache + li * 8;
-    auto load_chunk = [&](uint32_t c, uint4 (&kr)[IT]) {
-        const uint32_t jw = c * kAttnChunk + wave * (kAttnChunk / kAttnWaves) + ks;
+    const uint32_t c_first = split + splits * wave, c_step = splits * kAttnWaves;
+    // key groups (16 keys) of this wavefront; 0 for a wavefront without chunks
+    const uint32_t total = c_first < nact ? (nact - c_first + c_step - 1) / c_step * 4 : 0;
+    const uint16_t *kb = k_cache + cache + 8 * quad;
+    // group f -> B fragments of its 16 keys (clamped past the context / the
+    // wavefront's last group; such values are masked or unused)
+    auto load_grp = [&](uint32_t f, uint4 (&b)[KS]) {
+        const uint32_t fc = total ? (f < total ? f : total - 1) : 0;
+        const uint32_t j = (c_first + (fc / 4) * c_step) * kAttnChunk + (fc % 4) * 16 + col;
+        const uint32_t jc = j < kmax ? j : (kmax ? kmax - 1 : 0);
 #pragma unroll
-        for (int it = 0; it < IT; ++it) {
-            const uint32_t j = jw + it * KPI;
-            kr[it] = j < kmax ? *reinterpret_cast<const uint4 *>(kb + static_cast<uint64_t>(j) * HD)
-                              : make_uint4(0u, 0u, 0u, 0u);
-        }
+        for (int st = 0; st < KS; ++st) b[st] = *reinterpret_cast<const uint4 *>(kb + static_cast<uint64_t>(jc) * HD + 32 * st);
     };
-    uint4 kr[IT];
-    load_chunk(split, kr);  // in flight during the q set-up
-    float qf[G][8];
-    uint4 kn = make_uint4(0u, 0u, 0u, 0u);
+    // Loads go out in this order, unconditionally (clamped indices): the RoPE
+    // inputs, the q fragments, then the first two key groups, so the set-up
+    // waits for its own loads only.
+    const bool hlive = col < static_cast<uint32_t>(G);
+    const uint32_t hc = hlive ? col : 0;
+    uint4 a[KS];
+    uint4 x4, r4, c4, s4, v4;
+    const uint32_t tr = tid < (G + 1) * PPH ? tid : 0;
+    const uint32_t hh = tr / PPH, pp = tr % PPH;  // hh < G: query head h0 + hh; hh == G: the key
+    const uint16_t *row = q_src + static_cast<uint64_t>(r) * (n_heads + 2 * n_kv) * HD;
     if constexpr (ROPE) {
-        const uint16_t *row = q_src + static_cast<uint64_t>(r) * (n_heads + 2 * n_kv) * HD;
-        const uint16_t *c = cos_tab + static_cast<uint64_t>(pos) * HD;
-        const uint16_t *s = sin_tab + static_cast<uint64_t>(pos) * HD;
-        const bool owner = (pos / kAttnChunk) % splits == split;
-        if (tid < (G + 1) * PPH) {
-            const uint32_t hh = tid / PPH, p = tid % PPH;  // hh < G: query head h0 + hh; hh == G: the key
-            const uint16_t *head = row + static_cast<uint64_t>(hh < G ? h0 + hh : n_heads + kvh) * HD;
-            const uint4 ov = rope_piece(head, c, s, p, PPH / 2);
-            if (hh < G) {
-                float f[8];
-                unpack8(ov, f);
-#pragma unroll
-                for (int e = 0; e < 8; ++e) qs[hh][p * 8 + e] = f[e];
-            } else {
-                *reinterpret_cast<uint4 *>(knew + p * 8) = ov;
-                if (owner) *reinterpret_cast<uint4 *>(k_cache + cache + static_cast<uint64_t>(pos) * HD + p * 8) = ov;
-            }
-        } else if (owner && tid < (G + 2) * PPH) {
-            const uint32_t p = tid - (G + 1) * PPH;
-            *reinterpret_cast<uint4 *>(v_cache + cache + static_cast<uint64_t>(pos) * HD + p * 8) =
-                *reinterpret_cast<const uint4 *>(row + static_cast<uint64_t>(n_heads + n_kv + kvh) * HD + p * 8);
-        }
-        __syncthreads();
-#pragma unroll
-        for (int g = 0; g < G; ++g)
-#pragma unroll
-            for (int e = 0; e < 8; ++e) qf[g][e] = qs[g][li * 8 + e];
-        kn = *reinterpret_cast<const uint4 *>(knew + li * 8);
+        const uint16_t *head = row + static_cast<uint64_t>(hh < G ? h0 + hh : n_heads + kvh) * HD;
+        const uint32_t partner = pp < PPH / 2 ? pp + PPH / 2 : pp - PPH / 2;
+        x4 = *reinterpret_cast<const uint4 *>(head + pp * 8);
+        r4 = *reinterpret_cast<const uint4 *>(head + partner * 8);
+        c4 = *reinterpret_cast<const uint4 *>(cos_tab + static_cast<uint64_t>(pos) * HD + pp * 8);
+        s4 = *reinterpret_cast<const uint4 *>(sin_tab + static_cast<uint64_t>(pos) * HD + pp * 8);
+        const uint32_t tv = tid >= (G + 1) * PPH && tid < (G + 2) * PPH ? tid - (G + 1) * PPH : 0;
+        v4 = *reinterpret_cast<const uint4 *>(row + static_cast<uint64_t>(n_heads + n_kv + kvh) * HD + tv * 8);
     } else {
 #pragma unroll
-        for (int g = 0; g < G; ++g)
-            unpack8(*reinterpret_cast<const uint4 *>(q_src + (static_cast<uint64_t>(r) * n_heads + h0 + g) * HD + li * 8),
-                    qf[g]);
+        for (int st = 0; st < KS; ++st) {
+            const uint4 v = *reinterpret_cast<const uint4 *>(q_src + (static_cast<uint64_t>(r) * n_heads + h0 + hc) * HD +
+                                                             32 * st + 8 * quad);
+            a[st] = hlive ? v : make_uint4(0u, 0u, 0u, 0u);
+        }
     }
-    for (uint32_t c = split; c < nact; c += splits) {
-        const uint32_t j0 = c * kAttnChunk;
-        const uint32_t jw = j0 + wave * (kAttnChunk / kAttnWaves) + ks;
-        uint4 next[IT];
-        const bool more = c + splits < nact;
-        if (more) load_chunk(c + splits, next);  // the next chunk's keys load while this one is scored
-#pragma unroll
-        for (int it = 0; it < IT; ++it) {
-            const uint32_t j = jw + it * KPI;
-            float kf[8];
-            unpack8(ROPE && j == pos ? kn : kr[it], kf);
-#pragma unroll
-            for (int g = 0; g < G; ++g) {
-                float d = 0.f;
-#pragma unroll
-                for (int e = 0; e < 8; ++e) d += qf[g][e] * kf[e];
-                d = group_sum<LPK>(d);
-                if (li == 0) sc[g][j - j0] = j < ctx ? bf(rne(d)) * scale : -INFINITY;
+    uint4 b0[KS], b1[KS];
+    load_grp(0, b0);
+    load_grp(1, b1);
+    if constexpr (ROPE) {
+        const bool owner = (pos / kAttnChunk) % splits == split;
+        const uint4 ov = rope_apply(x4, r4, c4, s4, pp < PPH / 2);
+        if (tid < (G + 1) * PPH) {
+            if (hh < G) {
+                *reinterpret_cast<uint4 *>(&qb[hh][pp * 8]) = ov;
+            } else {
+                *reinterpret_cast<uint4 *>(knew + pp * 8) = ov;
+                if (owner) *reinterpret_cast<uint4 *>(k_cache + cache + static_cast<uint64_t>(pos) * HD + pp * 8) = ov;
             }
+        } else if (owner && tid < (G + 2) * PPH) {
+            *reinterpret_cast<uint4 *>(v_cache + cache + static_cast<uint64_t>(pos) * HD + (tid - (G + 1) * PPH) * 8) = v4;
         }
         __syncthreads();
-        static_assert(kAttnChunk == 64, "statistics pass assumes one score per lane");
-        for (uint32_t g = wave; g < G; g += kAttnWaves) {
-            const float x = sc[g][lane];
-            const float m = wave_max(x);
-            const float l = wave_sum(expf(x - m));
-            if (lane == 0) stats[(static_cast<uint64_t>(r) * n_heads + h0 + g) * nck + c] = make_float2(m, l);
-        }
-        const uint32_t valid = min(ctx - j0, static_cast<uint32_t>(kAttnChunk));
-        for (uint32_t i = tid; i < G * kAttnChunk; i += kAttnThreads) {
-            const uint32_t g = i / kAttnChunk, jj = i % kAttnChunk;
-            if (jj < valid) scores[(static_cast<uint64_t>(r) * n_heads + h0 + g) * max_len + j0 + jj] = sc[g][jj];
-        }
-        __syncthreads();  // sc is rewritten by the next chunk
-        if (more)
+        // A fragments: head `col` (zero for col >= G), dims 32 st + 8 quad.. of each step
 #pragma unroll
-            for (int it = 0; it < IT; ++it) kr[it] = next[it];
+        for (int st = 0; st < KS; ++st) {
+            const uint4 v = *reinterpret_cast<const uint4 *>(&qb[hc][32 * st + 8 * quad]);
+            a[st] = hlive ? v : make_uint4(0u, 0u, 0u, 0u);
+        }
+    }
+    if (total == 0) return;  // a wavefront without chunks (no barrier follows)
+    const uint4 *kn = reinterpret_cast<const uint4 *>(knew + 8 * quad);
+    for (uint32_t f0 = 0; f0 < total; f0 += 4) {
+        const uint32_t c = c_first + (f0 / 4) * c_step;
+        float sv[4][4];  // [group][i]: head quad * 4 + i, key c * 64 + group * 16 + col
+#pragma unroll
+        for (int grp = 0; grp < 4; ++grp) {
+            uint4(&b)[KS] = grp % 2 ? b1 : b0;
+            const uint32_t j = c * kAttnChunk + grp * 16 + col;
+            if constexpr (ROPE) {
+                if (j == pos) {
+#pragma unroll
+                    for (int st = 0; st < KS; ++st) b[st] = kn[4 * st];
+                }
+            }
+            attn_f32x4_t d = attn_mfma(a[0], b[0], attn_f32x4_t{0.f, 0.f, 0.f, 0.f});
+#pragma unroll
+            for (int st = 1; st < KS; ++st) d = attn_mfma(a[st], b[st], d);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) sv[grp][i] = j < ctx ? bf(rne(d[i])) * scale : -INFINITY;
+            load_grp(f0 + grp + 2, b);
+        }
+        // per head: (max, sum of exp) over the chunk's 64 keys
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const float m = group_max<16>(fmaxf(fmaxf(sv[0][i], sv[1][i]), fmaxf(sv[2][i], sv[3][i])));
+            const float l = group_sum<16>((expf(sv[0][i] - m) + expf(sv[1][i] - m)) + (expf(sv[2][i] - m) + expf(sv[3][i] - m)));
+            const uint32_t head = quad * 4 + i;
+            if (head < static_cast<uint32_t>(G)) {
+                float *srow = scores + (static_cast<uint64_t>(r) * n_heads + h0 + head) * max_len + c * kAttnChunk + col;
+#pragma unroll
+                for (int grp = 0; grp < 4; ++grp)
+                    if (c * kAttnChunk + grp * 16 + col < ctx) srow[grp * 16] = sv[grp][i];
+                if (col == 0) stats[(static_cast<uint64_t>(r) * n_heads + h0 + head) * nck + c] = make_float2(m, l);
+            }
+        }
     }
 }
 
@@ -307,6 +362,225 @@ __global__ __launch_bounds__(kAttnThreads) void attn_pv_kernel(
     }
 }
 
+// Chunked P.V: block (KV head, chunk, row) sums p_j v_j over the chunk's
+// keys for every dim. A lane holds 8 dims of one key (16-byte loads; a
+// wavefront load covers 64 / (HD/8) whole key rows). Each wavefront takes
+// every 4th tile of 16 keys on its own: it computes the row's softmax
+// statistics itself, stages its tile's probabilities in its own LDS slice
+// (no block barrier in the loop) and keeps two tiles of loads in flight. The
+// lanes' and wavefronts' partials are added in a fixed order. With one chunk
+// per row the result (RNE) goes to out, else the f32 partial goes to part
+// for attn_combine_kernel.
+constexpr int kPvWaveTile = 16;  // keys per wavefront tile
+
+template <int HD, int G>
+__global__ __launch_bounds__(kAttnThreads) void attn_pv_chunk_kernel(
+    const uint16_t *__restrict__ v_cache, uint64_t row_stride, const uint32_t *__restrict__ positions,
+    uint32_t pos_limit, uint32_t n_heads, uint32_t n_kv, uint32_t max_len, uint32_t nck, uint32_t chunks,
+    uint32_t chunk_keys, const float *__restrict__ scores, const float2 *__restrict__ stats,
+    uint16_t *__restrict__ out, float *__restrict__ part) {
+    constexpr int LPK = HD / 8, KPI = 64 / LPK;  // lanes per key, keys per load
+    constexpr int IT = kPvWaveTile / KPI;        // V loads per lane per tile
+    constexpr int NSW = (G * kPvWaveTile + 63) / 64;  // score loads per lane per tile
+    static_assert(IT >= 1, "a tile gives the wavefront whole loads");
+    __shared__ float pw[kAttnWaves][G][kPvWaveTile];
+    __shared__ float red[kAttnWaves][G][HD];
+    const uint32_t tid = threadIdx.x, r = blockIdx.y, kvh = blockIdx.x / chunks, c = blockIdx.x % chunks;
+    const uint32_t h0 = kvh * G;
+    const uint32_t pos = positions[r];
+    if (pos >= pos_limit) {  // a position the cache or the tables cannot hold: zero output (or the combine's)
+        if (chunks == 1)
+            for (uint32_t i = tid; i < G * HD; i += kAttnThreads) out[(static_cast<uint64_t>(r) * n_heads + h0) * HD + i] = 0;
+        return;
+    }
+    const uint32_t ctx = pos < max_len ? pos + 1 : max_len;
+    const uint32_t k0 = c * chunk_keys;
+    if (k0 >= ctx) return;  // a chunk past the context (never chunk 0)
+    const uint32_t k1 = min(k0 + chunk_keys, ctx);
+    const uint32_t nact = (ctx + kAttnChunk - 1) / kAttnChunk;
+    const uint32_t wave = tid >> 6, lane = tid & 63, kl = lane / LPK, dp = lane % LPK;
+    const uint32_t nt = (k1 - k0 + kPvWaveTile - 1) / kPvWaveTile;           // tiles of the chunk
+    const uint32_t wt = nt > wave ? (nt - wave + kAttnWaves - 1) / kAttnWaves : 0;  // this wavefront's
+    const uint16_t *vb = v_cache + static_cast<uint64_t>(r) * row_stride + static_cast<uint64_t>(kvh) * max_len * HD +
+                         dp * 8;
+    const float *srow = scores + (static_cast<uint64_t>(r) * n_heads + h0) * max_len;
+    // Tile i of this wavefront: its V rows for this lane, and the scores of
+    // entries t = lane + 64 n of its [G][16] block. Keys past k1 and tiles past
+    // the wavefront's last are clamped (loads stay unconditional; the values
+    // are masked or unused).
+    auto load_tile = [&](uint32_t i, uint4 (&vr)[IT], float (&sr)[NSW]) {
+        const uint32_t ic = wt ? (i < wt ? i : wt - 1) : 0;
+        const uint32_t t0 = k0 + (wave + ic * kAttnWaves) * kPvWaveTile;
+#pragma unroll
+        for (int it = 0; it < IT; ++it) {
+            const uint32_t j = t0 + it * KPI + kl;
+            vr[it] = *reinterpret_cast<const uint4 *>(vb + static_cast<uint64_t>(j < k1 ? j : k1 - 1) * HD);
+        }
+#pragma unroll
+        for (int n = 0; n < NSW; ++n) {
+            const uint32_t t = lane + n * 64;
+            const uint32_t g = t / kPvWaveTile < G ? t / kPvWaveTile : G - 1, j = t0 + t % kPvWaveTile;
+            sr[n] = srow[static_cast<uint64_t>(g) * max_len + (j < k1 ? j : k1 - 1)];
+        }
+    };
+    uint4 va[IT], vb2[IT];
+    float sa[NSW], sb[NSW];
+    load_tile(0, va, sa);
+    load_tile(1, vb2, sb);
+    // the row's softmax statistics, per wavefront (M, S the same everywhere):
+    // up to 128 chunks from registers (every head's loads issued together),
+    // longer rows in a loop
+    float mg[G], sg[G];
+    const float2 *st0 = stats + (static_cast<uint64_t>(r) * n_heads + h0) * nck;
+    if (nact <= 128) {
+        float2 sv[G][2];
+#pragma unroll
+        for (int g = 0; g < G; ++g)
+#pragma unroll
+            for (int n = 0; n < 2; ++n) {
+                const uint32_t cc = lane + 64 * n;
+                const float2 v = st0[static_cast<uint64_t>(g) * nck + (cc < nact ? cc : 0)];
+                sv[g][n] = cc < nact ? v : make_float2(-INFINITY, 0.f);
+            }
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+            mg[g] = wave_max(fmaxf(sv[g][0].x, sv[g][1].x));
+            float sum = 0.f;
+#pragma unroll
+            for (int n = 0; n < 2; ++n)
+                if (lane + 64 * n < nact) sum += sv[g][n].y * expf(sv[g][n].x - mg[g]);
+            sg[g] = wave_sum(sum);
+        }
+    } else {
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+            const float2 *st = st0 + static_cast<uint64_t>(g) * nck;
+            float m = -INFINITY;
+            for (uint32_t cc = lane; cc < nact; cc += 64) m = fmaxf(m, st[cc].x);
+            mg[g] = wave_max(m);
+            float sum = 0.f;
+            for (uint32_t cc = lane; cc < nact; cc += 64) {
+                const float2 v = st[cc];
+                sum += v.y * expf(v.x - mg[g]);
+            }
+            sg[g] = wave_sum(sum);
+        }
+    }
+    float acc[G][8];
+#pragma unroll
+    for (int g = 0; g < G; ++g)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) acc[g][e] = 0.f;
+    // the statistics of the head each of this lane's probability entries
+    // belongs to (fixed for the whole loop)
+    float lm[NSW], ls[NSW];
+#pragma unroll
+    for (int n = 0; n < NSW; ++n) {
+        const uint32_t g = (lane + n * 64) / kPvWaveTile;
+        lm[n] = mg[0], ls[n] = sg[0];
+#pragma unroll
+        for (int gg = 1; gg < G; ++gg)
+            if (gg == static_cast<int>(g)) lm[n] = mg[gg], ls[n] = sg[gg];
+    }
+    auto use_tile = [&](uint32_t i, const uint4 (&vr)[IT], const float (&sr)[NSW]) {
+        const uint32_t t0 = k0 + (wave + i * kAttnWaves) * kPvWaveTile;
+#pragma unroll
+        for (int n = 0; n < NSW; ++n) {
+            const uint32_t t = lane + n * 64, g = t / kPvWaveTile, jj = t % kPvWaveTile;
+            const float pv = t0 + jj < k1 ? bf(rne(expf(sr[n] - lm[n]) / ls[n])) : 0.f;
+            if (t < G * kPvWaveTile) pw[wave][g][jj] = pv;
+        }
+        __builtin_amdgcn_wave_barrier();  // this wavefront's writes before its reads
+#pragma unroll
+        for (int it = 0; it < IT; ++it) {
+            const uint32_t jj = it * KPI + kl;
+            float v[8];
+            unpack8(vr[it], v);
+#pragma unroll
+            for (int g = 0; g < G; ++g) {
+                const float pj = pw[wave][g][jj];
+#pragma unroll
+                for (int e = 0; e < 8; ++e) acc[g][e] += pj * v[e];
+            }
+        }
+        __builtin_amdgcn_wave_barrier();  // reads before the next tile's writes
+    };
+    for (uint32_t i = 0; i < wt; i += 2) {
+        use_tile(i, va, sa);
+        load_tile(i + 2, va, sa);
+        if (i + 1 < wt) use_tile(i + 1, vb2, sb);
+        load_tile(i + 3, vb2, sb);
+    }
+    // keys of one dim piece sit LPK lanes apart: add them with shuffles, then
+    // the wavefronts in order through LDS
+#pragma unroll
+    for (int off = LPK; off < 64; off <<= 1)
+#pragma unroll
+        for (int g = 0; g < G; ++g)
+#pragma unroll
+            for (int e = 0; e < 8; ++e) acc[g][e] += __shfl_xor(acc[g][e], off, 64);
+    if (lane < static_cast<uint32_t>(LPK)) {
+#pragma unroll
+        for (int g = 0; g < G; ++g)
+#pragma unroll
+            for (int e = 0; e < 8; ++e) red[wave][g][dp * 8 + e] = acc[g][e];
+    }
+    __syncthreads();
+    for (uint32_t i = tid; i < G * HD; i += kAttnThreads) {
+        const uint32_t g = i / HD, d = i % HD;
+        float o = 0.f;
+#pragma unroll
+        for (int w = 0; w < kAttnWaves; ++w) o += red[w][g][d];
+        if (chunks == 1)
+            out[(static_cast<uint64_t>(r) * n_heads + h0) * HD + i] = rne(o);
+        else
+            part[((static_cast<uint64_t>(r) * n_kv + kvh) * chunks + c) * (G * HD) + i] = o;
+    }
+}
+
+// Adds the chunked P.V partials of each (row, KV head): block (64 outputs,
+// KV head, row); the 4 wavefronts each add a contiguous quarter of the row's
+// active chunks in order (8 loads issued before their adds), then the
+// quarters are added in order, so the sum is the same every run.
+constexpr int kCombineOuts = 64;
+
+__global__ __launch_bounds__(kAttnThreads) void attn_combine_kernel(
+    const uint32_t *__restrict__ positions, uint32_t pos_limit, uint32_t n_heads, uint32_t n_kv, uint32_t width,
+    uint32_t max_len, uint32_t chunks, uint32_t chunk_keys, const float *__restrict__ part,
+    uint16_t *__restrict__ out) {
+    __shared__ float quarter_sum[kAttnWaves][kCombineOuts];
+    const uint32_t tid = threadIdx.x, e = tid % kCombineOuts, qw = tid / kCombineOuts;
+    const uint32_t i = blockIdx.x * kCombineOuts + e, kvh = blockIdx.y, r = blockIdx.z;
+    const uint32_t pos = positions[r];
+    uint16_t *orow = out + (static_cast<uint64_t>(r) * n_kv + kvh) * width;  // heads kvh*G.. of row r
+    if (pos >= pos_limit) {
+        if (qw == 0 && i < width) orow[i] = 0;
+        return;
+    }
+    const uint32_t ctx = pos < max_len ? pos + 1 : max_len;
+    const uint32_t nc = (ctx + chunk_keys - 1) / chunk_keys;
+    const uint32_t per = (nc + kAttnWaves - 1) / kAttnWaves;
+    const uint32_t c0 = qw * per, c1 = min(c0 + per, nc);
+    const float *pr = part + (static_cast<uint64_t>(r) * n_kv + kvh) * chunks * width + (i < width ? i : 0);
+    float o = 0.f;
+    for (uint32_t c = c0; c < c1; c += 8) {
+        float v[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) v[u] = pr[static_cast<uint64_t>(c + u < c1 ? c + u : c0) * width];
+#pragma unroll
+        for (int u = 0; u < 8; ++u)
+            if (c + u < c1) o += v[u];
+    }
+    quarter_sum[qw][e] = o;
+    __syncthreads();
+    if (qw == 0 && i < width) {
+        float t = quarter_sum[0][e];
+#pragma unroll
+        for (int w = 1; w < kAttnWaves; ++w) t += quarter_sum[w][e];
+        orow[i] = rne(t);
+    }
+}
+
 struct AttnArgs {
     const uint16_t *q_src, *cos_tab, *sin_tab;
     const uint32_t *positions;
@@ -337,6 +611,18 @@ static void launch_attention(hipStream_t stream, uint32_t rows, const AttnLayout
                        x.sin_tab, x.positions, x.pos_limit, x.k_cache, x.v_cache, x.row_stride, x.n_heads, x.n_kv,
                        x.max_len, static_cast<uint32_t>(a.nck), static_cast<uint32_t>(a.splits), x.scale, scores,
                        stats);
+    if (a.chunks) {
+        const uint32_t chunks = static_cast<uint32_t>(a.chunks), ck = static_cast<uint32_t>(a.chunk_keys);
+        float *part = reinterpret_cast<float *>(x.ws + a.part);
+        hipLaunchKernelGGL((attn_pv_chunk_kernel<HD, G>), dim3(x.n_kv * chunks, rows), dim3(kAttnThreads), 0, stream,
+                           x.v_cache, x.row_stride, x.positions, x.pos_limit, x.n_heads, x.n_kv, x.max_len,
+                           static_cast<uint32_t>(a.nck), chunks, ck, scores, stats, x.out, part);
+        if (chunks > 1)
+            hipLaunchKernelGGL(attn_combine_kernel, dim3((G * HD + kCombineOuts - 1) / kCombineOuts, x.n_kv, rows),
+                               dim3(kAttnThreads), 0, stream, x.positions, x.pos_limit, x.n_heads, x.n_kv,
+                               static_cast<uint32_t>(G * HD), x.max_len, chunks, ck, part, x.out);
+        return;
+    }
     switch (HD / a.slices / 2) {  // dim pairs per P.V block
         case 8: return launch_pv<G, 8>(stream, rows, a, x, HD, scores, stats);
         case 16: return launch_pv<G, 16>(stream, rows, a, x, HD, scores, stats);
@@ -386,11 +672,11 @@ int check_heads(const char *fn, int64_t n_heads, int64_t n_kv, int64_t head_dim)
     return FH_OK;
 }
 
-// The workspace holds rows * n_heads * (max_len + 2 * chunks) floats (scores,
-// statistics); refuse sizes whose byte counts would not fit comfortably in 64
-// bits.
+// The workspace holds fewer than rows * n_heads * (6 * max_len + 2 *
+// head_dim) floats (scores, statistics, P.V partials); refuse sizes whose
+// byte counts would not fit comfortably in 64 bits.
 int check_attn_size(const char *fn, int64_t rows, int64_t n_heads, int64_t head_dim, int64_t max_len) {
-    const long double floats = static_cast<long double>(rows) * n_heads * (3.0L * max_len + head_dim);
+    const long double floats = static_cast<long double>(rows) * n_heads * (6.0L * max_len + 2.0L * head_dim);
     if (floats > 0x1p56L)
         return fail(FH_ERR_INDEX_TOO_LARGE, "%s: attention workspace for %lld rows x %lld heads x %lld keys is too large",
                     fn, (long long)rows, (long long)n_heads, (long long)max_len);
@@ -413,7 +699,7 @@ int check_attention(const char *fn, fh_device *dev, int64_t rows, int64_t n_head
     if (max_len == 0) return fail(FH_ERR_INVALID_ARGUMENT, "%s: empty KV cache", fn);
     if (int rc = check_attn_size(fn, rows, n_heads, head_dim, max_len)) return rc;
     *a = attn_layout(rows, n_heads, n_kv, head_dim, max_len);
-    if (rows > 65535 || static_cast<uint64_t>(n_kv) * (a->splits + a->slices) > 0x7FFFFFFFu)
+    if (rows > 65535 || static_cast<uint64_t>(n_kv) * (a->splits + a->slices + a->chunks) > 0x7FFFFFFFu)
         return fail(FH_ERR_INDEX_TOO_LARGE, "%s: %lld rows x %llu splits exceed the grid", fn, (long long)rows,
                     (unsigned long long)(n_kv * a->splits));
     if (workspace_bytes < a->total)

@@ -22,18 +22,6 @@ __device__ __forceinline__ void unpack8(const uint4 v, float (&f)[8]) {
     }
 }
 
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
-    return v;
-}
-
-__device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
-    return v;
-}
-
 // Lane value of a DPP permutation within 16-lane rows (CDNA DPP controls:
 // 0xB1 quad_perm [1,0,3,2], 0x4E quad_perm [2,3,0,1], 0x141 row_half_mirror,
 // 0x140 row_mirror).
@@ -57,19 +45,50 @@ __device__ __forceinline__ float group_sum(float v) {
     return v;
 }
 
+// Maximum over aligned groups of N lanes, as group_sum.
+template <int N>
+__device__ __forceinline__ float group_max(float v) {
+    static_assert(N == 8 || N == 16 || N == 32, "group of 8, 16 or 32 lanes");
+    v = fmaxf(v, dpp_mov<0xB1>(v));
+    v = fmaxf(v, dpp_mov<0x4E>(v));
+    v = fmaxf(v, dpp_mov<0x141>(v));
+    if constexpr (N >= 16) v = fmaxf(v, dpp_mov<0x140>(v));
+    if constexpr (N == 32) v = fmaxf(v, __shfl_xor(v, 16, 64));
+    return v;
+}
+
+__device__ __forceinline__ float lane_value(float v, int lane) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), lane));
+}
+
+// Wavefront sum and maximum: DPP within each 16-lane row, then the four row
+// results read out and combined in a fixed order (uniform result, no LDS
+// round trips).
+__device__ __forceinline__ float wave_sum(float v) {
+    v = group_sum<16>(v);
+    return (lane_value(v, 0) + lane_value(v, 16)) + (lane_value(v, 32) + lane_value(v, 48));
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+    v = group_max<16>(v);
+    return fmaxf(fmaxf(lane_value(v, 0), lane_value(v, 16)), fmaxf(lane_value(v, 32), lane_value(v, 48)));
+}
+
 // RoPE (src/models/llama/rotary_emb.rs:62-85) of dims p*8 .. p*8+7 of one
 // head: x' = RNE(RNE(x * cos) + RNE(rot * sin)), rot = cat(-x2, x1); the
 // partner piece is the matching 8 dims of the other half (hp pieces per
 // half). head: the head's row; c, s: the position's table rows.
-__device__ __forceinline__ uint4 rope_piece(const uint16_t *head, const uint16_t *c, const uint16_t *s,
-                                            uint32_t p, uint32_t hp) {
-    const uint32_t partner = p < hp ? p + hp : p - hp;
-    const float sign = p < hp ? -1.0f : 1.0f;
+// The rotation of one piece from its loaded values: x (the piece), r (its
+// partner piece), c and s (the table rows' matching pieces); first_half:
+// rot = -partner.
+__device__ __forceinline__ uint4 rope_apply(const uint4 x4, const uint4 r4, const uint4 c4, const uint4 s4,
+                                            bool first_half) {
+    const float sign = first_half ? -1.0f : 1.0f;
     float xv[8], rv[8], cv[8], sv[8];
-    unpack8(*reinterpret_cast<const uint4 *>(head + p * 8), xv);
-    unpack8(*reinterpret_cast<const uint4 *>(head + partner * 8), rv);
-    unpack8(*reinterpret_cast<const uint4 *>(c + p * 8), cv);
-    unpack8(*reinterpret_cast<const uint4 *>(s + p * 8), sv);
+    unpack8(x4, xv);
+    unpack8(r4, rv);
+    unpack8(c4, cv);
+    unpack8(s4, sv);
     uint32_t o[4];
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
@@ -78,6 +97,13 @@ __device__ __forceinline__ uint4 rope_piece(const uint16_t *head, const uint16_t
         o[e] = lo | (hi << 16);
     }
     return make_uint4(o[0], o[1], o[2], o[3]);
+}
+
+__device__ __forceinline__ uint4 rope_piece(const uint16_t *head, const uint16_t *c, const uint16_t *s,
+                                            uint32_t p, uint32_t hp) {
+    const uint32_t partner = p < hp ? p + hp : p - hp;
+    return rope_apply(*reinterpret_cast<const uint4 *>(head + p * 8), *reinterpret_cast<const uint4 *>(head + partner * 8),
+                      *reinterpret_cast<const uint4 *>(c + p * 8), *reinterpret_cast<const uint4 *>(s + p * 8), p < hp);
 }
 
 }  // namespace fh

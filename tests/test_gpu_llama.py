@@ -223,8 +223,9 @@ def rope_ref(x, pos, cos, sin):
 
 # (n_heads, n_kv, head_dim, batch, max_len): group sizes 3 (Llama-3.2-3B), 4
 # (Llama-3.1-8B, batched decode at context 4096), 2, 1, 7.
+# batch * n_kv * max_len >= 16384 takes the chunked P.V with its combine pass
 DECODE_CASES = [(24, 8, 128, 1, 768), (32, 8, 128, 8, 4096), (4, 2, 64, 3, 40), (8, 8, 256, 2, 300),
-                (28, 4, 128, 2, 1100)]
+                (28, 4, 128, 2, 1100), (8, 8, 256, 4, 600), (24, 8, 128, 3, 2048)]
 
 
 @pytest.mark.parametrize("n_heads,n_kv,hd,batch,max_len", DECODE_CASES)
@@ -270,8 +271,9 @@ def test_decode_attention(device, n_heads, n_kv, hd, batch, max_len):
         assert_attention_close(got[b:b + 1], ref, flip, (b, p))
 
 
-def test_decode_attention_out_of_range_position(device):
-    n_heads, n_kv, hd, max_len = 4, 2, 64, 32
+@pytest.mark.parametrize("max_len", [32, 4096])  # sliced and chunked P.V
+def test_decode_attention_out_of_range_position(device, max_len):
+    n_heads, n_kv, hd = 4, 2, 64
     c = LlamaConfig(n_layers=1, hidden=256, n_heads=n_heads, n_kv_heads=n_kv, head_dim=hd, ffn=64, vocab=16)
     qkv = synth.bf16_normal(23, (2, (n_heads + 2 * n_kv) * hd))
     cos, sin = rope_tables(c, max_len)
