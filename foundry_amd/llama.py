@@ -29,6 +29,8 @@ are random-init (SplitMix64-seeded); no checkpoint is read.
 from __future__ import annotations
 
 import ctypes
+import json
+import os
 from dataclasses import dataclass, field
 
 import numpy as np
@@ -62,6 +64,88 @@ class LlamaConfig:
     rope_theta: float = 500000.0
     rope_scaling: RopeScaling | None = field(default_factory=RopeScaling)
     max_position_embeddings: int = 131072
+    eos_token_id: tuple = ()
+
+    @staticmethod
+    def parse(data: bytes) -> "LlamaConfig":
+        """LlamaConfig::parse (src/models/llama/config.rs:104-200): a config.json
+        of model_type "llama" with heads * head_dim == hidden (head_dim derived
+        when absent), heads a multiple of the KV heads, llama3 RoPE scaling or
+        none, and tied embeddings; LlamaError of the reference's kind
+        otherwise."""
+        from .weights import LlamaError
+
+        try:
+            f = json.loads(bytes(data).decode("utf-8"))
+        except (UnicodeDecodeError, ValueError) as e:
+            raise LlamaError("ConfigJson", str(e)) from None
+
+        def req(key, kind):
+            if not isinstance(f, dict) or key not in f:
+                raise LlamaError("ConfigJson", f"missing {key}")
+            v = f[key]
+            ok = {"usize": isinstance(v, int) and not isinstance(v, bool) and v >= 0,
+                  "f32": isinstance(v, (int, float)) and not isinstance(v, bool),
+                  "str": isinstance(v, str), "bool": isinstance(v, bool)}[kind]
+            if not ok:
+                raise LlamaError("ConfigJson", f"{key}={v!r}")
+            return v
+
+        model_type = req("model_type", "str")
+        hidden, inter, layers = req("hidden_size", "usize"), req("intermediate_size", "usize"), req("num_hidden_layers", "usize")
+        heads, kv = req("num_attention_heads", "usize"), req("num_key_value_heads", "usize")
+        eps, theta = req("rms_norm_eps", "f32"), req("rope_theta", "f32")
+        max_pos, vocab, tied = req("max_position_embeddings", "usize"), req("vocab_size", "usize"), req("tie_word_embeddings", "bool")
+        hd = f.get("head_dim")
+        if hd is not None and (not isinstance(hd, int) or isinstance(hd, bool) or hd < 0):
+            raise LlamaError("ConfigJson", f"head_dim={hd!r}")
+        eos = f.get("eos_token_id", None)
+        if isinstance(eos, int) and not isinstance(eos, bool) and 0 <= eos < 2 ** 32:
+            eos = (eos,)
+        elif isinstance(eos, list) and all(isinstance(e, int) and not isinstance(e, bool) and 0 <= e < 2 ** 32 for e in eos):
+            eos = tuple(eos)
+        else:
+            raise LlamaError("ConfigJson", f"eos_token_id={eos!r}")
+        rs = f.get("rope_scaling")
+        if rs is not None:
+            if not isinstance(rs, dict):
+                raise LlamaError("ConfigJson", "rope_scaling")
+            for key, kind in (("rope_type", str), ("factor", (int, float)), ("low_freq_factor", (int, float)),
+                              ("high_freq_factor", (int, float)), ("original_max_position_embeddings", int)):
+                if not isinstance(rs.get(key), kind) or isinstance(rs.get(key), bool):
+                    raise LlamaError("ConfigJson", f"rope_scaling.{key}")
+        if model_type != "llama":
+            raise LlamaError("ModelType", model_type)
+        head_dim = hd if hd is not None else (hidden // heads if heads else None)
+        if head_dim is None or heads * head_dim != hidden:
+            raise LlamaError("HiddenSizeMismatch", f"hidden {hidden}, heads {heads}, head_dim {hd}")
+        if kv == 0 or heads % kv != 0:
+            raise LlamaError("HeadRatio", f"heads {heads}, kv heads {kv}")
+        if rs is not None and rs["rope_type"] != "llama3":
+            raise LlamaError("RopeType", rs["rope_type"])
+        if not tied:
+            raise LlamaError("UntiedEmbeddings")
+        f32 = lambda v: float(np.float32(v))
+        scaling = None if rs is None else RopeScaling(f32(rs["factor"]), f32(rs["low_freq_factor"]),
+                                                      f32(rs["high_freq_factor"]),
+                                                      int(rs["original_max_position_embeddings"]))
+        return LlamaConfig(layers, hidden, heads, kv, head_dim, inter, vocab, f32(eps), f32(theta), scaling, max_pos,
+                           eos)
+
+    @staticmethod
+    def open(directory) -> "LlamaConfig":
+        """LlamaConfig::open: <directory>/config.json, at most 1 MiB."""
+        from .weights import LlamaError
+
+        path = os.path.join(directory, "config.json")
+        try:
+            if os.path.getsize(path) > 1024 * 1024:
+                raise LlamaError("ConfigTooLarge", path)
+            with open(path, "rb") as fh:
+                data = fh.read()
+        except OSError as e:
+            raise LlamaError("ConfigRead", str(e)) from None
+        return LlamaConfig.parse(data)
 
     @staticmethod
     def llama_3_2_3b() -> "LlamaConfig":
@@ -169,8 +253,10 @@ class Q4Llama:
     head_dim] (StaticCache, src/nn/kv_cache.rs:13-39). `max_tokens` bounds the
     tokens of one sequence in one forward."""
 
-    def __init__(self, dev: HipDevice, cfg: LlamaConfig, seed: int, max_len: int, max_tokens: int,
-                 batch: int = 1):
+    def __init__(self, dev: HipDevice, cfg: LlamaConfig, seed: int | None, max_len: int, max_tokens: int,
+                 batch: int = 1, weights=None):
+        """Weights are random-init from `seed`, or read from `weights` (a
+        foundry_amd.weights.Weights of q4 triplets; see from_checkpoint)."""
         self.dev, self.cfg, self.max_len = dev, cfg, max_len
         if max_len > cfg.max_position_embeddings:
             raise ValueError("max_len exceeds max_position_embeddings")
@@ -179,10 +265,18 @@ class Q4Llama:
         self.batch = int(batch)
         self.max_tokens = max(1, max_tokens)
         self.seq_bytes = cfg.n_kv_heads * max_len * cfg.head_dim * 2  # one sequence's cache, per layer
-        self.embed = _Q4(dev, *embed_weights(cfg, seed))
+        if weights is not None:
+            from .weights import llama_final_norm, llama_q4_embed, llama_q4_layer
+            src_embed, src_layer, src_norm = (lambda: llama_q4_embed(weights, cfg),
+                                              lambda l: llama_q4_layer(weights, cfg, l),
+                                              lambda: llama_final_norm(weights, cfg))
+        else:
+            src_embed, src_layer, src_norm = (lambda: embed_weights(cfg, seed), lambda l: layer_weights(cfg, seed, l),
+                                              lambda: final_norm_weight(cfg, seed))
+        self.embed = _Q4(dev, *src_embed())
         self.layers = []
         for layer in range(cfg.n_layers):
-            w = layer_weights(cfg, seed, layer)
+            w = src_layer(layer)
             self.layers.append({
                 "qkv": _Q4(dev, *w["qkv"]), "o": _Q4(dev, *w["o"]),
                 "gate_up": _Q4(dev, *w["gate_up"]), "down": _Q4(dev, *w["down"]),
@@ -191,7 +285,7 @@ class Q4Llama:
                 "k_cache": dev.zeros(self.batch * self.seq_bytes),
                 "v_cache": dev.zeros(self.batch * self.seq_bytes),
             })
-        self.final_norm = dev.storage_from_bytes(final_norm_weight(cfg, seed).tobytes())
+        self.final_norm = dev.storage_from_bytes(np.ascontiguousarray(src_norm()).tobytes())
         cos, sin = rope_tables(cfg, max_len)
         self.cos = dev.storage_from_bytes(cos.tobytes())
         self.sin = dev.storage_from_bytes(sin.tobytes())
@@ -220,6 +314,17 @@ class Q4Llama:
         self.dec_ws_bytes = _lib.decode_attention_workspace_bytes(bt, c.n_heads, c.n_kv_heads, c.head_dim, max_len)
         self.dec_ws = dev.zeros(self.dec_ws_bytes)
         self.seq_len = 0
+
+    @classmethod
+    def from_checkpoint(cls, dev: HipDevice, directory, max_len: int, max_tokens: int, batch: int = 1) -> "Q4Llama":
+        """A q4 checkpoint directory: config.json (LlamaConfig::open) and
+        model.safetensors or an index with shards, holding q4 triplets
+        ({name}.weight U32, .scales / .biases BF16) for the embedding (tied
+        LM head) and every projection, and BF16 norm weights
+        (src/models/llama/model.rs:130-160 names)."""
+        from .weights import Weights
+        cfg = LlamaConfig.open(directory)
+        return cls(dev, cfg, None, max_len, max_tokens, batch, weights=Weights.open(directory))
 
     # ---- thin wrappers over the C-ABI ----
     def _p(self, st: HipStorage, byte_offset: int = 0):

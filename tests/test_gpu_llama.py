@@ -443,3 +443,19 @@ def test_append_token_rows(device):
     want = np.zeros((4, 4), np.uint32)
     want[0, 0], want[1, 2] = 11, 22  # row 2 (position 4 < base) and row 3 (index 4 = capacity) write nothing
     assert np.array_equal(down(device, log, np.uint32, 16).reshape(4, 4), want)
+
+
+def test_checkpoint_model_equals_random_init(device, tmp_path):
+    """A q4 checkpoint (config.json + two safetensors shards of q4 triplets)
+    loaded through Q4Llama.from_checkpoint gives the same tokens and
+    bit-identical logits as the model built from the same weights in memory."""
+    from foundry_amd.weights import save_q4_llama
+
+    cfg, seed, max_len = TINY, 6, 48
+    layers = [layer_weights(cfg, seed, l) for l in range(cfg.n_layers)]
+    save_q4_llama(tmp_path, cfg, embed_weights(cfg, seed), layers, final_norm_weight(cfg, seed), shards=2)
+    prompt = synth.token_ids(13, 10, cfg.vocab)
+    a = Q4Llama(device, cfg, seed, max_len, max_tokens=len(prompt))
+    b = Q4Llama.from_checkpoint(device, tmp_path, max_len, max_tokens=len(prompt))
+    assert a.generate(prompt, 8).tolist() == b.generate(prompt, 8).tolist()
+    assert np.array_equal(a.logits(), b.logits())
