@@ -495,6 +495,44 @@ class Q4Llama:
             out[:, 0] = first
         return out[0] if single else out
 
+    def next_tokens(self) -> np.ndarray:
+        """Each sequence's greedy next id (reads back, so it synchronises)."""
+        out = np.empty(self.batch, dtype=np.uint32)
+        _lib.call("fh_download", self.dev.handle, out.ctypes.data_as(ctypes.c_void_p), self._p(self.buf["next"]),
+                  out.nbytes)
+        return out
+
+    def eager_step(self) -> None:
+        """One decode step launched op by op: every sequence's token in
+        buf['next'] at position buf['pos1'] -> its next token; position + 1."""
+        self._forward(1, self.buf["next"], self.buf["pos1"])
+        _lib.call("fh_advance_positions", self.dev.handle, self._p(self.buf["pos1"]), self.batch, 1)
+
+    def capture_step(self):
+        """The decode step (eager_step) captured once as a HIP graph; replay
+        it with .launch()."""
+        if getattr(self, "_step_graph", None) is None:
+            self.dev.capture_begin()
+            try:
+                self.eager_step()
+            except Exception:
+                self.dev.capture_end()
+                raise
+            self._step_graph = self.dev.capture_end()
+        return self._step_graph
+
+    def weight_bytes(self) -> int:
+        """Device bytes of the weights (packed words, scales, biases, norms)."""
+        q4 = [self.embed] + [L[k] for L in self.layers for k in ("qkv", "o", "gate_up", "down")]
+        n = sum(w.wq.nbytes + w.s.nbytes + w.b.nbytes for w in q4)
+        return n + sum(L[k].nbytes for L in self.layers for k in ("input_norm", "post_norm")) + self.final_norm.nbytes
+
+    def parameter_count(self) -> int:
+        """Logical parameters: every q4 weight element (not its scales and
+        biases) and every norm weight; the LM head shares the embedding."""
+        q4 = [self.embed] + [L[k] for L in self.layers for k in ("qkv", "o", "gate_up", "down")]
+        return sum(w.n * w.k for w in q4) + (2 * len(self.layers) + 1) * self.cfg.hidden
+
     def logits(self) -> np.ndarray:
         """Last computed logits (bf16 bits) of each sequence's final position:
         [vocab] for batch 1, else [batch, vocab]."""

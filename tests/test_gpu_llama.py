@@ -459,3 +459,30 @@ def test_checkpoint_model_equals_random_init(device, tmp_path):
     b = Q4Llama.from_checkpoint(device, tmp_path, max_len, max_tokens=len(prompt))
     assert a.generate(prompt, 8).tolist() == b.generate(prompt, 8).tolist()
     assert np.array_equal(a.logits(), b.logits())
+
+
+@pytest.mark.parametrize("profile", [None, "kernels"])
+def test_report_bench_matches_generation(device, profile):
+    """foundry_amd.report.bench (the reference's bench loop and report
+    schema) on a batch of two with depth rows: every run's greedy ids equal
+    generate()'s, the counts follow the config, and kernels mode records a
+    per-call GPU time for each decode step."""
+    import json as _json
+
+    from foundry_amd.report import BenchConfig, bench, draw_inputs
+
+    conf = BenchConfig(prompt_token_count=6, new_token_count=4, depth_token_count=3, warmup_run_count=1,
+                       run_count=2, batch_size=2, seed=1, profile=profile)
+    model = Q4Llama(device, TINY, 2, max_len=13, max_tokens=6, batch=2)
+    rep = bench(model, device, conf)
+    depth, prompt, _ = draw_inputs(conf, TINY.vocab)
+    want = model.generate(prompt, 4, depth=depth).tolist()
+    assert [r["token_ids"] for r in rep["runs"]] == [want, want]
+    assert all(len(r["decode"]) == 3 and r["prompt_step_ns"] > 0 for r in rep["runs"])
+    assert [s["context_tokens"] for s in rep["runs"][0]["decode"]] == [9, 10, 11]
+    m = rep["metrics"]
+    assert m["decode_tokens_per_s"]["count"] == 2 and m["prompt_tokens_per_s"]["count"] == 2
+    assert rep["peak_memory_bytes"] > 0 and rep["session_peak_memory_bytes"] >= rep["peak_memory_bytes"]
+    if profile:
+        assert m["decode_kernel_gpu_ns"] and all("profile" in s for s in rep["runs"][0]["decode"])
+    _json.dumps(rep)
