@@ -11,23 +11,28 @@
 //     token's q and k and its cache write (StaticCache::update,
 //     src/nn/kv_cache.rs:41-80) happen inside the scores kernel.
 //
-// A row (a token, or a sequence) attends keys 0..ctx-1 of its KV head. Two
-// kernels, because each probability is rounded from the row's global max and
-// sum; neither combines across blocks (a device-scope fence per block costs
-// an L2 write-back on this part), and every block serves the G = n_heads /
-// n_kv query heads of its KV head, so a K or V row is read once for the group:
+// A row (a token, or a sequence) attends keys 0..ctx-1 of its KV head. The
+// scores and the P.V are separate launches, because each probability is
+// rounded from the row's global max and sum; no kernel waits on another
+// block (a device-scope fence per block costs an L2 write-back on this part),
+// and every block serves the G = n_heads / n_kv query heads of its KV head,
+// so a K or V row is read once for the group:
 //   attn_scores_kernel, block (KV head, split, row): chunks of kAttnChunk keys
-//     dealt round-robin to `splits` blocks; s_j = RNE(q.k_j) * scale to the
+//     dealt round-robin to the split blocks and their wavefronts;
+//     s_j = RNE(q.k_j) * scale from matrix-core dot products, written to the
 //     workspace with each chunk's (m_c = max s_j, l_c = sum exp(s_j - m_c)).
-//     A key row of HD bf16 is read by HD/8 lanes with 16-byte loads (one
-//     wavefront load covers 64 / (HD/8) whole keys); the lane partials are
-//     summed with DPP moves.
-//   attn_pv_kernel, block (KV head, slice, row): M = max m_c, S = sum l_c
-//     exp(m_c - M) (the same in every block), p_j = RNE(exp(s_j - M) / S), and
-//     sum_j p_j v_j over all keys for head_dim / slices of the dims, so each
-//     output element comes from one block in a fixed order.
-// splits and slices make rows * n_kv * splits about kAttnTargetBlocks: decode
-// spreads one row over many CUs, prefill keeps one block per (row, KV head).
+//   P.V, from M = max m_c and S = sum l_c exp(m_c - M) (the same in every
+//     block) and p_j = RNE(exp(s_j - M) / S), one of two ways:
+//     attn_pv_kernel, block (KV head, slice, row): all keys for head_dim /
+//       slices of the dims -- few, short rows;
+//     attn_pv_chunk_kernel, block (KV head, chunk, row): a chunk of keys for
+//       all dims, then attn_combine_kernel adds the chunks -- long or many
+//       rows.
+//   Either way each output element is a sum in a fixed order, so results do
+//   not change from run to run.
+// splits, slices and chunks make rows * n_kv * (blocks per pair) about
+// kAttnTargetBlocks: decode spreads one row over many CUs, prefill keeps one
+// block per (row, KV head).
 #include "decoder_common.hpp"
 
 #ifndef FH_PV_CHUNKED_MIN_KEYS

@@ -158,6 +158,16 @@ static int create(int ordinal, int mode, fh_device **out, const char *fn) {
         delete dev;
         return fail(FH_ERR_DEVICE_UNAVAILABLE, "%s: event creation failed", fn);
     }
+    if (hipMalloc(&dev->pack_area, kPackAreaBytes) != hipSuccess ||
+        hipMalloc(&dev->partial_area, kPartialAreaBytes) != hipSuccess) {
+        hipFree(dev->pack_area);
+        hipEventDestroy(dev->timer_begin);
+        hipEventDestroy(dev->timer_end);
+        hipStreamDestroy(dev->stream);
+        delete dev;
+        return fail(FH_ERR_ALLOCATION, "%s: the device's %llu-byte work areas could not be allocated", fn,
+                    static_cast<unsigned long long>(kPackAreaBytes + kPartialAreaBytes));
+    }
     *out = dev;
     return FH_OK;
 }
@@ -180,6 +190,8 @@ int fh_device_destroy(fh_device *dev) {
     }
     hipError_t err = hipStreamSynchronize(dev->stream);
     for (auto &kv : dev->allocs) hipFree(reinterpret_cast<void *>(kv.first));
+    hipFree(dev->pack_area);
+    hipFree(dev->partial_area);
     for (auto &iv : dev->intervals) {
         if (iv.first) hipEventDestroy(iv.first);
         if (iv.second) hipEventDestroy(iv.second);

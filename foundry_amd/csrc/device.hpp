@@ -27,11 +27,24 @@ struct fh_graph {
     int ordinal = 0;
 };
 
+namespace fh {
+// Bytes of each device's pack area: the matrix-core GEMV's normalised x image
+// (8 rows of up to 16384 values as fragments, two slots, their group sums,
+// padding to whole wavefronts), written by the pack kernel and copied by the
+// GEMV's prologue in stream order.
+constexpr uint64_t kPackAreaBytes = 8ull * 16384 * 2 + (16384 / 64) * 8 * 4 + 2048;
+// Bytes of each device's partial area: the f32 partial sums [ranges][rows][n]
+// of a GEMV split over K ranges, added by its combine kernel.
+constexpr uint64_t kPartialAreaBytes = 4ull << 20;
+}  // namespace fh
+
 struct fh_device {
     int ordinal = 0;
     hipStream_t stream = nullptr;
     std::string name;
     uint32_t compute_units = 0;  // sizes persistent grids
+    void *pack_area = nullptr;     // kPackAreaBytes, owned by the device (not in allocs)
+    void *partial_area = nullptr;  // kPartialAreaBytes, likewise
     // base address -> size of every live allocation this device made
     std::map<uintptr_t, size_t> allocs;
     uint64_t live_bytes = 0;

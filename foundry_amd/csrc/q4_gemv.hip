@@ -80,4 +80,18 @@ void launch_q4_gemv_mfma(hipStream_t stream, uint32_t cus, int m, const GemvArgs
     }
 }
 
+// Launches the pack kernel for m (2..8) RMSNorm rows of a (k <= kMfPackMaxK)
+// into the device's pack area.
+void launch_mf_pack(hipStream_t stream, int m, const GemvArgs &a, void *area) {
+    switch (m) {
+        case 2: launch_mf_pack_m<2>(stream, a, area); break;
+        case 3: launch_mf_pack_m<3>(stream, a, area); break;
+        case 4: launch_mf_pack_m<4>(stream, a, area); break;
+        case 5: launch_mf_pack_m<5>(stream, a, area); break;
+        case 6: launch_mf_pack_m<6>(stream, a, area); break;
+        case 7: launch_mf_pack_m<7>(stream, a, area); break;
+        default: launch_mf_pack_m<8>(stream, a, area);
+    }
+}
+
 }  // namespace fh

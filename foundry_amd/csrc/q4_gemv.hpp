@@ -428,6 +428,10 @@ struct GemvArgs {
     int y_is_f32;
     int pro, epi;
     GemvFusion fu;
+    // matrix-core GEMV over K ranges: k is one range's length, the weight
+    // rows hold kranges of them (0 or 1: k is the whole row); y then takes
+    // f32 partial sums [kranges][rows][y_ld]
+    uint32_t kranges = 0;
 };
 
 template <int M, int L, int CPL, bool FULL, int PRO, int EPI>

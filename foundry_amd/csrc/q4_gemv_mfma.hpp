@@ -22,6 +22,12 @@
 // - Scale and bias load 2*CH groups per instruction; weight loads run two
 //   chunks (CH group pairs each) ahead of the MFMAs, across task boundaries,
 //   with clamped (never guarded) addresses, so every wait counts exactly.
+// - Every block stages all of x in LDS. Plain x: the prologue loads it in
+//   1 KB runs and permutes it into fragments. With RMSNorm (fh_q4_matmul_
+//   rmsnorm, fh_q4_gate_up_silu) a separate pack kernel normalises x once
+//   and writes the finished LDS image to the device's pack area, and the
+//   prologue only copies it: per-block normalisation of 8 rows was VALU-bound
+//   (about 8 us of every launch).
 // - Work: blocks of 16 wavefronts, persistent; a task is one output tile
 //   (gate and up tiles together for the SiLU epilogue) over a K slice; S
 //   wavefronts split K (S = 1..16) and add their partial tiles in LDS in a
@@ -29,6 +35,7 @@
 //   variant over one weight.
 #pragma once
 
+#include "decoder_common.hpp"
 #include "q4_gemv.hpp"
 
 namespace fh {
@@ -53,17 +60,22 @@ constexpr int mf_tiles_per_task() {
 }
 
 // LDS bytes: staged x fragments, a zero slot and a dummy slot, group sums X
-// [G][8], the staged norm weight (norm), the partial tiles of the K split,
-// the norm's per-wavefront sums.
-__host__ __device__ constexpr uint32_t mf_lds_bytes(uint32_t m, uint32_t k, int nt, bool norm) {
-    return m * k * 2 + 32 + (k / kGroup) * 8 * 4 + (norm ? k * 2 : 0) + kMfWaves * nt * 4 * 64 * 4 +
-           kMfWaves * 8 * 4;
+// [G][8], the partial tiles of the K split.
+__host__ __device__ constexpr uint32_t mf_lds_bytes(uint32_t m, uint32_t k, int nt) {
+    return m * k * 2 + 32 + (k / kGroup) * 8 * 4 + kMfWaves * nt * 4 * 64 * 4;
+}
+
+// 16-byte slots of the packed LDS image: fragments, the zero and dummy
+// slots, X [G][8], rounded up to whole wavefronts (the tail lands in the
+// K-split area, unused until the main loop).
+__host__ __device__ constexpr uint32_t mf_image_slots(uint32_t m, uint32_t k) {
+    return (m * k / 8 + 2 + (k / kGroup) * 2 + 63) / 64 * 64;
 }
 
 // Largest x row count (<= 8) whose staged copy fits the LDS budget.
-inline uint32_t mf_rows_per_launch(uint32_t k, int nt, bool norm) {
+inline uint32_t mf_rows_per_launch(uint32_t k, int nt) {
     uint32_t r = 8;
-    while (r > 0 && mf_lds_bytes(r, k, nt, norm) > kMfLdsLimit) --r;
+    while (r > 0 && mf_lds_bytes(r, k, nt) > kMfLdsLimit) --r;
     return r;
 }
 
@@ -96,35 +108,58 @@ __device__ __forceinline__ float mf_piece_sum(const uint4 p) {
            ((bf16_to_f32(p.x >> 16) + bf16_to_f32(p.y >> 16)) + (bf16_to_f32(p.z >> 16) + bf16_to_f32(p.w >> 16)));
 }
 
-// Items the prologue stages in straight-line code (rounds of kMfThreads);
+// 16-byte pieces of plain x rows per thread the prologue stages in
+// straight-line code (rounds of kMfThreads: 8 x 4096 values, 4 x 14336);
 // beyond, it loops (and the first weight loads wait for it).
-template <int PRO>
-constexpr uint32_t mf_straight_rounds() {
-    return PRO == kProRmsNorm ? 1 : 2;
+constexpr uint32_t kMfPlainRounds = 8;
+
+// Swizzle of the fragment row for word w % 4 == j: XOR keeps the M rows of a
+// fragment column on distinct slots, and spreads the 8 pieces of one group
+// (j = 0..3, two word columns) over distinct LDS banks (M a power of two).
+template <int M>
+__host__ __device__ constexpr uint32_t mf_swz(uint32_t j) {
+    return M == 8 ? 2 * j : M == 4 ? j : M == 2 ? (j >> 1) : 0u;
 }
 
-// M: x rows (1..8). CH: group pairs per chunk (2 or 4). ksplit: wavefronts
-// per task (divides 16; k / 64 / ksplit is a multiple of 2 * CH).
+// LDS slot of column piece c (8 values) of x row m: word w = c % 16 of group
+// pair p = c / 16 feeds MFMA j = w % 4 of quarter w / 4, so the slot is
+// ((p * 4 + j) * 4 + w / 4) * M + (m ^ mf_swz(j)).
+template <int M>
+__device__ __forceinline__ uint32_t mf_slot(uint32_t m, uint32_t c) {
+    const uint32_t p = c >> 4, w = c & 15, j = w & 3;
+    return ((p * 4 + j) * 4 + (w >> 2)) * M + (m ^ mf_swz<M>(j));
+}
+
+// M: x rows (1..8). CH: group pairs per chunk (1, 2 or 4). ksplit:
+// wavefronts per task (divides 16; k / 64 / ksplit is a multiple of 2 * CH).
 template <int M, int PRO, int EPI, int CH>
 __global__ __launch_bounds__(kMfThreads) void q4_gemv_mfma_kernel(
     const uint16_t *__restrict__ x, uint32_t x_ld, const uint32_t *__restrict__ wq,
     const uint16_t *__restrict__ scales, const uint16_t *__restrict__ biases, uint32_t n, uint32_t k,
-    void *__restrict__ y, uint32_t y_ld, int y_is_f32, GemvFusion fu, uint32_t ksplit) {
+    void *__restrict__ y, uint32_t y_ld, int y_is_f32, uint32_t ksplit) {
     constexpr int NT = mf_tiles_per_task<EPI>();
-    constexpr bool kNorm = PRO == kProRmsNorm;
+    constexpr bool kPacked = PRO == kProRmsNorm;  // x: mf_pack_kernel's image of RMSNorm(x + res)
     static_assert(kMfWaves / 2 * M * 16 <= kMfThreads, "a K-split round stores one output per thread at most");
     extern __shared__ uint4 lds[];
     const uint32_t G = k / kGroup;
-    const uint32_t wpr = k / 8;  // packed words per weight row
+    const uint32_t wpr = k / 8;  // packed words per row of the K range (x fragments)
+    // K range blockIdx.y of gridDim.y: weight rows hold all of them; y takes
+    // this range's f32 partial sums at [blockIdx.y][M][y_ld]
+    const uint32_t w_ld = wpr * gridDim.y, sb_ld = G * gridDim.y;
+    if (gridDim.y > 1) {
+        x += static_cast<uint64_t>(blockIdx.y) * k;
+        wq += static_cast<uint64_t>(blockIdx.y) * wpr;
+        scales += static_cast<uint64_t>(blockIdx.y) * G;
+        biases += static_cast<uint64_t>(blockIdx.y) * G;
+        y = static_cast<float *>(y) + static_cast<uint64_t>(blockIdx.y) * M * y_ld;
+    }
     const uint32_t n_out = EPI == kEpiSiluMul ? n / 2 : n;
     const uint32_t tiles = n_out / 16;
     uint4 *xa = lds;                                         // [G/2][4 j][4 q][M] fragments
     const uint32_t zero = M * wpr;                           // a zero fragment (dead A lanes)
     const uint32_t dummy = zero + 1;                         // write-only slot for dead items
     float *xsum = reinterpret_cast<float *>(lds + dummy + 1);  // [G][8]
-    uint4 *wsh = reinterpret_cast<uint4 *>(xsum + G * 8);    // [k/8] norm weight pieces (permuted)
-    float *red = reinterpret_cast<float *>(wsh + (kNorm ? wpr : 0));  // [16][NT][4][64]
-    float *nsum = red + kMfWaves * NT * 4 * 64;              // [16][8]
+    float *red = xsum + G * 8;                               // [16][NT][4][64]
 
     const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const uint32_t col = lane & 15, quarter = lane >> 4, hi = quarter >> 1;
@@ -150,18 +185,21 @@ __global__ __launch_bounds__(kMfThreads) void q4_gemv_mfma_kernel(
 #pragma unroll
         for (int t = 0; t < NT; ++t) {
             const uint64_t row = wrow(tile, t);
-            const uint4 *wp = reinterpret_cast<const uint4 *>(wq + row * wpr + p0 * 16 + quarter * 4);
+            const uint4 *wp = reinterpret_cast<const uint4 *>(wq + row * w_ld + p0 * 16 + quarter * 4);
 #pragma unroll
             for (int c2 = 0; c2 < CH; ++c2) cb.w[c2][t] = wp[c2 * 4];
-            const uint16_t *sp = scales + row * G + p0 * 2, *bp = biases + row * G + p0 * 2;
+            const uint16_t *sp = scales + row * sb_ld + p0 * 2, *bp = biases + row * sb_ld + p0 * 2;
             if constexpr (CH == 4) {
                 const uint4 sv = *reinterpret_cast<const uint4 *>(sp), bv = *reinterpret_cast<const uint4 *>(bp);
                 cb.s[0][t] = sv.x, cb.s[1][t] = sv.y, cb.s[2][t] = sv.z, cb.s[3][t] = sv.w;
                 cb.b[0][t] = bv.x, cb.b[1][t] = bv.y, cb.b[2][t] = bv.z, cb.b[3][t] = bv.w;
-            } else {
+            } else if constexpr (CH == 2) {
                 const uint2 sv = *reinterpret_cast<const uint2 *>(sp), bv = *reinterpret_cast<const uint2 *>(bp);
                 cb.s[0][t] = sv.x, cb.s[1][t] = sv.y;
                 cb.b[0][t] = bv.x, cb.b[1][t] = bv.y;
+            } else {
+                cb.s[0][t] = *reinterpret_cast<const uint32_t *>(sp);
+                cb.b[0][t] = *reinterpret_cast<const uint32_t *>(bp);
             }
         }
     };
@@ -176,137 +214,56 @@ __global__ __launch_bounds__(kMfThreads) void q4_gemv_mfma_kernel(
         __builtin_amdgcn_sched_barrier(0);
     };
 
-    // ---- prologue: stage x (or RMSNorm(x + res)) as fragments, and X ----
-    // Item e = (m * G + g) * 2 + h: pieces 4h..4h+3 (8 values each) of group
-    // g of row m. Word w (0..15) of pair p takes fragment ((p * 4 + w % 4) *
-    // 4 + w / 4) * M + m.
-    const uint32_t items = M * G * 2;
-    const uint32_t x_stride = kNorm ? k : x_ld;
-    const bool has_res = kNorm && fu.res != nullptr;
-    const uint16_t *res_src = has_res ? fu.res : x;  // loaded unconditionally; used only with a residual
-    auto frag = [&](uint32_t m, uint32_t g, uint32_t pc) {  // pc: piece in group (0..7)
-        const uint32_t w = (g & 1) * 8 + pc;
-        return (((g >> 1) * 4 + (w & 3)) * 4 + (w >> 2)) * M + m;
-    };
-    struct Item {
-        uint4 v[4], r[kNorm ? 4 : 1];
-    };
-    auto item_load = [&](uint32_t e, Item &it) {
-        const uint32_t ec = e < items ? e : 0;
-        const uint32_t m = ec / (2 * G), g = (ec >> 1) % G, h = ec & 1;
-        const uint64_t o = static_cast<uint64_t>(m) * x_stride + g * kGroup + h * 32;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) it.v[i] = *reinterpret_cast<const uint4 *>(x + o + i * 8);
-        if constexpr (kNorm) {
-#pragma unroll
-            for (int i = 0; i < 4; ++i) it.r[i] = *reinterpret_cast<const uint4 *>(res_src + o + i * 8);
-        }
-    };
-    float ss[M];
-#pragma unroll
-    for (int m = 0; m < M; ++m) ss[m] = 0.f;
-    // pass 1: h = x (+ res) staged; X (plain) or sum of squares (norm)
-    auto item_pass1 = [&](uint32_t e, const Item &it) {
-        const bool live = e < items;
-        const uint32_t ec = live ? e : 0;
-        const uint32_t m = ec / (2 * G), g = (ec >> 1) % G, h = ec & 1;
-        const uint64_t o = static_cast<uint64_t>(m) * x_stride + g * kGroup + h * 32;
-        float acc = 0.f;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            uint4 hv = it.v[i];
-            if constexpr (kNorm) {
-                if (has_res) {
-                    hv = gemv_pairwise(hv, it.r[i], [](float a, float b) { return a + b; });
-                    if (blockIdx.x == 0 && fu.res_out && live) *reinterpret_cast<uint4 *>(fu.res_out + o + i * 8) = hv;
-                }
-                const uint32_t w4[4] = {hv.x, hv.y, hv.z, hv.w};
-#pragma unroll
-                for (int e2 = 0; e2 < 4; ++e2) {
-                    const float lo = bf16_to_f32(w4[e2] & 0xFFFFu), up = bf16_to_f32(w4[e2] >> 16);
-                    acc += lo * lo;
-                    acc += up * up;
-                }
-                xa[live ? frag(m, g, h * 4 + i) : dummy] = gemv_permute(hv);
-            } else {
-                const uint4 p = gemv_permute(hv);
-                xa[live ? frag(m, g, h * 4 + i) : dummy] = p;
-                acc += mf_piece_sum(p);
-            }
-        }
-        if constexpr (kNorm) {
-#pragma unroll
-            for (int mm = 0; mm < M; ++mm)
-                if (live && mm == static_cast<int>(m)) ss[mm] += acc;
-        } else {
-            acc += __shfl_xor(acc, 1, 64);  // the item's other half (lanes e, e ^ 1)
-            if (live && h == 0) xsum[g * 8 + m] = acc;
-        }
-    };
-    uint4 wn = make_uint4(0u, 0u, 0u, 0u);  // this thread's norm-weight piece
-    auto wn_load = [&]() {
-        if constexpr (kNorm) wn = *reinterpret_cast<const uint4 *>(fu.w + (threadIdx.x < wpr ? threadIdx.x : 0) * 8);
-    };
-    auto wn_stage = [&]() {
-        if constexpr (kNorm) *(threadIdx.x < wpr ? wsh + threadIdx.x : xa + dummy) = gemv_permute(wn);
-    };
-    constexpr uint32_t kStraight = mf_straight_rounds<PRO>() * kMfThreads;
-    if (items <= kStraight && (!kNorm || wpr <= kMfThreads)) {
-        Item it[mf_straight_rounds<PRO>()];
-#pragma unroll
-        for (uint32_t rr = 0; rr < mf_straight_rounds<PRO>(); ++rr) item_load(threadIdx.x + rr * kMfThreads, it[rr]);
-        wn_load();
+    // ---- prologue: stage x as fragments, and X ----
+    if constexpr (kPacked) {
+        // x is the LDS image mf_pack_kernel wrote (fragments, zero slot,
+        // dummy slot, X, padded to whole wavefronts): loaded straight into
+        // LDS, 1 KB per wavefront instruction, before the weights; the
+        // barrier below waits for it
+        const uint32_t total = mf_image_slots(M, k);
+        for (uint32_t i0 = wave * 64; i0 < total; i0 += kMfThreads)
+            __builtin_amdgcn_global_load_lds(reinterpret_cast<const uint4 *>(x) + i0 + lane,
+                                             (__attribute__((address_space(3))) void *)(lds + i0),
+                                             16, 0, 0);
         prefetch();
-#pragma unroll
-        for (uint32_t rr = 0; rr < mf_straight_rounds<PRO>(); ++rr) item_pass1(threadIdx.x + rr * kMfThreads, it[rr]);
-        wn_stage();
     } else {
-        for (uint32_t e0 = 0; e0 < items; e0 += kMfThreads) {
-            Item it;
-            item_load(e0 + threadIdx.x, it);
-            item_pass1(e0 + threadIdx.x, it);
+        // Piece Q (16 bytes, 8 values) is column piece Q % ppr of row Q / ppr.
+        // Round i of thread t takes piece i * kMfThreads + t, so each load
+        // instruction of a wavefront reads 1 KB of consecutive pieces, and a
+        // group's 8 pieces sit in 8 neighbouring lanes (group sums by DPP).
+        const uint32_t ppr = k / 8;  // pieces per row
+        const uint32_t pieces = M * ppr;
+        auto piece_load = [&](uint32_t q) {
+            const uint32_t qc = q < pieces ? q : 0u;
+            return *reinterpret_cast<const uint4 *>(x + static_cast<uint64_t>(qc / ppr) * x_ld + (qc % ppr) * 8);
+        };
+        // stores a piece (unpermuted values) as a fragment and its group's X
+        auto piece_stage = [&](uint32_t q, const uint4 v) {
+            const bool live = q < pieces;
+            const uint32_t qc = live ? q : 0u;
+            const uint32_t m = qc / ppr, c = qc % ppr;
+            const uint4 p = gemv_permute(v);
+            if (live) xa[mf_slot<M>(m, c)] = p;
+            const float gsum = group_sum<8>(mf_piece_sum(p));
+            if (live && (c & 7) == 0) xsum[(c >> 3) * 8 + m] = gsum;
+        };
+        constexpr uint32_t kRounds = kMfPlainRounds;
+        if (pieces <= kRounds * kMfThreads) {
+            uint4 v[kRounds];
+#pragma unroll
+            for (uint32_t rr = 0; rr < kRounds; ++rr) v[rr] = piece_load(threadIdx.x + rr * kMfThreads);
+            prefetch();
+#pragma unroll
+            for (uint32_t rr = 0; rr < kRounds; ++rr) piece_stage(threadIdx.x + rr * kMfThreads, v[rr]);
+        } else {
+            for (uint32_t q0 = 0; q0 < pieces; q0 += kMfThreads)
+                piece_stage(q0 + threadIdx.x, piece_load(q0 + threadIdx.x));
+            prefetch();
         }
-        if constexpr (kNorm) {
-            for (uint32_t t = threadIdx.x; t < wpr; t += kMfThreads)
-                wsh[t] = gemv_permute(*reinterpret_cast<const uint4 *>(fu.w + t * 8));
-        }
-        prefetch();
+        // the zero fragment; X = 0 for rows M..7 (the pack image holds them)
+        for (uint32_t t = threadIdx.x; t < (8 - M) * G; t += kMfThreads) xsum[(t % G) * 8 + M + t / G] = 0.f;
     }
-    // the zero fragment; X = 0 for rows M..7
-    if (threadIdx.x == 0) xa[zero] = make_uint4(0u, 0u, 0u, 0u);
-    for (uint32_t t = threadIdx.x; t < (8 - M) * G; t += kMfThreads) xsum[(t % G) * 8 + M + t / G] = 0.f;
-    if constexpr (kNorm) {
-#pragma unroll
-        for (int m = 0; m < M; ++m) {
-            float v = ss[m];
-#pragma unroll
-            for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
-            if (lane == 0) nsum[wave * 8 + m] = v;
-        }
-        __syncthreads();
-        // pass 2: x' = RNE(RNE(h * scale) * w) in place, and X
-        for (uint32_t e0 = 0; e0 < items; e0 += kMfThreads) {
-            const uint32_t e = e0 + threadIdx.x;
-            const bool live = e < items;
-            const uint32_t ec = live ? e : 0;
-            const uint32_t m = ec / (2 * G), g = (ec >> 1) % G, h = ec & 1;
-            float tot = 0.f;
-            for (int w = 0; w < kMfWaves; ++w) tot += nsum[w * 8 + m];
-            const float scale = 1.0f / sqrtf(tot * fu.dim_inv + fu.eps);
-            float acc = 0.f;
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const uint32_t f = frag(m, g, h * 4 + i);
-                const uint4 p = gemv_pairwise(xa[f], wsh[g * 8 + h * 4 + i], [scale](float hh, float gg) {
-                    return bf16_to_f32(f32_to_bf16_rne(hh * scale)) * gg;
-                });
-                xa[live ? f : dummy] = p;
-                acc += mf_piece_sum(p);
-            }
-            acc += __shfl_xor(acc, 1, 64);
-            if (live && h == 0) xsum[g * 8 + m] = acc;
-        }
-    }
+    if (!kPacked && threadIdx.x == 0) xa[zero] = make_uint4(0u, 0u, 0u, 0u);
     __syncthreads();
 
     // ---- main loop ----
@@ -316,8 +273,10 @@ __global__ __launch_bounds__(kMfThreads) void q4_gemv_mfma_kernel(
     // zero fragment (stride 0: every fragment of a dead lane reads it)
     const uint32_t am = col & 7;
     const bool alive = (col >> 3) == hi && am < static_cast<uint32_t>(M);
-    const uint4 *abase = alive ? xa + quarter * M + am : xa + zero;
-    const uint32_t astride = alive ? 4 * M : 0;  // per (pair, j) step
+    const uint4 *abase[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) abase[j] = alive ? xa + j * 4 * M + quarter * M + (am ^ mf_swz<M>(j)) : xa + zero;
+    const uint32_t astride = alive ? 16 * M : 0;  // per pair
 
     mf_f32x4_t acc[NT];
 #pragma unroll
@@ -326,7 +285,7 @@ __global__ __launch_bounds__(kMfThreads) void q4_gemv_mfma_kernel(
     // the task of round r is complete: even + odd halves, the K slices, epilogue, store
     auto finish = [&](uint32_t r) {
         auto store = [&](uint32_t m, uint32_t c, uint32_t tile, float v) {
-            const uint64_t o = static_cast<uint64_t>(m) * y_ld + tile * 16 + c;
+            const uint32_t o = m * y_ld + tile * 16 + c;  // < 2^31 (mf_eligible)
             if (y_is_f32)
                 static_cast<float *>(y)[o] = v;
             else
@@ -383,8 +342,11 @@ __global__ __launch_bounds__(kMfThreads) void q4_gemv_mfma_kernel(
 
     uint32_t cr = 0, cc = 0;  // compute position: round, chunk in task
     // Chunks past `total` (to an even count) compute on reloaded operands and
-    // are dropped: loads and MFMAs stay unconditional.
-    for (uint32_t c0 = 0; c0 < total; c0 += 2) {
+    // are dropped: loads and MFMAs stay unconditional. total >= 1 for every
+    // launch, so the loop runs its body before the first test (a loop that
+    // might not run would let the prefetch sink below the prologue barrier).
+    uint32_t c0 = 0;
+    do {
 #pragma unroll
         for (int d = 0; d < 2; ++d) {
             const uint32_t p0 = (ks * gs) / 2 + cc * CH;
@@ -394,7 +356,7 @@ __global__ __launch_bounds__(kMfThreads) void q4_gemv_mfma_kernel(
                 const float4 xv = *reinterpret_cast<const float4 *>(xsum + (2 * p + hi) * 8 + 4 * (quarter & 1));
                 uint4 a[4];
 #pragma unroll
-                for (int j = 0; j < 4; ++j) a[j] = abase[(p * 4 + j) * astride];
+                for (int j = 0; j < 4; ++j) a[j] = abase[j][p * astride];
 #pragma unroll
                 for (int t = 0; t < NT; ++t) {
                     const uint4 wv = buf[d].w[c2][t];
@@ -426,7 +388,87 @@ __global__ __launch_bounds__(kMfThreads) void q4_gemv_mfma_kernel(
                 ++cr;
             }
         }
+        c0 += 2;
+    } while (c0 < total);
+}
+
+// ---- the pack kernel: RMSNorm(x + res) once, as the GEMV's LDS image ----
+
+constexpr uint32_t kMfPackMaxK = 16384;
+constexpr int kMfPackThreads = 512;
+constexpr int kMfPackPieces = kMfPackMaxK / 8 / kMfPackThreads;  // 16-byte pieces per thread
+static_assert(mf_image_slots(8, kMfPackMaxK) * 16ull <= kPackAreaBytes, "the pack area holds the image of 8 rows");
+
+// Block m (one per x row, k <= kMfPackMaxK): h = x (+ res) (to res_out when
+// given), the row's scale = 1 / sqrt(mean(h^2) + eps) and x' = RNE(RNE(h *
+// scale) * w), RmsNorm's rounding points (src/nn/norm.rs:32-50); x' goes to
+// img as the GEMV's LDS image: fragments (mf_slot), the zero slot, a dummy
+// slot, then X [G][8] = group sums of x' (block 0 writes the zero slot and the
+// zeros of rows M..7). Sums run in a fixed order.
+template <int M>
+__global__ __launch_bounds__(kMfPackThreads) void mf_pack_kernel(const uint16_t *__restrict__ x, GemvFusion fu,
+                                                                uint32_t k, uint4 *__restrict__ img) {
+    __shared__ float part[kMfPackThreads / 64];
+    const uint32_t m = blockIdx.x, ppr = k / 8, G = k / kGroup, t = threadIdx.x;
+    const uint32_t lane = t & 63, wave = t >> 6;
+    const bool has_res = fu.res != nullptr;
+    const uint16_t *xr = x + static_cast<uint64_t>(m) * k;
+    const uint16_t *rr = (has_res ? fu.res : x) + static_cast<uint64_t>(m) * k;  // used only with a residual
+    uint4 h[kMfPackPieces], r[kMfPackPieces], w[kMfPackPieces];
+#pragma unroll
+    for (int i = 0; i < kMfPackPieces; ++i) {
+        const uint32_t c = t + i * kMfPackThreads, cc = c < ppr ? c : 0u;
+        h[i] = *reinterpret_cast<const uint4 *>(xr + cc * 8);
+        r[i] = *reinterpret_cast<const uint4 *>(rr + cc * 8);
+        w[i] = *reinterpret_cast<const uint4 *>(fu.w + cc * 8);
     }
+    float ss = 0.f;
+#pragma unroll
+    for (int i = 0; i < kMfPackPieces; ++i) {
+        const uint32_t c = t + i * kMfPackThreads;
+        const bool live = c < ppr;
+        if (has_res) {
+            h[i] = gemv_pairwise(h[i], r[i], [](float a, float b) { return a + b; });
+            if (fu.res_out && live) *reinterpret_cast<uint4 *>(fu.res_out + static_cast<uint64_t>(m) * k + c * 8) = h[i];
+        }
+        const uint32_t w4[4] = {h[i].x, h[i].y, h[i].z, h[i].w};
+        float sq = 0.f;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const float lo = bf16_to_f32(w4[e] & 0xFFFFu), up = bf16_to_f32(w4[e] >> 16);
+            sq += lo * lo;
+            sq += up * up;
+        }
+        ss += live ? sq : 0.f;
+    }
+    ss = wave_sum(ss);
+    if (lane == 0) part[wave] = ss;
+    __syncthreads();
+    float tot = 0.f;
+#pragma unroll
+    for (int i = 0; i < kMfPackThreads / 64; ++i) tot += part[i];
+    const float scale = 1.0f / sqrtf(tot * fu.dim_inv + fu.eps);
+    float *xs = reinterpret_cast<float *>(img + static_cast<uint64_t>(M) * ppr + 2);
+    if (m == 0 && t == 0) img[static_cast<uint64_t>(M) * ppr] = make_uint4(0u, 0u, 0u, 0u);  // the zero slot
+#pragma unroll
+    for (int i = 0; i < kMfPackPieces; ++i) {
+        const uint32_t c = t + i * kMfPackThreads;
+        const bool live = c < ppr;
+        const uint4 p = gemv_permute(gemv_pairwise(h[i], w[i], [scale](float hh, float gg) {
+            return bf16_to_f32(f32_to_bf16_rne(hh * scale)) * gg;
+        }));
+        if (live) img[mf_slot<M>(m, c)] = p;
+        const float gsum = group_sum<8>(mf_piece_sum(p));
+        if (live && (c & 7) == 0) xs[(c >> 3) * 8 + m] = gsum;
+    }
+    if (m == 0)
+        for (uint32_t j = t; j < (8 - M) * G; j += kMfPackThreads) xs[(j % G) * 8 + M + j / G] = 0.f;
+}
+
+template <int M>
+inline void launch_mf_pack_m(hipStream_t stream, const GemvArgs &a, void *area) {
+    hipLaunchKernelGGL(mf_pack_kernel<M>, dim3(M), dim3(kMfPackThreads), 0, stream, a.x, a.fu, a.k,
+                       static_cast<uint4 *>(area));
 }
 
 // Picks the K split (wavefronts per task) from the weight's 16-row tiles, its
@@ -434,13 +476,13 @@ __global__ __launch_bounds__(kMfThreads) void q4_gemv_mfma_kernel(
 // the same weight (SiLU pairs included) adds the same partial sums in the
 // same order: the fewest rounds of tiles times groups per wavefront (the
 // critical path), then the fewest rounds, then the smallest split (less
-// reduction). A split leaves each wavefront a multiple of 4 groups; 0 if none
+// reduction). A split leaves each wavefront a multiple of 2 groups; 0 if none
 // does.
 inline uint32_t pick_mf_split(uint32_t weight_tiles, uint32_t groups, uint32_t cus) {
     uint32_t best_s = 0;
     uint64_t best_cost = ~0ull, best_rounds = ~0ull;
     for (uint32_t s = 1; s <= static_cast<uint32_t>(kMfWaves); s *= 2) {
-        if (groups % (s * 4) != 0) continue;
+        if (groups % (s * 2) != 0) continue;
         const uint32_t slots = kMfWaves / s;
         const uint32_t need = (weight_tiles + slots - 1) / slots;
         const uint64_t blocks = need < cus ? need : cus;
@@ -458,21 +500,23 @@ inline uint32_t pick_mf_split(uint32_t weight_tiles, uint32_t groups, uint32_t c
 template <int M, int PRO, int EPI, int CH>
 inline void launch_gemv_mfma_t(hipStream_t stream, uint32_t cus, const GemvArgs &a, uint32_t ksplit) {
     auto kernel = q4_gemv_mfma_kernel<M, PRO, EPI, CH>;
-    const uint32_t lds = mf_lds_bytes(M, a.k, mf_tiles_per_task<EPI>(), PRO == kProRmsNorm);
+    const uint32_t lds = mf_lds_bytes(M, a.k, mf_tiles_per_task<EPI>());
     int per_cu = 0;
     if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, kMfThreads, lds) != hipSuccess || per_cu < 1)
         per_cu = 1;
     const uint32_t n_out = EPI == kEpiSiluMul ? a.n / 2 : a.n;
     const uint32_t slots = kMfWaves / ksplit;
     const uint32_t need = (n_out / 16 + slots - 1) / slots;
-    const uint32_t cap = cus * static_cast<uint32_t>(per_cu);
-    hipLaunchKernelGGL(kernel, dim3(need < cap ? need : cap), dim3(kMfThreads), lds, stream, a.x, a.x_ld, a.wq,
-                       a.s, a.b, a.n, a.k, a.y, a.y_ld, a.y_is_f32, a.fu, ksplit);
+    const uint32_t ranges = a.kranges > 1 ? a.kranges : 1;
+    const uint32_t cap = (cus / ranges > 0 ? cus / ranges : 1) * static_cast<uint32_t>(per_cu);
+    hipLaunchKernelGGL(kernel, dim3(need < cap ? need : cap, a.kranges > 1 ? a.kranges : 1), dim3(kMfThreads), lds,
+                       stream, a.x, a.x_ld, a.wq, a.s, a.b, a.n, a.k, a.y, a.y_ld, a.y_is_f32, ksplit);
 }
 
 // Whether the matrix-core GEMV takes this launch of 2..8 rows: k a multiple of
 // 256 with a K split for it, 16-row output tiles, 16-byte aligned operands,
-// and at least 2 x rows staged per launch (the caller splits larger m).
+// at least 2 x rows staged per launch (the caller splits larger m), and with
+// RMSNorm rows the pack area can hold.
 inline bool mf_eligible(uint32_t m, const GemvArgs &a) {
     const uint32_t n_out = a.epi == kEpiSiluMul ? a.n / 2 : a.n;
     if (m < 2 || m > 8 || a.k == 0 || a.k % (kGroup * 4) != 0 || n_out == 0 || n_out % 16 != 0 ||
@@ -480,7 +524,9 @@ inline bool mf_eligible(uint32_t m, const GemvArgs &a) {
         return false;
     if ((reinterpret_cast<uintptr_t>(a.wq) | reinterpret_cast<uintptr_t>(a.s) | reinterpret_cast<uintptr_t>(a.b)) & 15u)
         return false;
-    return mf_rows_per_launch(a.k, a.epi == kEpiSiluMul ? 2 : 1, a.pro == kProRmsNorm) >= 2;
+    if (a.pro == kProRmsNorm && a.k > kMfPackMaxK) return false;  // the pack area's row limit
+    if (static_cast<uint64_t>(m) * a.y_ld >= (1ull << 31)) return false;  // 32-bit output offsets
+    return mf_rows_per_launch(a.k, a.epi == kEpiSiluMul ? 2 : 1) >= 2;
 }
 
 // Defined in q4_gemv_m<M>.hip.
@@ -488,23 +534,36 @@ template <int M>
 void launch_gemv_mfma_m(hipStream_t stream, uint32_t cus, const GemvArgs &a);
 
 // Chunk width: 4 group pairs when each wavefront's slice allows it (one
-// 16-byte scale and one bias load per 8 groups), else 2; the SiLU variant
-// keeps 2 (two tiles of buffers).
+// 16-byte scale and one bias load per 8 groups), else 2, else 1; the SiLU
+// variant takes at most 2 (two tiles of buffers).
 template <int M>
 inline void launch_gemv_mfma_dispatch(hipStream_t stream, uint32_t cus, const GemvArgs &a) {
     const uint32_t groups = a.k / kGroup;
-    const uint32_t ksplit = pick_mf_split(a.n / 16, groups, cus);
-    const bool wide = (groups / ksplit) % 8 == 0;
+    const uint32_t ranges = a.kranges > 1 ? a.kranges : 1;
+    const uint32_t ksplit = pick_mf_split(a.n / 16, groups, cus / ranges > 0 ? cus / ranges : 1);
+    const uint32_t gs = groups / ksplit;
+    const int ch = gs % 8 == 0 && a.epi != kEpiSiluMul ? 4 : gs % 4 == 0 ? 2 : 1;
+#define FH_MF_LAUNCH(P, E)                                                                 \
+    do {                                                                                   \
+        if (ch == 4) launch_gemv_mfma_t<M, P, E, 4>(stream, cus, a, ksplit);                \
+        else if (ch == 2) launch_gemv_mfma_t<M, P, E, 2>(stream, cus, a, ksplit);           \
+        else launch_gemv_mfma_t<M, P, E, 1>(stream, cus, a, ksplit);                        \
+    } while (0)
     if (a.epi == kEpiSiluMul) {
-        if (a.pro == kProRmsNorm) launch_gemv_mfma_t<M, kProRmsNorm, kEpiSiluMul, 2>(stream, cus, a, ksplit);
-        else launch_gemv_mfma_t<M, kProNone, kEpiSiluMul, 2>(stream, cus, a, ksplit);
+        // (the 4-pair width is never taken with two tiles of buffers)
+        if (a.pro == kProRmsNorm) {
+            if (ch == 1) launch_gemv_mfma_t<M, kProRmsNorm, kEpiSiluMul, 1>(stream, cus, a, ksplit);
+            else launch_gemv_mfma_t<M, kProRmsNorm, kEpiSiluMul, 2>(stream, cus, a, ksplit);
+        } else {
+            if (ch == 1) launch_gemv_mfma_t<M, kProNone, kEpiSiluMul, 1>(stream, cus, a, ksplit);
+            else launch_gemv_mfma_t<M, kProNone, kEpiSiluMul, 2>(stream, cus, a, ksplit);
+        }
     } else if (a.pro == kProRmsNorm) {
-        if (wide) launch_gemv_mfma_t<M, kProRmsNorm, kEpiNone, 4>(stream, cus, a, ksplit);
-        else launch_gemv_mfma_t<M, kProRmsNorm, kEpiNone, 2>(stream, cus, a, ksplit);
+        FH_MF_LAUNCH(kProRmsNorm, kEpiNone);
     } else {
-        if (wide) launch_gemv_mfma_t<M, kProNone, kEpiNone, 4>(stream, cus, a, ksplit);
-        else launch_gemv_mfma_t<M, kProNone, kEpiNone, 2>(stream, cus, a, ksplit);
+        FH_MF_LAUNCH(kProNone, kEpiNone);
     }
+#undef FH_MF_LAUNCH
 }
 
 }  // namespace fh

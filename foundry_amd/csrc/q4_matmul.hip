@@ -13,6 +13,7 @@ int check_q4_table(const fh_device *dev, const char *fn, const uint32_t *wq,
                    int64_t group);
 void launch_q4_gemv(hipStream_t stream, uint32_t cus, int m, const GemvArgs &a);
 void launch_q4_gemv_mfma(hipStream_t stream, uint32_t cus, int m, const GemvArgs &a);
+void launch_mf_pack(hipStream_t stream, int m, const GemvArgs &a, void *area);
 uint32_t gemv_rows_per_launch(uint32_t k, bool norm);
 void launch_q4_gemm(hipStream_t stream, const uint16_t *x, uint32_t x_ld, const uint32_t *wq,
                     const uint16_t *s, const uint16_t *b, uint32_t m, uint32_t n, uint32_t k,
@@ -23,13 +24,92 @@ constexpr int64_t kGemvMaxRows = 8;
 
 // Launches the GEMV over m rows in groups whose staged x fits LDS (every
 // prologue and epilogue is row-independent): the matrix-core kernel for
-// groups of 2..8 rows where it takes the shape, else the dot2 kernel; x,
-// res, res_out and y advance by their row strides. y_cols: columns of y per
-// row.
+// groups of 2..8 rows where it takes the shape (after the pack kernel for
+// RMSNorm rows), else the dot2 kernel; x, res, res_out and y advance by their
+// row strides. y_cols: columns of y per row.
+// Ranges of K a matrix-core GEMV may be split into (partial sums per range).
+constexpr uint32_t kMfMaxRanges = 8;
+// x bytes per block the range count aims at (each block stages its range of
+// every x row).
+constexpr uint32_t kMfRangeXBytes = 32 * 1024;
+
+// Adds the K-range partial sums [ranges][rows][n] of a split GEMV in range
+// order (4 outputs per thread, every range's load issued first) and writes y
+// (RNE to bf16, or f32).
+__global__ __launch_bounds__(256) void mf_combine_kernel(const float *__restrict__ part, uint32_t ranges,
+                                                         uint32_t rows, uint32_t n, void *__restrict__ y,
+                                                         uint32_t y_ld, int y_is_f32) {
+    const uint32_t i = (blockIdx.x * 256 + threadIdx.x) * 4;
+    const uint32_t ic = i < rows * n ? i : 0u;
+    const uint32_t m = ic / n, c = ic % n;
+    float4 q[kMfMaxRanges];
+#pragma unroll
+    for (uint32_t r = 0; r < kMfMaxRanges; ++r)
+        q[r] = *reinterpret_cast<const float4 *>(part + (static_cast<uint64_t>(r < ranges ? r : 0u) * rows + m) * n + c);
+    float4 v = q[0];
+#pragma unroll
+    for (uint32_t r = 1; r < kMfMaxRanges; ++r)
+        if (r < ranges) v = make_float4(v.x + q[r].x, v.y + q[r].y, v.z + q[r].z, v.w + q[r].w);
+    if (i >= rows * n) return;
+    const uint64_t o = static_cast<uint64_t>(m) * y_ld + c;
+    if (y_is_f32) {
+        float *yo = static_cast<float *>(y) + o;
+        yo[0] = v.x, yo[1] = v.y, yo[2] = v.z, yo[3] = v.w;
+    } else {
+        uint16_t *yo = static_cast<uint16_t *>(y) + o;
+        yo[0] = static_cast<uint16_t>(f32_to_bf16_rne(v.x));
+        yo[1] = static_cast<uint16_t>(f32_to_bf16_rne(v.y));
+        yo[2] = static_cast<uint16_t>(f32_to_bf16_rne(v.z));
+        yo[3] = static_cast<uint16_t>(f32_to_bf16_rne(v.w));
+    }
+}
+
+// K ranges for m plain rows whose x does not fit LDS over the whole row:
+// ranges of a multiple of 512 values (every range's scale and bias rows
+// start 16-byte aligned) that hold all m rows, preferring the fewest whose
+// staged x is at most kMfRangeXBytes, else the fewest that fit; 0 if none.
+static uint32_t mf_k_ranges(fh_device *dev, int64_t m, const GemvArgs &a) {
+    if (a.pro != kProNone || a.epi != kEpiNone || a.n % 4 != 0) return 0;
+    for (int pass = 0; pass < 2; ++pass) {
+        for (uint32_t r = 2; r <= kMfMaxRanges; ++r) {
+            if (a.k % (r * 512) != 0) continue;
+            const uint32_t kp = a.k / r;
+            if (pass == 0 && static_cast<uint64_t>(kp) * m * 2 > kMfRangeXBytes) continue;
+            if (static_cast<uint64_t>(r) * m * a.n * 4 > kPartialAreaBytes) continue;
+            const uint32_t cus = dev->compute_units / r > 0 ? dev->compute_units / r : 1;
+            if (mf_rows_per_launch(kp, 1) >= m && pick_mf_split(a.n / 16, kp / kGroup, cus) != 0) return r;
+        }
+    }
+    return 0;
+}
+
 int launch_gemv_rows(fh_device *dev, const char *fn, int64_t m, const GemvArgs &base, int64_t y_cols) {
     const bool mf = m >= 2 && mf_eligible(static_cast<uint32_t>(m), base);
-    const int64_t per = mf ? mf_rows_per_launch(base.k, base.epi == kEpiSiluMul ? 2 : 1, base.pro == kProRmsNorm)
+    const int64_t per = mf ? mf_rows_per_launch(base.k, base.epi == kEpiSiluMul ? 2 : 1)
                            : gemv_rows_per_launch(base.k, base.pro == kProRmsNorm);
+    if (mf && per < m) {
+        // all rows over K ranges instead of row groups over all of K: the
+        // weights are read once, each block stages one range of x, and the
+        // combine kernel adds the ranges' f32 sums (the device's partial area)
+        if (const uint32_t ranges = mf_k_ranges(dev, m, base)) {
+            GemvArgs a = base;
+            a.k = base.k / ranges;
+            a.kranges = ranges;
+            a.y = dev->partial_area;
+            a.y_is_f32 = 1;
+            a.y_ld = base.n;
+            if (int rc = dispatch(dev, fn, [&] {
+                    launch_q4_gemv_mfma(dev->stream, dev->compute_units, static_cast<int>(m), a);
+                }))
+                return rc;
+            const uint32_t outs = static_cast<uint32_t>(m) * base.n;
+            return dispatch(dev, fn, [&] {
+                hipLaunchKernelGGL(mf_combine_kernel, dim3((outs / 4 + 255) / 256), dim3(256), 0, dev->stream,
+                                   static_cast<const float *>(dev->partial_area), ranges, static_cast<uint32_t>(m),
+                                   base.n, base.y, static_cast<uint32_t>(y_cols), base.y_is_f32);
+            });
+        }
+    }
     for (int64_t r0 = 0; r0 < m; r0 += per) {
         const int rows = static_cast<int>(m - r0 < per ? m - r0 : per);
         GemvArgs a = base;
@@ -38,6 +118,12 @@ int launch_gemv_rows(fh_device *dev, const char *fn, int64_t m, const GemvArgs &
         if (a.fu.res_out) a.fu.res_out += r0 * base.k;
         a.y = base.y_is_f32 ? static_cast<void *>(static_cast<float *>(base.y) + r0 * y_cols)
                             : static_cast<void *>(static_cast<uint16_t *>(base.y) + r0 * y_cols);
+        if (mf && rows >= 2 && a.pro == kProRmsNorm) {
+            // RMSNorm rows: normalised once into the pack area, which the
+            // matrix-core GEMV then takes as its x
+            if (int rc = dispatch(dev, fn, [&] { launch_mf_pack(dev->stream, rows, a, dev->pack_area); })) return rc;
+            a.x = static_cast<const uint16_t *>(dev->pack_area);
+        }
         int rc = dispatch(dev, fn, [&] {
             if (mf && rows >= 2)
                 launch_q4_gemv_mfma(dev->stream, dev->compute_units, rows, a);

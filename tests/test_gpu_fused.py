@@ -68,7 +68,7 @@ def bits(a):
 
 
 @pytest.mark.parametrize("m,k,with_res", [(1, 3072, False), (1, 3072, True), (3, 3072, True), (8, 3072, True),
-                                          (8, 4096, False), (2, 8192, True)])
+                                          (8, 4096, False), (2, 8192, True), (8, 8192, True), (5, 6144, False)])
 def test_matmul_rmsnorm(device, oracle, m, k, with_res):
     n = 1024
     x = synth.bf16_normal(30 + m, (m, k))
