@@ -212,8 +212,9 @@ def test_gemv_golden(device):
         check_matmul(y32, y16, g["gemv_y64"])
 
 
-def test_gemv_strided_x(device, oracle):
-    run_linear(device, oracle, 3, 512, 1024, seed=77, x_ld=1024 + 64)
+@pytest.mark.parametrize("m,n,k,x_ld", [(3, 512, 1024, 1024 + 64), (8, 256, 14336, 14336 + 128)])
+def test_gemv_strided_x(device, oracle, m, n, k, x_ld):
+    run_linear(device, oracle, m, n, k, seed=77, x_ld=x_ld)
 
 
 # ---------------- GEMM (m > 8) ----------------
