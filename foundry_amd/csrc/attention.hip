@@ -45,7 +45,10 @@ constexpr int kAttnChunk = 64;
 constexpr int kAttnThreads = 256;
 constexpr int kAttnWaves = kAttnThreads / 64;
 constexpr int kAttnMaxGroup = 8;
-constexpr uint64_t kAttnTargetBlocks = 1024;
+#ifndef FH_ATTN_TARGET_BLOCKS
+#define FH_ATTN_TARGET_BLOCKS 1024
+#endif
+constexpr uint64_t kAttnTargetBlocks = FH_ATTN_TARGET_BLOCKS;
 
 // Workspace: per-chunk softmax statistics [rows][n_heads][nck] float2, then
 // the scores [rows][n_heads][max_len] f32, then (chunked P.V) the partial
