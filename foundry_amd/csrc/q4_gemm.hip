@@ -4,16 +4,17 @@
 //
 // Compute-bound (about 1700 FLOP per HBM byte at the Llama-3.2-3B MLP shape).
 // Design for CDNA4:
-// - Block tile 256 (rows of X) x 256 (weight rows), K step 64 = one
-//   quantisation group, 512 threads = 8 wavefronts in a 2 x 4 arrangement
-//   (two per SIMD, so one wavefront's dequantisation overlaps the other's
-//   MFMAs). Each wavefront owns a 128 x 64 output tile: 4 x 2 accumulators of
-//   v_mfma_f32_32x32x16_bf16 (fp32, 128 registers per lane).
+// - Block tile 256 (rows of X) x 256 (weight rows), or 256 x 128 when the
+//   larger tile would leave CUs idle; K step 64 = one quantisation group;
+//   512 threads = 8 wavefronts (two per SIMD, so one wavefront's
+//   dequantisation overlaps the other's MFMAs), 2 x 4 of 128 x 64 tiles
+//   (4 x 2 accumulators of v_mfma_f32_32x32x16_bf16, fp32, 128 registers per
+//   lane) or 4 x 2 of 64 x 64.
 // - LDS holds two stages of both tiles (X and dequantised W, bf16, row pitch
 //   72 so 16-byte fragment reads and writes are conflict-free): 144 KiB of the
-//   CU's 160 KiB. One barrier per K step: while step i is computed from one
-//   stage, step i+1's global loads are in flight and then written to the
-//   other.
+//   CU's 160 KiB at 256 x 256. One barrier per K step: while step i is
+//   computed from one stage, step i+1's global loads are in flight and then
+//   written to the other.
 // - Weights are dequantised in registers on the way to LDS: each thread owns
 //   32 nibbles of one weight row for the step (inside one group: one scale and
 //   bias), converts each nibble exactly (v_cvt_f32_ubyte), forms s*q + b with
@@ -28,17 +29,24 @@
 
 namespace fh {
 
-constexpr int kBM = 256;
-constexpr int kBN = 256;
 constexpr int kBK = 64;
 constexpr int kPitch = kBK + 8;  // bf16 elements per LDS row
-constexpr int kTileElems = kBM * kPitch;
-constexpr uint32_t kGemmLds = 4u * kTileElems * 2u;  // 2 stages x (X + W), bytes
-constexpr int WM = 2, WN = 4;                        // wavefront arrangement
-constexpr int kGemmThreads = 64 * WM * WN;
-constexpr int TI = kBM / WM / 32, TJ = kBN / WN / 32;  // 32x32 MFMA tiles per wavefront
-constexpr int kXPieces = kBM * kBK / 8 / kGemmThreads;  // 16-byte X pieces per thread
-constexpr int kWPieces = kBN * 2 / kGemmThreads;        // 16-byte W pieces per thread
+
+// Block tile BM x BN, WM x WN wavefronts each owning (BM/WM) x (BN/WN).
+template <int BM, int BN, int WM, int WN>
+struct GemmTile {
+    static constexpr int kThreads = 64 * WM * WN;
+    static constexpr int kXElems = BM * kPitch, kWElems = BN * kPitch;  // one stage
+    static constexpr uint32_t kLds = 2u * (kXElems + kWElems) * 2u;      // 2 stages, bytes
+    static constexpr int TI = BM / WM / 32, TJ = BN / WN / 32;           // 32x32 MFMA tiles per wavefront
+    static constexpr int kXPieces = BM * kBK / 8 / kThreads;             // 16-byte X pieces per thread
+    // 16-byte W pieces per thread; with fewer pieces than threads, the first
+    // BN * 2 threads (whole wavefronts) stage one each
+    static constexpr int kWPieces = BN * 2 >= kThreads ? BN * 2 / kThreads : 1;
+    static constexpr int kWThreads = BN * 2 >= kThreads ? kThreads : BN * 2;
+    static_assert(kXPieces >= 1 && BM * kBK / 8 % kThreads == 0 && BN * 2 % kWThreads == 0 && kWThreads % 64 == 0,
+                  "every staging thread stages whole pieces");
+};
 
 typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8_t;
 typedef __attribute__((ext_vector_type(16))) float f32x16_t;
@@ -67,15 +75,20 @@ __device__ __forceinline__ uint4 dequant_word(uint32_t w, float s, float b) {
     return o;
 }
 
-__global__ __launch_bounds__(kGemmThreads) void q4_gemm_kernel(
+template <int BM, int BN, int WM, int WN>
+__global__ __launch_bounds__(64 * WM * WN) void q4_gemm_kernel(
     const uint16_t *__restrict__ x, uint32_t x_ld, const uint32_t *__restrict__ wq,
     const uint16_t *__restrict__ scales, const uint16_t *__restrict__ biases, uint32_t m,
     uint32_t n, uint32_t k, void *__restrict__ y, int y_is_f32) {
+    using T = GemmTile<BM, BN, WM, WN>;
+    constexpr int kGemmThreads = T::kThreads, TI = T::TI, TJ = T::TJ;
+    constexpr int kXPieces = T::kXPieces, kWPieces = T::kWPieces;
+    constexpr int kBM = BM, kBN = BN;
     extern __shared__ __attribute__((aligned(16))) uint16_t smem[];
     uint16_t *const xs0 = smem;
-    uint16_t *const ws0 = smem + kTileElems;
-    uint16_t *const xs1 = smem + 2 * kTileElems;
-    uint16_t *const ws1 = smem + 3 * kTileElems;
+    uint16_t *const ws0 = smem + T::kXElems;
+    uint16_t *const xs1 = smem + T::kXElems + T::kWElems;
+    uint16_t *const ws1 = smem + 2 * T::kXElems + T::kWElems;
 
     const uint32_t tid = threadIdx.x;
     const uint32_t lane = tid & 63;
@@ -103,9 +116,10 @@ __global__ __launch_bounds__(kGemmThreads) void q4_gemm_kernel(
             else
                 xr[i] = make_uint4(0u, 0u, 0u, 0u);
         }
+        if (tid >= T::kWThreads) return;  // whole wavefronts
 #pragma unroll
         for (int i = 0; i < kWPieces; ++i) {
-            const uint32_t idx = tid + kGemmThreads * i;
+            const uint32_t idx = tid + T::kWThreads * i;
             const uint32_t r = idx >> 1, half = idx & 1;
             const uint64_t row = n0 + r < n ? n0 + r : 0;
             wr[i] = reinterpret_cast<const uint4 *>(wq + row * kw + k0 / 8)[half];
@@ -121,9 +135,10 @@ __global__ __launch_bounds__(kGemmThreads) void q4_gemm_kernel(
             const uint32_t r = idx >> 3, piece = idx & 7;
             *reinterpret_cast<uint4 *>(&xs[r * kPitch + piece * 8]) = xr[i];
         }
+        if (tid >= T::kWThreads) return;
 #pragma unroll
         for (int i = 0; i < kWPieces; ++i) {
-            const uint32_t idx = tid + kGemmThreads * i;
+            const uint32_t idx = tid + T::kWThreads * i;
             const uint32_t r = idx >> 1, half = idx & 1;
             uint4 *dst = reinterpret_cast<uint4 *>(&ws[r * kPitch + half * 32]);
             const float s = bf16_to_f32(sr[i]), b = bf16_to_f32(br[i]);
@@ -203,19 +218,36 @@ __global__ __launch_bounds__(kGemmThreads) void q4_gemm_kernel(
         }
 }
 
-void launch_q4_gemm(hipStream_t stream, const uint16_t *x, uint32_t x_ld, const uint32_t *wq,
-                    const uint16_t *s, const uint16_t *b, uint32_t m, uint32_t n, uint32_t k,
-                    void *y, int y_is_f32) {
+template <int BM, int BN, int WM, int WN>
+static void launch_gemm_tile(hipStream_t stream, const uint16_t *x, uint32_t x_ld, const uint32_t *wq,
+                             const uint16_t *s, const uint16_t *b, uint32_t m, uint32_t n, uint32_t k, void *y,
+                             int y_is_f32) {
+    using T = GemmTile<BM, BN, WM, WN>;
     static bool lds_opt_in = false;
     if (!lds_opt_in) {
         // more than 64 KiB of dynamic LDS needs the kernel's opt-in
-        (void)hipFuncSetAttribute(reinterpret_cast<const void *>(q4_gemm_kernel),
-                                  hipFuncAttributeMaxDynamicSharedMemorySize, kGemmLds);
+        (void)hipFuncSetAttribute(reinterpret_cast<const void *>(q4_gemm_kernel<BM, BN, WM, WN>),
+                                  hipFuncAttributeMaxDynamicSharedMemorySize, T::kLds);
         lds_opt_in = true;
     }
-    dim3 grid((n + kBN - 1) / kBN, (m + kBM - 1) / kBM);
-    hipLaunchKernelGGL(q4_gemm_kernel, grid, dim3(kGemmThreads), kGemmLds, stream, x, x_ld, wq, s,
-                       b, m, n, k, y, y_is_f32);
+    dim3 grid((n + BN - 1) / BN, (m + BM - 1) / BM);
+    hipLaunchKernelGGL((q4_gemm_kernel<BM, BN, WM, WN>), grid, dim3(T::kThreads), T::kLds, stream, x, x_ld, wq, s, b,
+                       m, n, k, y, y_is_f32);
+}
+
+// 256 x 256 tiles, or 256 x 128 when the larger tile leaves CUs idle: each
+// weight element is still dequantised once per 256 rows of X, and the
+// down-projection shape (2048 x 3072 x 8192) gets 192 blocks instead of 96
+// (249 -> 186 us; the 2048 x 8192 x 3072 shape stays at 256 x 256, 139 us
+// against 164).
+void launch_q4_gemm(hipStream_t stream, uint32_t cus, const uint16_t *x, uint32_t x_ld, const uint32_t *wq,
+                    const uint16_t *s, const uint16_t *b, uint32_t m, uint32_t n, uint32_t k, void *y,
+                    int y_is_f32) {
+    const uint64_t big = static_cast<uint64_t>((n + 255) / 256) * ((m + 255) / 256);
+    if (big < cus)
+        launch_gemm_tile<256, 128, 4, 2>(stream, x, x_ld, wq, s, b, m, n, k, y, y_is_f32);
+    else
+        launch_gemm_tile<256, 256, 2, 4>(stream, x, x_ld, wq, s, b, m, n, k, y, y_is_f32);
 }
 
 }  // namespace fh
