@@ -190,7 +190,7 @@ def test_embed_empty(device):
     "m,n,k",
     [(1, 8192, 3072), (1, 3072, 8192), (1, 1000, 64), (1, 1024, 3072), (3, 40, 128),
      (2, 4096, 4096), (4, 333, 192), (8, 14336, 4096), (8, 4096, 14336), (5, 3072, 8192),
-     (7, 129, 1024), (1, 17, 30720), (6, 256, 10240), (8, 512, 24576)],
+     (7, 129, 1024), (1, 17, 30720), (6, 256, 10240), (8, 512, 24576), (5, 128, 14336), (3, 64, 24576)],
 )
 def test_gemv_parity(device, oracle, m, n, k):
     err = run_linear(device, oracle, m, n, k, seed=1000 + m * 7 + n + k)
