@@ -534,15 +534,35 @@ template <int M>
 void launch_gemv_mfma_m(hipStream_t stream, uint32_t cus, const GemvArgs &a);
 
 // Chunk width: 4 group pairs when each wavefront's slice allows it (one
-// 16-byte scale and one bias load per 8 groups), else 2, else 1; the SiLU
-// variant takes at most 2 (two tiles of buffers).
+// 16-byte scale and one bias load per 8 groups), else 2, else 1, at most
+// half the slice; the SiLU variant takes at most 2 (two tiles of buffers).
 template <int M>
 inline void launch_gemv_mfma_dispatch(hipStream_t stream, uint32_t cus, const GemvArgs &a) {
     const uint32_t groups = a.k / kGroup;
     const uint32_t ranges = a.kranges > 1 ? a.kranges : 1;
     const uint32_t ksplit = pick_mf_split(a.n / 16, groups, cus / ranges > 0 ? cus / ranges : 1);
     const uint32_t gs = groups / ksplit;
-    const int ch = gs % 8 == 0 && a.epi != kEpiSiluMul ? 4 : gs % 4 == 0 ? 2 : 1;
+    // Chunks go in pairs, so an odd chunk count per wavefront loads and
+    // computes one chunk twice: take the widest chunk whose count (rounds of
+    // tiles x chunks per task, rounds as launch_gemv_mfma_t sizes the grid at
+    // one block per CU) is even or at least 5, else the narrowest.
+    const uint32_t ranges_ = a.kranges > 1 ? a.kranges : 1;
+    const uint32_t cap = cus / ranges_ > 0 ? cus / ranges_ : 1;
+    const uint32_t slots = kMfWaves / ksplit;
+    const uint32_t task_tiles = (a.epi == kEpiSiluMul ? a.n / 2 : a.n) / 16;
+    const uint32_t need = (task_tiles + slots - 1) / slots;
+    const uint32_t blocks = need < cap ? need : cap;
+    const uint32_t rounds = (task_tiles + blocks * slots - 1) / (blocks * slots);
+    int ch = 1;
+    for (const int c : {4, 2, 1}) {
+        if (c == 4 && a.epi == kEpiSiluMul) continue;
+        if (gs % (2 * c) != 0) continue;
+        const uint32_t total = rounds * (gs / (2 * c));
+        if (total % 2 == 0 || total >= 5) {
+            ch = c;
+            break;
+        }
+    }
 #define FH_MF_LAUNCH(P, E)                                                                 \
     do {                                                                                   \
         if (ch == 4) launch_gemv_mfma_t<M, P, E, 4>(stream, cus, a, ksplit);                \
