@@ -26,8 +26,13 @@
 //   1 KB runs and permutes it into fragments. With RMSNorm (fh_q4_matmul_
 //   rmsnorm, fh_q4_gate_up_silu) a separate pack kernel normalises x once
 //   and writes the finished LDS image to the device's pack area, and the
-//   prologue only copies it: per-block normalisation of 8 rows was VALU-bound
-//   (about 8 us of every launch).
+//   prologue only copies it (global_load_lds_dwordx4, straight into LDS):
+//   per-block normalisation of 8 rows was VALU-bound (about 8 us of every
+//   launch).
+// - Rows whose x does not fit LDS over the whole row (8 x 14336, the down
+//   projection) run over K ranges: blockIdx.y picks the range, each block
+//   stages that range of x, and the f32 partial tiles go to the device's
+//   partial area for mf_combine_kernel (q4_matmul.hip) to add in order.
 // - Work: blocks of 16 wavefronts, persistent; a task is one output tile
 //   (gate and up tiles together for the SiLU epilogue) over a K slice; S
 //   wavefronts split K (S = 1..16) and add their partial tiles in LDS in a
