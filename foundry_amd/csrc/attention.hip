@@ -33,6 +33,12 @@
 // splits, slices and chunks make rows * n_kv * (blocks per pair) about
 // kAttnTargetBlocks: decode spreads one row over many CUs, prefill keeps one
 // block per (row, KV head).
+// Decode over a cache of at most 1024 positions (head_dim 64 or 128) runs
+// instead as ONE launch, attn_decode_short_kernel: each block scores all of
+// its KV head's keys itself (16 wavefronts, a chunk each), meets the chunks'
+// statistics at block barriers and sums P.V for a 16-dim slice of V. Its
+// cost is the keys every block pulls through one CU (about 34 GB/s per CU
+// in the matrix-core fragment pattern), so it only pays for short caches.
 #include "decoder_common.hpp"
 
 #ifndef FH_PV_CHUNKED_MIN_KEYS
@@ -589,6 +595,255 @@ __global__ __launch_bounds__(kAttnThreads) void attn_combine_kernel(
     }
 }
 
+// Decode attention over a cache of at most kShortKeys positions in ONE
+// launch: block (part, KV head, row) of 16 wavefronts, wavefront w owning
+// chunk w (keys 64 w .. 64 w + 63).
+//   1. Every block rotates the row's q and key (LDS); part 0 writes the new
+//      key and value to the cache.
+//   2. A wavefront scores its chunk on the matrix cores (the fragments of
+//      attn_scores_kernel), then moves the live rows of the 16x16 results
+//      (G of 16 heads) through LDS so that lane = key and one register per
+//      head: the softmax arithmetic then runs on G values per lane, not 16.
+//      s_j = RNE(q.k_j) * scale; the chunk's max per head goes to LDS.
+//   3. M = max over the chunks; e_j = exp(s_j - M); the chunk's sum of e_j
+//      per head goes to LDS.
+//   4. S = sum of the chunk sums (a fixed 16-lane tree, the same in every
+//      wavefront and block); p_j = RNE(e_j / S), the reference's rounding
+//      point, into the wavefront's LDS slice.
+//   5. The wavefront sums p_j v_j over its keys for the block's DB dims
+//      (part * DB ..), lanes (dim pair, key slot); slots are added within
+//      aligned lane groups, then the wavefronts' partials in wavefront order.
+// Every output is a sum in a fixed order. The head_dim / DB parts of a KV
+// head each read all of its keys (for the scores) and DB dims of its
+// values; blocks of one KV head are n_kv apart in the grid, which the
+// dispatcher deals round-robin to the XCDs, so with 8 KV heads a head's
+// parts share an L2.
+constexpr int kShortThreads = 1024;
+constexpr int kShortWaves = kShortThreads / 64;
+constexpr uint32_t kShortKeys = kShortWaves * kAttnChunk;
+
+template <int HD, int G, int DB>
+__global__ __launch_bounds__(kShortThreads) void attn_decode_short_kernel(
+    const uint16_t *__restrict__ qkv, const uint16_t *__restrict__ cos_tab, const uint16_t *__restrict__ sin_tab,
+    const uint32_t *__restrict__ positions, uint32_t pos_limit, uint16_t *__restrict__ k_cache,
+    uint16_t *__restrict__ v_cache, uint64_t row_stride, uint32_t n_heads, uint32_t n_kv, uint32_t max_len,
+    float scale, uint16_t *__restrict__ out) {
+    constexpr int KS = HD / 32;           // MFMA k steps per key group
+    constexpr uint32_t PPH = HD / 8;      // 8-dim pieces per head
+    constexpr int NQ = (G + 3) / 4;       // 16-lane rows of the results holding live heads
+    constexpr int HP = NQ * 4;            // head slots per key after the move
+    constexpr int PAIRS = DB / 2;         // dim pairs of the block
+    constexpr int SLOTS = 64 / PAIRS;     // key slots per wavefront (adjacent lanes)
+    constexpr int KPS = kAttnChunk / SLOTS;  // keys per slot
+    static_assert(HD == 64 || HD == 128, "a wavefront holds a chunk's key fragments in registers");
+    static_assert(G <= kAttnMaxGroup && (G + 2) * PPH <= kShortThreads, "RoPE lanes fit the block");
+    static_assert((DB == 16 || DB == 32) && HD % DB == 0, "4 or 8 key slots");
+    __shared__ __align__(16) uint16_t qb[G][HD];
+    __shared__ __align__(16) uint16_t knew[HD];
+    __shared__ __align__(16) float sc[kShortWaves][kAttnChunk][HP];  // raw dot products, lane = key
+    __shared__ __align__(16) float pw[kShortWaves][G][kAttnChunk];   // probabilities
+    __shared__ float cmax[kShortWaves][G], csum[kShortWaves][G];
+    __shared__ float red[kShortWaves][G][DB];
+    const uint32_t tid = threadIdx.x, r = blockIdx.y, kvh = blockIdx.x % n_kv, part = blockIdx.x / n_kv;
+    const uint32_t h0 = kvh * G, d0 = part * DB;
+    const uint32_t wave = tid >> 6, lane = tid & 63, col = lane & 15, quad = lane >> 4;
+    uint16_t *orow = out + (static_cast<uint64_t>(r) * n_heads + h0) * HD + d0;
+    const uint32_t pos = positions[r];
+    if (pos >= pos_limit) {  // a position the cache or the tables cannot hold: zero output, no cache write
+        if (tid < G * DB) orow[(tid / DB) * HD + tid % DB] = 0;
+        return;
+    }
+    const uint32_t ctx = pos + 1;  // pos < pos_limit <= max_len <= kShortKeys
+    const uint32_t nact = (ctx + kAttnChunk - 1) / kAttnChunk;
+    const bool active = wave < nact;
+    const uint32_t c0 = wave * kAttnChunk;
+    const uint64_t cache = static_cast<uint64_t>(r) * row_stride + static_cast<uint64_t>(kvh) * max_len * HD;
+    const uint16_t *row = qkv + static_cast<uint64_t>(r) * (n_heads + 2 * n_kv) * HD;
+    // RoPE inputs first (thread hh < G: query head h0 + hh, hh == G: the key;
+    // then the value's pieces), so the set-up waits for its own loads only
+    uint4 x4, r4, c4, s4, v4;
+    const uint32_t tr = tid < (G + 1) * PPH ? tid : 0;
+    const uint32_t hh = tr / PPH, pp = tr % PPH;
+    const bool rope_wave = wave * 64 < (G + 2) * PPH;  // wavefronts holding RoPE or value lanes
+    if (rope_wave) {
+        const uint16_t *head = row + static_cast<uint64_t>(hh < G ? h0 + hh : n_heads + kvh) * HD;
+        const uint32_t partner = pp < PPH / 2 ? pp + PPH / 2 : pp - PPH / 2;
+        x4 = *reinterpret_cast<const uint4 *>(head + pp * 8);
+        r4 = *reinterpret_cast<const uint4 *>(head + partner * 8);
+        c4 = *reinterpret_cast<const uint4 *>(cos_tab + static_cast<uint64_t>(pos) * HD + pp * 8);
+        s4 = *reinterpret_cast<const uint4 *>(sin_tab + static_cast<uint64_t>(pos) * HD + pp * 8);
+        const uint32_t tv = tid >= (G + 1) * PPH && tid < (G + 2) * PPH ? tid - (G + 1) * PPH : 0;
+        v4 = *reinterpret_cast<const uint4 *>(row + static_cast<uint64_t>(n_heads + n_kv + kvh) * HD + tv * 8);
+    }
+    // this wavefront's 4 key groups (keys below pos from the cache, clamped
+    // otherwise: key pos comes from LDS, later ones are masked)
+    uint4 b[4][KS];
+    // V: lane (dim pair dp, slot vs) holds dims d0 + 2 dp, +1 of keys
+    // c0 + KPS vs + t; keys past pos are zero, key pos is the new value
+    const uint32_t dp = lane / SLOTS, vs = lane % SLOTS;
+    uint32_t vr[KPS];
+    const uint32_t vnew =
+        *reinterpret_cast<const uint32_t *>(row + static_cast<uint64_t>(n_heads + n_kv + kvh) * HD + d0 + 2 * dp);
+    if (active) {
+        const uint16_t *kb = k_cache + cache + 8 * quad;
+#pragma unroll
+        for (int grp = 0; grp < 4; ++grp) {
+            const uint32_t j = c0 + grp * 16 + col;
+            const uint32_t jc = j < pos ? j : (pos ? pos - 1 : 0);
+#pragma unroll
+            for (int st = 0; st < KS; ++st)
+                b[grp][st] = *reinterpret_cast<const uint4 *>(kb + static_cast<uint64_t>(jc) * HD + 32 * st);
+        }
+        const uint16_t *vb = v_cache + cache + d0 + 2 * dp;
+#pragma unroll
+        for (int t = 0; t < KPS; ++t) {
+            const uint32_t j = c0 + KPS * vs + t;
+            const uint32_t jc = j < pos ? j : (pos ? pos - 1 : 0);
+            vr[t] = *reinterpret_cast<const uint32_t *>(vb + static_cast<uint64_t>(jc) * HD);
+        }
+    }
+    if (rope_wave) {
+        const uint4 ov = rope_apply(x4, r4, c4, s4, pp < PPH / 2);
+        if (tid < (G + 1) * PPH) {
+            if (hh < G) {
+                *reinterpret_cast<uint4 *>(&qb[hh][pp * 8]) = ov;
+            } else {
+                *reinterpret_cast<uint4 *>(knew + pp * 8) = ov;
+                if (part == 0) *reinterpret_cast<uint4 *>(k_cache + cache + static_cast<uint64_t>(pos) * HD + pp * 8) = ov;
+            }
+        } else if (part == 0 && tid < (G + 2) * PPH) {
+            *reinterpret_cast<uint4 *>(v_cache + cache + static_cast<uint64_t>(pos) * HD + (tid - (G + 1) * PPH) * 8) = v4;
+        }
+    }
+    __syncthreads();
+    const uint32_t j = c0 + lane;  // this lane's key after the move
+    float sv[G];
+    if (active) {
+        const bool hlive = col < static_cast<uint32_t>(G);
+        const uint32_t hc = hlive ? col : 0;
+        uint4 a[KS];
+#pragma unroll
+        for (int st = 0; st < KS; ++st) {
+            const uint4 v = *reinterpret_cast<const uint4 *>(&qb[hc][32 * st + 8 * quad]);
+            a[st] = hlive ? v : make_uint4(0u, 0u, 0u, 0u);
+        }
+        const uint4 *kn = reinterpret_cast<const uint4 *>(knew + 8 * quad);
+#pragma unroll
+        for (int grp = 0; grp < 4; ++grp) {
+            if (c0 + grp * 16 + col == pos) {
+#pragma unroll
+                for (int st = 0; st < KS; ++st) b[grp][st] = kn[4 * st];
+            }
+            attn_f32x4_t d = attn_mfma(a[0], b[grp][0], attn_f32x4_t{0.f, 0.f, 0.f, 0.f});
+#pragma unroll
+            for (int st = 1; st < KS; ++st) d = attn_mfma(a[st], b[grp][st], d);
+            // result lane (key col, row quad) holds heads 4 quad .. 4 quad + 3
+            if (quad < static_cast<uint32_t>(NQ))
+                *reinterpret_cast<float4 *>(&sc[wave][grp * 16 + col][4 * quad]) = make_float4(d[0], d[1], d[2], d[3]);
+        }
+        __builtin_amdgcn_wave_barrier();  // this wavefront's writes before its reads
+        float dv[HP];
+#pragma unroll
+        for (int q = 0; q < NQ; ++q) {
+            const float4 v = *reinterpret_cast<const float4 *>(&sc[wave][lane][4 * q]);
+            dv[4 * q] = v.x, dv[4 * q + 1] = v.y, dv[4 * q + 2] = v.z, dv[4 * q + 3] = v.w;
+        }
+#pragma unroll
+        for (int h = 0; h < G; ++h) {
+            sv[h] = j < ctx ? bf(rne(dv[h])) * scale : -INFINITY;
+            const float m = wave_max(sv[h]);
+            if (lane == 0) cmax[wave][h] = m;
+        }
+    }
+    __syncthreads();
+    // per-head totals over the chunks: row q of the wavefront reduces head
+    // 4 n + q over chunk `col` (lanes past the active chunks hold the identity)
+    auto row_reduce = [&](bool is_max, float (&res)[G]) {
+#pragma unroll
+        for (int n = 0; n < NQ; ++n) {
+            const uint32_t h = 4 * n + quad;
+            const bool live = col < nact && h < static_cast<uint32_t>(G);
+            const uint32_t cc = live ? col : 0, hc = live ? h : 0;
+            const float x = live ? (is_max ? cmax[cc][hc] : csum[cc][hc]) : (is_max ? -INFINITY : 0.f);
+            const float t = is_max ? group_max<16>(x) : group_sum<16>(x);
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+                if (4 * n + q < G) res[4 * n + q] = lane_value(t, 16 * q);
+        }
+    };
+    float e[G];
+    if (active) {
+        float mg[G];
+        row_reduce(true, mg);
+#pragma unroll
+        for (int h = 0; h < G; ++h) {
+            e[h] = expf(sv[h] - mg[h]);
+            const float l = wave_sum(e[h]);
+            if (lane == 0) csum[wave][h] = l;
+        }
+    }
+    __syncthreads();
+    float acc[G][2];
+#pragma unroll
+    for (int g = 0; g < G; ++g) acc[g][0] = acc[g][1] = 0.f;
+    if (active) {
+        float sg[G];
+        row_reduce(false, sg);
+#pragma unroll
+        for (int h = 0; h < G; ++h) pw[wave][h][lane] = bf(rne(e[h] / sg[h]));
+        __builtin_amdgcn_wave_barrier();  // this wavefront's probabilities before its reads
+#pragma unroll
+        for (int t4 = 0; t4 < KPS / 4; ++t4) {
+            float v0[4], v1[4];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const uint32_t t = 4 * t4 + u, jk = c0 + KPS * vs + t;
+                const uint32_t w = jk < pos ? vr[t] : (jk == pos ? vnew : 0u);
+                v0[u] = bf(w & 0xFFFFu);
+                v1[u] = bf(w >> 16);
+            }
+#pragma unroll
+            for (int g = 0; g < G; ++g) {
+                const float4 p4 = *reinterpret_cast<const float4 *>(&pw[wave][g][KPS * vs + 4 * t4]);
+                acc[g][0] += p4.x * v0[0];
+                acc[g][1] += p4.x * v1[0];
+                acc[g][0] += p4.y * v0[1];
+                acc[g][1] += p4.y * v1[1];
+                acc[g][0] += p4.z * v0[2];
+                acc[g][1] += p4.z * v1[2];
+                acc[g][0] += p4.w * v0[3];
+                acc[g][1] += p4.w * v1[3];
+            }
+        }
+        // the slots of a dim pair are adjacent lanes: add them in their group
+#pragma unroll
+        for (int g = 0; g < G; ++g)
+#pragma unroll
+            for (int k = 0; k < 2; ++k) {
+                if constexpr (SLOTS == 8) {
+                    acc[g][k] = group_sum<8>(acc[g][k]);
+                } else {
+                    acc[g][k] += dpp_mov<0xB1>(acc[g][k]);
+                    acc[g][k] += dpp_mov<0x4E>(acc[g][k]);
+                }
+            }
+        if (vs == 0) {
+#pragma unroll
+            for (int g = 0; g < G; ++g) {
+                red[wave][g][2 * dp] = acc[g][0];
+                red[wave][g][2 * dp + 1] = acc[g][1];
+            }
+        }
+    }
+    __syncthreads();
+    if (tid < G * DB) {
+        const uint32_t g = tid / DB, dd = tid % DB;
+        float o = red[0][g][dd];
+        for (uint32_t w = 1; w < nact; ++w) o += red[w][g][dd];
+        orow[g * HD + dd] = rne(o);
+    }
+}
+
 struct AttnArgs {
     const uint16_t *q_src, *cos_tab, *sin_tab;
     const uint32_t *positions;
@@ -663,6 +918,51 @@ static bool launch_attention_shape(int64_t head_dim, int64_t g, hipStream_t stre
     FH_ATTN_HD(256)
 #undef FH_ATTN_HD
 #undef FH_ATTN_G
+    return false;
+}
+
+// Caches of at most this many positions take attn_decode_short_kernel
+// (head_dim 64 or 128).
+#ifndef FH_DECODE_SHORT_MAX_LEN
+#define FH_DECODE_SHORT_MAX_LEN 1024
+#endif
+constexpr uint32_t kDecodeShortMaxLen = FH_DECODE_SHORT_MAX_LEN;
+static_assert(kDecodeShortMaxLen <= kShortKeys, "one chunk per wavefront");
+
+#ifndef FH_DECODE_SHORT_DIMS
+#define FH_DECODE_SHORT_DIMS 16
+#endif
+constexpr int kShortDims = FH_DECODE_SHORT_DIMS;  // V dims per block
+
+template <int HD, int G>
+static void launch_decode_short(hipStream_t stream, uint32_t rows, const AttnArgs &x) {
+    const dim3 grid(x.n_kv * (HD / kShortDims), rows);
+    hipLaunchKernelGGL((attn_decode_short_kernel<HD, G, kShortDims>), grid, dim3(kShortThreads), 0, stream, x.q_src, x.cos_tab,
+                       x.sin_tab, x.positions, x.pos_limit, x.k_cache, x.v_cache, x.row_stride, x.n_heads, x.n_kv,
+                       x.max_len, x.scale, x.out);
+}
+
+static bool launch_decode_short_shape(int64_t head_dim, int64_t g, hipStream_t stream, uint32_t rows,
+                                      const AttnArgs &x) {
+#define FH_SHORT_G(HD, GG)                                         \
+    case GG:                                                       \
+        launch_decode_short<HD, GG>(stream, rows, x);              \
+        return true;
+#define FH_SHORT_HD(HD)                                            \
+    if (head_dim == HD) switch (g) {                               \
+            FH_SHORT_G(HD, 1)                                      \
+            FH_SHORT_G(HD, 2)                                      \
+            FH_SHORT_G(HD, 3)                                      \
+            FH_SHORT_G(HD, 4)                                      \
+            FH_SHORT_G(HD, 5)                                      \
+            FH_SHORT_G(HD, 6)                                      \
+            FH_SHORT_G(HD, 7)                                      \
+            FH_SHORT_G(HD, 8)                                      \
+        }
+    FH_SHORT_HD(64)
+    FH_SHORT_HD(128)
+#undef FH_SHORT_HD
+#undef FH_SHORT_G
     return false;
 }
 
@@ -792,7 +1092,11 @@ extern "C" int fh_decode_attention(fh_device *dev, const uint16_t *qkv, int64_t 
     const AttnArgs x{qkv, cos_tab, sin_tab, positions, limit, k_cache, v_cache, row_stride,
                      static_cast<uint32_t>(n_heads), static_cast<uint32_t>(n_kv), static_cast<uint32_t>(max_len),
                      scale, static_cast<char *>(workspace), out};
+    // short caches: one launch (no workspace use); otherwise scores, then P.V
+    const bool short_cache = static_cast<uint64_t>(max_len) <= kDecodeShortMaxLen && head_dim != 256;
     return dispatch(dev, fn, [&] {
-        launch_attention_shape<true>(head_dim, n_heads / n_kv, dev->stream, static_cast<uint32_t>(batch), a, x);
+        if (!short_cache ||
+            !launch_decode_short_shape(head_dim, n_heads / n_kv, dev->stream, static_cast<uint32_t>(batch), x))
+            launch_attention_shape<true>(head_dim, n_heads / n_kv, dev->stream, static_cast<uint32_t>(batch), a, x);
     });
 }

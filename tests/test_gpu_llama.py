@@ -222,10 +222,14 @@ def rope_ref(x, pos, cos, sin):
 
 
 # (n_heads, n_kv, head_dim, batch, max_len): group sizes 3 (Llama-3.2-3B), 4
-# (Llama-3.1-8B, batched decode at context 4096), 2, 1, 7.
+# (Llama-3.1-8B, batched decode at context 4096), 2, 1, 7, 8, 5.
+# Caches of at most 1024 positions with head_dim 64 or 128 take the one-launch
+# kernel (one chunk per wavefront: 1024 is all 16 of them, 65 a second chunk
+# of one key); longer caches and head_dim 256 take scores + P.V, where
 # batch * n_kv * max_len >= 16384 takes the chunked P.V with its combine pass
 DECODE_CASES = [(24, 8, 128, 1, 768), (32, 8, 128, 8, 4096), (4, 2, 64, 3, 40), (8, 8, 256, 2, 300),
-                (28, 4, 128, 2, 1100), (8, 8, 256, 4, 600), (24, 8, 128, 3, 2048)]
+                (28, 4, 128, 2, 1100), (8, 8, 256, 4, 600), (24, 8, 128, 3, 2048), (32, 8, 128, 4, 1024),
+                (8, 1, 128, 2, 130), (2, 2, 64, 3, 65), (28, 4, 128, 2, 1000), (20, 4, 64, 2, 512)]
 
 
 @pytest.mark.parametrize("n_heads,n_kv,hd,batch,max_len", DECODE_CASES)
@@ -271,7 +275,7 @@ def test_decode_attention(device, n_heads, n_kv, hd, batch, max_len):
         assert_attention_close(got[b:b + 1], ref, flip, (b, p))
 
 
-@pytest.mark.parametrize("max_len", [32, 4096])  # sliced and chunked P.V
+@pytest.mark.parametrize("max_len", [32, 1100, 4096])  # one launch, sliced and chunked P.V
 def test_decode_attention_out_of_range_position(device, max_len):
     n_heads, n_kv, hd = 4, 2, 64
     c = LlamaConfig(n_layers=1, hidden=256, n_heads=n_heads, n_kv_heads=n_kv, head_dim=hd, ffn=64, vocab=16)
