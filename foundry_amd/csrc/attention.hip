@@ -112,8 +112,11 @@ static AttnLayout attn_layout(uint64_t rows, uint64_t n_heads, uint64_t n_kv, ui
 // block) and 16 keys as B columns; a lane loads 16 bytes of its key per
 // instruction (16 key rows x 64 bytes per wavefront load). Each wavefront
 // scores whole chunks of kAttnChunk keys on its own (chunks split +
-// splits * (wave + 4 i)) and reduces the chunk's max and sum of exp across
-// its 16-lane rows, so the loop has no block barrier.
+// splits * (wave + 4 i)), so the loop has no block barrier. The results'
+// live rows (G of the 16 heads) go through the wavefront's LDS slice to
+// lane = key, one register per head: the rounding, exp and the chunk's max
+// and sum then cost G operations per lane instead of 16, and each head's
+// scores leave as one 256-byte store.
 typedef __attribute__((ext_vector_type(8))) __bf16 attn_bf16x8_t;
 typedef __attribute__((ext_vector_type(4))) float attn_f32x4_t;
 
@@ -130,10 +133,13 @@ __global__ __launch_bounds__(kAttnThreads) void attn_scores_kernel(
     uint32_t nck, uint32_t splits, float scale, float *__restrict__ scores, float2 *__restrict__ stats) {
     constexpr int KS = HD / 32;       // MFMA k steps per key group
     constexpr uint32_t PPH = HD / 8;  // 8-dim pieces per head
+    constexpr int NQ = (G + 3) / 4;   // 16-lane rows of the results holding live heads
+    constexpr int HP = NQ * 4;        // head slots per key after the move
     static_assert(kAttnChunk == 64, "a chunk is 4 groups of 16 keys");
     static_assert(G <= 16, "query heads fit the MFMA rows");
     __shared__ __align__(16) uint16_t qb[ROPE ? G : 1][ROPE ? HD : 8];
     __shared__ __align__(16) uint16_t knew[ROPE ? HD : 8];
+    __shared__ __align__(16) float sc[kAttnWaves][kAttnChunk][HP];  // raw dot products, lane = key
     const uint32_t tid = threadIdx.x, r = blockIdx.y, kvh = blockIdx.x / splits, split = blockIdx.x % splits;
     const uint32_t pos = positions[r];
     if (pos >= pos_limit) return;
@@ -213,13 +219,11 @@ __global__ __launch_bounds__(kAttnThreads) void attn_scores_kernel(
     const uint4 *kn = reinterpret_cast<const uint4 *>(knew + 8 * quad);
     for (uint32_t f0 = 0; f0 < total; f0 += 4) {
         const uint32_t c = c_first + (f0 / 4) * c_step;
-        float sv[4][4];  // [group][i]: head quad * 4 + i, key c * 64 + group * 16 + col
 #pragma unroll
         for (int grp = 0; grp < 4; ++grp) {
             uint4(&b)[KS] = grp % 2 ? b1 : b0;
-            const uint32_t j = c * kAttnChunk + grp * 16 + col;
             if constexpr (ROPE) {
-                if (j == pos) {
+                if (c * kAttnChunk + grp * 16 + col == pos) {
 #pragma unroll
                     for (int st = 0; st < KS; ++st) b[st] = kn[4 * st];
                 }
@@ -227,23 +231,30 @@ __global__ __launch_bounds__(kAttnThreads) void attn_scores_kernel(
             attn_f32x4_t d = attn_mfma(a[0], b[0], attn_f32x4_t{0.f, 0.f, 0.f, 0.f});
 #pragma unroll
             for (int st = 1; st < KS; ++st) d = attn_mfma(a[st], b[st], d);
-#pragma unroll
-            for (int i = 0; i < 4; ++i) sv[grp][i] = j < ctx ? bf(rne(d[i])) * scale : -INFINITY;
+            // result lane (key col, row quad) holds heads 4 quad .. 4 quad + 3
+            if (quad < static_cast<uint32_t>(NQ))
+                *reinterpret_cast<float4 *>(&sc[wave][grp * 16 + col][4 * quad]) = make_float4(d[0], d[1], d[2], d[3]);
             load_grp(f0 + grp + 2, b);
         }
-        // per head: (max, sum of exp) over the chunk's 64 keys
+        __builtin_amdgcn_wave_barrier();  // this wavefront's writes before its reads
+        float dv[HP];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const float m = group_max<16>(fmaxf(fmaxf(sv[0][i], sv[1][i]), fmaxf(sv[2][i], sv[3][i])));
-            const float l = group_sum<16>((expf(sv[0][i] - m) + expf(sv[1][i] - m)) + (expf(sv[2][i] - m) + expf(sv[3][i] - m)));
-            const uint32_t head = quad * 4 + i;
-            if (head < static_cast<uint32_t>(G)) {
-                float *srow = scores + (static_cast<uint64_t>(r) * n_heads + h0 + head) * max_len + c * kAttnChunk + col;
+        for (int q = 0; q < NQ; ++q) {
+            const float4 v = *reinterpret_cast<const float4 *>(&sc[wave][lane][4 * q]);
+            dv[4 * q] = v.x, dv[4 * q + 1] = v.y, dv[4 * q + 2] = v.z, dv[4 * q + 3] = v.w;
+        }
+        __builtin_amdgcn_wave_barrier();  // its reads before the next chunk's writes
+        // lane = key c * 64 + lane: per head, the score and the chunk's
+        // (max, sum of exp) over its 64 keys
+        const uint32_t j = c * kAttnChunk + lane;
 #pragma unroll
-                for (int grp = 0; grp < 4; ++grp)
-                    if (c * kAttnChunk + grp * 16 + col < ctx) srow[grp * 16] = sv[grp][i];
-                if (col == 0) stats[(static_cast<uint64_t>(r) * n_heads + h0 + head) * nck + c] = make_float2(m, l);
-            }
+        for (int h = 0; h < G; ++h) {
+            const float sv = j < ctx ? bf(rne(dv[h])) * scale : -INFINITY;
+            const float m = wave_max(sv);
+            const float l = wave_sum(expf(sv - m));
+            const uint64_t hrow = static_cast<uint64_t>(r) * n_heads + h0 + h;
+            if (j < ctx) scores[hrow * max_len + j] = sv;
+            if (lane == 0) stats[hrow * nck + c] = make_float2(m, l);
         }
     }
 }
