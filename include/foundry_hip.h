@@ -240,7 +240,9 @@ int fh_decode_attention_workspace(int64_t batch, int64_t n_heads, int64_t n_kv, 
 /* The decode step's attention for a batch of sequences that each add one
  * token: fh_rope_kv's RoPE of the token's q and k and its cache write at
  * positions[b], then fh_attention over keys 0..positions[b] of sequence b --
- * the same rounding points, in two kernel launches instead of three. qkv:
+ * the same rounding points, in two kernel launches instead of three, or in
+ * one when max_len <= 1024 and head_dim is 64 or 128 (the workspace is then
+ * not touched, but is still checked and required). qkv:
  * [batch, (n_heads + 2 n_kv) * head_dim]; cos_tab/sin_tab: [table_len,
  * head_dim]; positions: device u32 [batch]; k_cache/v_cache: [batch, n_kv,
  * max_len, head_dim] (one cache per sequence); out: [batch, n_heads *
