@@ -259,6 +259,105 @@ __global__ __launch_bounds__(kAttnThreads) void attn_scores_kernel(
     }
 }
 
+// Prefill scores over query-row tiles: block (KV head, split, tile of
+// QR = 16 / G query rows). The MFMA's A rows are (query row r / G, head
+// r % G), all live when G divides 16, so each key fragment a wavefront loads
+// serves QR rows of the tile instead of one (attn_scores_kernel serves one
+// row per block and re-reads its keys for every row). Row qi attends keys
+// 0 .. ctx_qi - 1 and a chunk is scored when any row of the tile reaches it.
+// Scores and each (row, head)'s per-chunk (max, sum of exp) go to the
+// workspace as attn_scores_kernel writes them; a chunk past a row's context
+// writes nothing for that row (its P.V reads only its own chunks).
+template <int HD, int G>
+__global__ __launch_bounds__(kAttnThreads) void attn_scores_tile_kernel(
+    const uint16_t *__restrict__ q, const uint32_t *__restrict__ positions, uint32_t rows,
+    const uint16_t *__restrict__ k_cache, uint32_t n_heads, uint32_t max_len, uint32_t nck, uint32_t splits,
+    float scale, float *__restrict__ scores, float2 *__restrict__ stats) {
+    constexpr int KS = HD / 32;             // MFMA k steps per key group
+    constexpr uint32_t QR = 16 / G;         // query rows per tile
+    constexpr uint32_t LIVE = QR * G;       // live A rows
+    static_assert(G <= 16 && kAttnChunk == 64, "a chunk is 4 groups of 16 keys");
+    const uint32_t tid = threadIdx.x, kvh = blockIdx.x / splits, split = blockIdx.x % splits;
+    const uint32_t r0 = blockIdx.y * QR, h0 = kvh * G;
+    const uint32_t wave = tid >> 6, lane = tid & 63, col = lane & 15, quad = lane >> 4;
+    // contexts of the tile's rows (0 past the last row); the tile's longest
+    uint32_t ctxq[QR];
+    uint32_t cmax = 0;
+#pragma unroll
+    for (uint32_t qi = 0; qi < QR; ++qi) {
+        const uint32_t r = r0 + qi;
+        const uint32_t p = r < rows ? positions[r] : 0u;
+        ctxq[qi] = r < rows ? (p < max_len ? p + 1 : max_len) : 0u;
+        cmax = ctxq[qi] > cmax ? ctxq[qi] : cmax;
+    }
+    // the contexts of this lane's 4 result rows 4 quad + i (compile-time
+    // selection: no dynamically indexed private array)
+    uint32_t ctxr[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const uint32_t rr = quad * 4 + i;
+        ctxr[i] = 0;
+#pragma unroll
+        for (uint32_t qi = 0; qi < QR; ++qi)
+            if (rr < LIVE && rr / G == qi) ctxr[i] = ctxq[qi];
+    }
+    const uint32_t nact = (cmax + kAttnChunk - 1) / kAttnChunk;
+    const uint32_t c_first = split + splits * wave, c_step = splits * kAttnWaves;
+    const uint32_t total = c_first < nact ? (nact - c_first + c_step - 1) / c_step * 4 : 0;
+    if (total == 0) return;  // a wavefront without chunks (no barrier in this kernel)
+    const uint16_t *kb = k_cache + static_cast<uint64_t>(kvh) * max_len * HD + 8 * quad;
+    auto load_grp = [&](uint32_t f, uint4 (&b)[KS]) {
+        const uint32_t fc = f < total ? f : total - 1;
+        const uint32_t j = (c_first + (fc / 4) * c_step) * kAttnChunk + (fc % 4) * 16 + col;
+        const uint32_t jc = j < cmax ? j : cmax - 1;
+#pragma unroll
+        for (int st = 0; st < KS; ++st) b[st] = *reinterpret_cast<const uint4 *>(kb + static_cast<uint64_t>(jc) * HD + 32 * st);
+    };
+    // A fragments: row col = (query row col / G, head col % G), dims 32 st + 8 quad
+    const uint32_t qa = col / G, ha = col % G;
+    const bool alive = col < LIVE && r0 + qa < rows;
+    const uint16_t *qrow = q + (static_cast<uint64_t>(alive ? r0 + qa : 0) * n_heads + h0 + (alive ? ha : 0)) * HD + 8 * quad;
+    uint4 a[KS];
+#pragma unroll
+    for (int st = 0; st < KS; ++st) {
+        const uint4 v = *reinterpret_cast<const uint4 *>(qrow + 32 * st);
+        a[st] = alive ? v : make_uint4(0u, 0u, 0u, 0u);
+    }
+    uint4 b0[KS], b1[KS];
+    load_grp(0, b0);
+    load_grp(1, b1);
+    for (uint32_t f0 = 0; f0 < total; f0 += 4) {
+        const uint32_t c = c_first + (f0 / 4) * c_step;
+        float sv[4][4];  // [group][i]: result row quad * 4 + i, key c * 64 + group * 16 + col
+#pragma unroll
+        for (int grp = 0; grp < 4; ++grp) {
+            uint4(&b)[KS] = grp % 2 ? b1 : b0;
+            const uint32_t j = c * kAttnChunk + grp * 16 + col;
+            attn_f32x4_t d = attn_mfma(a[0], b[0], attn_f32x4_t{0.f, 0.f, 0.f, 0.f});
+#pragma unroll
+            for (int st = 1; st < KS; ++st) d = attn_mfma(a[st], b[st], d);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) sv[grp][i] = j < ctxr[i] ? bf(rne(d[i])) * scale : -INFINITY;
+            load_grp(f0 + grp + 2, b);
+        }
+        // per result row: (max, sum of exp) over the chunk's 64 keys
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const float m = group_max<16>(fmaxf(fmaxf(sv[0][i], sv[1][i]), fmaxf(sv[2][i], sv[3][i])));
+            const float l = group_sum<16>((expf(sv[0][i] - m) + expf(sv[1][i] - m)) + (expf(sv[2][i] - m) + expf(sv[3][i] - m)));
+            const uint32_t rr = quad * 4 + i;
+            if (rr < LIVE && c * kAttnChunk < ctxr[i]) {  // the row is live and reaches this chunk
+                const uint64_t hrow = static_cast<uint64_t>(r0 + rr / G) * n_heads + h0 + rr % G;
+                float *srow = scores + hrow * max_len + c * kAttnChunk + col;
+#pragma unroll
+                for (int grp = 0; grp < 4; ++grp)
+                    if (c * kAttnChunk + grp * 16 + col < ctxr[i]) srow[grp * 16] = sv[grp][i];
+                if (col == 0) stats[hrow * nck + c] = make_float2(m, l);
+            }
+        }
+    }
+}
+
 // P.V over a slice of 2P dims of head_dim for all keys of the row: block
 // (KV head, slice, row). Thread (pair q, key slot s) owns dims d0 + 2q, +1 and
 // keys j = s, s + S, ... (S = 256 / P slots); tiles of T keys are staged as
@@ -880,11 +979,25 @@ template <int HD, int G, bool ROPE>
 static void launch_attention(hipStream_t stream, uint32_t rows, const AttnLayout &a, const AttnArgs &x) {
     auto *stats = reinterpret_cast<float2 *>(x.ws);
     auto *scores = reinterpret_cast<float *>(x.ws + a.scores);
-    const dim3 grid(static_cast<uint32_t>(x.n_kv * a.splits), rows);
-    hipLaunchKernelGGL((attn_scores_kernel<HD, G, ROPE>), grid, dim3(kAttnThreads), 0, stream, x.q_src, x.cos_tab,
-                       x.sin_tab, x.positions, x.pos_limit, x.k_cache, x.v_cache, x.row_stride, x.n_heads, x.n_kv,
-                       x.max_len, static_cast<uint32_t>(a.nck), static_cast<uint32_t>(a.splits), x.scale, scores,
-                       stats);
+    if constexpr (ROPE) {
+        const dim3 grid(static_cast<uint32_t>(x.n_kv * a.splits), rows);
+        hipLaunchKernelGGL((attn_scores_kernel<HD, G, ROPE>), grid, dim3(kAttnThreads), 0, stream, x.q_src,
+                           x.cos_tab, x.sin_tab, x.positions, x.pos_limit, x.k_cache, x.v_cache, x.row_stride,
+                           x.n_heads, x.n_kv, x.max_len, static_cast<uint32_t>(a.nck),
+                           static_cast<uint32_t>(a.splits), x.scale, scores, stats);
+    } else {
+        // query-row tiles (one shared cache); splits make about
+        // kAttnTargetBlocks blocks in all, as for the per-row kernel
+        constexpr uint32_t kQR = 16 / G;
+        const uint64_t tiles = (rows + kQR - 1) / kQR;
+        const uint64_t blocks = tiles * x.n_kv;
+        const uint64_t want = (kAttnTargetBlocks + blocks - 1) / blocks;
+        const uint32_t splits = static_cast<uint32_t>(want < a.nck ? want : a.nck);
+        const dim3 grid(static_cast<uint32_t>(x.n_kv * splits), static_cast<uint32_t>(tiles));
+        hipLaunchKernelGGL((attn_scores_tile_kernel<HD, G>), grid, dim3(kAttnThreads), 0, stream, x.q_src,
+                           x.positions, rows, x.k_cache, x.n_heads, x.max_len, static_cast<uint32_t>(a.nck), splits,
+                           x.scale, scores, stats);
+    }
     if (a.chunks) {
         const uint32_t chunks = static_cast<uint32_t>(a.chunks), ck = static_cast<uint32_t>(a.chunk_keys);
         float *part = reinterpret_cast<float *>(x.ws + a.part);
