@@ -21,6 +21,9 @@
 //     dealt round-robin to the split blocks and their wavefronts;
 //     s_j = RNE(q.k_j) * scale from matrix-core dot products, written to the
 //     workspace with each chunk's (m_c = max s_j, l_c = sum exp(s_j - m_c)).
+//     Decode uses it; fh_attention uses attn_scores_tile_kernel, the same
+//     per row but with a block serving a tile of 16 / G query rows, so that
+//     every key it loads serves the whole tile.
 //   P.V, from M = max m_c and S = sum l_c exp(m_c - M) (the same in every
 //     block) and p_j = RNE(exp(s_j - M) / S), one of two ways:
 //     attn_pv_kernel, block (KV head, slice, row): all keys for head_dim /
