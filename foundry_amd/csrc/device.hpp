@@ -34,8 +34,9 @@ namespace fh {
 // GEMV's prologue in stream order.
 constexpr uint64_t kPackAreaBytes = 8ull * 16384 * 2 + (16384 / 64) * 8 * 4 + 2048;
 // Bytes of each device's partial area: the f32 partial sums [ranges][rows][n]
-// of a GEMV split over K ranges, added by its combine kernel.
-constexpr uint64_t kPartialAreaBytes = 4ull << 20;
+// of a GEMV split over K ranges, or [splits][m][n] of a GEMM split over K,
+// added in order by the matching combine kernel.
+constexpr uint64_t kPartialAreaBytes = 32ull << 20;
 }  // namespace fh
 
 struct fh_device {

@@ -98,6 +98,13 @@ __global__ __launch_bounds__(64 * WM * WN) void q4_gemm_kernel(
     const uint32_t n0 = blockIdx.x * kBN;
     const uint32_t kw = k / 8;       // words per weight row
     const uint32_t kg = k / kGroup;  // groups per weight row
+    // K split blockIdx.z of gridDim.z: K steps [st0, st0 + steps); y then
+    // takes this split's f32 partial tile at [blockIdx.z][m][n]
+    const uint32_t steps_all = k / kBK;
+    const uint32_t per_split = (steps_all + gridDim.z - 1) / gridDim.z;
+    const uint32_t st0 = blockIdx.z * per_split < steps_all ? blockIdx.z * per_split : steps_all;
+    const uint32_t steps = st0 + per_split < steps_all ? per_split : steps_all - st0;
+    if (gridDim.z > 1) y = static_cast<float *>(y) + static_cast<uint64_t>(blockIdx.z) * m * n;
 
     // One K step in registers: X pieces (256 rows x 8 sixteen-byte pieces;
     // thread t holds pieces t + 512 i) and W pieces (256 rows x 2 sixteen-byte
@@ -182,16 +189,15 @@ __global__ __launch_bounds__(64 * WM * WN) void q4_gemm_kernel(
     };
 
     // Two LDS stages, one barrier per step.
-    const uint32_t steps = k / kBK;
     if (steps > 0) {
-        load_tiles(0);
+        load_tiles(st0 * kBK);
         store_tiles(xs0, ws0);
         __syncthreads();
     }
     for (uint32_t st = 0; st < steps; ++st) {
         const bool odd = st & 1;
         const bool more = st + 1 < steps;
-        if (more) load_tiles((st + 1) * kBK);
+        if (more) load_tiles((st0 + st + 1) * kBK);
         compute(odd ? xs1 : xs0, odd ? ws1 : ws0);
         if (more) store_tiles(odd ? xs0 : xs1, odd ? ws0 : ws1);
         __syncthreads();
@@ -221,7 +227,7 @@ __global__ __launch_bounds__(64 * WM * WN) void q4_gemm_kernel(
 template <int BM, int BN, int WM, int WN>
 static void launch_gemm_tile(hipStream_t stream, const uint16_t *x, uint32_t x_ld, const uint32_t *wq,
                              const uint16_t *s, const uint16_t *b, uint32_t m, uint32_t n, uint32_t k, void *y,
-                             int y_is_f32) {
+                             int y_is_f32, uint32_t splits) {
     using T = GemmTile<BM, BN, WM, WN>;
     static bool lds_opt_in = false;
     if (!lds_opt_in) {
@@ -230,24 +236,91 @@ static void launch_gemm_tile(hipStream_t stream, const uint16_t *x, uint32_t x_l
                                   hipFuncAttributeMaxDynamicSharedMemorySize, T::kLds);
         lds_opt_in = true;
     }
-    dim3 grid((n + BN - 1) / BN, (m + BM - 1) / BM);
+    dim3 grid((n + BN - 1) / BN, (m + BM - 1) / BM, splits);
     hipLaunchKernelGGL((q4_gemm_kernel<BM, BN, WM, WN>), grid, dim3(T::kThreads), T::kLds, stream, x, x_ld, wq, s, b,
                        m, n, k, y, y_is_f32);
+}
+
+// Adds the f32 partials of a GEMM split over K in split order: y[i] =
+// RNE(sum_s part[s][i]) (or the f32 sum). Each thread takes 4 consecutive
+// outputs; its kMaxGemmSplits loads are issued before any add (clamped to
+// the last split, whose extra values are not added).
+constexpr uint32_t kMaxGemmSplits = 8;
+
+__global__ __launch_bounds__(256) void gemm_split_reduce_kernel(const float *__restrict__ part, uint32_t splits,
+                                                                 uint64_t count, void *__restrict__ y,
+                                                                 int y_is_f32) {
+    const uint64_t i0 = (static_cast<uint64_t>(blockIdx.x) * 256 + threadIdx.x) * 4;
+    if (i0 >= count) return;
+    if (count % 4 == 0) {  // every split's partial is then 16-byte aligned
+        float4 v[kMaxGemmSplits];
+#pragma unroll
+        for (uint32_t sp = 0; sp < kMaxGemmSplits; ++sp)
+            v[sp] = *reinterpret_cast<const float4 *>(part + static_cast<uint64_t>(sp < splits ? sp : splits - 1) * count + i0);
+        float4 o = v[0];
+#pragma unroll
+        for (uint32_t sp = 1; sp < kMaxGemmSplits; ++sp)
+            if (sp < splits) {
+                o.x += v[sp].x;
+                o.y += v[sp].y;
+                o.z += v[sp].z;
+                o.w += v[sp].w;
+            }
+        if (y_is_f32) {
+            float *yf = static_cast<float *>(y) + i0;
+            yf[0] = o.x;
+            yf[1] = o.y;
+            yf[2] = o.z;
+            yf[3] = o.w;
+        } else {
+            uint16_t *yb = static_cast<uint16_t *>(y) + i0;
+            yb[0] = static_cast<uint16_t>(f32_to_bf16_rne(o.x));
+            yb[1] = static_cast<uint16_t>(f32_to_bf16_rne(o.y));
+            yb[2] = static_cast<uint16_t>(f32_to_bf16_rne(o.z));
+            yb[3] = static_cast<uint16_t>(f32_to_bf16_rne(o.w));
+        }
+        return;
+    }
+    for (uint64_t i = i0; i < i0 + 4 && i < count; ++i) {
+        float o = part[i];
+        for (uint32_t sp = 1; sp < splits; ++sp) o += part[static_cast<uint64_t>(sp) * count + i];
+        if (y_is_f32)
+            static_cast<float *>(y)[i] = o;
+        else
+            static_cast<uint16_t *>(y)[i] = static_cast<uint16_t>(f32_to_bf16_rne(o));
+    }
 }
 
 // 256 x 256 tiles, or 256 x 128 when the larger tile leaves CUs idle: each
 // weight element is still dequantised once per 256 rows of X, and the
 // down-projection shape (2048 x 3072 x 8192) gets 192 blocks instead of 96
 // (249 -> 186 us; the 2048 x 8192 x 3072 shape stays at 256 x 256, 139 us
-// against 164).
+// against 164). When even the small tiles leave more than half the CUs idle
+// (prompt-length m such as 512 against n = 3072 or 5120), K is split over
+// up to kMaxGemmSplits ranges so that tiles x splits about fills the chip;
+// the splits' f32 partials go to `area` (kPartialAreaBytes) and
+// gemm_split_reduce_kernel adds them in order.
 void launch_q4_gemm(hipStream_t stream, uint32_t cus, const uint16_t *x, uint32_t x_ld, const uint32_t *wq,
                     const uint16_t *s, const uint16_t *b, uint32_t m, uint32_t n, uint32_t k, void *y,
-                    int y_is_f32) {
+                    int y_is_f32, void *area) {
     const uint64_t big = static_cast<uint64_t>((n + 255) / 256) * ((m + 255) / 256);
-    if (big < cus)
-        launch_gemm_tile<256, 128, 4, 2>(stream, x, x_ld, wq, s, b, m, n, k, y, y_is_f32);
-    else
-        launch_gemm_tile<256, 256, 2, 4>(stream, x, x_ld, wq, s, b, m, n, k, y, y_is_f32);
+    if (big >= cus) return launch_gemm_tile<256, 256, 2, 4>(stream, x, x_ld, wq, s, b, m, n, k, y, y_is_f32, 1);
+    const uint64_t tiles = static_cast<uint64_t>((n + 127) / 128) * ((m + 255) / 256);
+    const uint64_t steps = k / kBK;
+    uint64_t splits = 1;
+    if (area != nullptr && 2 * tiles <= cus) {
+        splits = cus / tiles;
+        if (splits > kMaxGemmSplits) splits = kMaxGemmSplits;
+        if (splits > steps / 4) splits = steps / 4;  // at least 4 K steps per split
+        while (splits > 1 && splits * m * n * 4 > kPartialAreaBytes) --splits;
+        if (splits < 1) splits = 1;
+    }
+    if (splits == 1) return launch_gemm_tile<256, 128, 4, 2>(stream, x, x_ld, wq, s, b, m, n, k, y, y_is_f32, 1);
+    launch_gemm_tile<256, 128, 4, 2>(stream, x, x_ld, wq, s, b, m, n, k, area, 1, static_cast<uint32_t>(splits));
+    const uint64_t count = static_cast<uint64_t>(m) * n;
+    const uint64_t blocks = (count + 1023) / 1024;
+    hipLaunchKernelGGL(gemm_split_reduce_kernel, dim3(static_cast<uint32_t>(blocks)), dim3(256), 0, stream,
+                       static_cast<const float *>(area), static_cast<uint32_t>(splits), count, y, y_is_f32);
 }
 
 }  // namespace fh

@@ -17,7 +17,7 @@ void launch_mf_pack(hipStream_t stream, int m, const GemvArgs &a, void *area);
 uint32_t gemv_rows_per_launch(uint32_t k, bool norm);
 void launch_q4_gemm(hipStream_t stream, uint32_t cus, const uint16_t *x, uint32_t x_ld, const uint32_t *wq,
                     const uint16_t *s, const uint16_t *b, uint32_t m, uint32_t n, uint32_t k,
-                    void *y, int y_is_f32);
+                    void *y, int y_is_f32, void *area);
 
 // Row counts up to this go to the GEMV.
 constexpr int64_t kGemvMaxRows = 8;
@@ -178,7 +178,7 @@ extern "C" int fh_q4_matmul(fh_device *dev, const uint16_t *x, int64_t m, int64_
     }
     return dispatch(dev, fn, [&] {
         launch_q4_gemm(dev->stream, dev->compute_units, x, ld32, wq, scales, biases, static_cast<uint32_t>(m), n32,
-                       k32, y, y_is_f32);
+                       k32, y, y_is_f32, dev->partial_area);
     });
 }
 

@@ -231,6 +231,15 @@ def test_gemm_config3_shapes_sampled(device, oracle):
     run_linear(device, oracle, 2048, 3072, 8192, seed=4, sample=(96, 3072))
 
 
+# Prompt-length rows whose tiles leave CUs idle split K (up to 8 ranges of
+# at least 4 steps, f32 partials added in order): the config-4 prefill's
+# down (5 splits) and q/k/v (3 splits) shapes, and m * n not a multiple of 4
+# (the reduce's scalar tail).
+@pytest.mark.parametrize("m,n,k", [(512, 3072, 8192), (512, 5120, 3072), (35, 198, 2048)])
+def test_gemm_split_k(device, oracle, m, n, k):
+    run_linear(device, oracle, m, n, k, seed=5000 + m + n, sample=(64, n) if m > 64 else None)
+
+
 def test_gemm_golden(device):
     with np.load(GOLDEN) as g:
         w = weight(device, g["gemm_wq"], g["gemm_s"], g["gemm_b"])
