@@ -296,8 +296,8 @@ def test_decode_attention_out_of_range_position(device, max_len):
     assert not down(device, vc, np.uint16, 2 * n_kv * max_len * hd).any()
 
 
-def test_silu_mul(device):
-    rows, f = 3, 8192
+@pytest.mark.parametrize("rows,f", [(3, 8192), (5, 13)])  # 16-byte pieces; f % 8 != 0 one value at a time
+def test_silu_mul(device, rows, f):
     gu = synth.bf16_normal(9, (rows, 2 * f))
     gu[0, :8] = np.array([0x0000, 0x8000, 0x4120, 0xC120, 0x42C8, 0xC2C8, 0x3F80, 0xBF80], dtype=np.uint16)
     s = up(device, gu)
