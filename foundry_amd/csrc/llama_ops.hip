@@ -190,6 +190,25 @@ __global__ __launch_bounds__(256) void silu_mul_kernel(const uint16_t *__restric
     }
 }
 
+// Row argmax of bf16 values; ties go to the lowest index. One block of 1024
+// threads per row, 16-byte loads (8 values) per thread per step.
+constexpr int kArgmaxThreads = 1024;
+
+__device__ __forceinline__ void take_max(float &best, uint32_t &idx, float v, uint32_t i) {
+    if (v > best || (v == best && i < idx)) {
+        best = v;
+        idx = i;
+    }
+}
+
+// Per thread, kArgmaxBatch 16-byte loads are issued together before any is
+// compared, so a row costs one or two memory round trips instead of one per
+// load. The loads are unconditional (indices past the row are clamped to its
+// last piece and ignored): a guarded load sits in its own basic block, where
+// the compiler drains every outstanding load before issuing it. Lanes then
+// wavefronts reduce with the same (max, lowest index) rule.
+constexpr int kArgmaxBatch = 16;
+
 __global__ __launch_bounds__(kArgmaxThreads) void argmax_kernel(const uint16_t *__restrict__ x, uint32_t n,
                                                                 uint32_t *__restrict__ out) {
     __shared__ float bv[kArgmaxThreads / 64];
