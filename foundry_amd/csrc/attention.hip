@@ -665,6 +665,171 @@ __global__ __launch_bounds__(kAttnThreads) void attn_pv_chunk_kernel(
     }
 }
 
+// Prefill P.V on the matrix cores: block (KV head, chunk, tile of R = 16 / G
+// query rows), the MFMA's 16 A rows being (row r / G, head r % G) as in
+// attn_scores_tile_kernel. A = the probabilities of 32 keys, formed from the
+// workspace scores and the row's M and S by the rounding rule of the other
+// P.V kernels; B = V of those keys for 16 dims. Wavefront w takes the
+// chunk's 32-key steps w, w + 4, ...: it loads the keys' V coalesced (a lane
+// holds 8 keys x 8 dims), transposes each 8 x 8 block of bf16 in registers
+// and stores it as [dim][key] rows of its own LDS slice, so each B fragment
+// (8 keys of one dim) is one 16-byte read. The wavefronts' sums are added in
+// order through LDS: one chunk writes RNE(out), several write f32 partials
+// for attn_combine_kernel. Rows with no key in the chunk write nothing.
+constexpr int kPvtPitch = 40;  // bf16 per transposed V row in LDS: 32 keys + 8 of padding
+
+template <int HD, int G>
+__global__ __launch_bounds__(kAttnThreads) void attn_pv_tile_kernel(
+    const uint16_t *__restrict__ v_cache, const uint32_t *__restrict__ positions, uint32_t rows, uint32_t n_heads,
+    uint32_t n_kv, uint32_t max_len, uint32_t nck, uint32_t chunks, uint32_t chunk_keys,
+    const float *__restrict__ scores, const float2 *__restrict__ stats, uint16_t *__restrict__ out,
+    float *__restrict__ part) {
+    constexpr uint32_t R = 16 / G, LIVE = R * G;
+    constexpr int DT = HD / 16;  // 16-dim tiles of the output
+    static_assert(HD == 128, "a lane transposes 8 keys x 8 dims, 16 pieces per key row");
+    static_assert(sizeof(uint16_t) * kAttnWaves * HD * kPvtPitch >= sizeof(float) * kAttnWaves * 16 * HD,
+                  "the wavefronts' sums fit the transposed-V area");
+    __shared__ __align__(16) uint16_t vt[kAttnWaves][HD][kPvtPitch];
+    const uint32_t tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, col = lane & 15, quad = lane >> 4;
+    const uint32_t kvh = blockIdx.x / chunks, c = blockIdx.x % chunks;
+    const uint32_t r0 = blockIdx.y * R, h0 = kvh * G;
+    uint32_t ctxq[R];
+    uint32_t cmax = 0;
+#pragma unroll
+    for (uint32_t qi = 0; qi < R; ++qi) {
+        const uint32_t r = r0 + qi;
+        const uint32_t p = r < rows ? positions[r] : 0u;
+        ctxq[qi] = r < rows ? (p < max_len ? p + 1 : max_len) : 0u;
+        cmax = ctxq[qi] > cmax ? ctxq[qi] : cmax;
+    }
+    const uint32_t k0 = c * chunk_keys;
+    const uint32_t kend = k0 + chunk_keys < cmax ? k0 + chunk_keys : cmax;  // keys the tile reads in this chunk
+    if (k0 >= kend) return;  // no row of the tile reaches this chunk (no barrier yet)
+    // this lane's A row (query row qa, head ha) and its statistics
+    const uint32_t qa = col / G, ha = col % G;
+    const bool alive = col < LIVE && r0 + qa < rows;
+    uint32_t ctx_a = 0;
+#pragma unroll
+    for (uint32_t qi = 0; qi < R; ++qi)
+        if (alive && qa == qi) ctx_a = ctxq[qi];
+    const uint64_t hrow = static_cast<uint64_t>(alive ? r0 + qa : 0) * n_heads + h0 + (alive ? ha : 0);
+    const float2 *st = stats + hrow * nck;
+    const uint32_t nact = (ctx_a + kAttnChunk - 1) / kAttnChunk;
+    // M and S: the 4 quads of a row take chunks quad, quad + 4, ...; combined
+    // over the quads in a fixed order, so all 4 hold the same values
+    float mloc = -INFINITY;
+    for (uint32_t cc = quad; cc < nact; cc += 4) mloc = fmaxf(mloc, st[cc].x);
+    mloc = fmaxf(mloc, __shfl_xor(mloc, 16, 64));
+    const float mrow = fmaxf(mloc, __shfl_xor(mloc, 32, 64));
+    float sloc = 0.f;
+    for (uint32_t cc = quad; cc < nact; cc += 4) {
+        const float2 v = st[cc];
+        sloc += v.y * expf(v.x - mrow);
+    }
+    sloc += __shfl_xor(sloc, 16, 64);
+    const float srow_sum = sloc + __shfl_xor(sloc, 32, 64);
+    const float *srow = scores + hrow * max_len;
+    const uint32_t kend_a = alive ? (k0 + chunk_keys < ctx_a ? k0 + chunk_keys : ctx_a) : 0u;  // this row's keys end
+    // V: lane (key octet j, piece pv) loads keys 8 j .. 8 j + 7 of a step, dims 8 pv .. 8 pv + 7
+    const uint32_t vj = lane >> 4, pv = lane & 15;
+    const uint16_t *vb = v_cache + static_cast<uint64_t>(kvh) * max_len * HD + pv * 8;
+    const uint32_t nsteps = (kend - k0 + 31) / 32;
+    auto load_v = [&](uint32_t s, uint4 (&v)[8]) {
+        const uint32_t sc = s < nsteps ? s : nsteps - 1;
+        const uint32_t kb = k0 + sc * 32 + 8 * vj;
+#pragma unroll
+        for (int t = 0; t < 8; ++t) {
+            const uint32_t key = kb + t < kend ? kb + t : kend - 1;
+            v[t] = *reinterpret_cast<const uint4 *>(vb + static_cast<uint64_t>(key) * HD);
+        }
+    };
+    auto load_s = [&](uint32_t s, float (&sv)[8]) {
+        const uint32_t sc = s < nsteps ? s : nsteps - 1;
+        const uint32_t kb = k0 + sc * 32 + 8 * quad;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) sv[e] = srow[kb + e < kend ? kb + e : k0];
+    };
+    attn_f32x4_t acc[DT];
+#pragma unroll
+    for (int t = 0; t < DT; ++t) acc[t] = attn_f32x4_t{0.f, 0.f, 0.f, 0.f};
+    uint16_t(*vw)[kPvtPitch] = vt[wave];
+    uint4 va[8];
+    float sa[8];
+    uint32_t s = wave;
+    if (s < nsteps) {
+        load_v(s, va);
+        load_s(s, sa);
+    }
+    for (; s < nsteps; s += kAttnWaves) {
+        uint4 vn[8];
+        float sn[8];
+        const bool more = s + kAttnWaves < nsteps;
+        if (more) {  // the next step's loads are in flight while this one is used
+            load_v(s + kAttnWaves, vn);
+            load_s(s + kAttnWaves, sn);
+        }
+        // transpose: dim 8 pv + d of keys 8 vj .. 8 vj + 7 as one 16-byte row piece
+#pragma unroll
+        for (int d = 0; d < 8; ++d) {
+            uint32_t w[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const uint4 &a = va[2 * i], &b = va[2 * i + 1];
+                const uint32_t aw = d / 2 == 0 ? a.x : d / 2 == 1 ? a.y : d / 2 == 2 ? a.z : a.w;
+                const uint32_t bw = d / 2 == 0 ? b.x : d / 2 == 1 ? b.y : d / 2 == 2 ? b.z : b.w;
+                w[i] = d % 2 ? (aw >> 16) | (bw & 0xFFFF0000u) : (aw & 0xFFFFu) | (bw << 16);
+            }
+            *reinterpret_cast<uint4 *>(&vw[8 * pv + d][8 * vj]) = make_uint4(w[0], w[1], w[2], w[3]);
+        }
+        // A: the probabilities of keys 8 quad .. 8 quad + 7 of the step for this lane's row
+        const uint32_t kb = k0 + s * 32 + 8 * quad;
+        uint32_t pw2[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const float p0 = kb + 2 * i < kend_a ? bf(rne(expf(sa[2 * i] - mrow) / srow_sum)) : 0.f;
+            const float p1 = kb + 2 * i + 1 < kend_a ? bf(rne(expf(sa[2 * i + 1] - mrow) / srow_sum)) : 0.f;
+            pw2[i] = (__float_as_uint(p0) >> 16) | (__float_as_uint(p1) & 0xFFFF0000u);
+        }
+        const uint4 a = make_uint4(pw2[0], pw2[1], pw2[2], pw2[3]);
+        __builtin_amdgcn_wave_barrier();  // this wavefront's V rows before its reads
+#pragma unroll
+        for (int t = 0; t < DT; ++t) {
+            const uint4 b = *reinterpret_cast<const uint4 *>(&vw[16 * t + col][8 * quad]);
+            acc[t] = attn_mfma(a, b, acc[t]);
+        }
+        __builtin_amdgcn_wave_barrier();  // its reads before the next step's writes
+        if (more) {
+#pragma unroll
+            for (int t = 0; t < 8; ++t) va[t] = vn[t];
+#pragma unroll
+            for (int e = 0; e < 8; ++e) sa[e] = sn[e];
+        }
+    }
+    // the wavefronts' sums, added in wavefront order: result lane (dim col of
+    // tile t, row quad) holds rows 4 quad + i
+    __syncthreads();  // every wavefront is done with its V slice
+    float(*red)[16][HD] = reinterpret_cast<float(*)[16][HD]>(&vt[0][0][0]);
+#pragma unroll
+    for (int t = 0; t < DT; ++t)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) red[wave][quad * 4 + i][16 * t + col] = acc[t][i];
+    __syncthreads();
+    for (uint32_t o = tid; o < LIVE * HD; o += kAttnThreads) {
+        const uint32_t rr = o / HD, d = o % HD, qi = rr / G, h = rr % G;
+        uint32_t ctx_r = 0;
+#pragma unroll
+        for (uint32_t q = 0; q < R; ++q)
+            if (q == qi) ctx_r = ctxq[q];
+        if (k0 >= ctx_r) continue;  // past the row's context, or a row past the last
+        const float v = ((red[0][rr][d] + red[1][rr][d]) + red[2][rr][d]) + red[3][rr][d];
+        const uint32_t r = r0 + qi;
+        if (chunks == 1)
+            out[(static_cast<uint64_t>(r) * n_heads + h0 + h) * HD + d] = rne(v);
+        else
+            part[((static_cast<uint64_t>(r) * n_kv + kvh) * chunks + c) * (G * HD) + h * HD + d] = v;
+    }
+}
+
 // Adds the chunked P.V partials of each (row, KV head): block (64 outputs,
 // KV head, row); the 4 wavefronts each add a contiguous quarter of the row's
 // active chunks in order (8 loads issued before their adds), then the
@@ -1000,6 +1165,22 @@ static void launch_attention(hipStream_t stream, uint32_t rows, const AttnLayout
         hipLaunchKernelGGL((attn_scores_tile_kernel<HD, G>), grid, dim3(kAttnThreads), 0, stream, x.q_src,
                            x.positions, rows, x.k_cache, x.n_heads, x.max_len, static_cast<uint32_t>(a.nck), splits,
                            x.scale, scores, stats);
+    }
+    if constexpr (!ROPE && HD == 128) {
+        // prefill: P.V on the matrix cores over the same query-row tiles
+        constexpr uint32_t kQR = 16 / G;
+        const uint32_t tiles = (rows + kQR - 1) / kQR;
+        const uint32_t chunks = a.chunks ? static_cast<uint32_t>(a.chunks) : 1u;
+        const uint32_t ck = a.chunks ? static_cast<uint32_t>(a.chunk_keys) : x.max_len;
+        float *part = reinterpret_cast<float *>(x.ws + a.part);
+        hipLaunchKernelGGL((attn_pv_tile_kernel<HD, G>), dim3(x.n_kv * chunks, tiles), dim3(kAttnThreads), 0, stream,
+                           x.v_cache, x.positions, rows, x.n_heads, x.n_kv, x.max_len, static_cast<uint32_t>(a.nck),
+                           chunks, ck, scores, stats, x.out, part);
+        if (chunks > 1)
+            hipLaunchKernelGGL(attn_combine_kernel, dim3((G * HD + kCombineOuts - 1) / kCombineOuts, x.n_kv, rows),
+                               dim3(kAttnThreads), 0, stream, x.positions, x.pos_limit, x.n_heads, x.n_kv,
+                               static_cast<uint32_t>(G * HD), x.max_len, chunks, ck, part, x.out);
+        return;
     }
     if (a.chunks) {
         const uint32_t chunks = static_cast<uint32_t>(a.chunks), ck = static_cast<uint32_t>(a.chunk_keys);
