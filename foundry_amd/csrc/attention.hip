@@ -31,8 +31,11 @@
 //     attn_pv_chunk_kernel, block (KV head, chunk, row): a chunk of keys for
 //       all dims, then attn_combine_kernel adds the chunks -- long or many
 //       rows.
-//   Either way each output element is a sum in a fixed order, so results do
-//   not change from run to run.
+//   fh_attention with head_dim 128 uses attn_pv_tile_kernel instead: the
+//   query-row tiles of the scores, P.V on the matrix cores (M and S combined
+//   over each row's chunks in another fixed order).
+//   Every output element is a sum in a fixed order, so results do not
+//   change from run to run.
 // splits, slices and chunks make rows * n_kv * (blocks per pair) about
 // kAttnTargetBlocks: decode spreads one row over many CUs, prefill keeps one
 // block per (row, KV head).
