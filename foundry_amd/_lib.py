@@ -64,6 +64,33 @@ class Profile(ctypes.Structure):
     ]
 
 
+class Q4Weight(ctypes.Structure):
+    """fh_q4_weight."""
+    _fields_ = [("wq", ctypes.c_void_p), ("scales", ctypes.c_void_p), ("biases", ctypes.c_void_p),
+                ("n", ctypes.c_int64), ("k", ctypes.c_int64)]
+
+
+class LlamaLayer(ctypes.Structure):
+    """fh_llama_layer."""
+    _fields_ = [("qkv", Q4Weight), ("o", Q4Weight), ("gate_up", Q4Weight), ("down", Q4Weight),
+                ("input_norm", ctypes.c_void_p), ("post_norm", ctypes.c_void_p),
+                ("k_cache", ctypes.c_void_p), ("v_cache", ctypes.c_void_p)]
+
+
+class LlamaModel(ctypes.Structure):
+    """fh_llama_model."""
+    _fields_ = [(name, ctypes.c_int64) for name in ("n_layers", "hidden", "n_heads", "n_kv_heads", "head_dim",
+                                                    "ffn", "vocab", "batch", "max_len", "max_tokens")] + [
+        ("rms_norm_eps", ctypes.c_float), ("scale", ctypes.c_float),
+        ("layers", ctypes.POINTER(LlamaLayer)), ("embed", Q4Weight),
+        ("final_norm", ctypes.c_void_p), ("cos_tab", ctypes.c_void_p), ("sin_tab", ctypes.c_void_p),
+    ] + [(name, ctypes.c_void_p) for name in ("h", "h2", "x", "qkv", "q", "attn", "o", "gate_up", "act",
+                                              "logits")] + [
+        ("attn_workspace", ctypes.c_void_p), ("attn_workspace_bytes", ctypes.c_uint64),
+        ("decode_workspace", ctypes.c_void_p), ("decode_workspace_bytes", ctypes.c_uint64),
+    ]
+
+
 class HipError(RuntimeError):
     """An fh_status other than OK, with the library's message."""
 
@@ -120,6 +147,7 @@ SIGNATURES = {
     "fh_argmax": [_vp, _vp, _i64, _i64, _vp],
     "fh_advance_positions": [_vp, _vp, _i64, _i64],
     "fh_append_token": [_vp, _vp, _i64, _vp, _vp, _i64, _i64],
+    "fh_llama_forward": [_vp, _vp, _i64, _vp, _vp, _vp],
 }
 
 _lib = None

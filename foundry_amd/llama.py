@@ -22,8 +22,10 @@ Fusions that keep each output row's arithmetic unchanged:
   buffers), SiLU*up inside the gate/up GEMV (fh_q4_gate_up_silu), and one
   new token's RoPE and cache write inside attention (fh_decode_attention).
 
-The decode step reads its token id and position from device memory, so it is
-captured once as a HIP graph and replayed for every generated token. Weights
+The layer loop itself runs in the library (fh_llama_forward over an
+fh_llama_model table built once here). The decode step reads its token id and
+position from device memory, so it is captured once as a HIP graph and
+replayed for every generated token. Weights
 are random-init (SplitMix64-seeded); no checkpoint is read.
 """
 from __future__ import annotations
@@ -314,6 +316,30 @@ class Q4Llama:
         self.dec_ws_bytes = _lib.decode_attention_workspace_bytes(bt, c.n_heads, c.n_kv_heads, c.head_dim, max_len)
         self.dec_ws = dev.zeros(self.dec_ws_bytes)
         self.seq_len = 0
+        self._model = self._native_model()
+
+    def _native_model(self) -> _lib.LlamaModel:
+        """The fh_llama_model that fh_llama_forward runs: the config, every
+        layer's device operands and the forward's buffers (device pointers)."""
+        c, b = self.cfg, self.buf
+
+        def q4(w: _Q4) -> _lib.Q4Weight:
+            return _lib.Q4Weight(w.wq.ptr, w.s.ptr, w.b.ptr, w.n, w.k)
+
+        self._layer_table = (_lib.LlamaLayer * len(self.layers))(*[
+            _lib.LlamaLayer(q4(L["qkv"]), q4(L["o"]), q4(L["gate_up"]), q4(L["down"]), L["input_norm"].ptr,
+                            L["post_norm"].ptr, L["k_cache"].ptr, L["v_cache"].ptr) for L in self.layers])
+        m = _lib.LlamaModel(n_layers=c.n_layers, hidden=c.hidden, n_heads=c.n_heads, n_kv_heads=c.n_kv_heads,
+                            head_dim=c.head_dim, ffn=c.ffn, vocab=c.vocab, batch=self.batch, max_len=self.max_len,
+                            max_tokens=self.max_tokens, rms_norm_eps=c.rms_norm_eps, scale=self.scale,
+                            layers=self._layer_table, embed=q4(self.embed), final_norm=self.final_norm.ptr,
+                            cos_tab=self.cos.ptr, sin_tab=self.sin.ptr, attn_workspace=self.attn_ws.ptr,
+                            attn_workspace_bytes=self.attn_ws_bytes, decode_workspace=self.dec_ws.ptr,
+                            decode_workspace_bytes=self.dec_ws_bytes)
+        for name, key in (("h", "h"), ("h2", "h2"), ("x", "x"), ("qkv", "qkv"), ("q", "q"), ("attn", "attn"),
+                          ("o", "o"), ("gate_up", "gu"), ("act", "act"), ("logits", "logits")):
+            setattr(m, name, b[key].ptr)
+        return m
 
     @classmethod
     def from_checkpoint(cls, dev: HipDevice, directory, max_len: int, max_tokens: int, batch: int = 1) -> "Q4Llama":
@@ -326,101 +352,16 @@ class Q4Llama:
         cfg = LlamaConfig.open(directory)
         return cls(dev, cfg, None, max_len, max_tokens, batch, weights=Weights.open(directory))
 
-    # ---- thin wrappers over the C-ABI ----
     def _p(self, st: HipStorage, byte_offset: int = 0):
         return ctypes.c_void_p(st.ptr + byte_offset)
 
-    def _linear(self, x: HipStorage, rows: int, w: _Q4, y: HipStorage, x_off: int = 0, x_ld: int | None = None):
-        _lib.call("fh_q4_matmul", self.dev.handle, self._p(x, x_off), rows, w.k, w.k if x_ld is None else x_ld,
-                  self._p(w.wq), self._p(w.s), self._p(w.b), w.n, GROUP, self._p(y), _lib.BF16)
-
-    def _linear_norm(self, x: HipStorage, res, res_out, weight: HipStorage, rows: int, w: _Q4, y: HipStorage,
-                     off: int = 0, y_off: int = 0):
-        """y = rms_norm(x [+ res]) W^T in one GEMV (res_out <- x + res)."""
-        _lib.call("fh_q4_matmul_rmsnorm", self.dev.handle, self._p(x, off),
-                  None if res is None else self._p(res, off), None if res_out is None else self._p(res_out, off),
-                  self._p(weight), ctypes.c_float(self.cfg.rms_norm_eps), rows, w.k, self._p(w.wq), self._p(w.s),
-                  self._p(w.b), w.n, GROUP, self._p(y, y_off), _lib.BF16)
-
-    def _attention(self, L, seq_tokens: int, positions: HipStorage):
-        """q,k = rope(q,k); cache k,v; attn = sdpa(q, cache) for every
-        sequence (src/models/llama/attention.rs:91-131)."""
-        c, d, b = self.cfg, self.dev.handle, self.buf
-        if seq_tokens == 1:
-            # one new token per sequence: RoPE and the cache write fused into attention
-            _lib.call("fh_decode_attention", d, self._p(b["qkv"]), self.batch, c.n_heads, c.n_kv_heads, c.head_dim,
-                      self._p(self.cos), self._p(self.sin), self.max_len, self._p(positions),
-                      self._p(L["k_cache"]), self._p(L["v_cache"]), self.max_len, ctypes.c_float(self.scale),
-                      self._p(self.dec_ws), self.dec_ws_bytes, self._p(b["attn"]))
-            return
-        hq = c.n_heads * c.head_dim
-        for sq in range(self.batch):
-            r0, cache = sq * seq_tokens, sq * self.seq_bytes
-            _lib.call("fh_rope_kv", d, self._p(b["qkv"], r0 * c.qkv_rows * 2), seq_tokens, c.n_heads, c.n_kv_heads,
-                      c.head_dim, self._p(self.cos), self._p(self.sin), self.max_len, self._p(positions, r0 * 4),
-                      self._p(L["k_cache"], cache), self._p(L["v_cache"], cache), self.max_len,
-                      self._p(b["q"], r0 * hq * 2))
-            _lib.call("fh_attention", d, self._p(b["q"], r0 * hq * 2), self._p(L["k_cache"], cache),
-                      self._p(L["v_cache"], cache), self._p(positions, r0 * 4), seq_tokens, c.n_heads, c.n_kv_heads,
-                      c.head_dim, self.max_len, ctypes.c_float(self.scale), self._p(self.attn_ws),
-                      self.attn_ws_bytes, self._p(b["attn"], r0 * hq * 2))
-
     def _forward(self, seq_tokens: int, ids: HipStorage, positions: HipStorage):
         """One forward over `seq_tokens` rows of every sequence (rows ordered
-        sequence-major); leaves each sequence's next id in buf['next']."""
-        c, d, b = self.cfg, self.dev.handle, self.buf
-        tokens = self.batch * seq_tokens
-        _lib.call("fh_q4_embed", d, self._p(self.embed.wq), self._p(self.embed.s), self._p(self.embed.b),
-                  c.vocab, c.hidden, GROUP, self._p(ids), tokens, self._p(b["h"]))
-        fused = tokens <= 8  # GEMV rows: the norms and SiLU go inside the linears
-        h, h_alt = b["h"], b["h2"]
-        pending = None  # output of the previous block still to be added to h
-        for L in self.layers:
-            if not fused:
-                self._norm(tokens, pending, L["input_norm"])
-                self._linear(b["x"], tokens, L["qkv"], b["qkv"])
-            elif pending is None:
-                self._linear_norm(h, None, None, L["input_norm"], tokens, L["qkv"], b["qkv"])
-            else:
-                self._linear_norm(pending, h, h_alt, L["input_norm"], tokens, L["qkv"], b["qkv"])
-                h, h_alt = h_alt, h
-            self._attention(L, seq_tokens, positions)
-            self._linear(b["attn"], tokens, L["o"], b["o"])
-            if fused:
-                # act = silu_mul(rms_norm(o + h) [Wgate; Wup]^T) in one GEMV
-                w = L["gate_up"]
-                _lib.call("fh_q4_gate_up_silu", d, self._p(b["o"]), self._p(h), self._p(h_alt), self._p(L["post_norm"]),
-                          ctypes.c_float(c.rms_norm_eps), tokens, w.k, self._p(w.wq), self._p(w.s), self._p(w.b), w.n,
-                          GROUP, self._p(b["act"]))
-                h, h_alt = h_alt, h
-            else:
-                self._norm(tokens, b["o"], L["post_norm"])
-                self._linear(b["x"], tokens, L["gate_up"], b["gu"])
-                _lib.call("fh_silu_mul", d, self._p(b["gu"]), tokens, c.ffn, self._p(b["act"]))
-            self._linear(b["act"], tokens, L["down"], b["o"])
-            pending = b["o"]
-        # logits of each sequence's last row (src/models/llama/model.rs:112-121)
-        last = (seq_tokens - 1) * c.hidden * 2
-        if fused and seq_tokens == 1:
-            self._linear_norm(pending, h, None, self.final_norm, self.batch, self.embed, b["logits"])
-        elif fused:
-            for sq in range(self.batch):
-                self._linear_norm(pending, h, None, self.final_norm, 1, self.embed, b["logits"],
-                                  off=sq * seq_tokens * c.hidden * 2 + last, y_off=sq * c.vocab * 2)
-        else:
-            self._norm(tokens, pending, self.final_norm)
-            self._linear(b["x"], self.batch, self.embed, b["logits"], x_off=last, x_ld=seq_tokens * c.hidden)
-        _lib.call("fh_argmax", d, self._p(b["logits"]), self.batch, c.vocab, self._p(b["next"]))
-
-    def _norm(self, tokens: int, pending, weight: HipStorage):
-        """x = rms_norm(h [+ pending]); h updated in place when pending."""
-        c, b = self.cfg, self.buf
-        if pending is None:
-            _lib.call("fh_rms_norm", self.dev.handle, self._p(b["h"]), None, None, self._p(weight), tokens,
-                      c.hidden, ctypes.c_float(c.rms_norm_eps), self._p(b["x"]))
-        else:
-            _lib.call("fh_rms_norm", self.dev.handle, self._p(pending), self._p(b["h"]), self._p(b["h"]),
-                      self._p(weight), tokens, c.hidden, ctypes.c_float(c.rms_norm_eps), self._p(b["x"]))
+        sequence-major), issued by fh_llama_forward: embedding, every layer,
+        the LM head of each sequence's last row and its argmax, which is left
+        in buf['next'] (src/models/llama/model.rs:92-121)."""
+        _lib.call("fh_llama_forward", self.dev.handle, ctypes.addressof(self._model), seq_tokens, self._p(ids),
+                  self._p(positions), self._p(self.buf["next"]))
 
     def _upload(self, st: HipStorage, arr: np.ndarray):
         _lib.call("fh_upload", self.dev.handle, self._p(st), arr.ctypes.data_as(ctypes.c_void_p), arr.nbytes)

@@ -38,7 +38,7 @@
 extern "C" {
 #endif
 
-#define FH_ABI_VERSION 1
+#define FH_ABI_VERSION 2
 
 typedef struct fh_device fh_device;
 typedef struct fh_graph fh_graph;
@@ -300,6 +300,70 @@ int fh_append_token(fh_device *dev, const uint32_t *token, int64_t rows, uint32_
 
 /* positions[i] += by for i < n, on the device's stream. */
 int fh_advance_positions(fh_device *dev, uint32_t *positions, int64_t n, int64_t by);
+
+/* ======================================================================
+ * The decoder forward issued from native code: the layer loop that a
+ * caller would otherwise drive op by op, so an eager prefill is not bound
+ * by per-call host overhead.
+ * ====================================================================== */
+
+/* A q4 weight: n rows of k columns (group 64), as fh_q4_matmul takes it. */
+typedef struct fh_q4_weight {
+    const uint32_t *wq;
+    const uint16_t *scales;
+    const uint16_t *biases;
+    int64_t n;
+    int64_t k;
+} fh_q4_weight;
+
+/* One decoder layer (LlamaDecoderLayer, src/models/llama/model.rs:47, :254-280):
+ * qkv = [Wq; Wk; Wv] and gate_up = [Wgate; Wup] rows; bf16 norm weights
+ * [hidden]; caches [batch, n_kv, max_len, head_dim]. */
+typedef struct fh_llama_layer {
+    fh_q4_weight qkv, o, gate_up, down;
+    const uint16_t *input_norm;
+    const uint16_t *post_norm;
+    uint16_t *k_cache;
+    uint16_t *v_cache;
+} fh_llama_layer;
+
+/* A Llama model on one device and the buffers of one forward. rows =
+ * batch * max_tokens: h, h2, x, o [rows, hidden]; qkv [rows, (n_heads +
+ * 2 n_kv) * head_dim]; q, attn [rows, n_heads * head_dim]; gate_up
+ * [rows, 2 ffn]; act [rows, ffn]; logits [batch, vocab]. cos_tab/sin_tab:
+ * [max_len, head_dim]. Workspaces: at least fh_attention_workspace(
+ * max_tokens, ...) and fh_decode_attention_workspace(batch, ...) bytes.
+ * `layers` is a host array of n_layers entries. */
+typedef struct fh_llama_model {
+    int64_t n_layers, hidden, n_heads, n_kv_heads, head_dim, ffn, vocab;
+    int64_t batch, max_len, max_tokens;
+    float rms_norm_eps;
+    float scale;
+    const fh_llama_layer *layers;
+    fh_q4_weight embed;
+    const uint16_t *final_norm;
+    const uint16_t *cos_tab;
+    const uint16_t *sin_tab;
+    uint16_t *h, *h2, *x, *qkv, *q, *attn, *o, *gate_up, *act, *logits;
+    void *attn_workspace;
+    uint64_t attn_workspace_bytes;
+    void *decode_workspace;
+    uint64_t decode_workspace_bytes;
+} fh_llama_model;
+
+/* LlamaModel::forward (src/models/llama/model.rs:92-121) and the greedy
+ * pick of Decoder::step (src/generate/mod.rs:150-204): ids and positions
+ * (device u32 [batch, seq_tokens], sequence-major) run through the embedding,
+ * every layer and the tied LM head of each sequence's last row; next (device
+ * u32 [batch]) gets each sequence's argmax. The same op sequence as calling
+ * the ops above one by one: up to 8 rows the RMSNorms, residual adds and SiLU
+ * go inside the GEMVs and one new token's RoPE and cache write inside
+ * fh_decode_attention; above 8 rows the unfused ops run, and prefill
+ * attention runs one sequence at a time. The operands are checked before
+ * any work is issued; every op checks its own ranges as it runs. May be
+ * captured (fh_capture_begin). 1 <= seq_tokens <= max_tokens. */
+int fh_llama_forward(fh_device *dev, const fh_llama_model *model, int64_t seq_tokens,
+                     const uint32_t *ids, const uint32_t *positions, uint32_t *next);
 
 #ifdef __cplusplus
 }

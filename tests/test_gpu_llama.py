@@ -436,6 +436,22 @@ def test_batched_step_argument_errors(device):
         Q4Llama(device, TINY, 1, 16, max_tokens=4, batch=0)
 
 
+def test_llama_forward_checks_the_model_first(device):
+    """fh_llama_forward rejects a layer whose weight shape does not fit the
+    config, and a token count above max_tokens, before issuing any work; the
+    device stays usable."""
+    model = Q4Llama(device, TINY, 1, 16, max_tokens=4, batch=2)
+    b = model.buf
+    model._layer_table[1].o.n += 64
+    with pytest.raises(_lib.HipError, match="layer 1 o"):
+        model._forward(2, b["ids"], b["positions"])
+    model._layer_table[1].o.n -= 64
+    with pytest.raises(_lib.HipError, match="max_tokens"):
+        model._forward(5, b["ids"], b["positions"])
+    model.step(np.ones((2, 3), np.uint32), 0)
+    assert down(device, b["next"], np.uint32, 2).shape == (2,)
+
+
 def test_append_token_rows(device):
     """fh_append_token logs each sequence's token at its own position; a
     position before base or past capacity writes nothing."""

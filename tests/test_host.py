@@ -115,6 +115,40 @@ def test_abi_version_matches_header():
     assert _lib.load().fh_abi_version() == version
 
 
+def _c_layout(struct: str, fields) -> list[int]:
+    """sizeof and offsetof of a header struct, from a C program built with gcc."""
+    import shutil
+    import subprocess
+    import tempfile
+
+    if shutil.which("gcc") is None:
+        pytest.skip("gcc is not available")
+    body = "".join(f'    printf("%zu\\n", offsetof({struct}, {f}));\n' for f in fields)
+    src = (f'#include <stdio.h>\n#include <stddef.h>\n#include "{HEADER}"\n'
+           f'int main(void) {{\n    printf("%zu\\n", sizeof({struct}));\n{body}    return 0;\n}}\n')
+    with tempfile.TemporaryDirectory() as tmp:
+        c, exe = os.path.join(tmp, "layout.c"), os.path.join(tmp, "layout")
+        with open(c, "w") as f:
+            f.write(src)
+        subprocess.run(["gcc", "-std=c99", "-o", exe, c], check=True, capture_output=True)
+        out = subprocess.run([exe], check=True, capture_output=True, text=True).stdout
+    return [int(v) for v in out.split()]
+
+
+@pytest.mark.parametrize("struct, cls", [("fh_q4_weight", _lib.Q4Weight), ("fh_llama_layer", _lib.LlamaLayer),
+                                         ("fh_llama_model", _lib.LlamaModel)])
+def test_model_structs_match_the_header(struct, cls):
+    fields = [f[0] for f in cls._fields_]
+    assert _c_layout(struct, fields) == [ctypes.sizeof(cls)] + [getattr(cls, f).offset for f in fields]
+
+
+def test_llama_forward_rejects_a_null_device_and_model():
+    lib = _lib.load()
+    m = _lib.LlamaModel()
+    assert lib.fh_llama_forward(None, ctypes.addressof(m), 1, None, None, None) == _lib.ERR_INVALID_ARGUMENT
+    assert "fh_llama_forward" in _lib.last_error()
+
+
 def test_calls_without_a_device_return_errors_not_crashes():
     lib = _lib.load()
     handle = ctypes.c_void_p()
