@@ -13,6 +13,30 @@ namespace fh {
 __device__ __forceinline__ uint16_t rne(float v) { return static_cast<uint16_t>(f32_to_bf16_rne(v)); }
 __device__ __forceinline__ float bf(uint16_t b) { return bf16_to_f32(b); }
 
+// Elements i .. i + 7 of a GEMM split over K (f32 partials [splits][...],
+// `stride` elements apart, i a multiple of 4): each the RNE to bf16 of its
+// partials added in split order, the sum gemm_split_reduce_kernel forms;
+// packed two per word. Every split's loads are issued before any add.
+__device__ __forceinline__ uint4 split_sum8(const float *__restrict__ part, uint32_t splits, uint64_t stride,
+                                            uint64_t i) {
+    float4 lo[kMaxGemmSplits], hi[kMaxGemmSplits];
+#pragma unroll
+    for (uint32_t sp = 0; sp < kMaxGemmSplits; ++sp) {
+        const float *p = part + static_cast<uint64_t>(sp < splits ? sp : splits - 1) * stride + i;
+        lo[sp] = *reinterpret_cast<const float4 *>(p);
+        hi[sp] = *reinterpret_cast<const float4 *>(p + 4);
+    }
+    float4 a = lo[0], b = hi[0];
+#pragma unroll
+    for (uint32_t sp = 1; sp < kMaxGemmSplits; ++sp)
+        if (sp < splits) {
+            a.x += lo[sp].x, a.y += lo[sp].y, a.z += lo[sp].z, a.w += lo[sp].w;
+            b.x += hi[sp].x, b.y += hi[sp].y, b.z += hi[sp].z, b.w += hi[sp].w;
+        }
+    return make_uint4(rne(a.x) | static_cast<uint32_t>(rne(a.y)) << 16, rne(a.z) | static_cast<uint32_t>(rne(a.w)) << 16,
+                      rne(b.x) | static_cast<uint32_t>(rne(b.y)) << 16, rne(b.z) | static_cast<uint32_t>(rne(b.w)) << 16);
+}
+
 __device__ __forceinline__ void unpack8(const uint4 v, float (&f)[8]) {
     const uint32_t w[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll

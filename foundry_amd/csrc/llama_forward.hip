@@ -6,12 +6,27 @@
 // of LlamaMlp::forward (src/models/llama/mlp.rs:49-58), then the greedy pick
 // of Decoder::step (src/generate/mod.rs:192-204). Each step is one of the
 // library's ops, called as a host would call it, so the results are those of
-// the op-by-op sequence; what this saves is the host's per-op cost (argument
-// marshalling in an interpreted caller), which bounds an eager prefill whose
-// kernels take a few microseconds each.
+// the op-by-op sequence. One difference in how they run: above 8 rows, a
+// linear whose GEMM splits K hands its f32 partials straight to the RMSNorm
+// or SiLU that consumes its output, which adds them in the order of the
+// GEMM's own reduce (the same bf16 values, one launch and one round trip of
+// the output fewer).
 #include <utility>
 
 #include "device.hpp"
+
+namespace fh {
+int check_q4_table(const fh_device *dev, const char *fn, const uint32_t *wq, const uint16_t *scales,
+                   const uint16_t *biases, int64_t rows, int64_t k, int64_t group);
+uint32_t launch_q4_gemm_deferred(hipStream_t stream, uint32_t cus, const uint16_t *x, uint32_t x_ld,
+                                 const uint32_t *wq, const uint16_t *s, const uint16_t *b, uint32_t m, uint32_t n,
+                                 uint32_t k, void *y, int y_is_f32, void *area);
+void launch_rms_norm_partials(hipStream_t stream, const float *part, uint32_t splits, const uint16_t *res,
+                              uint16_t *res_out, const uint16_t *w, uint32_t rows, uint32_t dim, float eps,
+                              uint16_t *y);
+void launch_silu_mul_partials(hipStream_t stream, const float *part, uint32_t splits, uint32_t rows, uint32_t f,
+                              uint16_t *out);
+}  // namespace fh
 
 namespace {
 
@@ -74,6 +89,83 @@ int norm(fh_device *d, const fh_llama_model &m, int64_t rows, const uint16_t *pe
                        m.hidden, m.rms_norm_eps, m.x);
 }
 
+bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+// The checks fh_q4_matmul makes for a GEMM of rows > 8 rows into y (bf16).
+int check_gemm(fh_device *d, const char *fn, const uint16_t *x, int64_t rows, int64_t x_ld, const fh_q4_weight &w,
+               const uint16_t *y) {
+    FH_TRY(fh::check_q4_table(d, fn, w.wq, w.scales, w.biases, w.n, w.k, kGroup));
+    if (rows > 65535ll * 128) return fail(FH_ERR_INDEX_TOO_LARGE, "%s: m > 65535*128 rows", fn);
+    if (x_ld < w.k || x_ld % 8 != 0 || x_ld > 0x7FFFFFFFll || !aligned16(x) || !aligned16(y))
+        return fail(FH_ERR_INVALID_ARGUMENT, "%s: linear operands must be 16-byte aligned with a row stride that is "
+                    "a multiple of 8 and at least k", fn);
+    FH_TRY(fh::check_range(d, x, (static_cast<uint64_t>(rows - 1) * x_ld + w.k) * 2, fn, "x"));
+    return fh::check_range(d, y, static_cast<uint64_t>(rows) * w.n * 2, fn, "y");
+}
+
+// Runs the GEMM, leaving its K-split partials (if it splits) in the
+// device's partial area for the consumer to add; returns the split count.
+int gemm_deferred(fh_device *d, const char *fn, const uint16_t *x, int64_t rows, int64_t x_ld, const fh_q4_weight &w,
+                  uint16_t *y, uint32_t *splits) {
+    FH_TRY(fh::set_current(d, fn));
+    return fh::dispatch(d, fn, [&] {
+        *splits = fh::launch_q4_gemm_deferred(d->stream, d->compute_units, x, static_cast<uint32_t>(x_ld), w.wq,
+                                              w.scales, w.biases, static_cast<uint32_t>(rows),
+                                              static_cast<uint32_t>(w.n), static_cast<uint32_t>(w.k), y, 0,
+                                              d->partial_area);
+    });
+}
+
+// Above 8 rows: y = x W^T through fh_q4_matmul's checks and kernels, but
+// when the GEMM splits K its partials stay in the device's partial area and
+// y is not written: the op that consumes y forms each value from them in
+// split order (the value the reduce would store), so the reduce launch and
+// y's round trip go away and the results are those of the op sequence.
+int linear_deferred(fh_device *d, const uint16_t *x, int64_t rows, int64_t x_ld, const fh_q4_weight &w, uint16_t *y,
+                    uint32_t *splits) {
+    const char *fn = "fh_llama_forward";
+    FH_TRY(check_gemm(d, fn, x, rows, x_ld, w, y));
+    return gemm_deferred(d, fn, x, rows, x_ld, w, y, splits);
+}
+
+// m.x = rms_norm(h [+ pending]), h updated when pending is given; pending is
+// the output of linear_deferred with `splits` K splits.
+int add_norm(fh_device *d, const fh_llama_model &m, int64_t rows, const uint16_t *pending, uint32_t splits,
+             const uint16_t *norm_w) {
+    if (pending == nullptr || splits <= 1) return norm(d, m, rows, pending, norm_w);
+    const char *fn = "fh_llama_forward";
+    const uint64_t bytes = static_cast<uint64_t>(rows) * m.hidden * 2;
+    if (m.hidden % 8 != 0 || m.hidden > 8192 || !aligned16(m.h) || !aligned16(m.x) || !aligned16(norm_w))
+        return fail(FH_ERR_UNSUPPORTED, "%s: the norm needs hidden %% 8 == 0, at most 8192, aligned operands", fn);
+    FH_TRY(fh::check_range(d, m.h, bytes, fn, "h"));
+    FH_TRY(fh::check_range(d, m.x, bytes, fn, "x"));
+    FH_TRY(fh::check_range(d, norm_w, static_cast<uint64_t>(m.hidden) * 2, fn, "norm weight"));
+    return fh::dispatch(d, fn, [&] {
+        fh::launch_rms_norm_partials(d->stream, static_cast<const float *>(d->partial_area), splits, m.h, m.h, norm_w,
+                                     static_cast<uint32_t>(rows), static_cast<uint32_t>(m.hidden), m.rms_norm_eps,
+                                     m.x);
+    });
+}
+
+// Above 8 rows: gate_up = m.x [Wgate; Wup]^T; act = silu(gate) * up, the
+// SiLU forming gate and up from the GEMM's split partials (linear_deferred).
+int linear_silu(fh_device *d, const fh_llama_model &m, int64_t rows, const fh_q4_weight &w) {
+    const char *fn = "fh_llama_forward";
+    if (m.ffn % 8 != 0 || !aligned16(m.act)) {
+        FH_TRY(linear(d, m.x, rows, m.hidden, w, m.gate_up));
+        return fh_silu_mul(d, m.gate_up, rows, m.ffn, m.act);
+    }
+    FH_TRY(check_gemm(d, fn, m.x, rows, m.hidden, w, m.gate_up));
+    FH_TRY(fh::check_range(d, m.act, static_cast<uint64_t>(rows) * m.ffn * 2, fn, "act"));
+    uint32_t splits = 1;
+    FH_TRY(gemm_deferred(d, fn, m.x, rows, m.hidden, w, m.gate_up, &splits));
+    if (splits == 1) return fh_silu_mul(d, m.gate_up, rows, m.ffn, m.act);
+    return fh::dispatch(d, fn, [&] {
+        fh::launch_silu_mul_partials(d->stream, static_cast<const float *>(d->partial_area), splits,
+                                     static_cast<uint32_t>(rows), static_cast<uint32_t>(m.ffn), m.act);
+    });
+}
+
 // q,k = rope(q,k); cache k,v; attn = sdpa(q, cache) for every sequence.
 int attention(fh_device *d, const fh_llama_model &m, const fh_llama_layer &L, int64_t seq_tokens,
               const uint32_t *positions) {
@@ -115,10 +207,11 @@ extern "C" int fh_llama_forward(fh_device *dev, const fh_llama_model *model, int
     // block's output (pending) is added inside the next RMSNorm
     uint16_t *h = m.h, *h_alt = m.h2;
     const uint16_t *pending = nullptr;
+    uint32_t pending_splits = 1;  // above 8 rows: K splits of the GEMM behind pending
     for (int64_t l = 0; l < m.n_layers; ++l) {
         const fh_llama_layer &L = m.layers[l];
         if (!fused) {
-            FH_TRY(norm(dev, m, tokens, pending, L.input_norm));
+            FH_TRY(add_norm(dev, m, tokens, pending, pending_splits, L.input_norm));
             FH_TRY(linear(dev, m.x, tokens, m.hidden, L.qkv, m.qkv));
         } else if (pending == nullptr) {
             FH_TRY(linear_norm(dev, m, h, nullptr, nullptr, L.input_norm, tokens, L.qkv, m.qkv));
@@ -127,17 +220,24 @@ extern "C" int fh_llama_forward(fh_device *dev, const fh_llama_model *model, int
             std::swap(h, h_alt);
         }
         FH_TRY(attention(dev, m, L, seq_tokens, positions));
+        if (!fused) {
+            // o, then h += o and x = rms_norm(h); gate/up and SiLU; down (its
+            // output is added by the next RMSNorm)
+            uint32_t o_splits = 1;
+            FH_TRY(linear_deferred(dev, m.attn, tokens, hq, L.o, m.o, &o_splits));
+            FH_TRY(add_norm(dev, m, tokens, m.o, o_splits, L.post_norm));
+            FH_TRY(linear_silu(dev, m, tokens, L.gate_up));
+            FH_TRY(linear_deferred(dev, m.act, tokens, m.ffn, L.down, m.o, &pending_splits));
+            pending = m.o;
+            continue;
+        }
         FH_TRY(linear(dev, m.attn, tokens, hq, L.o, m.o));
-        if (fused) {
+        {
             // act = silu_mul(rms_norm(o + h) [Wgate; Wup]^T) in one GEMV
             const fh_q4_weight &w = L.gate_up;
             FH_TRY(fh_q4_gate_up_silu(dev, m.o, h, h_alt, L.post_norm, m.rms_norm_eps, tokens, w.k, w.wq, w.scales,
                                       w.biases, w.n, kGroup, m.act));
             std::swap(h, h_alt);
-        } else {
-            FH_TRY(norm(dev, m, tokens, m.o, L.post_norm));
-            FH_TRY(linear(dev, m.x, tokens, m.hidden, L.gate_up, m.gate_up));
-            FH_TRY(fh_silu_mul(dev, m.gate_up, tokens, m.ffn, m.act));
         }
         FH_TRY(linear(dev, m.act, tokens, m.ffn, L.down, m.o));
         pending = m.o;
@@ -157,7 +257,7 @@ extern "C" int fh_llama_forward(fh_device *dev, const fh_llama_model *model, int
                                m.logits + sq * m.vocab));
         }
     } else {
-        FH_TRY(norm(dev, m, tokens, pending, m.final_norm));
+        FH_TRY(add_norm(dev, m, tokens, pending, pending_splits, m.final_norm));
         FH_TRY(linear(dev, m.x + last, m.batch, seq_tokens * m.hidden, m.embed, m.logits));
     }
     return fh_argmax(dev, m.logits, m.batch, m.vocab, next);

@@ -49,15 +49,21 @@ __device__ __forceinline__ float block_max(float v, float *red) {
 // kNormChunks pieces of 8 per thread). With `res`, h = RNE(x + res) is formed
 // first (the residual add, src/models/llama/model.rs:254-279) and written to
 // res_out. y = RNE(RNE(h * scale) * w), scale = 1 / sqrt(sum(h^2) * (1/dim) + eps).
+// With PART, x is not read: each x value is formed from the f32 partials of
+// the GEMM that produced it (split_sum8, the value gemm_split_reduce_kernel
+// would have stored), so the norm stands in for that reduce.
 constexpr int kNormThreads = 256;
 constexpr int kNormChunks = 4;  // dim <= 256 * 8 * 4 = 8192
 
+template <bool PART>
 __global__ __launch_bounds__(kNormThreads) void rms_norm_kernel(const uint16_t *__restrict__ x,
                                                                 const uint16_t *__restrict__ res,
                                                                 uint16_t *__restrict__ res_out,
                                                                 const uint16_t *__restrict__ w,
                                                                 uint32_t dim, float eps, float dim_inv,
-                                                                uint16_t *__restrict__ y) {
+                                                                uint16_t *__restrict__ y,
+                                                                const float *__restrict__ part, uint32_t splits,
+                                                                uint64_t part_stride) {
     __shared__ float red[kNormThreads / 64];
     const uint64_t base = static_cast<uint64_t>(blockIdx.x) * dim;
     const uint32_t pieces = dim / 8;
@@ -73,7 +79,8 @@ __global__ __launch_bounds__(kNormThreads) void rms_norm_kernel(const uint16_t *
     for (int c = 0; c < kNormChunks; ++c) {
         const uint32_t piece = threadIdx.x + c * kNormThreads;
         if (piece < pieces) {
-            const uint4 xv = *reinterpret_cast<const uint4 *>(x + base + piece * 8);
+            const uint4 xv = PART ? split_sum8(part, splits, part_stride, base + piece * 8)
+                                  : *reinterpret_cast<const uint4 *>(x + base + piece * 8);
             const uint32_t xw[4] = {xv.x, xv.y, xv.z, xv.w};
             uint32_t hw[4];
             if (res) {
@@ -166,8 +173,12 @@ __device__ __forceinline__ uint16_t silu_mul1(uint16_t gb, uint16_t ub) {
     return rne(bf(rne(g / den)) * u);
 }
 
+// With part (vec only), g and u are formed from the f32 partials of the
+// gate/up GEMM (split_sum8), which stands in for its reduce.
 __global__ __launch_bounds__(256) void silu_mul_kernel(const uint16_t *__restrict__ gu, uint32_t f, uint32_t rows,
-                                                       int vec, uint16_t *__restrict__ out) {
+                                                       int vec, uint16_t *__restrict__ out,
+                                                       const float *__restrict__ part, uint32_t splits,
+                                                       uint64_t part_stride) {
     const uint32_t c0 = (blockIdx.x * 256 + threadIdx.x) * 8;
     if (c0 >= f) return;
     for (uint32_t r = blockIdx.y; r < rows; r += gridDim.y) {
@@ -175,8 +186,9 @@ __global__ __launch_bounds__(256) void silu_mul_kernel(const uint16_t *__restric
         const uint16_t *u = g + f;
         uint16_t *o = out + static_cast<uint64_t>(r) * f;
         if (vec) {
-            const uint4 gv = *reinterpret_cast<const uint4 *>(g + c0);
-            const uint4 uv = *reinterpret_cast<const uint4 *>(u + c0);
+            const uint64_t gi = static_cast<uint64_t>(r) * 2 * f + c0;
+            const uint4 gv = part ? split_sum8(part, splits, part_stride, gi) : *reinterpret_cast<const uint4 *>(g + c0);
+            const uint4 uv = part ? split_sum8(part, splits, part_stride, gi + f) : *reinterpret_cast<const uint4 *>(u + c0);
             const uint32_t gw[4] = {gv.x, gv.y, gv.z, gv.w}, uw[4] = {uv.x, uv.y, uv.z, uv.w};
             uint32_t ow[4];
 #pragma unroll
@@ -280,6 +292,22 @@ __global__ void advance_kernel(uint32_t *__restrict__ p, uint32_t n, uint32_t by
     if (i < n) p[i] += by;
 }
 
+// Launches for a consumer that stands in for a split GEMM's reduce (part:
+// [splits][rows][width] f32, the operands checked by the caller).
+void launch_rms_norm_partials(hipStream_t stream, const float *part, uint32_t splits, const uint16_t *res,
+                              uint16_t *res_out, const uint16_t *w, uint32_t rows, uint32_t dim, float eps,
+                              uint16_t *y) {
+    hipLaunchKernelGGL(rms_norm_kernel<true>, dim3(rows), dim3(kNormThreads), 0, stream, nullptr, res, res_out, w,
+                       dim, eps, 1.0f / static_cast<float>(dim), y, part, splits, static_cast<uint64_t>(rows) * dim);
+}
+
+void launch_silu_mul_partials(hipStream_t stream, const float *part, uint32_t splits, uint32_t rows, uint32_t f,
+                              uint16_t *out) {
+    const dim3 grid((f + 2047) / 2048, rows < 65535 ? rows : 65535);
+    hipLaunchKernelGGL(silu_mul_kernel, grid, dim3(256), 0, stream, nullptr, f, rows, 1, out, part, splits,
+                       static_cast<uint64_t>(rows) * 2 * f);
+}
+
 }  // namespace fh
 
 using namespace fh;
@@ -312,9 +340,9 @@ extern "C" int fh_rms_norm(fh_device *dev, const uint16_t *x, const uint16_t *re
     if (int rc = set_current(dev, fn)) return rc;
     const float dim_inv = 1.0f / static_cast<float>(dim);
     return dispatch(dev, fn, [&] {
-        hipLaunchKernelGGL(rms_norm_kernel, dim3(static_cast<uint32_t>(rows)), dim3(kNormThreads), 0,
+        hipLaunchKernelGGL(rms_norm_kernel<false>, dim3(static_cast<uint32_t>(rows)), dim3(kNormThreads), 0,
                            dev->stream, x, residual, residual_out, weight,
-                           static_cast<uint32_t>(dim), eps, dim_inv, y);
+                           static_cast<uint32_t>(dim), eps, dim_inv, y, nullptr, 1u, uint64_t{0});
     });
 }
 
@@ -368,7 +396,7 @@ extern "C" int fh_silu_mul(fh_device *dev, const uint16_t *gate_up, int64_t rows
     const dim3 grid(static_cast<uint32_t>((f + 2047) / 2048), static_cast<uint32_t>(rows < 65535 ? rows : 65535));
     return dispatch(dev, fn, [&] {
         hipLaunchKernelGGL(silu_mul_kernel, grid, dim3(256), 0, dev->stream, gate_up, static_cast<uint32_t>(f),
-                           static_cast<uint32_t>(rows), vec, out);
+                           static_cast<uint32_t>(rows), vec, out, nullptr, 1u, uint64_t{0});
     });
 }
 

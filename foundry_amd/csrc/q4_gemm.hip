@@ -245,7 +245,6 @@ static void launch_gemm_tile(hipStream_t stream, const uint16_t *x, uint32_t x_l
 // RNE(sum_s part[s][i]) (or the f32 sum). Each thread takes 4 consecutive
 // outputs; its kMaxGemmSplits loads are issued before any add (clamped to
 // the last split, whose extra values are not added).
-constexpr uint32_t kMaxGemmSplits = 8;
 
 __global__ __launch_bounds__(256) void gemm_split_reduce_kernel(const float *__restrict__ part, uint32_t splits,
                                                                  uint64_t count, void *__restrict__ y,
@@ -299,12 +298,17 @@ __global__ __launch_bounds__(256) void gemm_split_reduce_kernel(const float *__r
 // (prompt-length m such as 512 against n = 3072 or 5120), K is split over
 // up to kMaxGemmSplits ranges so that tiles x splits about fills the chip;
 // the splits' f32 partials go to `area` (kPartialAreaBytes) and
-// gemm_split_reduce_kernel adds them in order.
-void launch_q4_gemm(hipStream_t stream, uint32_t cus, const uint16_t *x, uint32_t x_ld, const uint32_t *wq,
-                    const uint16_t *s, const uint16_t *b, uint32_t m, uint32_t n, uint32_t k, void *y,
-                    int y_is_f32, void *area) {
+// gemm_split_reduce_kernel adds them in order. launch_q4_gemm_deferred stops
+// before that add and returns the split count (1: y was written), so that a
+// consumer of y can add the partials itself, in the same order.
+uint32_t launch_q4_gemm_deferred(hipStream_t stream, uint32_t cus, const uint16_t *x, uint32_t x_ld,
+                                 const uint32_t *wq, const uint16_t *s, const uint16_t *b, uint32_t m, uint32_t n,
+                                 uint32_t k, void *y, int y_is_f32, void *area) {
     const uint64_t big = static_cast<uint64_t>((n + 255) / 256) * ((m + 255) / 256);
-    if (big >= cus) return launch_gemm_tile<256, 256, 2, 4>(stream, x, x_ld, wq, s, b, m, n, k, y, y_is_f32, 1);
+    if (big >= cus) {
+        launch_gemm_tile<256, 256, 2, 4>(stream, x, x_ld, wq, s, b, m, n, k, y, y_is_f32, 1);
+        return 1;
+    }
     const uint64_t tiles = static_cast<uint64_t>((n + 127) / 128) * ((m + 255) / 256);
     const uint64_t steps = k / kBK;
     uint64_t splits = 1;
@@ -315,12 +319,23 @@ void launch_q4_gemm(hipStream_t stream, uint32_t cus, const uint16_t *x, uint32_
         while (splits > 1 && splits * m * n * 4 > kPartialAreaBytes) --splits;
         if (splits < 1) splits = 1;
     }
-    if (splits == 1) return launch_gemm_tile<256, 128, 4, 2>(stream, x, x_ld, wq, s, b, m, n, k, y, y_is_f32, 1);
+    if (splits == 1) {
+        launch_gemm_tile<256, 128, 4, 2>(stream, x, x_ld, wq, s, b, m, n, k, y, y_is_f32, 1);
+        return 1;
+    }
     launch_gemm_tile<256, 128, 4, 2>(stream, x, x_ld, wq, s, b, m, n, k, area, 1, static_cast<uint32_t>(splits));
+    return static_cast<uint32_t>(splits);
+}
+
+void launch_q4_gemm(hipStream_t stream, uint32_t cus, const uint16_t *x, uint32_t x_ld, const uint32_t *wq,
+                    const uint16_t *s, const uint16_t *b, uint32_t m, uint32_t n, uint32_t k, void *y,
+                    int y_is_f32, void *area) {
+    const uint32_t splits = launch_q4_gemm_deferred(stream, cus, x, x_ld, wq, s, b, m, n, k, y, y_is_f32, area);
+    if (splits == 1) return;
     const uint64_t count = static_cast<uint64_t>(m) * n;
     const uint64_t blocks = (count + 1023) / 1024;
     hipLaunchKernelGGL(gemm_split_reduce_kernel, dim3(static_cast<uint32_t>(blocks)), dim3(256), 0, stream,
-                       static_cast<const float *>(area), static_cast<uint32_t>(splits), count, y, y_is_f32);
+                       static_cast<const float *>(area), splits, count, y, y_is_f32);
 }
 
 }  // namespace fh

@@ -452,6 +452,77 @@ def test_llama_forward_checks_the_model_first(device):
     assert down(device, b["next"], np.uint32, 2).shape == (2,)
 
 
+def _op_by_op_forward(model, seq_tokens):
+    """The forward above 8 rows as separate C-ABI ops on the model's own
+    buffers: the sequence fh_llama_forward stands for."""
+    c, d, b, P, call = model.cfg, model.dev.handle, model.buf, model._p, _lib.call
+    tokens, hq, eps = model.batch * seq_tokens, c.n_heads * c.head_dim, ctypes.c_float(c.rms_norm_eps)
+
+    def lin(x, rows, w, y, x_off=0, x_ld=None):
+        call("fh_q4_matmul", d, P(x, x_off), rows, w.k, w.k if x_ld is None else x_ld, P(w.wq), P(w.s), P(w.b), w.n,
+             64, P(y), _lib.BF16)
+
+    def norm(pending, weight):
+        res = None if pending is None else P(b["h"])
+        call("fh_rms_norm", d, P(b["h"] if pending is None else pending), res, res, P(weight), tokens, c.hidden, eps,
+             P(b["x"]))
+
+    call("fh_q4_embed", d, P(model.embed.wq), P(model.embed.s), P(model.embed.b), c.vocab, c.hidden, 64, P(b["ids"]),
+         tokens, P(b["h"]))
+    pending = None
+    for L in model.layers:
+        norm(pending, L["input_norm"])
+        lin(b["x"], tokens, L["qkv"], b["qkv"])
+        for sq in range(model.batch):
+            r0, cache = sq * seq_tokens, sq * model.seq_bytes
+            call("fh_rope_kv", d, P(b["qkv"], r0 * c.qkv_rows * 2), seq_tokens, c.n_heads, c.n_kv_heads, c.head_dim,
+                 P(model.cos), P(model.sin), model.max_len, P(b["positions"], r0 * 4), P(L["k_cache"], cache),
+                 P(L["v_cache"], cache), model.max_len, P(b["q"], r0 * hq * 2))
+            call("fh_attention", d, P(b["q"], r0 * hq * 2), P(L["k_cache"], cache), P(L["v_cache"], cache),
+                 P(b["positions"], r0 * 4), seq_tokens, c.n_heads, c.n_kv_heads, c.head_dim, model.max_len,
+                 ctypes.c_float(model.scale), P(model.attn_ws), model.attn_ws_bytes, P(b["attn"], r0 * hq * 2))
+        lin(b["attn"], tokens, L["o"], b["o"])
+        norm(b["o"], L["post_norm"])
+        lin(b["x"], tokens, L["gate_up"], b["gu"])
+        call("fh_silu_mul", d, P(b["gu"]), tokens, c.ffn, P(b["act"]))
+        lin(b["act"], tokens, L["down"], b["o"])
+        pending = b["o"]
+    norm(pending, model.final_norm)
+    lin(b["x"], model.batch, model.embed, b["logits"], x_off=(seq_tokens - 1) * c.hidden * 2,
+        x_ld=seq_tokens * c.hidden)
+    call("fh_argmax", d, P(b["logits"]), model.batch, c.vocab, P(b["next"]))
+
+
+# hidden 512 and FFN 1024: the o, gate/up and down GEMMs of these row counts
+# split K (2, 2 and 4 splits), so fh_llama_forward's norms and SiLU form
+# their inputs from the partials
+SPLIT = LlamaConfig(n_layers=2, hidden=512, n_heads=8, n_kv_heads=2, head_dim=64, ffn=1024, vocab=1000)
+
+
+@pytest.mark.parametrize("batch,t", [(2, 20), (1, 300)])
+def test_llama_forward_equals_the_op_sequence(device, batch, t):
+    """fh_llama_forward above 8 rows (split GEMMs feeding the norms and
+    SiLU) gives bit-identical logits, hidden states and next ids to the
+    same forward issued op by op."""
+    model = Q4Llama(device, SPLIT, 5, 512, max_tokens=t, batch=batch)
+    b, c = model.buf, SPLIT
+    ids = synth.token_ids(11, batch * t, c.vocab).reshape(batch, t)
+    model._upload(b["ids"], np.ascontiguousarray(ids, dtype=np.uint32))
+    model._upload(b["positions"], np.tile(np.arange(t, dtype=np.uint32), batch))
+    rows = batch * t
+
+    def state():
+        return (down(device, b["logits"], np.uint16, batch * c.vocab), down(device, b["h"], np.uint16, rows * c.hidden),
+                down(device, b["next"], np.uint32, batch))
+
+    model._forward(t, b["ids"], b["positions"])
+    native = state()
+    _op_by_op_forward(model, t)
+    ops = state()
+    for got, exp, what in zip(native, ops, ("logits", "h", "next")):
+        assert np.array_equal(got, exp), f"{what}: {np.count_nonzero(got != exp)} of {got.size} differ"
+
+
 def test_append_token_rows(device):
     """fh_append_token logs each sequence's token at its own position; a
     position before base or past capacity writes nothing."""
