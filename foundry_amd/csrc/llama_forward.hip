@@ -7,8 +7,8 @@
 // of Decoder::step (src/generate/mod.rs:192-204). Each step is one of the
 // library's ops, called as a host would call it, so the results are those of
 // the op-by-op sequence. One difference in how they run: above 8 rows, a
-// linear whose GEMM splits K hands its f32 partials straight to the RMSNorm
-// or SiLU that consumes its output, which adds them in the order of the
+// linear whose GEMM splits K hands its f32 partials straight to the RMSNorm,
+// SiLU or RoPE that consumes its output, which adds them in the order of the
 // GEMM's own reduce (the same bf16 values, one launch and one round trip of
 // the output fewer).
 #include <utility>
@@ -26,6 +26,10 @@ void launch_rms_norm_partials(hipStream_t stream, const float *part, uint32_t sp
                               uint16_t *y);
 void launch_silu_mul_partials(hipStream_t stream, const float *part, uint32_t splits, uint32_t rows, uint32_t f,
                               uint16_t *out);
+int rope_kv(fh_device *dev, const char *fn, const uint16_t *qkv, const float *part, uint32_t splits,
+            uint64_t part_stride, int64_t tokens, int64_t n_heads, int64_t n_kv, int64_t head_dim,
+            const uint16_t *cos_tab, const uint16_t *sin_tab, int64_t table_len, const uint32_t *positions,
+            uint16_t *k_cache, uint16_t *v_cache, int64_t max_len, uint16_t *q_out);
 }  // namespace fh
 
 namespace {
@@ -167,8 +171,10 @@ int linear_silu(fh_device *d, const fh_llama_model &m, int64_t rows, const fh_q4
 }
 
 // q,k = rope(q,k); cache k,v; attn = sdpa(q, cache) for every sequence.
+// Above one token per sequence, qkv may be the q/k/v GEMM's split partials
+// (qkv_splits > 1, linear_deferred), which the RoPE then adds itself.
 int attention(fh_device *d, const fh_llama_model &m, const fh_llama_layer &L, int64_t seq_tokens,
-              const uint32_t *positions) {
+              const uint32_t *positions, uint32_t qkv_splits) {
     if (seq_tokens == 1)
         return fh_decode_attention(d, m.qkv, m.batch, m.n_heads, m.n_kv_heads, m.head_dim, m.cos_tab, m.sin_tab,
                                    m.max_len, positions, L.k_cache, L.v_cache, m.max_len, m.scale,
@@ -179,8 +185,11 @@ int attention(fh_device *d, const fh_llama_model &m, const fh_llama_layer &L, in
     for (int64_t sq = 0; sq < m.batch; ++sq) {
         const int64_t r0 = sq * seq_tokens;
         uint16_t *kc = L.k_cache + sq * seq_cache, *vc = L.v_cache + sq * seq_cache;
-        FH_TRY(fh_rope_kv(d, m.qkv + r0 * qkv_n, seq_tokens, m.n_heads, m.n_kv_heads, m.head_dim, m.cos_tab,
-                          m.sin_tab, m.max_len, positions + r0, kc, vc, m.max_len, m.q + r0 * hq));
+        const float *part = qkv_splits > 1 ? static_cast<const float *>(d->partial_area) + r0 * qkv_n : nullptr;
+        FH_TRY(fh::rope_kv(d, "fh_llama_forward", m.qkv + r0 * qkv_n, part, qkv_splits,
+                           static_cast<uint64_t>(m.batch * seq_tokens * qkv_n), seq_tokens, m.n_heads, m.n_kv_heads,
+                           m.head_dim, m.cos_tab, m.sin_tab, m.max_len, positions + r0, kc, vc, m.max_len,
+                           m.q + r0 * hq));
         FH_TRY(fh_attention(d, m.q + r0 * hq, kc, vc, positions + r0, seq_tokens, m.n_heads, m.n_kv_heads,
                             m.head_dim, m.max_len, m.scale, m.attn_workspace, m.attn_workspace_bytes,
                             m.attn + r0 * hq));
@@ -210,16 +219,21 @@ extern "C" int fh_llama_forward(fh_device *dev, const fh_llama_model *model, int
     uint32_t pending_splits = 1;  // above 8 rows: K splits of the GEMM behind pending
     for (int64_t l = 0; l < m.n_layers; ++l) {
         const fh_llama_layer &L = m.layers[l];
+        uint32_t qkv_splits = 1;
         if (!fused) {
             FH_TRY(add_norm(dev, m, tokens, pending, pending_splits, L.input_norm));
-            FH_TRY(linear(dev, m.x, tokens, m.hidden, L.qkv, m.qkv));
+            // one token per sequence: fh_decode_attention reads qkv itself
+            if (seq_tokens > 1)
+                FH_TRY(linear_deferred(dev, m.x, tokens, m.hidden, L.qkv, m.qkv, &qkv_splits));
+            else
+                FH_TRY(linear(dev, m.x, tokens, m.hidden, L.qkv, m.qkv));
         } else if (pending == nullptr) {
             FH_TRY(linear_norm(dev, m, h, nullptr, nullptr, L.input_norm, tokens, L.qkv, m.qkv));
         } else {
             FH_TRY(linear_norm(dev, m, pending, h, h_alt, L.input_norm, tokens, L.qkv, m.qkv));
             std::swap(h, h_alt);
         }
-        FH_TRY(attention(dev, m, L, seq_tokens, positions));
+        FH_TRY(attention(dev, m, L, seq_tokens, positions, qkv_splits));
         if (!fused) {
             // o, then h += o and x = rms_norm(h); gate/up and SiLU; down (its
             // output is added by the next RMSNorm)

@@ -130,11 +130,19 @@ __global__ __launch_bounds__(kNormThreads) void rms_norm_kernel(const uint16_t *
 // x' = RNE(RNE(x * cos) + RNE(rot * sin)), rot = cat(-x2, x1). A thread
 // handles 8 consecutive dims (16-byte loads); its rotation partner is the
 // matching 8 dims of the other half (head_dim is a multiple of 16).
+// With part, the qkv values are formed from the f32 partials of the q/k/v
+// GEMM (split_sum8; row t at part + t * width), which stands in for its reduce.
+__device__ __forceinline__ uint4 qkv_piece(const uint16_t *row, const float *part, uint32_t splits, uint64_t stride,
+                                           uint64_t row0, uint32_t e) {
+    return part ? split_sum8(part, splits, stride, row0 + e) : *reinterpret_cast<const uint4 *>(row + e);
+}
+
 __global__ __launch_bounds__(256) void rope_kv_kernel(
     const uint16_t *__restrict__ qkv, uint32_t n_heads, uint32_t n_kv, uint32_t head_dim,
     const uint16_t *__restrict__ cos_tab, const uint16_t *__restrict__ sin_tab, uint32_t table_len,
     const uint32_t *__restrict__ positions, uint16_t *__restrict__ k_cache,
-    uint16_t *__restrict__ v_cache, uint32_t max_len, uint16_t *__restrict__ q_out) {
+    uint16_t *__restrict__ v_cache, uint32_t max_len, uint16_t *__restrict__ q_out,
+    const float *__restrict__ part, uint32_t splits, uint64_t part_stride) {
     const uint32_t t = blockIdx.x;
     const uint32_t pos = positions[t];
     // positions are device data the host cannot check: a position outside the
@@ -146,9 +154,15 @@ __global__ __launch_bounds__(256) void rope_kv_kernel(
     const uint16_t *s = sin_tab + static_cast<uint64_t>(pos) * head_dim;
     const uint32_t ppw = head_dim / 8, hp = ppw / 2;  // pieces per head, per half
     const uint32_t rot_pieces = (n_heads + n_kv) * ppw;
+    const uint64_t row0 = static_cast<uint64_t>(t) * width;
     for (uint32_t i = threadIdx.x; i < rot_pieces; i += blockDim.x) {
         const uint32_t h = i / ppw, p = i % ppw;
-        const uint4 ov = rope_piece(row + h * head_dim, c, s, p, hp);
+        const uint32_t partner = p < hp ? p + hp : p - hp;
+        const uint4 ov = part ? rope_apply(qkv_piece(row, part, splits, part_stride, row0, h * head_dim + p * 8),
+                                           qkv_piece(row, part, splits, part_stride, row0, h * head_dim + partner * 8),
+                                           *reinterpret_cast<const uint4 *>(c + p * 8),
+                                           *reinterpret_cast<const uint4 *>(s + p * 8), p < hp)
+                              : rope_piece(row + h * head_dim, c, s, p, hp);
         if (h < n_heads)
             *reinterpret_cast<uint4 *>(q_out + (static_cast<uint64_t>(t) * n_heads + h) * head_dim + p * 8) = ov;
         else
@@ -158,7 +172,7 @@ __global__ __launch_bounds__(256) void rope_kv_kernel(
     for (uint32_t i = threadIdx.x; i < n_kv * ppw; i += blockDim.x) {
         const uint32_t kh = i / ppw, p = i % ppw;
         *reinterpret_cast<uint4 *>(v_cache + (static_cast<uint64_t>(kh) * max_len + pos) * head_dim + p * 8) =
-            *reinterpret_cast<const uint4 *>(vrow + i * 8);
+            qkv_piece(vrow, part, splits, part_stride, row0 + rot_pieces * 8, i * 8);
     }
 }
 
@@ -346,12 +360,15 @@ extern "C" int fh_rms_norm(fh_device *dev, const uint16_t *x, const uint16_t *re
     });
 }
 
-extern "C" int fh_rope_kv(fh_device *dev, const uint16_t *qkv, int64_t tokens, int64_t n_heads,
-                          int64_t n_kv, int64_t head_dim, const uint16_t *cos_tab,
-                          const uint16_t *sin_tab, int64_t table_len, const uint32_t *positions,
-                          uint16_t *k_cache, uint16_t *v_cache, int64_t max_len,
-                          uint16_t *q_out) {
-    const char *fn = "fh_rope_kv";
+namespace fh {
+
+// fh_rope_kv, its qkv either bf16 (part null) or the f32 partials of a GEMM
+// split over K: `splits` slices [tokens][width] that are part_stride floats
+// apart inside the device's partial area.
+int rope_kv(fh_device *dev, const char *fn, const uint16_t *qkv, const float *part, uint32_t splits,
+            uint64_t part_stride, int64_t tokens, int64_t n_heads, int64_t n_kv, int64_t head_dim,
+            const uint16_t *cos_tab, const uint16_t *sin_tab, int64_t table_len, const uint32_t *positions,
+            uint16_t *k_cache, uint16_t *v_cache, int64_t max_len, uint16_t *q_out) {
     if (int rc = check_usable(dev, fn)) return rc;
     if (int rc = fh_check_dims(fn, {tokens, n_heads, n_kv, head_dim, table_len, max_len})) return rc;
     if (tokens == 0) return FH_OK;
@@ -364,7 +381,14 @@ extern "C" int fh_rope_kv(fh_device *dev, const uint16_t *qkv, int64_t tokens, i
         if (reinterpret_cast<uintptr_t>(p) % 16 != 0)
             return fail(FH_ERR_INVALID_ARGUMENT, "%s: operands must be 16-byte aligned", fn);
     const uint64_t width = static_cast<uint64_t>(n_heads + 2 * n_kv) * head_dim;
-    if (int rc = check_range(dev, qkv, tokens * width * 2, fn, "qkv")) return rc;
+    if (part == nullptr) {
+        if (int rc = check_range(dev, qkv, tokens * width * 2, fn, "qkv")) return rc;
+    } else {
+        const uintptr_t area = reinterpret_cast<uintptr_t>(dev->partial_area), at = reinterpret_cast<uintptr_t>(part);
+        if (splits < 2 || splits > kMaxGemmSplits || part_stride < tokens * width || at < area || at % 16 != 0 ||
+            (at - area) / 4 + (splits - 1) * part_stride + tokens * width > kPartialAreaBytes / 4)
+            return fail(FH_ERR_INVALID_ARGUMENT, "%s: split partials outside the device's partial area", fn);
+    }
     if (int rc = check_range(dev, cos_tab, static_cast<uint64_t>(table_len) * head_dim * 2, fn, "cos")) return rc;
     if (int rc = check_range(dev, sin_tab, static_cast<uint64_t>(table_len) * head_dim * 2, fn, "sin")) return rc;
     if (int rc = check_range(dev, positions, static_cast<uint64_t>(tokens) * 4, fn, "positions")) return rc;
@@ -378,8 +402,19 @@ extern "C" int fh_rope_kv(fh_device *dev, const uint16_t *qkv, int64_t tokens, i
                            dev->stream, qkv, static_cast<uint32_t>(n_heads),
                            static_cast<uint32_t>(n_kv), static_cast<uint32_t>(head_dim), cos_tab,
                            sin_tab, static_cast<uint32_t>(table_len), positions, k_cache, v_cache,
-                           static_cast<uint32_t>(max_len), q_out);
+                           static_cast<uint32_t>(max_len), q_out, part, splits, part_stride);
     });
+}
+
+}  // namespace fh
+
+extern "C" int fh_rope_kv(fh_device *dev, const uint16_t *qkv, int64_t tokens, int64_t n_heads,
+                          int64_t n_kv, int64_t head_dim, const uint16_t *cos_tab,
+                          const uint16_t *sin_tab, int64_t table_len, const uint32_t *positions,
+                          uint16_t *k_cache, uint16_t *v_cache, int64_t max_len,
+                          uint16_t *q_out) {
+    return fh::rope_kv(dev, "fh_rope_kv", qkv, nullptr, 1u, 0u, tokens, n_heads, n_kv, head_dim, cos_tab, sin_tab,
+                       table_len, positions, k_cache, v_cache, max_len, q_out);
 }
 
 extern "C" int fh_silu_mul(fh_device *dev, const uint16_t *gate_up, int64_t rows, int64_t f,

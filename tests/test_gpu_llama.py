@@ -454,7 +454,8 @@ def test_llama_forward_checks_the_model_first(device):
 
 def _op_by_op_forward(model, seq_tokens):
     """The forward above 8 rows as separate C-ABI ops on the model's own
-    buffers: the sequence fh_llama_forward stands for."""
+    buffers: the sequence fh_llama_forward stands for (one token per
+    sequence: fh_decode_attention)."""
     c, d, b, P, call = model.cfg, model.dev.handle, model.buf, model._p, _lib.call
     tokens, hq, eps = model.batch * seq_tokens, c.n_heads * c.head_dim, ctypes.c_float(c.rms_norm_eps)
 
@@ -473,7 +474,7 @@ def _op_by_op_forward(model, seq_tokens):
     for L in model.layers:
         norm(pending, L["input_norm"])
         lin(b["x"], tokens, L["qkv"], b["qkv"])
-        for sq in range(model.batch):
+        for sq in range(model.batch if seq_tokens > 1 else 0):
             r0, cache = sq * seq_tokens, sq * model.seq_bytes
             call("fh_rope_kv", d, P(b["qkv"], r0 * c.qkv_rows * 2), seq_tokens, c.n_heads, c.n_kv_heads, c.head_dim,
                  P(model.cos), P(model.sin), model.max_len, P(b["positions"], r0 * 4), P(L["k_cache"], cache),
@@ -481,6 +482,10 @@ def _op_by_op_forward(model, seq_tokens):
             call("fh_attention", d, P(b["q"], r0 * hq * 2), P(L["k_cache"], cache), P(L["v_cache"], cache),
                  P(b["positions"], r0 * 4), seq_tokens, c.n_heads, c.n_kv_heads, c.head_dim, model.max_len,
                  ctypes.c_float(model.scale), P(model.attn_ws), model.attn_ws_bytes, P(b["attn"], r0 * hq * 2))
+        if seq_tokens == 1:
+            call("fh_decode_attention", d, P(b["qkv"]), model.batch, c.n_heads, c.n_kv_heads, c.head_dim,
+                 P(model.cos), P(model.sin), model.max_len, P(b["positions"]), P(L["k_cache"]), P(L["v_cache"]),
+                 model.max_len, ctypes.c_float(model.scale), P(model.dec_ws), model.dec_ws_bytes, P(b["attn"]))
         lin(b["attn"], tokens, L["o"], b["o"])
         norm(b["o"], L["post_norm"])
         lin(b["x"], tokens, L["gate_up"], b["gu"])
@@ -493,17 +498,18 @@ def _op_by_op_forward(model, seq_tokens):
     call("fh_argmax", d, P(b["logits"]), model.batch, c.vocab, P(b["next"]))
 
 
-# hidden 512 and FFN 1024: the o, gate/up and down GEMMs of these row counts
-# split K (2, 2 and 4 splits), so fh_llama_forward's norms and SiLU form
-# their inputs from the partials
+# hidden 512 and FFN 1024: the q/k/v, o, gate/up and down GEMMs of these row
+# counts split K (2, 2, 2 and 4 splits), so fh_llama_forward's RoPE, norms
+# and SiLU form their inputs from the partials
 SPLIT = LlamaConfig(n_layers=2, hidden=512, n_heads=8, n_kv_heads=2, head_dim=64, ffn=1024, vocab=1000)
 
 
-@pytest.mark.parametrize("batch,t", [(2, 20), (1, 300)])
+@pytest.mark.parametrize("batch,t", [(2, 20), (1, 300), (12, 1)])
 def test_llama_forward_equals_the_op_sequence(device, batch, t):
-    """fh_llama_forward above 8 rows (split GEMMs feeding the norms and
-    SiLU) gives bit-identical logits, hidden states and next ids to the
-    same forward issued op by op."""
+    """fh_llama_forward above 8 rows (split GEMMs feeding the RoPE, norms
+    and SiLU; 12 sequences of one token: unfused ops around the decode
+    attention) gives bit-identical logits, hidden states and next ids to
+    the same forward issued op by op."""
     model = Q4Llama(device, SPLIT, 5, 512, max_tokens=t, batch=batch)
     b, c = model.buf, SPLIT
     ids = synth.token_ids(11, batch * t, c.vocab).reshape(batch, t)
