@@ -201,7 +201,7 @@ def bench_decode(dev, new_tokens: int, agreement: int, seed: int = 0):
     build_s = time.perf_counter() - t0
     # one untimed run of the same prompt first, as the reference's bench runs
     # whole warm-up runs before its measured ones (src/bench/mod.rs:157-170)
-    model.generate(prompt, 4)
+    model.generate(prompt, min(4, max_len - len(prompt)))
     gc.collect()
     dev.timer_begin()
     model.prefill(prompt)
