@@ -359,9 +359,14 @@ typedef struct fh_llama_model {
  * the ops above one by one: up to 8 rows the RMSNorms, residual adds and SiLU
  * go inside the GEMVs and one new token's RoPE and cache write inside
  * fh_decode_attention; above 8 rows the unfused ops run, and prefill
- * attention runs one sequence at a time. The operands are checked before
- * any work is issued; every op checks its own ranges as it runs. May be
- * captured (fh_capture_begin). 1 <= seq_tokens <= max_tokens. */
+ * attention runs one sequence at a time. Above 8 rows a GEMM that splits K
+ * passes its f32 partials (the device's partial area) to the RoPE, RMSNorm
+ * or SiLU after it, which adds them in the order of the GEMM's own reduce:
+ * the results are bit-identical to the op sequence, but the buffers o,
+ * gate_up and (seq_tokens > 1) qkv are then not written. The weight shapes
+ * are checked against the config before any work is issued; every op checks
+ * its own ranges as it runs. May be captured (fh_capture_begin).
+ * 1 <= seq_tokens <= max_tokens. */
 int fh_llama_forward(fh_device *dev, const fh_llama_model *model, int64_t seq_tokens,
                      const uint32_t *ids, const uint32_t *positions, uint32_t *next);
 
