@@ -306,6 +306,69 @@ __global__ void advance_kernel(uint32_t *__restrict__ p, uint32_t n, uint32_t by
     if (i < n) p[i] += by;
 }
 
+// Long aligned rows take two passes: kArgmaxSegs blocks per row each reduce
+// one segment to (value bits, index) in the device's partial area, then one
+// wavefront per row picks the winner among the segments. (max, lowest index)
+// orders all non-NaN values totally, so the winner is the one-block kernel's;
+// NaN is never taken, and a row of NaN gives index 0 in both.
+constexpr uint32_t kArgmaxSegs = 64;
+constexpr int kArgmaxSegThreads = 256;
+constexpr uint32_t kArgmaxTwoPassMinN = 16384;
+
+__global__ __launch_bounds__(kArgmaxSegThreads) void argmax_seg_kernel(const uint16_t *__restrict__ x, uint32_t n,
+                                                                       uint32_t seg_pieces, uint2 *__restrict__ part) {
+    __shared__ float bv[kArgmaxSegThreads / 64];
+    __shared__ uint32_t bi[kArgmaxSegThreads / 64];
+    const uint16_t *row = x + static_cast<uint64_t>(blockIdx.y) * n;
+    const uint32_t pieces = n / 8, p0 = blockIdx.x * seg_pieces;
+    const uint32_t p1 = p0 + seg_pieces < pieces ? p0 + seg_pieces : pieces;
+    float best = -INFINITY;
+    uint32_t idx = 0xFFFFFFFFu;
+    for (uint32_t p = p0 + threadIdx.x; p < p1; p += kArgmaxSegThreads) {
+        const uint4 v = *reinterpret_cast<const uint4 *>(row + static_cast<uint64_t>(p) * 8);
+        const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            take_max(best, idx, bf(w[e] & 0xFFFFu), p * 8 + 2 * e);
+            take_max(best, idx, bf(w[e] >> 16), p * 8 + 2 * e + 1);
+        }
+    }
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) {
+        const float ov = __shfl_xor(best, off, 64);
+        const uint32_t oi = __shfl_xor(idx, off, 64);
+        take_max(best, idx, ov, oi);
+    }
+    const uint32_t wave = threadIdx.x >> 6;
+    if ((threadIdx.x & 63) == 0) {
+        bv[wave] = best;
+        bi[wave] = idx;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        for (int w = 1; w < kArgmaxSegThreads / 64; ++w) take_max(best, idx, bv[w], bi[w]);
+        if (idx == 0xFFFFFFFFu) best = -INFINITY;
+        part[static_cast<uint64_t>(blockIdx.y) * gridDim.x + blockIdx.x] = make_uint2(__float_as_uint(best), idx);
+    }
+}
+
+__global__ __launch_bounds__(64) void argmax_join_kernel(const uint2 *__restrict__ part, uint32_t segs,
+                                                         uint32_t *__restrict__ out) {
+    float best = -INFINITY;
+    uint32_t idx = 0xFFFFFFFFu;
+    for (uint32_t sg = threadIdx.x; sg < segs; sg += 64) {
+        const uint2 p = part[static_cast<uint64_t>(blockIdx.x) * segs + sg];
+        take_max(best, idx, __uint_as_float(p.x), p.y);
+    }
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) {
+        const float ov = __shfl_xor(best, off, 64);
+        const uint32_t oi = __shfl_xor(idx, off, 64);
+        take_max(best, idx, ov, oi);
+    }
+    if (threadIdx.x == 0) out[blockIdx.x] = idx == 0xFFFFFFFFu ? 0u : idx;
+}
+
 // Launches for a consumer that stands in for a split GEMM's reduce (part:
 // [splits][rows][width] f32, the operands checked by the caller).
 void launch_rms_norm_partials(hipStream_t stream, const float *part, uint32_t splits, const uint16_t *res,
@@ -444,6 +507,20 @@ extern "C" int fh_argmax(fh_device *dev, const uint16_t *x, int64_t rows, int64_
     if (int rc = check_range(dev, x, static_cast<uint64_t>(rows) * n * 2, fn, "x")) return rc;
     if (int rc = check_range(dev, out, static_cast<uint64_t>(rows) * 4, fn, "out")) return rc;
     if (int rc = set_current(dev, fn)) return rc;
+    const bool two_pass = n >= kArgmaxTwoPassMinN && n % 8 == 0 && (reinterpret_cast<uintptr_t>(x) & 15u) == 0 &&
+                          rows <= 65535 && dev->partial_area != nullptr &&
+                          static_cast<uint64_t>(rows) * kArgmaxSegs * sizeof(uint2) <= kPartialAreaBytes;
+    if (two_pass) {
+        const uint32_t pieces = static_cast<uint32_t>(n / 8);
+        const uint32_t seg_pieces = (pieces + kArgmaxSegs - 1) / kArgmaxSegs;
+        uint2 *part = static_cast<uint2 *>(dev->partial_area);
+        return dispatch(dev, fn, [&] {
+            hipLaunchKernelGGL(argmax_seg_kernel, dim3(kArgmaxSegs, static_cast<uint32_t>(rows)),
+                               dim3(kArgmaxSegThreads), 0, dev->stream, x, static_cast<uint32_t>(n), seg_pieces, part);
+            hipLaunchKernelGGL(argmax_join_kernel, dim3(static_cast<uint32_t>(rows)), dim3(64), 0, dev->stream,
+                               static_cast<const uint2 *>(part), kArgmaxSegs, out);
+        });
+    }
     return dispatch(dev, fn, [&] {
         hipLaunchKernelGGL(argmax_kernel, dim3(static_cast<uint32_t>(rows)), dim3(kArgmaxThreads), 0,
                            dev->stream, x, static_cast<uint32_t>(n), out);

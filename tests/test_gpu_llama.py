@@ -345,6 +345,39 @@ def test_argmax_long_rows(device, n):
     assert got.tolist() == [R.argmax(R.from_bf16(x[0])), R.argmax(R.from_bf16(x[1]))] == [17, n - 1]
 
 
+def test_argmax_two_pass_segments(device):
+    """Rows of 16384 values or more (aligned, n % 8 == 0) take the two-pass
+    form (64 segments, then a join): ties in different segments, ties inside
+    one, NaN beside a finite maximum, all NaN and all -inf rows give the
+    one-block kernel's answers (the n = 16376 rows run that kernel)."""
+    n = 128256
+    x = synth.bf16_normal(12, (6, n))
+    x[0, [70000, 5000, 126000]] = 0x4400  # tied across segments: 5000
+    x[1, [2009, 2010]] = 0x4400  # tied inside a segment: 2009
+    x[2, ::3] = 0x7FC0  # NaN is never the maximum
+    x[2, 99999] = 0x4480
+    x[3, :] = 0x7FC0  # all NaN: index 0
+    x[4, :] = 0xFF80  # all -inf: index 0
+    x[5, n - 1] = 0x4480  # the last value
+    out = device.empty(6 * 4)
+    got = []
+    for width in (n, 16376):
+        s = up(device, np.ascontiguousarray(x[:, :width]))
+        _lib.call("fh_argmax", device.handle, ctypes.c_void_p(s.ptr), 6, width, ctypes.c_void_p(out.ptr))
+        got.append(down(device, out, np.uint32, 6).tolist())
+    assert got[0] == [5000, 2009, 99999, 0, 0, n - 1]
+
+    def expected(row):
+        v = R.from_bf16(row).astype(np.float32)
+        if np.isnan(v).all():
+            return 0
+        v[np.isnan(v)] = -np.inf  # NaN is never taken
+        return R.argmax(v)
+
+    assert got[1] == [expected(r) for r in x[:, :16376]]
+    assert got[1][:2] == [5000, 2009] and got[1][3:5] == [0, 0]
+
+
 def _ref_model(cfg, seed, max_len):
     layers = [layer_weights(cfg, seed, l) for l in range(cfg.n_layers)]
     return R.RefLlama(cfg, embed_weights(cfg, seed), layers, final_norm_weight(cfg, seed), max_len)
