@@ -53,6 +53,8 @@ int check_range(const fh_device *dev, const void *ptr, uint64_t nbytes, const ch
         return fail(FH_ERR_OUT_OF_BOUNDS,
                     "%s: %s needs %llu bytes but its allocation has %llu past the pointer", fn,
                     what, (unsigned long long)nbytes, (unsigned long long)(size - (p - base)));
+    // a graph being captured retains every allocation its ops touch
+    if (dev->capturing) dev->capture_bases.insert(base);
     return FH_OK;
 }
 
@@ -94,6 +96,73 @@ void record_profile_end(fh_device *dev, hipEvent_t begin) {
     }
     // STEPS: one interval opened by the first dispatch, closed at take time
     dev->intervals.emplace_back(begin, nullptr);
+}
+
+// 16 bytes per thread: one 16-byte store where the piece is whole and
+// aligned, byte stores at an unaligned head or a ragged tail.
+__global__ __launch_bounds__(256) void zero_fill_kernel(uint8_t *__restrict__ p, uint64_t n) {
+    const uint64_t i = (static_cast<uint64_t>(blockIdx.x) * 256 + threadIdx.x) * 16;
+    if (i >= n) return;
+    if (i + 16 <= n && (reinterpret_cast<uintptr_t>(p + i) & 15) == 0) {
+        *reinterpret_cast<uint4 *>(p + i) = make_uint4(0, 0, 0, 0);
+        return;
+    }
+    for (uint64_t j = i; j < i + 16 && j < n; ++j) p[j] = 0;
+}
+
+int zero_fill(fh_device *dev, const char *fn, void *ptr, uint64_t nbytes) {
+    if (nbytes == 0) return FH_OK;
+    const uint64_t blocks = (nbytes + 16 * 256 - 1) / (16 * 256);
+    if (blocks > 0x7FFFFFFFull) return fail(FH_ERR_INDEX_TOO_LARGE, "%s: fill of %llu bytes", fn,
+                                            static_cast<unsigned long long>(nbytes));
+    return dispatch(dev, fn, [&] {
+        hipLaunchKernelGGL(zero_fill_kernel, dim3(static_cast<uint32_t>(blocks)), dim3(256), 0, dev->stream,
+                           static_cast<uint8_t *>(ptr), nbytes);
+    });
+}
+
+// Frees an allocation that is no longer in dev->allocs and that no live graph
+// uses, after the work queued on the stream ends.
+static hipError_t release(fh_device *dev, uintptr_t base, size_t size) {
+    hipError_t err = hipStreamSynchronize(dev->stream);
+    hipError_t ferr = hipFree(reinterpret_cast<void *>(base));
+    dev->live_bytes -= size;
+    return err != hipSuccess ? err : ferr;
+}
+
+// Drops one graph's hold on each of its allocations; frees those the caller
+// already released once no graph uses them.
+static hipError_t drop_graph_refs(fh_device *dev, const fh_graph *g) {
+    hipError_t first = hipSuccess;
+    for (uintptr_t base : g->bases) {
+        auto r = dev->graph_refs.find(base);
+        if (r == dev->graph_refs.end()) continue;
+        if (--r->second > 0) continue;
+        dev->graph_refs.erase(r);
+        auto z = dev->retired.find(base);
+        if (z == dev->retired.end()) continue;
+        const size_t size = z->second;
+        dev->retired.erase(z);
+        hipError_t err = release(dev, base, size);
+        if (first == hipSuccess) first = err;
+    }
+    return first;
+}
+
+// fh_free outside capture: a retained allocation is retired (no longer
+// usable by ops, freed with its last graph), any other one freed now.
+static int free_now(fh_device *dev, std::map<uintptr_t, size_t>::iterator it, const char *fn) {
+    const uintptr_t base = it->first;
+    const size_t size = it->second;
+    dev->allocs.erase(it);
+    if (dev->graph_refs.count(base)) {
+        dev->retired[base] = size;
+        return FH_OK;
+    }
+    hipSetDevice(dev->ordinal);
+    hipError_t err = release(dev, base, size);
+    if (err != hipSuccess) return device_error(dev, err, fn, "hipStreamSynchronize/hipFree");
+    return FH_OK;
 }
 
 static void note_allocation(fh_device *dev, uint64_t nbytes) {
@@ -168,6 +237,9 @@ static int create(int ordinal, int mode, fh_device **out, const char *fn) {
         return fail(FH_ERR_ALLOCATION, "%s: the device's %llu-byte work areas could not be allocated", fn,
                     static_cast<unsigned long long>(kPackAreaBytes + kPartialAreaBytes));
     }
+    // the work areas are device memory the ops use: counted in the peaks
+    dev->live_bytes = kPackAreaBytes + kPartialAreaBytes;
+    dev->peak_bytes = dev->run_peak_bytes = dev->live_bytes;
     *out = dev;
     return FH_OK;
 }
@@ -189,7 +261,10 @@ int fh_device_destroy(fh_device *dev) {
         if (g) hipGraphDestroy(g);
     }
     hipError_t err = hipStreamSynchronize(dev->stream);
+    // graphs outlive their device only as handles: they can no longer launch
+    for (fh_graph *g : dev->graphs) g->dev = nullptr;
     for (auto &kv : dev->allocs) hipFree(reinterpret_cast<void *>(kv.first));
+    for (auto &kv : dev->retired) hipFree(reinterpret_cast<void *>(kv.first));
     hipFree(dev->pack_area);
     hipFree(dev->partial_area);
     for (auto &iv : dev->intervals) {
@@ -260,19 +335,17 @@ int fh_free(fh_device *dev, void *ptr) {
     const char *fn = "fh_free";
     if (!dev) return fail(FH_ERR_INVALID_ARGUMENT, "%s: device is null", fn);
     if (!ptr) return FH_OK;
-    if (dev->capturing) return fail(FH_ERR_CAPTURE, "%s: cannot free while capturing", fn);
     auto it = dev->allocs.find(reinterpret_cast<uintptr_t>(ptr));
     if (it == dev->allocs.end())
         return fail(FH_ERR_FOREIGN_STORAGE, "%s: pointer is not an allocation of this device", fn);
-    hipSetDevice(dev->ordinal);
-    // queued work may still read the buffer
-    hipError_t err = hipStreamSynchronize(dev->stream);
-    dev->live_bytes -= it->second;
-    dev->allocs.erase(it);
-    hipError_t ferr = hipFree(ptr);
-    if (err != hipSuccess) return device_error(dev, err, fn, "hipStreamSynchronize");
-    if (ferr != hipSuccess) return device_error(dev, ferr, fn, "hipFree");
-    return FH_OK;
+    if (dev->capturing) {
+        // the capture may already use it: decided at fh_capture_end
+        for (void *q : dev->deferred_frees)
+            if (q == ptr) return FH_OK;
+        dev->deferred_frees.push_back(ptr);
+        return FH_OK;
+    }
+    return free_now(dev, it, fn);
 }
 
 int fh_upload(fh_device *dev, void *dst, const void *src, size_t nbytes) {
@@ -391,8 +464,28 @@ int fh_capture_begin(fh_device *dev) {
     hipError_t err = hipStreamBeginCapture(dev->stream, hipStreamCaptureModeThreadLocal);
     if (err != hipSuccess) return device_error(dev, err, fn, "hipStreamBeginCapture");
     dev->capturing = true;
+    dev->capture_bases.clear();
     return FH_OK;
 }
+
+namespace {
+
+// Carries out the frees asked for during a capture that has just ended
+// (after the new graph, if any, took its references).
+int run_deferred_frees(fh_device *dev, const char *fn) {
+    std::vector<void *> pending;
+    pending.swap(dev->deferred_frees);
+    int rc = FH_OK;
+    for (void *p : pending) {
+        auto it = dev->allocs.find(reinterpret_cast<uintptr_t>(p));
+        if (it == dev->allocs.end()) continue;
+        const int r = free_now(dev, it, fn);
+        if (rc == FH_OK) rc = r;
+    }
+    return rc;
+}
+
+}  // namespace
 
 int fh_capture_end(fh_device *dev, fh_graph **out) {
     const char *fn = "fh_capture_end";
@@ -404,14 +497,21 @@ int fh_capture_end(fh_device *dev, fh_graph **out) {
     hipGraph_t graph = nullptr;
     hipError_t err = hipStreamEndCapture(dev->stream, &graph);
     dev->capturing = false;
-    if (err != hipSuccess) return device_error(dev, err, fn, "hipStreamEndCapture");
+    std::set<uintptr_t> bases;
+    bases.swap(dev->capture_bases);
+    if (err != hipSuccess) {
+        run_deferred_frees(dev, fn);
+        return device_error(dev, err, fn, "hipStreamEndCapture");
+    }
     if (dev->failed) {
         if (graph) hipGraphDestroy(graph);
+        run_deferred_frees(dev, fn);
         return fail(FH_ERR_FAILED, "%s: a launch failed during capture", fn);
     }
     fh_graph *g = new (std::nothrow) fh_graph();
     if (!g) {
         hipGraphDestroy(graph);
+        run_deferred_frees(dev, fn);
         return fail(FH_ERR_ALLOCATION, "%s: out of host memory", fn);
     }
     g->graph = graph;
@@ -420,17 +520,22 @@ int fh_capture_end(fh_device *dev, fh_graph **out) {
     if (err != hipSuccess) {
         hipGraphDestroy(graph);
         delete g;
+        run_deferred_frees(dev, fn);
         return device_error(dev, err, fn, "hipGraphInstantiate");
     }
+    g->dev = dev;
+    g->bases.assign(bases.begin(), bases.end());
+    for (uintptr_t b : g->bases) dev->graph_refs[b] += 1;
+    dev->graphs.insert(g);
     *out = g;
-    return FH_OK;
+    return run_deferred_frees(dev, fn);
 }
 
 int fh_graph_launch(fh_device *dev, fh_graph *graph) {
     const char *fn = "fh_graph_launch";
     if (int rc = check_usable(dev, fn)) return rc;
     if (!graph) return fail(FH_ERR_INVALID_ARGUMENT, "%s: graph is null", fn);
-    if (graph->ordinal != dev->ordinal)
+    if (graph->dev != dev)
         return fail(FH_ERR_FOREIGN_STORAGE, "%s: graph was captured on another device", fn);
     if (dev->capturing) return fail(FH_ERR_CAPTURE, "%s: the device is capturing", fn);
     if (int rc = set_current(dev, fn)) return rc;
@@ -438,11 +543,23 @@ int fh_graph_launch(fh_device *dev, fh_graph *graph) {
 }
 
 int fh_graph_destroy(fh_graph *graph) {
+    const char *fn = "fh_graph_destroy";
     if (!graph) return FH_OK;
     hipSetDevice(graph->ordinal);
+    fh_device *dev = graph->dev;
+    // a replay still queued on the stream reads the exec's nodes and the
+    // allocations it retains: let it finish first
+    hipError_t err = dev ? hipStreamSynchronize(dev->stream) : hipSuccess;
     if (graph->exec) hipGraphExecDestroy(graph->exec);
     if (graph->graph) hipGraphDestroy(graph->graph);
+    hipError_t rerr = hipSuccess;
+    if (dev) {
+        dev->graphs.erase(graph);
+        rerr = drop_graph_refs(dev, graph);
+    }
     delete graph;
+    if (err != hipSuccess) return device_error(dev, err, fn, "hipStreamSynchronize");
+    if (rerr != hipSuccess) return device_error(dev, rerr, fn, "hipFree");
     return FH_OK;
 }
 

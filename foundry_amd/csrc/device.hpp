@@ -7,6 +7,7 @@
 #include <cstdarg>
 #include <cstdint>
 #include <map>
+#include <set>
 #include <string>
 #include <utility>
 #include <vector>
@@ -25,6 +26,11 @@ struct fh_graph {
     hipGraph_t graph = nullptr;
     hipGraphExec_t exec = nullptr;
     int ordinal = 0;
+    // The device that captured it (null once that device is destroyed) and
+    // the base address of every allocation its captured ops touched: the
+    // graph retains them, so none is freed while the graph can replay.
+    fh_device *dev = nullptr;
+    std::vector<uintptr_t> bases;
 };
 
 namespace fh {
@@ -55,6 +61,17 @@ struct fh_device {
     uint64_t run_peak_bytes = 0;
     bool failed = false;
     bool capturing = false;
+    // Graph lifetime. While capturing, every allocation an op's range check
+    // accepts is noted in capture_bases; fh_capture_end hands the set to the
+    // new graph and counts it in graph_refs (base -> live graphs that use
+    // it). fh_free of a retained allocation moves it to retired (base ->
+    // size), freed when its last graph is destroyed; frees asked for during
+    // capture wait in deferred_frees until fh_capture_end.
+    mutable std::set<uintptr_t> capture_bases;
+    std::map<uintptr_t, uint32_t> graph_refs;
+    std::map<uintptr_t, size_t> retired;
+    std::vector<void *> deferred_frees;
+    std::set<fh_graph *> graphs;
     int profile_mode = FH_PROFILE_OFF;
     fh_profile counters{};
     // per-dispatch event pairs (KERNELS mode) or the span of a step (STEPS)
@@ -85,6 +102,10 @@ int device_error(fh_device *dev, hipError_t err, const char *fn, const char *cal
 // checks the launch status, and counts the dispatch.
 template <typename Launch>
 int dispatch(fh_device *dev, const char *fn, Launch &&launch);
+
+// Writes nbytes of zeros at ptr on the device's stream with a kernel (not
+// hipMemsetAsync: a captured memset node is not reliable on replay).
+int zero_fill(fh_device *dev, const char *fn, void *ptr, uint64_t nbytes);
 
 hipEvent_t take_event(fh_device *dev);
 void record_profile_begin(fh_device *dev, hipEvent_t *begin);

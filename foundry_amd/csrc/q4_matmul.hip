@@ -166,6 +166,8 @@ extern "C" int fh_q4_matmul(fh_device *dev, const uint16_t *x, int64_t m, int64_
     const uint64_t y_bytes = static_cast<uint64_t>(m) * n * (y_is_f32 ? 4 : 2);
     if (int rc = check_range(dev, y, y_bytes, fn, "y")) return rc;
     if (int rc = set_current(dev, fn)) return rc;
+    // an empty sum: every output is RNE(0) = 0, and no kernel may read x or W
+    if (k == 0) return zero_fill(dev, fn, y, y_bytes);
 
     const uint32_t k32 = static_cast<uint32_t>(k), n32 = static_cast<uint32_t>(n);
     const uint32_t ld32 = static_cast<uint32_t>(x_ld);
@@ -255,6 +257,8 @@ extern "C" int fh_q4_matmul_rmsnorm(fh_device *dev, const uint16_t *x, const uin
     if (int rc = check_norm_operands(dev, fn, x, residual, residual_out, norm_weight, m, k)) return rc;
     if (m == 0 || n == 0) return FH_OK;
     if (int rc = set_current(dev, fn)) return rc;
+    // empty rows: h and the normalised x are empty, y = x' W^T is zeros
+    if (k == 0) return zero_fill(dev, fn, y, static_cast<uint64_t>(m) * n * (y_dtype == FH_F32 ? 4 : 2));
     const uint32_t k32 = static_cast<uint32_t>(k), n32 = static_cast<uint32_t>(n);
     const GemvArgs a{x, k32, wq, scales, biases, n32, k32, y, n32, y_dtype == FH_F32, kProRmsNorm, kEpiNone,
                      GemvFusion{residual, residual_out, norm_weight, eps, 1.0f / static_cast<float>(k)}};
@@ -272,6 +276,8 @@ extern "C" int fh_q4_gate_up_silu(fh_device *dev, const uint16_t *x, const uint1
     if (int rc = check_norm_operands(dev, fn, x, residual, residual_out, norm_weight, m, k)) return rc;
     if (m == 0 || n == 0) return FH_OK;
     if (int rc = set_current(dev, fn)) return rc;
+    // empty rows: gate and up are zeros, and RNE(RNE(silu(0)) * 0) = 0
+    if (k == 0) return zero_fill(dev, fn, act, static_cast<uint64_t>(m) * (n / 2) * 2);
     const uint32_t k32 = static_cast<uint32_t>(k), n32 = static_cast<uint32_t>(n);
     const GemvArgs a{x, k32, wq, scales, biases, n32, k32, act, n32 / 2, 0, norm ? kProRmsNorm : kProNone,
                      kEpiSiluMul, GemvFusion{residual, residual_out, norm_weight, eps, 1.0f / static_cast<float>(k)}};

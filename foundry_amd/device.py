@@ -11,30 +11,38 @@ src/metal/mod.rs:187-200 does.
 from __future__ import annotations
 
 import ctypes
+import warnings
 from dataclasses import dataclass
 
 import numpy as np
 
 from . import _lib
-from .primitive import DType, QuantizedIndexSelect, QuantizedMatmul, TensorError, output
+from .primitive import (Binary, Cat, Copy, DType, IndexSelect, Matmul, QuantizedIndexSelect, QuantizedMatmul,
+                        Reduce, SliceScatter, TensorError, ToDtype, Unary, check_shape, output)
 
 
 class HipStorage:
     """One device allocation. Freed when the last reference drops, as the
     reference's Rc<Storage> is (src/nn/tensor.rs:49-53)."""
 
-    __slots__ = ("device", "ptr", "nbytes", "__weakref__")
+    __slots__ = ("device", "ptr", "nbytes", "views", "__weakref__")
 
     def __init__(self, device: "HipDevice", ptr: int, nbytes: int):
         self.device = device
         self.ptr = ptr
         self.nbytes = nbytes
+        self.views = 0  # live Tensor views (Rc::get_mut's uniqueness test)
 
     def __del__(self):
         dev = self.device
         if dev is not None and dev._handle and self.ptr:
-            _lib.load().fh_free(dev._handle, ctypes.c_void_p(self.ptr))
+            lib = _lib.load()
+            rc = lib.fh_free(dev._handle, ctypes.c_void_p(self.ptr))
             self.ptr = 0
+            if rc != _lib.OK:
+                # a destructor cannot raise: report the lost allocation
+                warnings.warn(f"fh_free failed ({_lib.STATUS_NAMES.get(rc, rc)}): "
+                              f"{lib.fh_last_error().decode(errors='replace')}", RuntimeWarning)
 
 
 @dataclass(frozen=True)
@@ -50,11 +58,14 @@ class Layout:
         strides, acc = [], 1
         for d in reversed(shape):
             strides.append(acc)
-            acc *= max(int(d), 1)
+            acc *= int(d)
         return Layout(tuple(int(d) for d in shape), tuple(reversed(strides)), 0)
 
     def is_contiguous(self) -> bool:
-        return self.strides == Layout.contiguous(self.shape).strides
+        """Layout::is_contiguous (src/nn/layout.rs:33-40): a dim of size one
+        may have any stride."""
+        want = Layout.contiguous(self.shape).strides
+        return all(n == 1 or st == w for n, st, w in zip(self.shape, self.strides, want))
 
     @property
     def numel(self) -> int:
@@ -62,6 +73,55 @@ class Layout:
         for d in self.shape:
             n *= d
         return n
+
+    def view(self) -> "_lib.View":
+        return _lib.View.of(self.shape, self.strides, self.offset)
+
+    def reshape(self, shape) -> "Layout":
+        """Layout::reshape (src/nn/layout.rs:42-60)."""
+        shape = check_shape(shape)
+        if not self.is_contiguous():
+            raise TensorError("ReshapeNonContiguous")
+        if Layout.contiguous(shape).numel != self.numel:
+            raise TensorError("NumelMismatch", f"{self.shape} -> {shape}")
+        c = Layout.contiguous(shape)
+        return Layout(c.shape, c.strides, self.offset)
+
+    def permute(self, dims) -> "Layout":
+        """Layout::permute (src/nn/layout.rs:62-92)."""
+        dims = tuple(int(d) for d in dims)
+        if sorted(dims) != list(range(len(self.shape))):
+            raise TensorError("InvalidPermutation", f"{dims} of rank {len(self.shape)}")
+        return Layout(tuple(self.shape[d] for d in dims), tuple(self.strides[d] for d in dims), self.offset)
+
+    def narrow(self, dim: int, start: int, length: int) -> "Layout":
+        """Layout::narrow (src/nn/layout.rs:94-130)."""
+        if not 0 <= dim < len(self.shape):
+            raise TensorError("DimOutOfRange", f"dim {dim}")
+        if start < 0 or length < 0 or start + length > self.shape[dim]:
+            raise TensorError("NarrowOutOfBounds", f"{start}+{length} of {self.shape[dim]}")
+        shape = self.shape[:dim] + (int(length),) + self.shape[dim + 1:]
+        return Layout(shape, self.strides, self.offset + start * self.strides[dim])
+
+    def expand(self, shape) -> "Layout":
+        """Layout::expand (src/nn/layout.rs:132-170): new leading dims and
+        dims of size one take stride 0."""
+        shape = check_shape(shape)
+        lead = len(shape) - len(self.shape)
+        if lead < 0:
+            raise TensorError("ExpandIncompatible", f"{self.shape} -> {shape}")
+        strides = []
+        for d, n in enumerate(shape):
+            s = d - lead
+            if s < 0:
+                strides.append(0)
+            elif self.shape[s] == n:
+                strides.append(self.strides[s])
+            elif self.shape[s] == 1:
+                strides.append(0)
+            else:
+                raise TensorError("ExpandIncompatible", f"{self.shape} -> {shape}")
+        return Layout(shape, tuple(strides), self.offset)
 
 
 @dataclass(frozen=True)
@@ -182,7 +242,7 @@ class HipDevice:
             raise _lib.HipError(_lib.ERR_FOREIGN_STORAGE, "storage was produced by another device")
 
     def run(self, op, inputs, output_shape, dtype) -> HipStorage:
-        """Runs a q4 op into fresh contiguous storage (Device::run)."""
+        """Runs an op into fresh contiguous storage (Device::run)."""
         for operand in inputs:
             self._owns(operand)
         shape, out_dtype = output(op, [(o.dtype, o.layout.shape) for o in inputs])
@@ -218,7 +278,58 @@ class HipDevice:
                       ctypes.c_void_p(s.address()), ctypes.c_void_p(b.address()), rows, shape[1],
                       op.group, ctypes.c_void_p(ids.address()), shape[0], ctypes.c_void_p(out.ptr))
             return out
-        raise _lib.HipError(_lib.ERR_INVALID_ARGUMENT, f"unsupported op {op!r}")
+        self._run_standard(op, inputs, shape, out_dtype, out)
+        return out
+
+    def _run_standard(self, op, inputs, shape, dtype, out) -> None:
+        """The reference's own Ops through the strided entry points
+        (MetalDevice::run, src/metal/mod.rs:639-695)."""
+        h, dst = self.handle, ctypes.c_void_p(out.ptr)
+
+        def base(o):
+            return ctypes.c_void_p(o.storage.ptr)
+
+        def view(o):
+            return ctypes.byref(o.layout.view())
+
+        if isinstance(op, Unary):
+            (x,) = inputs
+            _lib.call("fh_unary", h, int(op.op), int(x.dtype), base(x), view(x), dst)
+        elif isinstance(op, Binary):
+            a, b = inputs
+            _lib.call("fh_binary", h, int(op.op), int(a.dtype), base(a), view(a), base(b), view(b), dst)
+        elif isinstance(op, Reduce):
+            (x,) = inputs
+            _lib.call("fh_reduce", h, int(op.op), int(x.dtype), base(x), view(x), op.dim, dst)
+        elif isinstance(op, Matmul):
+            a, b = inputs
+            _lib.call("fh_matmul", h, int(a.dtype), base(a), view(a), base(b), view(b), dst)
+        elif isinstance(op, Copy):
+            (x,) = inputs
+            _lib.call("fh_copy_strided", h, int(x.dtype), base(x), view(x), dst)
+        elif isinstance(op, ToDtype):
+            (x,) = inputs
+            _lib.call("fh_to_dtype", h, int(x.dtype), base(x), view(x), int(dtype), dst)
+        elif isinstance(op, IndexSelect):
+            t, i = inputs
+            _lib.call("fh_index_select", h, int(t.dtype), base(t), view(t), base(i), view(i), dst)
+        elif isinstance(op, Cat):
+            a, b = inputs
+            _lib.call("fh_cat", h, int(a.dtype), op.dim, base(a), view(a), base(b), view(b), dst)
+        else:
+            raise _lib.HipError(_lib.ERR_INVALID_ARGUMENT, f"unsupported op {op!r}")
+
+    def run_in_place(self, op, target: Operand, inputs) -> None:
+        """Device::run_in_place (src/metal/mod.rs:697-725): SliceScatter of
+        one source into a contiguous target this device owns."""
+        if not isinstance(op, SliceScatter) or len(inputs) != 1:
+            raise _lib.HipError(_lib.ERR_INVALID_ARGUMENT, f"run_in_place supports SliceScatter only, got {op!r}")
+        self._owns(target)
+        (src,) = inputs
+        self._owns(src)
+        _lib.call("fh_slice_scatter", self.handle, int(target.dtype), op.dim, op.start,
+                  ctypes.c_void_p(target.storage.ptr), ctypes.byref(target.layout.view()),
+                  ctypes.c_void_p(src.storage.ptr), ctypes.byref(src.layout.view()))
 
     # ---- batching and timing (CommandStream counterpart) ----
     def capture_begin(self) -> None:
@@ -239,7 +350,9 @@ class HipDevice:
 
 
 class HipGraph:
-    """A captured sequence of ops, replayed with ``launch``."""
+    """A captured sequence of ops, replayed with ``launch``. The library
+    keeps every allocation the graph's ops touched alive until the graph is
+    destroyed, so storages dropped meanwhile cannot be reused under it."""
 
     def __init__(self, device: HipDevice, handle: int):
         self.device = device
