@@ -109,14 +109,22 @@ int fh_device_stream(fh_device *dev, void **stream);
  * zero_fill != 0 the memory is cleared before any later op on the stream
  * reads it (Device::zeros). */
 int fh_alloc(fh_device *dev, size_t nbytes, int zero_fill, void **out);
-/* Frees an allocation of this device after the work queued on it ends. */
+/* Frees an allocation of this device after the work queued on it ends.
+ * A live graph retains every allocation its captured ops touched, as a
+ * Metal command buffer retains its buffers (src/metal/mod.rs:288-292): the
+ * allocation is then no longer usable by ops but stays allocated until the
+ * last graph that uses it is destroyed. A free asked for while capturing is
+ * carried out at fh_capture_end, on the same rule. */
 int fh_free(fh_device *dev, void *ptr);
 /* Host -> device copy into an owned range; ordered on the stream. */
 int fh_upload(fh_device *dev, void *dst, const void *src, size_t nbytes);
 /* Device -> host copy of an owned range; synchronises first. */
 int fh_download(fh_device *dev, void *dst, const void *src, size_t nbytes);
 
-/* ---- memory and profile counters (src/nn/primitive.rs:75-83) ---- */
+/* ---- memory and profile counters (src/nn/primitive.rs:75-83) ----
+ * Bytes counted: every live allocation (including retired ones a graph still
+ * holds) plus the device's own work areas (the 33 MB of GEMV/GEMM partial
+ * sums and the batched GEMV's x image), allocated at creation. */
 int fh_max_memory_allocated(const fh_device *dev, fh_allocated_memory *out);
 int fh_reset_run_memory_peak(fh_device *dev);
 int fh_run_memory_peak(const fh_device *dev, fh_allocated_memory *out);
@@ -130,8 +138,14 @@ int fh_take_profile(fh_device *dev, fh_profile *out);
  * them at once. Between begin and end, ops are validated and recorded, not
  * run; fh_graph_launch replays the recording on the device's stream. ---- */
 int fh_capture_begin(fh_device *dev);
+/* Ends the capture; the graph retains the allocations its ops touched. */
 int fh_capture_end(fh_device *dev, fh_graph **out);
+/* FH_ERR_FOREIGN_STORAGE for a graph of another (or a destroyed) device. */
 int fh_graph_launch(fh_device *dev, fh_graph *graph);
+/* Waits for the device's queued work (a replay may still be running), then
+ * destroys the graph and releases its allocations; any the caller already
+ * freed are freed now. A graph may outlive its device (it can then only be
+ * destroyed). */
 int fh_graph_destroy(fh_graph *graph);
 
 /* ---- event timing on the device's stream ---- */
@@ -177,6 +191,89 @@ int fh_q4_matmul(fh_device *dev, const uint16_t *x, int64_t m, int64_t k,
 int fh_q4_dequant(fh_device *dev, const uint32_t *wq, const uint16_t *scales,
                   const uint16_t *biases, int64_t rows, int64_t k, int64_t group,
                   uint16_t *out);
+
+/* ======================================================================
+ * Strided ops: the reference's non-quantized Ops (src/nn/primitive.rs:48-68)
+ * over strided views, so that a backend can run every Op of the unchanged
+ * model code (Device::run and Device::run_in_place, src/metal/mod.rs:639-
+ * 725). Each entry point is one plain kernel of the Metal kernel it replaces
+ * (src/metal/kernels/{copy,unary,binary,reduce,matmul,index_select,
+ * slice_scatter}.metal) with the same arithmetic: fp32 math on values
+ * decoded from the dtype, the output rounded once (RNE for bf16).
+ *
+ * A view is the reference's Layout flattened as StridedArgs is
+ * (src/metal/args.rs:22-29): element offset, rank 0..4, sizes and strides in
+ * elements (strides >= 0; a broadcast dim has stride 0). The pointer passed
+ * beside a view is the storage base; the view addresses base + offset + sum
+ * i_d * stride_d. Every element a view addresses must lie in one live
+ * allocation of the device. Outputs are fresh and contiguous, as
+ * Device::run returns them; shape rules are those of primitive::output
+ * (src/nn/primitive.rs:146-289). dtype is an fh_dtype.
+ * ====================================================================== */
+
+typedef struct fh_view {
+    int64_t offset;
+    int32_t ndim;
+    int64_t dims[4];
+    int64_t strides[4];
+} fh_view;
+
+/* UnaryOp, BinaryOp, ReduceOp (src/nn/primitive.rs:14-46) */
+typedef enum fh_unary_op { FH_NEG = 0, FH_EXP = 1, FH_SQRT = 2, FH_RECIPROCAL = 3 } fh_unary_op;
+typedef enum fh_binary_op { FH_ADD = 0, FH_SUB = 1, FH_MUL = 2, FH_DIV = 3 } fh_binary_op;
+typedef enum fh_reduce_op { FH_SUM = 0, FH_AMAX = 1, FH_ARGMAX = 2 } fh_reduce_op;
+
+/* Op::Copy (copy_strided, copy.metal:1-13): dst = the view's elements in
+ * row-major order. Any dtype. */
+int fh_copy_strided(fh_device *dev, int dtype, const void *src, const fh_view *view, void *dst);
+
+/* Op::ToDtype (to_dtype_strided, copy.metal:15-36): F32 <-> BF16 (RNE with
+ * the quiet-NaN rule); the same float dtype is a copy. */
+int fh_to_dtype(fh_device *dev, int from, const void *src, const fh_view *view, int to, void *dst);
+
+/* Op::Unary (unary_strided, unary.metal:1-40) on F32 or BF16. */
+int fh_unary(fh_device *dev, int op, int dtype, const void *src, const fh_view *view, void *dst);
+
+/* Op::Binary (binary_strided, binary.metal:1-44). Both views have the
+ * output's dims: a caller broadcasts first by expanding (stride 0), as
+ * Tensor::binary does (src/nn/tensor.rs:332-343). */
+int fh_binary(fh_device *dev, int op, int dtype, const void *lhs, const fh_view *lhs_view,
+              const void *rhs, const fh_view *rhs_view, void *dst);
+
+/* Op::Reduce{op, dim} (reduce_rows / argmax_rows, reduce.metal:1-93): one
+ * block of 256 threads per output element; thread t folds k = t, t + 256,
+ * ..., then a halving tree, the reference's order (its sums are bit-equal).
+ * Output dims = the view's with dims[dim] = 1, contiguous; SUM/AMAX keep the
+ * dtype, ARGMAX writes u32 (first index on ties). AMAX/ARGMAX over an empty
+ * dim are refused (TensorError::EmptyReduction); an empty SUM is 0. */
+int fh_reduce(fh_device *dev, int op, int dtype, const void *src, const fh_view *view, int32_t dim,
+              void *dst);
+
+/* Op::Matmul (MetalDevice::matmul, src/metal/mod.rs:434-481; matmul_tiled,
+ * matmul.metal:29-65): lhs [..., m, k] x rhs [..., k, n] with equal batch
+ * dims, out [..., m, n]; fp32 sums in order of k, output rounded once.
+ * Any strides are read in place (no operand copy). */
+int fh_matmul(fh_device *dev, int dtype, const void *lhs, const fh_view *lhs_view, const void *rhs,
+              const fh_view *rhs_view, void *dst);
+
+/* Op::IndexSelect{dim 0} (index_select_rows, index_select.metal:11-29):
+ * table 2-D [rows, cols] (F32 or BF16), ids U32 1-D [n] -> dst [n, cols];
+ * an id >= rows gives a zero row. */
+int fh_index_select(fh_device *dev, int dtype, const void *table, const fh_view *table_view,
+                    const uint32_t *ids, const fh_view *ids_view, void *dst);
+
+/* Op::Cat{dim} (MetalDevice::cat, src/metal/mod.rs:502-524): dst = lhs then
+ * rhs along dim; all other dims equal. */
+int fh_cat(fh_device *dev, int dtype, int32_t dim, const void *lhs, const fh_view *lhs_view,
+           const void *rhs, const fh_view *rhs_view, void *dst);
+
+/* Device::run_in_place(Op::SliceScatter{dim, start}) (src/metal/mod.rs:697-
+ * 725; slice_scatter_strided, slice_scatter.metal:1-21): writes src into
+ * target[..., start : start + src.dims[dim], ...] in place. The target view
+ * is contiguous (Tensor::slice_scatter requires it, src/nn/tensor.rs:
+ * 307-316) and src may be strided. */
+int fh_slice_scatter(fh_device *dev, int dtype, int32_t dim, int64_t start, void *target,
+                     const fh_view *target_view, const void *src, const fh_view *src_view);
 
 /* ======================================================================
  * Decoder-step ops: the plumbing around the q4 linears that a Llama decode
