@@ -205,11 +205,12 @@ class _Q4:
         self.b = dev.storage_from_bytes(np.ascontiguousarray(b).tobytes())
 
 
-def layer_weights(cfg: LlamaConfig, seed: int, layer: int):
+def layer_weights(cfg: LlamaConfig, seed: int, layer: int, centre: float = 8.0):
     """Host-side random-init q4 weights of one layer: dict of (wq, s, b)
     triplets and bf16 norm weights. Layer l's packed words are layer 0's xor a
     per-layer constant (uniform nibbles stay uniform), so building a
-    28-layer model costs one layer's draws."""
+    28-layer model costs one layer's draws. ``centre`` sets the biases
+    (synth.q4_weights): 8 is the task's distribution, 7.5 zero-mean weights."""
     key = np.uint32((0x9E3779B9 * (layer + 1)) & 0xFFFFFFFF)
     out = {}
     for name, (n, k, s_off) in {
@@ -218,7 +219,7 @@ def layer_weights(cfg: LlamaConfig, seed: int, layer: int):
         "gate_up": (2 * cfg.ffn, cfg.hidden, 3),
         "down": (cfg.hidden, cfg.ffn, 4),
     }.items():
-        wq, s, b = _cached_q4(seed * 16 + s_off, n, k)
+        wq, s, b = _cached_q4(seed * 16 + s_off, n, k, centre)
         out[name] = (wq ^ key if layer else wq, s, b)
     for name, s_off in (("input_norm", 5), ("post_norm", 6)):
         out[name] = _norm_weight(seed * 16 + s_off + 97 * layer, cfg.hidden)
@@ -228,10 +229,10 @@ def layer_weights(cfg: LlamaConfig, seed: int, layer: int):
 _CACHE: dict = {}
 
 
-def _cached_q4(seed: int, n: int, k: int):
-    key = (seed, n, k)
+def _cached_q4(seed: int, n: int, k: int, centre: float = 8.0):
+    key = (seed, n, k, centre)
     if key not in _CACHE:
-        _CACHE[key] = synth.q4_weights(seed, n, k, GROUP)
+        _CACHE[key] = synth.q4_weights(seed, n, k, GROUP, centre)
     return _CACHE[key]
 
 
@@ -240,8 +241,8 @@ def _norm_weight(seed: int, n: int) -> np.ndarray:
     return synth.bf16_rne((1.0 + 0.1 * z).astype(np.float32))
 
 
-def embed_weights(cfg: LlamaConfig, seed: int):
-    return _cached_q4(seed * 16 + 7, cfg.vocab, cfg.hidden)
+def embed_weights(cfg: LlamaConfig, seed: int, centre: float = 8.0):
+    return _cached_q4(seed * 16 + 7, cfg.vocab, cfg.hidden, centre)
 
 
 def final_norm_weight(cfg: LlamaConfig, seed: int):
@@ -256,8 +257,9 @@ class Q4Llama:
     tokens of one sequence in one forward."""
 
     def __init__(self, dev: HipDevice, cfg: LlamaConfig, seed: int | None, max_len: int, max_tokens: int,
-                 batch: int = 1, weights=None):
-        """Weights are random-init from `seed`, or read from `weights` (a
+                 batch: int = 1, weights=None, centre: float = 8.0):
+        """Weights are random-init from `seed` (biases centred at -centre * s,
+        see layer_weights), or read from `weights` (a
         foundry_amd.weights.Weights of q4 triplets; see from_checkpoint)."""
         self.dev, self.cfg, self.max_len = dev, cfg, max_len
         if max_len > cfg.max_position_embeddings:
@@ -273,7 +275,8 @@ class Q4Llama:
                                               lambda l: llama_q4_layer(weights, cfg, l),
                                               lambda: llama_final_norm(weights, cfg))
         else:
-            src_embed, src_layer, src_norm = (lambda: embed_weights(cfg, seed), lambda l: layer_weights(cfg, seed, l),
+            src_embed, src_layer, src_norm = (lambda: embed_weights(cfg, seed, centre),
+                                              lambda l: layer_weights(cfg, seed, l, centre),
                                               lambda: final_norm_weight(cfg, seed))
         self.embed = _Q4(dev, *src_embed())
         self.layers = []

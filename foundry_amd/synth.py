@@ -71,8 +71,10 @@ def _normal(d0: np.ndarray, d1: np.ndarray) -> np.ndarray:
     return np.sqrt(-2.0 * np.log(u1)) * np.cos(6.283185307179586 * u2)
 
 
-def q4_weights(seed: int, rows: int, k: int, group: int = 64):
-    """Returns (wq u32[rows, k/8], scales bf16[rows, k/group], biases bf16[...])."""
+def q4_weights(seed: int, rows: int, k: int, group: int = 64, centre: float = 8.0):
+    """Returns (wq u32[rows, k/8], scales bf16[rows, k/group], biases bf16[...]).
+    ``centre`` 8 is the task's distribution (b = -8 s + N(0, 1e-3), so the
+    weights have mean -s/2); 7.5 gives zero-mean weights."""
     words = rows * (k // 8)
     word_draws = (words + 1) // 2
     ngroups = rows * (k // group)
@@ -81,7 +83,7 @@ def q4_weights(seed: int, rows: int, k: int, group: int = 64):
     s = bf16_rne((0.004 + 0.016 * _unit(draws(seed, word_draws, ngroups))).astype(np.float32))
     db = draws(seed, word_draws + ngroups, 2 * ngroups)
     z = _normal(db[0::2], db[1::2])
-    bias = (-8.0 * bf16_to_f32(s).astype(np.float64) + 1e-3 * z).astype(np.float32)
+    bias = (-centre * bf16_to_f32(s).astype(np.float64) + 1e-3 * z).astype(np.float32)
     b = bf16_rne(bias)
     return wq, s.reshape(rows, k // group), b.reshape(rows, k // group)
 

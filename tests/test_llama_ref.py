@@ -149,3 +149,177 @@ def test_compare_generation_reference_cases():
     assert (r["compared_tokens"], r["matched_tokens"], r["close"]) == (1, 1, True)
     r = c([4], [[4]], [], [])
     assert (r["compared_tokens"], r["close"]) == (0, False)
+
+
+# ---------------- RoPE rotation and layer composition ----------------
+# The reference has no test of apply_rotary_pos_emb / rotate_half
+# (src/models/llama/rotary_emb.rs:62-85) or of the decoder's wiring
+# (src/models/llama/model.rs:254-279); these closed forms pin them.
+
+from foundry_amd import synth  # noqa: E402
+from foundry_amd.llama import LlamaConfig  # noqa: E402
+
+TINY = LlamaConfig(1, 128, 2, 1, 64, 128, 256)
+
+
+def _zeros_q4(n, k):
+    return (np.zeros((n, k // 8), np.uint32), np.zeros((n, k // 64), np.uint16), np.zeros((n, k // 64), np.uint16))
+
+
+def _tiny_model(cfg=TINY, zero=(), seed=3, layers=1, max_len=8):
+    """RefLlama with seeded weights; every name in `zero` gets all-zero
+    scales and biases (w = 0)."""
+    shapes = {"qkv": (cfg.qkv_rows, cfg.hidden), "o": (cfg.hidden, cfg.n_heads * cfg.head_dim),
+              "gate_up": (2 * cfg.ffn, cfg.hidden), "down": (cfg.hidden, cfg.ffn)}
+    Ls = []
+    for li in range(layers):
+        L = {}
+        for j, (name, (n, k)) in enumerate(shapes.items()):
+            L[name] = _zeros_q4(n, k) if name in zero else synth.q4_weights(seed + 10 * li + j, n, k, centre=7.5)
+        for j, name in enumerate(("input_norm", "post_norm")):
+            L[name] = synth.bf16_rne((1 + 0.1 * synth.bf16_to_f32(synth.bf16_normal(seed + 50 + 10 * li + j,
+                                                                                    (cfg.hidden,)))).astype(np.float32))
+        Ls.append(L)
+    embed = synth.q4_weights(seed + 99, cfg.vocab, cfg.hidden, centre=7.5)
+    final = synth.bf16_rne((1 + 0.1 * synth.bf16_to_f32(synth.bf16_normal(seed + 98, (cfg.hidden,)))).astype(np.float32))
+    return R.RefLlama(cfg, embed, Ls, final, max_len), Ls, embed, final
+
+
+def test_rope_at_position_zero_is_the_identity():
+    m, *_ = _tiny_model()
+    x = R.rne(np.random.default_rng(4).standard_normal((3, 2, 64)).astype(np.float32))
+    assert np.array_equal(m.rope(x, np.zeros(3, np.int64)), x)
+
+
+def test_rope_of_unit_vectors_gives_the_rotation_columns():
+    """x = e_i (i < d/2) -> RNE(cos t_i) at i, RNE(sin t_i) at i + d/2;
+    x = e_{i+d/2} -> -RNE(sin t_i) at i, RNE(cos t_i) at i + d/2, with
+    t_i = position * inv_freq_i in fp32. A swapped half or a sign error in
+    rotate_half fails one of the two."""
+    m, *_ = _tiny_model(max_len=4000)
+    d, half = 64, 32
+    f = R.inv_freq(d, TINY.rope_theta, (32.0, 1.0, 4.0, 8192))
+    for pos in (1, 7, 3999):
+        for i in (0, 5, half - 1):
+            t = np.float64(np.float32(pos) * f[i])
+            c, s = np.cos(t), np.sin(t)
+            ei = np.zeros((1, 1, d), np.float32)
+            ei[0, 0, i] = 1.0
+            out = m.rope(ei, np.array([pos]))[0, 0].astype(np.float64)
+            ulp = 2.0 ** -8
+            assert abs(out[i] - c) <= ulp * max(abs(c), 2 ** -126) and abs(out[i + half] - s) <= ulp * max(abs(s), 2 ** -126)
+            assert np.count_nonzero(np.delete(out, [i, i + half])) == 0
+            ej = np.zeros((1, 1, d), np.float32)
+            ej[0, 0, i + half] = 1.0
+            out = m.rope(ej, np.array([pos]))[0, 0].astype(np.float64)
+            assert abs(out[i] + s) <= ulp * max(abs(s), 2 ** -126) and abs(out[i + half] - c) <= ulp * max(abs(c), 2 ** -126)
+            assert np.count_nonzero(np.delete(out, [i, i + half])) == 0
+
+
+def _ulp_close(got, want, ulps=1.0):
+    got, want = np.asarray(got, np.float64), np.asarray(want, np.float64)
+    u = 2.0 ** (np.floor(np.log2(np.maximum(np.abs(want), 2.0 ** -126))) - 7)
+    return np.abs(got - want) <= ulps * u
+
+
+def test_forward_with_zero_o_and_down_is_the_embedding_through_the_head():
+    """Every layer adds RNE(h + 0): the logits are the final RMSNorm of the
+    last id's embedding row times the tied table (float64 here)."""
+    m, Ls, embed, final = _tiny_model(zero=("o", "down"), layers=2)
+    ids = [17, 250, 3]
+    logits = m.forward(ids, np.arange(3)).astype(np.float64)
+    E = R.dequant_f32(*embed).astype(np.float64)
+    h = R.rne(E[3].astype(np.float32))[None, :]
+    x = R.rms_norm(h, R.from_bf16(final), TINY.rms_norm_eps).astype(np.float64)
+    want = x[0] @ E.T
+    assert np.mean(_ulp_close(logits, want)) >= 0.99
+    assert np.all(_ulp_close(logits, want, 2.0) | (np.abs(logits - want) <= 1e-6 * np.max(np.abs(want))))
+    # a residual stream that took another row, or skipped the final norm, does not match
+    bad_row = R.rms_norm(R.rne(E[17].astype(np.float32))[None, :], R.from_bf16(final), TINY.rms_norm_eps)[0]
+    assert np.mean(_ulp_close(logits, bad_row.astype(np.float64) @ E.T)) < 0.5
+    assert np.mean(_ulp_close(logits, h[0].astype(np.float64) @ E.T)) < 0.5
+
+
+def test_forward_with_zero_qkv_leaves_only_the_mlp():
+    """q = k = v = 0 gives attention 0 and o-projection 0, so one layer is
+    h + down(silu(gate) * up) on the post-attention norm of h itself."""
+    m, Ls, embed, final = _tiny_model(zero=("qkv",))
+    ids = [9, 40]
+    m.forward(ids, np.arange(2))
+    E = R.dequant_f32(*embed)
+    h = R.rne(E[np.asarray(ids)])
+    L = Ls[0]
+    x = R.rms_norm(h, R.from_bf16(L["post_norm"]), TINY.rms_norm_eps)
+    gu = R.rne((x.astype(np.float64) @ R.dequant_f32(*L["gate_up"]).astype(np.float64).T).astype(np.float32))
+    act = R.silu_mul(gu[:, :TINY.ffn], gu[:, TINY.ffn:])
+    want_h = R.rne((h.astype(np.float64) + R.rne((act.astype(np.float64) @ R.dequant_f32(*L["down"]).astype(np.float64).T)
+                                                 .astype(np.float32))).astype(np.float32))
+    xf = R.rms_norm(want_h, R.from_bf16(final), TINY.rms_norm_eps)[-1].astype(np.float64)
+    want = xf @ E.astype(np.float64).T
+    got = m.forward(ids, np.arange(2)).astype(np.float64)  # same inputs again (the cache is overwritten)
+    assert np.mean(_ulp_close(got, want, 2.0)) >= 0.98
+    # with the MLP taken from the input norm instead, it does not match
+    x_bad = R.rms_norm(h, R.from_bf16(L["input_norm"]), TINY.rms_norm_eps)
+    gu_b = R.rne((x_bad.astype(np.float64) @ R.dequant_f32(*L["gate_up"]).astype(np.float64).T).astype(np.float32))
+    hb = R.rne((h.astype(np.float64) + R.rne((R.silu_mul(gu_b[:, :TINY.ffn], gu_b[:, TINY.ffn:]).astype(np.float64)
+                                              @ R.dequant_f32(*L["down"]).astype(np.float64).T).astype(np.float32))).astype(np.float32))
+    wb = R.rms_norm(hb, R.from_bf16(final), TINY.rms_norm_eps)[-1].astype(np.float64) @ E.astype(np.float64).T
+    assert np.mean(_ulp_close(got, wb, 2.0)) < 0.5
+
+
+def test_forward_takes_v_from_its_slice_and_q_from_its_slice():
+    """Zero MLP (gate/up w = 0 gives act = 0). One token at position 0 attends
+    only itself with p = 1, so its attention output is exactly its v slice.
+    With the q rows zeroed as well, the second token's scores are 0 whatever
+    k is, so p = RNE(1/2) on both keys: out = RNE(RNE(0.5) (v0 + v1))."""
+    cfg = TINY
+    m, Ls, embed, final = _tiny_model(zero=("gate_up",))
+    E = R.dequant_f32(*embed)
+    L = Ls[0]
+    W = R.dequant_f32(*L["qkv"]).astype(np.float64)
+    hq, hk = cfg.n_heads * cfg.head_dim, cfg.n_kv_heads * cfg.head_dim
+    Wo = R.dequant_f32(*L["o"]).astype(np.float64)
+
+    def head_out(h, attn):
+        h1 = R.rne((h.astype(np.float64) + R.rne((attn.astype(np.float64) @ Wo.T).astype(np.float32))).astype(np.float32))
+        return R.rms_norm(h1, R.from_bf16(final), cfg.rms_norm_eps)[-1].astype(np.float64) @ E.astype(np.float64).T
+
+    h = R.rne(E[[5]])
+    x = R.rms_norm(h, R.from_bf16(L["input_norm"]), cfg.rms_norm_eps).astype(np.float64)
+    v = R.rne((x @ W[hq + hk:].T).astype(np.float32))  # [1, hk]; every q head reads kv head 0
+    attn = np.tile(v, (1, cfg.n_heads))
+    got = m.forward([5], np.array([0])).astype(np.float64)
+    assert np.mean(_ulp_close(got, head_out(h, attn), 2.0)) >= 0.98
+    k_as_v = np.tile(R.rne((x @ W[hq:hq + hk].T).astype(np.float32)), (1, cfg.n_heads))
+    assert np.mean(_ulp_close(got, head_out(h, k_as_v), 2.0)) < 0.5
+
+    wq, s, b = L["qkv"]
+    s, b = s.copy(), b.copy()
+    s[:hq], b[:hq] = 0, 0
+    m2 = R.RefLlama(cfg, embed, [dict(L, qkv=(wq, s, b))], final, 8)
+    h2 = R.rne(E[[5, 7]])
+    x2 = R.rms_norm(h2, R.from_bf16(L["input_norm"]), cfg.rms_norm_eps).astype(np.float64)
+    v2 = R.rne((x2 @ W[hq + hk:].T).astype(np.float32)).astype(np.float64)
+    half = np.float64(R.rne(np.float32(0.5))[0])
+    attn2 = np.tile(R.rne((half * v2[0] + half * v2[1]).astype(np.float32))[None, :], (1, cfg.n_heads))
+    got2 = m2.forward([5, 7], np.arange(2)).astype(np.float64)
+    assert np.mean(_ulp_close(got2, head_out(h2, np.vstack([attn2, attn2])), 2.0)) >= 0.98
+
+
+def test_rope_pins_reject_planted_rotations():
+    """rotate_half with its halves swapped, or without the minus sign, moves
+    sin to the wrong place or sign on unit vectors."""
+    m, *_ = _tiny_model(max_len=16)
+    planted = {
+        "swapped": lambda x: np.concatenate([x[..., 32:], -x[..., :32]], axis=-1),
+        "unsigned": lambda x: np.concatenate([x[..., 32:], x[..., :32]], axis=-1),
+    }
+    ej = np.zeros((1, 1, 64), np.float32)
+    ej[0, 0, 32 + 3] = 1.0
+    good = m.rope(ej, np.array([9]))[0, 0]
+    for name, rot in planted.items():
+        c, s = m.cos[[9]][:, None, :], m.sin[[9]][:, None, :]
+        bad = R.rne(R.rne(ej * c) + R.rne(rot(ej) * s))[0, 0]
+        assert not np.array_equal(bad, good), name
+        assert bad[3] != -m.sin[9, 3] or bad[32 + 3] != m.cos[9, 3], name
+    assert good[3] == -m.sin[9, 3] and good[32 + 3] == m.cos[9, 3]
