@@ -91,6 +91,20 @@ class LlamaModel(ctypes.Structure):
     ]
 
 
+class View(ctypes.Structure):
+    """fh_view: a strided view (src/metal/args.rs:22-29), in elements."""
+    _fields_ = [("offset", ctypes.c_int64), ("ndim", ctypes.c_int32), ("dims", ctypes.c_int64 * 4),
+                ("strides", ctypes.c_int64 * 4)]
+
+    @staticmethod
+    def of(shape, strides, offset: int = 0) -> "View":
+        v = View()
+        v.offset, v.ndim = int(offset), len(shape)
+        for d, (n, st) in enumerate(zip(shape, strides)):
+            v.dims[d], v.strides[d] = int(n), int(st)
+        return v
+
+
 class HipError(RuntimeError):
     """An fh_status other than OK, with the library's message."""
 
@@ -148,6 +162,15 @@ SIGNATURES = {
     "fh_advance_positions": [_vp, _vp, _i64, _i64],
     "fh_append_token": [_vp, _vp, _i64, _vp, _vp, _i64, _i64],
     "fh_llama_forward": [_vp, _vp, _i64, _vp, _vp, _vp],
+    "fh_copy_strided": [_vp, _int, _vp, ctypes.POINTER(View), _vp],
+    "fh_to_dtype": [_vp, _int, _vp, ctypes.POINTER(View), _int, _vp],
+    "fh_unary": [_vp, _int, _int, _vp, ctypes.POINTER(View), _vp],
+    "fh_binary": [_vp, _int, _int, _vp, ctypes.POINTER(View), _vp, ctypes.POINTER(View), _vp],
+    "fh_reduce": [_vp, _int, _int, _vp, ctypes.POINTER(View), ctypes.c_int32, _vp],
+    "fh_matmul": [_vp, _int, _vp, ctypes.POINTER(View), _vp, ctypes.POINTER(View), _vp],
+    "fh_index_select": [_vp, _int, _vp, ctypes.POINTER(View), _vp, ctypes.POINTER(View), _vp],
+    "fh_cat": [_vp, _int, ctypes.c_int32, _vp, ctypes.POINTER(View), _vp, ctypes.POINTER(View), _vp],
+    "fh_slice_scatter": [_vp, _int, ctypes.c_int32, _i64, _vp, ctypes.POINTER(View), _vp, ctypes.POINTER(View)],
 }
 
 _lib = None

@@ -1,8 +1,10 @@
-"""Op vocabulary and output rules for the q4 path.
+"""Op vocabulary and output rules.
 
-Mirrors src/nn/primitive.rs (``Op``, ``output``, the shape rules at :146-289)
-and src/nn/dtype.rs / shape.rs, extended with the two quantized ops the
-reference lacks:
+Mirrors src/nn/primitive.rs (``Op``, ``output``, the shape rules at :146-367)
+and src/nn/dtype.rs / shape.rs: the reference's nine Ops (``Unary``,
+``Binary``, ``Reduce``, ``Matmul``, ``Copy``, ``ToDtype``, ``IndexSelect``,
+``Cat``, ``SliceScatter``), extended with the two quantized ops the reference
+lacks:
 
 - ``QuantizedMatmul(bits=4, group=64)``: inputs ``[x, wq, scales, biases]``,
   ``x`` float ``[rows, K]``, ``wq`` U32 ``[N, K/8]``, ``scales``/``biases``
@@ -64,6 +66,188 @@ def check_shape(dims) -> tuple[int, ...]:
     return dims
 
 
+class UnaryOp(enum.IntEnum):
+    """src/nn/primitive.rs:14-24; values match fh_unary_op."""
+
+    NEG = 0
+    EXP = 1
+    SQRT = 2
+    RECIPROCAL = 3
+
+
+class BinaryOp(enum.IntEnum):
+    """src/nn/primitive.rs:26-36; values match fh_binary_op."""
+
+    ADD = 0
+    SUB = 1
+    MUL = 2
+    DIV = 3
+
+
+class ReduceOp(enum.IntEnum):
+    """src/nn/primitive.rs:38-46; values match fh_reduce_op."""
+
+    SUM = 0
+    AMAX = 1
+    ARGMAX = 2
+
+
+@dataclass(frozen=True)
+class Unary:
+    op: UnaryOp
+    name = "unary"
+
+
+@dataclass(frozen=True)
+class Binary:
+    op: BinaryOp
+    name = "binary"
+
+
+@dataclass(frozen=True)
+class Reduce:
+    op: ReduceOp
+    dim: int
+    name = "reduce"
+
+
+@dataclass(frozen=True)
+class Matmul:
+    name = "matmul"
+
+
+@dataclass(frozen=True)
+class Copy:
+    name = "copy"
+
+
+@dataclass(frozen=True)
+class ToDtype:
+    dtype: "DType"
+    name = "to_dtype"
+
+
+@dataclass(frozen=True)
+class IndexSelect:
+    dim: int
+    name = "index_select"
+
+
+@dataclass(frozen=True)
+class Cat:
+    dim: int
+    name = "cat"
+
+
+@dataclass(frozen=True)
+class SliceScatter:
+    dim: int
+    start: int
+    name = "slice_scatter"
+
+
+def size(shape, dim: int) -> int:
+    """Shape::size (src/nn/shape.rs:41-53)."""
+    if not 0 <= dim < len(shape):
+        raise TensorError("DimOutOfRange", f"dim {dim} of {shape}")
+    return shape[dim]
+
+
+def with_dim(shape, dim: int, n: int) -> tuple[int, ...]:
+    """Shape::with_dim (src/nn/shape.rs:96-108)."""
+    size(shape, dim)
+    return check_shape(shape[:dim] + (n,) + shape[dim + 1:])
+
+
+def broadcast(lhs, rhs) -> tuple[int, ...]:
+    """Shape::broadcast (src/nn/shape.rs:62-94): right-aligned; equal sizes
+    or a size of one."""
+    nd = max(len(lhs), len(rhs))
+    out = []
+    for i in range(1, nd + 1):
+        a = lhs[-i] if i <= len(lhs) else 1
+        b = rhs[-i] if i <= len(rhs) else 1
+        if a == b or b == 1:
+            out.append(a)
+        elif a == 1:
+            out.append(b)
+        else:
+            raise TensorError("BroadcastIncompatible", f"{lhs} and {rhs}")
+    return check_shape(tuple(reversed(out)))
+
+
+def _require_same_float(a: DType, b: DType) -> DType:
+    if a != b:
+        raise TensorError("DTypeMismatch", f"{DType(a).name} and {DType(b).name}")
+    return _require_float(a)
+
+
+def _dims_equal_except(a, b, dim: int) -> bool:
+    return len(a) == len(b) and all(i == dim or x == y for i, (x, y) in enumerate(zip(a, b)))
+
+
+def _output_standard(op, inputs):
+    """src/nn/primitive.rs:146-207 for the reference's own Ops."""
+    def arity(n):
+        if len(inputs) != n:
+            raise TensorError("OperandCount", f"{op.name} takes {n} operands, got {len(inputs)}")
+    if isinstance(op, Unary):
+        arity(1)
+        return inputs[0][1], _require_float(inputs[0][0])
+    if isinstance(op, Binary):
+        arity(2)
+        dtype = _require_same_float(inputs[0][0], inputs[1][0])
+        return broadcast(inputs[0][1], inputs[1][1]), dtype
+    if isinstance(op, Reduce):
+        arity(1)
+        dtype, shape = inputs[0]
+        dtype = _require_float(dtype)
+        n = size(shape, op.dim)
+        if op.op in (ReduceOp.AMAX, ReduceOp.ARGMAX) and n == 0:
+            raise TensorError("EmptyReduction", f"{ReduceOp(op.op).name} over dim {op.dim} of {shape}")
+        return with_dim(shape, op.dim, 1), (DType.U32 if op.op == ReduceOp.ARGMAX else dtype)
+    if isinstance(op, Matmul):
+        arity(2)
+        dtype = _require_same_float(inputs[0][0], inputs[1][0])
+        lhs, rhs = inputs[0][1], inputs[1][1]
+        if len(lhs) < 2 or len(rhs) < 2 or lhs[:-2] != rhs[:-2] or lhs[-1] != rhs[-2]:
+            raise TensorError("MatmulIncompatible", f"{lhs} x {rhs}")
+        return with_dim(lhs, len(lhs) - 1, rhs[-1]), dtype
+    if isinstance(op, Copy):
+        arity(1)
+        return inputs[0][1], inputs[0][0]
+    if isinstance(op, ToDtype):
+        arity(1)
+        _require_float(inputs[0][0])
+        return inputs[0][1], _require_float(op.dtype)
+    if isinstance(op, IndexSelect):
+        arity(2)
+        (t_dt, table), (i_dt, ids) = inputs
+        dtype = _require_float(t_dt)
+        if i_dt is not DType.U32:
+            raise TensorError("IndicesNotU32", f"{DType(i_dt).name}")
+        if op.dim != 0 or len(table) != 2 or len(ids) != 1:
+            raise TensorError("IndexSelectIncompatible", f"dim {op.dim}, table {table}, indices {ids}")
+        return check_shape((ids[0], table[1])), dtype
+    if isinstance(op, Cat):
+        arity(2)
+        dtype = _require_same_float(inputs[0][0], inputs[1][0])
+        lhs, rhs = inputs[0][1], inputs[1][1]
+        a, b = size(lhs, op.dim), size(rhs, op.dim)
+        if not _dims_equal_except(lhs, rhs, op.dim):
+            raise TensorError("CatIncompatible", f"{lhs} and {rhs} along {op.dim}")
+        return with_dim(lhs, op.dim, a + b), dtype
+    if isinstance(op, SliceScatter):
+        arity(2)
+        dtype = _require_same_float(inputs[0][0], inputs[1][0])
+        target, src = inputs[0][1], inputs[1][1]
+        t, n = size(target, op.dim), size(src, op.dim)
+        if op.start < 0 or op.start + n > t or not _dims_equal_except(target, src, op.dim):
+            raise TensorError("SliceScatterOutOfBounds", f"{src} into {target} at {op.start} along {op.dim}")
+        return target, dtype
+    return None
+
+
 @dataclass(frozen=True)
 class QuantizedMatmul:
     bits: int = 4
@@ -115,8 +299,11 @@ def _check_q4_weight(op, wq, scales, biases, incompatible: str) -> tuple[int, in
 
 
 def output(op, inputs) -> tuple[tuple[int, ...], DType]:
-    """src/nn/primitive.rs:146-207 for the q4 ops: (output shape, dtype)."""
+    """src/nn/primitive.rs:146-207: (output shape, dtype) of any Op."""
     inputs = [(DType(dt), check_shape(shape)) for dt, shape in inputs]
+    std = _output_standard(op, inputs)
+    if std is not None:
+        return std
     if isinstance(op, QuantizedMatmul):
         if len(inputs) != 4:
             raise TensorError("OperandCount", f"{op.name} takes 4 operands, got {len(inputs)}")

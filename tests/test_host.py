@@ -136,7 +136,7 @@ def _c_layout(struct: str, fields) -> list[int]:
 
 
 @pytest.mark.parametrize("struct, cls", [("fh_q4_weight", _lib.Q4Weight), ("fh_llama_layer", _lib.LlamaLayer),
-                                         ("fh_llama_model", _lib.LlamaModel)])
+                                         ("fh_llama_model", _lib.LlamaModel), ("fh_view", _lib.View)])
 def test_model_structs_match_the_header(struct, cls):
     fields = [f[0] for f in cls._fields_]
     assert _c_layout(struct, fields) == [ctypes.sizeof(cls)] + [getattr(cls, f).offset for f in fields]
@@ -177,3 +177,75 @@ def test_product_package_does_not_import_the_oracle():
                     text = f.read()
                 assert not re.search(r"^\s*(import|from)\s+oracle", text, flags=re.M), name
                 assert "liboracle" not in text, name
+
+
+# ---- views and the standard Ops' output rules ----
+
+def test_layout_views_follow_the_reference():
+    """src/nn/layout.rs tests (:202-313): permute, narrow, reshape, expand."""
+    lay = Layout.contiguous((2, 3, 4))
+    p = lay.permute((2, 0, 1))
+    assert (p.shape, p.strides, p.is_contiguous()) == ((4, 2, 3), (1, 12, 4), False)
+    for bad in ((0, 1), (0, 0, 1), (0, 1, 3)):
+        with pytest.raises(TensorError) as e:
+            lay.permute(bad)
+        assert e.value.kind == "InvalidPermutation"
+    n = lay.narrow(1, 1, 2)
+    assert (n.shape, n.strides, n.offset) == ((2, 2, 4), (12, 4, 1), 4)
+    for args, kind in (((1, 2, 2), "NarrowOutOfBounds"), ((3, 0, 1), "DimOutOfRange")):
+        with pytest.raises(TensorError) as e:
+            lay.narrow(*args)
+        assert e.value.kind == kind
+    r = lay.narrow(0, 1, 1).reshape((3, 4))
+    assert (r.strides, r.offset) == ((4, 1), 12)
+    with pytest.raises(TensorError) as e:
+        Layout.contiguous((2, 3)).permute((1, 0)).reshape((6,))
+    assert e.value.kind == "ReshapeNonContiguous"
+    with pytest.raises(TensorError) as e:
+        Layout.contiguous((2, 3)).reshape((5,))
+    assert e.value.kind == "NumelMismatch"
+    x = Layout.contiguous((3, 1)).expand((2, 3, 4))
+    assert (x.shape, x.strides) == ((2, 3, 4), (0, 1, 0))
+    with pytest.raises(TensorError) as e:
+        Layout.contiguous((3, 2)).expand((3, 4))
+    assert e.value.kind == "ExpandIncompatible"
+    # a dim of size one may carry any stride and still be contiguous
+    assert Layout((2, 1, 3), (3, 99, 1)).is_contiguous()
+
+
+def test_standard_op_output_rules():
+    """src/nn/primitive.rs:146-367 and its tests: shapes, dtypes and the
+    TensorError kinds."""
+    from foundry_amd.primitive import (Binary, BinaryOp, Cat, Copy, IndexSelect, Matmul, Reduce, ReduceOp,
+                                       SliceScatter, ToDtype, Unary, UnaryOp, broadcast)
+    F, B, U = DType.F32, DType.BF16, DType.U32
+    assert output(Unary(UnaryOp.EXP), [(B, (2, 3))]) == ((2, 3), B)
+    assert output(Binary(BinaryOp.ADD), [(F, (2, 3)), (F, (3,))]) == ((2, 3), F)
+    assert broadcast((4, 1, 3), (2, 1)) == (4, 2, 3)
+    assert output(Reduce(ReduceOp.SUM, 1), [(F, (2, 0))]) == ((2, 1), F)
+    assert output(Reduce(ReduceOp.ARGMAX, 0), [(B, (2, 3))]) == ((1, 3), U)
+    assert output(Matmul(), [(F, (2, 3, 40)), (F, (2, 40, 5))]) == ((2, 3, 5), F)
+    assert output(Copy(), [(U, (7,))]) == ((7,), U)
+    assert output(ToDtype(F), [(B, (4,))]) == ((4,), F)
+    assert output(IndexSelect(0), [(F, (3, 4)), (U, (2,))]) == ((2, 4), F)
+    assert output(Cat(1), [(F, (2, 1)), (F, (2, 3))]) == ((2, 4), F)
+    assert output(SliceScatter(1, 2), [(B, (2, 4, 3)), (B, (2, 1, 3))]) == ((2, 4, 3), B)
+    cases = [
+        (Unary(UnaryOp.NEG), [(U, (2,))], "DTypeNotFloat"),
+        (Unary(UnaryOp.NEG), [], "OperandCount"),
+        (Binary(BinaryOp.MUL), [(F, (2,)), (B, (2,))], "DTypeMismatch"),
+        (Binary(BinaryOp.MUL), [(F, (2, 3)), (F, (3, 2))], "BroadcastIncompatible"),
+        (Reduce(ReduceOp.AMAX, 1), [(F, (2, 0))], "EmptyReduction"),
+        (Reduce(ReduceOp.SUM, 2), [(F, (2, 3))], "DimOutOfRange"),
+        (Matmul(), [(F, (2, 3)), (F, (2, 3))], "MatmulIncompatible"),
+        (Matmul(), [(F, (2, 2, 3)), (F, (3, 3, 2))], "MatmulIncompatible"),
+        (ToDtype(U), [(F, (2,))], "DTypeNotFloat"),
+        (IndexSelect(0), [(F, (3, 4)), (F, (2,))], "IndicesNotU32"),
+        (IndexSelect(1), [(F, (3, 4)), (U, (2,))], "IndexSelectIncompatible"),
+        (Cat(0), [(F, (1, 3)), (F, (2, 2))], "CatIncompatible"),
+        (SliceScatter(1, 3), [(F, (2, 4, 3)), (F, (2, 2, 3))], "SliceScatterOutOfBounds"),
+    ]
+    for op, inputs, kind in cases:
+        with pytest.raises(TensorError) as e:
+            output(op, inputs)
+        assert e.value.kind == kind, (op, inputs)
