@@ -349,6 +349,77 @@ def test_graph_replay_matches_eager(device):
             assert np.array_equal(got[key], eager[key]), key
 
 
+def _live_bytes(dev) -> int:
+    """Bytes the device holds now: the run peak right after a reset."""
+    dev.reset_run_memory_peak()
+    return dev.run_memory_peak()["bytes"]
+
+
+def _alloc(dev, nbytes):
+    p = ctypes.c_void_p()
+    _lib.call("fh_alloc", dev.handle, nbytes, 0, ctypes.byref(p))
+    return p.value
+
+
+def test_graph_retains_allocations_freed_before_or_during_capture_end():
+    """A graph keeps every allocation its ops touched: freeing one after
+    capture (or during it) retires it until the graph is destroyed, so a
+    replay never reads freed memory. A free during capture of memory the graph
+    does not use happens at capture end."""
+    dev = HipDevice(0)
+    try:
+        wq, s, b = synth.q4_weights(71, 512, 1024)
+        x = synth.bf16_normal(72, (1, 1024))
+        ptrs = {}
+        for name, arr in (("wq", wq), ("s", s), ("b", b), ("x", x)):
+            ptrs[name] = _alloc(dev, arr.nbytes)
+            _lib.call("fh_upload", dev.handle, ctypes.c_void_p(ptrs[name]), arr.ctypes.data_as(ctypes.c_void_p),
+                      arr.nbytes)
+        y = _alloc(dev, 512 * 4)
+        unused = _alloc(dev, 1 << 20)
+
+        def gemv():
+            _lib.call("fh_q4_matmul", dev.handle, ctypes.c_void_p(ptrs["x"]), 1, 1024, 1024,
+                      ctypes.c_void_p(ptrs["wq"]), ctypes.c_void_p(ptrs["s"]), ctypes.c_void_p(ptrs["b"]), 512, 64,
+                      ctypes.c_void_p(y), _lib.F32)
+
+        def read_y():
+            out = np.empty(512, np.float32)
+            _lib.call("fh_download", dev.handle, out.ctypes.data_as(ctypes.c_void_p), ctypes.c_void_p(y), out.nbytes)
+            return out
+
+        gemv()
+        eager = read_y()
+        before = _live_bytes(dev)
+        dev.capture_begin()
+        gemv()
+        _lib.call("fh_free", dev.handle, ctypes.c_void_p(ptrs["wq"]))  # used by the capture: kept
+        _lib.call("fh_free", dev.handle, ctypes.c_void_p(unused))  # not used: freed at capture end
+        graph = dev.capture_end()
+        assert _live_bytes(dev) == before - (1 << 20)
+        _lib.call("fh_free", dev.handle, ctypes.c_void_p(ptrs["x"]))  # after capture: retired
+        assert _live_bytes(dev) == before - (1 << 20)
+        # retired allocations are no longer valid operands
+        with pytest.raises(_lib.HipError) as e:
+            gemv()
+        assert e.value.kind == "ForeignStorage"
+        for _ in range(3):
+            zero = np.zeros(512, np.float32)
+            _lib.call("fh_upload", dev.handle, ctypes.c_void_p(y), zero.ctypes.data_as(ctypes.c_void_p), zero.nbytes)
+            graph.launch()
+            assert np.array_equal(read_y(), eager)
+        del graph  # fh_graph_destroy: waits, then frees what the caller released
+        assert _live_bytes(dev) == before - (1 << 20) - wq.nbytes - x.nbytes
+        # a graph may outlive its device; it can then only be destroyed
+        dev.capture_begin()
+        _lib.call("fh_advance_positions", dev.handle, ctypes.c_void_p(y), 4, 1)
+        orphan = dev.capture_end()
+    finally:
+        dev.close()
+    assert _lib.load().fh_graph_destroy(ctypes.c_void_p(orphan._handle)) == _lib.OK
+    orphan._handle = None
+
+
 def test_profiled_device_counts_dispatches(device):
     prof = HipDevice.profiled(_lib.PROFILE_KERNELS)
     try:
