@@ -154,6 +154,8 @@ SIGNATURES = {
     "fh_decode_attention_workspace": [_i64, _i64, _i64, _i64, _i64, ctypes.POINTER(ctypes.c_uint64)],
     "fh_decode_attention": [_vp, _vp, _i64, _i64, _i64, _i64, _vp, _vp, _i64, _vp, _vp, _vp, _i64,
                             ctypes.c_float, _vp, ctypes.c_uint64, _vp],
+    "fh_decode_attention_noalloc": [_vp, _vp, _i64, _i64, _i64, _i64, _vp, _vp, _i64, _vp, _vp, _vp, _i64,
+                                    ctypes.c_float, _vp],
     "fh_q4_matmul_rmsnorm": [_vp, _vp, _vp, _vp, _vp, ctypes.c_float, _i64, _i64, _vp, _vp, _vp, _i64, _i64,
                              _vp, _int],
     "fh_q4_gate_up_silu": [_vp, _vp, _vp, _vp, _vp, ctypes.c_float, _i64, _i64, _vp, _vp, _vp, _i64, _i64, _vp],

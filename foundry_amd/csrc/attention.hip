@@ -1313,7 +1313,8 @@ int workspace_bytes(const char *fn, int64_t rows, int64_t n_heads, int64_t n_kv,
 
 // Shared validation of both entry points; fills the layout.
 int check_attention(const char *fn, fh_device *dev, int64_t rows, int64_t n_heads, int64_t n_kv, int64_t head_dim,
-                    int64_t max_len, void *workspace, uint64_t workspace_bytes, AttnLayout *a) {
+                    int64_t max_len, void *workspace, uint64_t workspace_bytes, AttnLayout *a,
+                    bool workspace_is_allocation = true) {
     if (int rc = check_heads(fn, n_heads, n_kv, head_dim)) return rc;
     if (max_len == 0) return fail(FH_ERR_INVALID_ARGUMENT, "%s: empty KV cache", fn);
     if (int rc = check_attn_size(fn, rows, n_heads, head_dim, max_len)) return rc;
@@ -1326,6 +1327,7 @@ int check_attention(const char *fn, fh_device *dev, int64_t rows, int64_t n_head
                     (unsigned long long)workspace_bytes, (unsigned long long)a->total);
     if (reinterpret_cast<uintptr_t>(workspace) & 15u)
         return fail(FH_ERR_INVALID_ARGUMENT, "%s: workspace must be 16-byte aligned", fn);
+    if (!workspace_is_allocation) return FH_OK;  // the device's static scratch, sized above
     return check_range(dev, workspace, a->total, fn, "workspace");
 }
 
@@ -1373,17 +1375,59 @@ extern "C" int fh_decode_attention_workspace(int64_t batch, int64_t n_heads, int
     return workspace_bytes("fh_decode_attention_workspace", batch, n_heads, n_kv, head_dim, max_len, bytes);
 }
 
-extern "C" int fh_decode_attention(fh_device *dev, const uint16_t *qkv, int64_t batch, int64_t n_heads,
-                                   int64_t n_kv, int64_t head_dim, const uint16_t *cos_tab,
-                                   const uint16_t *sin_tab, int64_t table_len, const uint32_t *positions,
-                                   uint16_t *k_cache, uint16_t *v_cache, int64_t max_len, float scale,
-                                   void *workspace, uint64_t workspace_bytes, uint16_t *out) {
-    const char *fn = "fh_decode_attention";
+// The no-allocation decode attention's workspace. A __device__ array exists
+// once per GPU the library runs on (each holds its own copy from the first
+// use until the process ends); host code reaches it only through the address
+// hipGetSymbolAddress gives for that GPU, kept in fh_device::scratch.
+constexpr uint64_t kScratchBytes = FH_DECODE_SCRATCH_BYTES;
+static __device__ __align__(256) char scratch[kScratchBytes];
+
+namespace fh {
+
+// Called once per device at creation, with that device current.
+int attention_scratch_setup(fh_device *dev) {
+    void *ptr = nullptr;
+    hipError_t err = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (err != hipSuccess || ptr == nullptr) {
+        (void)hipGetLastError();  // clears the runtime's last-error slot
+        return fail(FH_ERR_DEVICE_UNAVAILABLE, "fh_device_create: hipGetSymbolAddress(scratch) failed: %s",
+                    hipGetErrorString(err));
+    }
+    dev->scratch = ptr;
+    return FH_OK;
+}
+
+}  // namespace fh
+
+namespace {
+
+// fh_decode_attention with its workspace either a caller allocation (checked
+// against the device's allocations) or the device's scratch array.
+int decode_attention(const char *fn, fh_device *dev, const uint16_t *qkv, int64_t batch, int64_t n_heads,
+                     int64_t n_kv, int64_t head_dim, const uint16_t *cos_tab, const uint16_t *sin_tab,
+                     int64_t table_len, const uint32_t *positions, uint16_t *k_cache, uint16_t *v_cache,
+                     int64_t max_len, float scale, void *workspace, uint64_t workspace_bytes, bool scratch_ws,
+                     uint16_t *out) {
     if (int rc = check_usable(dev, fn)) return rc;
     if (int rc = fh_check_dims(fn, {batch, n_heads, n_kv, head_dim, table_len, max_len})) return rc;
     if (batch == 0) return FH_OK;
     AttnLayout a;
-    if (int rc = check_attention(fn, dev, batch, n_heads, n_kv, head_dim, max_len, workspace, workspace_bytes, &a))
+    if (scratch_ws) {
+        if (int rc = check_heads(fn, n_heads, n_kv, head_dim)) return rc;
+        if (max_len == 0) return fail(FH_ERR_INVALID_ARGUMENT, "%s: empty KV cache", fn);
+        if (int rc = check_attn_size(fn, batch, n_heads, head_dim, max_len)) return rc;
+        const uint64_t need = attn_layout(batch, n_heads, n_kv, head_dim, max_len).total;
+        if (need > kScratchBytes)
+            return fail(FH_ERR_UNSUPPORTED,
+                        "%s: these sizes need a %llu-byte workspace; the static one holds %llu (use "
+                        "fh_decode_attention with a caller workspace)",
+                        fn, (unsigned long long)need, (unsigned long long)kScratchBytes);
+        if (!dev->scratch) return fail(FH_ERR_DEVICE_UNAVAILABLE, "%s: the device has no scratch address", fn);
+        workspace = dev->scratch;
+        workspace_bytes = kScratchBytes;
+    }
+    if (int rc = check_attention(fn, dev, batch, n_heads, n_kv, head_dim, max_len, workspace, workspace_bytes, &a,
+                                 !scratch_ws))
         return rc;
     if ((reinterpret_cast<uintptr_t>(qkv) | reinterpret_cast<uintptr_t>(cos_tab) |
          reinterpret_cast<uintptr_t>(sin_tab) | reinterpret_cast<uintptr_t>(k_cache) |
@@ -1405,9 +1449,33 @@ extern "C" int fh_decode_attention(fh_device *dev, const uint16_t *qkv, int64_t 
                      scale, static_cast<char *>(workspace), out};
     // short caches: one launch (no workspace use); otherwise scores, then P.V
     const bool short_cache = static_cast<uint64_t>(max_len) <= kDecodeShortMaxLen && head_dim != 256;
-    return dispatch(dev, fn, [&] {
+    dev->no_alloc = scratch_ws;
+    const int rc = dispatch(dev, fn, [&] {
         if (!short_cache ||
             !launch_decode_short_shape(head_dim, n_heads / n_kv, dev->stream, static_cast<uint32_t>(batch), x))
             launch_attention_shape<true>(head_dim, n_heads / n_kv, dev->stream, static_cast<uint32_t>(batch), a, x);
     });
+    dev->no_alloc = false;
+    return rc;
+}
+
+}  // namespace
+
+extern "C" int fh_decode_attention(fh_device *dev, const uint16_t *qkv, int64_t batch, int64_t n_heads,
+                                   int64_t n_kv, int64_t head_dim, const uint16_t *cos_tab,
+                                   const uint16_t *sin_tab, int64_t table_len, const uint32_t *positions,
+                                   uint16_t *k_cache, uint16_t *v_cache, int64_t max_len, float scale,
+                                   void *workspace, uint64_t workspace_bytes, uint16_t *out) {
+    return decode_attention("fh_decode_attention", dev, qkv, batch, n_heads, n_kv, head_dim, cos_tab, sin_tab,
+                            table_len, positions, k_cache, v_cache, max_len, scale, workspace, workspace_bytes, false,
+                            out);
+}
+
+extern "C" int fh_decode_attention_noalloc(fh_device *dev, const uint16_t *qkv, int64_t batch, int64_t n_heads,
+                                           int64_t n_kv, int64_t head_dim, const uint16_t *cos_tab,
+                                           const uint16_t *sin_tab, int64_t table_len, const uint32_t *positions,
+                                           uint16_t *k_cache, uint16_t *v_cache, int64_t max_len, float scale,
+                                           uint16_t *out) {
+    return decode_attention("fh_decode_attention_noalloc", dev, qkv, batch, n_heads, n_kv, head_dim, cos_tab,
+                            sin_tab, table_len, positions, k_cache, v_cache, max_len, scale, nullptr, 0, true, out);
 }

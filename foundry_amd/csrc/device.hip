@@ -70,6 +70,7 @@ hipEvent_t take_event(fh_device *dev) {
         dev->event_pool.pop_back();
         return e;
     }
+    if (dev->no_alloc) return nullptr;  // profiling skips this dispatch
     hipEvent_t e = nullptr;
     if (hipEventCreate(&e) != hipSuccess) return nullptr;
     return e;
@@ -236,6 +237,15 @@ static int create(int ordinal, int mode, fh_device **out, const char *fn) {
         delete dev;
         return fail(FH_ERR_ALLOCATION, "%s: the device's %llu-byte work areas could not be allocated", fn,
                     static_cast<unsigned long long>(kPackAreaBytes + kPartialAreaBytes));
+    }
+    if (int rc = attention_scratch_setup(dev)) {
+        hipFree(dev->pack_area);
+        hipFree(dev->partial_area);
+        hipEventDestroy(dev->timer_begin);
+        hipEventDestroy(dev->timer_end);
+        hipStreamDestroy(dev->stream);
+        delete dev;
+        return rc;
     }
     // the work areas are device memory the ops use: counted in the peaks
     dev->live_bytes = kPackAreaBytes + kPartialAreaBytes;

@@ -72,6 +72,11 @@ struct fh_device {
     std::map<uintptr_t, size_t> retired;
     std::vector<void *> deferred_frees;
     std::set<fh_graph *> graphs;
+    // this GPU's copy of the no-allocation entry point's static workspace
+    void *scratch = nullptr;
+    // set while an entry point that must not allocate dispatches: profiling
+    // then uses pooled events only
+    bool no_alloc = false;
     int profile_mode = FH_PROFILE_OFF;
     fh_profile counters{};
     // per-dispatch event pairs (KERNELS mode) or the span of a step (STEPS)
@@ -102,6 +107,10 @@ int device_error(fh_device *dev, hipError_t err, const char *fn, const char *cal
 // checks the launch status, and counts the dispatch.
 template <typename Launch>
 int dispatch(fh_device *dev, const char *fn, Launch &&launch);
+
+// Looks up this GPU's address of the static decode-attention workspace
+// (attention.hip); called by device creation with the device current.
+int attention_scratch_setup(fh_device *dev);
 
 // Writes nbytes of zeros at ptr on the device's stream with a kernel (not
 // hipMemsetAsync: a captured memset node is not reliable on replay).

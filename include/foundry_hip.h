@@ -353,6 +353,23 @@ int fh_decode_attention(fh_device *dev, const uint16_t *qkv, int64_t batch, int6
                         uint16_t *k_cache, uint16_t *v_cache, int64_t max_len, float scale,
                         void *workspace, uint64_t workspace_bytes, uint16_t *out);
 
+/* fh_decode_attention without a workspace argument, for callers that cannot
+ * allocate (code under graph capture, tight serving loops, harnesses that
+ * forbid allocation). No counterpart in the reference. The workspace is a
+ * static array of FH_DECODE_SCRATCH_BYTES in device memory, one per GPU,
+ * held from the library's first use on that GPU until the process ends; this
+ * call allocates nothing (on a profiled device it records only pooled
+ * events). Sizes whose workspace (fh_decode_attention_workspace) exceeds it
+ * return FH_ERR_UNSUPPORTED. Every call on one GPU shares the array: calls
+ * that overlap on one GPU (from two fh_devices' streams) race. The workspace
+ * needs no initial contents, so nothing is cleared between calls. */
+#define FH_DECODE_SCRATCH_BYTES (32ull << 20)
+int fh_decode_attention_noalloc(fh_device *dev, const uint16_t *qkv, int64_t batch, int64_t n_heads,
+                                int64_t n_kv, int64_t head_dim, const uint16_t *cos_tab,
+                                const uint16_t *sin_tab, int64_t table_len, const uint32_t *positions,
+                                uint16_t *k_cache, uint16_t *v_cache, int64_t max_len, float scale,
+                                uint16_t *out);
+
 /* Decode-step fusions of the q4 Linear (m <= 8 rows, the GEMV; larger m
  * returns FH_ERR_UNSUPPORTED -- use the unfused ops). Same arithmetic as the
  * unfused sequence, with no intermediate tensor in memory:
