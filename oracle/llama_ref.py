@@ -8,8 +8,13 @@ tensor dtype, bf16):
 - RmsNorm (src/nn/norm.rs:32-50): fp32 sum of squares, scale =
   reciprocal(sqrt(ss * (1/dim) + eps)), y = RNE(RNE(x * scale) * w).
 - Linear (src/nn/linear.rs:22-35 -> matmul_tiled): fp32 accumulation of
-  x . (s*q + b), RNE output. (numpy's sgemm sums in a different order than
-  matmul_tiled's sequential k; within fp32 accumulation error.)
+  x . w, RNE output. (numpy's sgemm sums in a different order than
+  matmul_tiled's sequential k; within fp32 accumulation error.) w is the
+  weight value the q4 path is specified to consume: a call of at most
+  GEMV_MAX_ROWS rows (the decode GEMV) dequantises in registers to the fp32
+  s*q + b; a longer call (the prefill GEMM) feeds bf16 matrix cores with
+  dequantised tiles, i.e. the materialised bf16 weight RNE(s*q + b). `rows`
+  is the row count of the linear call the model makes (batch x tokens).
 - RoPE (src/models/llama/rotary_emb.rs:62-85): rot = cat(-x2, x1),
   RNE(RNE(x*cos) + RNE(rot*sin)); tables RNE(cos/sin(pos * inv_freq)) with
   the llama3 frequency scaling (:135-186).
@@ -29,6 +34,9 @@ RmsNorm, SiLU and SDPA.
 from __future__ import annotations
 
 import numpy as np
+
+# fh_q4_matmul runs the GEMV up to this many rows and the GEMM above.
+GEMV_MAX_ROWS = 8
 
 
 def rne(x) -> np.ndarray:
@@ -137,6 +145,7 @@ class RefLlama:
         scaling = None if sc is None else (sc.factor, sc.low_freq_factor, sc.high_freq_factor,
                                            sc.original_max_position_embeddings)
         self.cos, self.sin = rope_tables(cfg.head_dim, cfg.rope_theta, scaling, max_len)
+        self._bf16 = {}  # id(fp32 weights) -> their materialised bf16 values, for GEMM-sized calls
         self.reset()
 
     def reset(self):
@@ -147,8 +156,16 @@ class RefLlama:
     def rms_norm(self, h, w):
         return rms_norm(h, w, self.cfg.rms_norm_eps)
 
-    @staticmethod
-    def linear(x, w):
+    def linear(self, x, w, rows=None):
+        """RNE(x . w^T) in fp32, with w the fp32 dequantised weights for a
+        call of at most GEMV_MAX_ROWS rows (default: x's rows) and the
+        materialised bf16 weights RNE(w) above."""
+        rows = x.shape[0] if rows is None else rows
+        if rows > GEMV_MAX_ROWS:
+            key = id(w)
+            if key not in self._bf16:
+                self._bf16[key] = rne(w)
+            w = self._bf16[key]
         return rne(x @ w.T)
 
     def rope(self, x, pos):
@@ -157,17 +174,20 @@ class RefLlama:
         c, s = self.cos[pos][:, None, :], self.sin[pos][:, None, :]
         return rne(rne(x * c) + rne(rot * s))
 
-    def forward(self, ids, positions):
-        """Returns the last position's logits (float32 of bf16 values)."""
+    def forward(self, ids, positions, batch=1):
+        """Returns the last position's logits (float32 of bf16 values). The
+        sequence is one of `batch` run together: every linear call has batch
+        x len(ids) rows, the LM head `batch` (one last row per sequence)."""
         c = self.cfg
         t = len(ids)
+        rows = batch * t
         pos = np.asarray(positions)
         h = rne(self.embed_f[np.asarray(ids)])
         group = c.n_heads // c.n_kv_heads
         scale = np.float32(1.0) / np.sqrt(np.float32(c.head_dim), dtype=np.float32)
         for li, L in enumerate(self.layers):
             x = self.rms_norm(h, L["input_norm"])
-            qkv = self.linear(x, L["qkv"])
+            qkv = self.linear(x, L["qkv"], rows)
             hq, hk = c.n_heads * c.head_dim, c.n_kv_heads * c.head_dim
             q = qkv[:, :hq].reshape(t, c.n_heads, c.head_dim)
             k = qkv[:, hq:hq + hk].reshape(t, c.n_kv_heads, c.head_dim)
@@ -180,30 +200,36 @@ class RefLlama:
             for hh in range(c.n_heads):
                 kv = hh // group
                 out[:, hh, :] = sdpa(q[:, hh, :], self.k[li][kv, :ctx, :], self.v[li][kv, :ctx, :], pos, scale)
-            a = self.linear(out.reshape(t, -1), L["o"])
+            a = self.linear(out.reshape(t, -1), L["o"], rows)
             h = rne(h + a)
             x = self.rms_norm(h, L["post_norm"])
-            gu = self.linear(x, L["gate_up"])
+            gu = self.linear(x, L["gate_up"], rows)
             act = silu_mul(gu[:, :c.ffn], gu[:, c.ffn:])
-            h = rne(h + self.linear(act, L["down"]))
+            h = rne(h + self.linear(act, L["down"], rows))
         x = self.rms_norm(h, self.final_norm)
-        return self.linear(x[-1:], self.embed_f)[0]
+        return self.linear(x[-1:], self.embed_f, batch)[0]
 
-    def generate(self, prompt, new_tokens, top_k=5):
+    def generate(self, prompt, new_tokens, top_k=5, batch=1):
         """Greedy tokens and, per step, the top-k ids (ranked by logit, then
-        by the lowest id)."""
+        by the lowest id); `batch` as in forward."""
+        import time
+
         self.reset()
         ids = list(int(i) for i in prompt)
-        logits = self.forward(ids, np.arange(len(ids)))
+        t0 = time.perf_counter()
+        logits = self.forward(ids, np.arange(len(ids)), batch)
+        self.prefill_s = time.perf_counter() - t0
         self.first_logits = logits
         tokens, tops = [], []
+        t0 = time.perf_counter()
         for step in range(new_tokens):
             tokens.append(argmax(logits))
             tops.append(top_ids(logits, top_k))
             if step + 1 == new_tokens:
                 break
             p = len(prompt) + step
-            logits = self.forward([tokens[-1]], np.array([p]))
+            logits = self.forward([tokens[-1]], np.array([p]), batch)
+        self.decode_s = time.perf_counter() - t0  # new_tokens - 1 single-token forwards
         return np.array(tokens, dtype=np.uint32), tops
 
 

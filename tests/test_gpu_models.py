@@ -18,6 +18,10 @@ Bars (written here, per test):
   max|logit| on config 4: one bf16 ulp of the largest logits (0.125 at
   35.25). The GPU sums in other orders again; the bar is about four such
   ulps.
+- zero-mean weights (below): ZERO_MEAN_LOGIT_BAR = 0.2. There the softmax
+  amplifies every rounding difference: the same float32-against-float64
+  change moves the restatement's config-4 logits by 6.9e-2 of max|logit|;
+  the bar is three times that.
 - top-5 sets equal, except ids whose reference logit lies within the logits
   bar of the fifth largest (a near tie may order either way).
 - greedy tokens "close" by the reference's rule with top-k 5.
@@ -26,6 +30,14 @@ The task's random-init weights (b = -8 s + N(0, 1e-3)) have mean -s/2, which
 makes every greedy step pick the same id; the greedy comparison therefore
 also runs on zero-mean weights (b = -7.5 s + N(0, 1e-3)), where the chosen
 ids change from step to step.
+
+The restatement's linears take the weight value each kernel consumes: fp32
+s*q + b in the decode GEMV (calls of at most 8 rows), the materialised bf16
+RNE(s*q + b) in the prefill GEMM's matrix-core tiles. With zero-mean weights
+the softmax amplifies that difference: against fp32 weights throughout, the
+bf16 prefill weights alone move config 4's first-step logits by 0.38 of
+max|logit| (measured on the restatement itself: 3.6e-2 after one layer,
+7.6e-2 after two).
 """
 import json
 import os
@@ -41,6 +53,9 @@ pytestmark = pytest.mark.gpu
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 LOGIT_BAR = 1.5e-2
+# zero-mean weights: the restatement moves by 6.9e-2 of max|logit| on config 4
+# between float32 and float64 products (same weights), three times that
+ZERO_MEAN_LOGIT_BAR = 0.2
 
 C4 = LlamaConfig.llama_3_2_3b()
 C5 = LlamaConfig.llama_3_1_8b()
@@ -61,11 +76,11 @@ def logits_err(got, want) -> float:
     return float(np.max(np.abs(got - want)) / np.max(np.abs(want)))
 
 
-def assert_top5(got, want, what):
+def assert_top5(got, want, what, bar=LOGIT_BAR):
     g, w = R.top_ids(np.asarray(got, np.float32), 5), R.top_ids(np.asarray(want, np.float32), 5)
     want = np.asarray(want, np.float64)
     fifth = np.sort(want)[-5]
-    slack = LOGIT_BAR * np.max(np.abs(want))
+    slack = bar * np.max(np.abs(want))
     for i in set(g) ^ set(w):
         assert abs(want[i] - fifth) <= slack, f"{what}: top-5 {g} against {w}"
 
@@ -112,7 +127,8 @@ def test_config4_greedy_agreement_on_zero_mean_weights(device):
     report = R.compare_generation(got, gpu_tops(model, prompt, got), exp_tokens, exp_tops)
     print(f"[config 4 greedy, zero-mean weights] gpu={got.tolist()} ref={exp_tokens.tolist()} "
           f"distinct={len(set(got.tolist()))} first-step err {err:.3e} {report}", flush=True)
-    assert err <= LOGIT_BAR
+    assert err <= ZERO_MEAN_LOGIT_BAR
+    assert_top5(first, ref.first_logits, "config 4 zero-mean", ZERO_MEAN_LOGIT_BAR)
     assert report["close"], report
 
 
@@ -138,10 +154,10 @@ def test_config5_two_layers_decode_step_matches_the_restatement(device):
     for s in (0, 7):
         ref.reset()
         full = np.concatenate([depth[s], prompt[s]])
-        first = ref.forward(list(full), np.arange(d + p))
+        first = ref.forward(list(full), np.arange(d + p), batch=8)
         assert R.argmax(first) == int(got[s, 0]) or abs(float(first[got[s, 0]]) - float(np.max(first))) <= \
             LOGIT_BAR * np.max(np.abs(first)), f"sequence {s}: first token {got[s, 0]}"
-        want = ref.forward([int(got[s, 0])], np.array([d + p]))
+        want = ref.forward([int(got[s, 0])], np.array([d + p]), batch=8)
         err = logits_err(decode_logits[s], want)
         print(f"[config 5, 2 layers, seq {s}] decode-step logits err {err:.3e}; top5 gpu "
               f"{R.top_ids(decode_logits[s], 5)} ref {R.top_ids(want, 5)}", flush=True)

@@ -323,3 +323,24 @@ def test_rope_pins_reject_planted_rotations():
         assert not np.array_equal(bad, good), name
         assert bad[3] != -m.sin[9, 3] or bad[32 + 3] != m.cos[9, 3], name
     assert good[3] == -m.sin[9, 3] and good[32 + 3] == m.cos[9, 3]
+
+
+def test_linear_takes_each_kernels_weight_value():
+    """Up to 8 rows (the decode GEMV) the fp32 dequantised s*q + b; from 9
+    rows (the prefill GEMM's bf16 tiles) the materialised RNE(s*q + b). Both
+    within fp32 accumulation error of float64 on the matching weights, and
+    not of the other: the rule is what tells the two apart."""
+    m, *_ = _tiny_model()
+    rng = np.random.default_rng(11)
+    w = R.dequant_f32(*synth.q4_weights(12, 64, 256, centre=7.5))
+    assert np.mean(R.rne(w) != w) > 0.3  # the weights do round
+    for rows, weights in ((1, w), (8, w), (9, R.rne(w)), (40, R.rne(w))):
+        x = R.rne(rng.standard_normal((rows, 256)).astype(np.float32))
+        got = m.linear(x, w).astype(np.float64)
+        want = x.astype(np.float64) @ weights.astype(np.float64).T
+        other = x.astype(np.float64) @ (R.rne(w) if weights is w else w).astype(np.float64).T
+        assert np.all(_ulp_close(got, want) | (np.abs(got - want) <= 1e-5 * np.max(np.abs(want)))), rows
+        assert np.mean(_ulp_close(got, other, 0.5)) < 0.9, rows
+    # the row count of the model's call, not of x, decides (a batch of sequences)
+    x = R.rne(rng.standard_normal((1, 256)).astype(np.float32))
+    assert np.array_equal(m.linear(x, w, rows=16), R.rne(x @ R.rne(w).T))
