@@ -10,12 +10,28 @@ replayed as one HIP graph; event timing on the device's stream brackets the K
 timed steps. Algorithmic bytes per launch: 12,582,912 (nibbles) + 1,572,864
 (scales + biases) + 6,144 (x) + 16,384 (y) = 14,178,304.
 
-Secondary lines (same method): the LM-head GEMV (N=128256, K=3072), the q4
-embedding gather at B=4096 and the two config-3 prefill GEMMs.
+Every graph is also replayed MEDIAN_REPLAYS more times, each replay timed
+on its own with a pair of HIP events on the device's stream (the replays are
+enqueued back to back), and the median replay is reported per launch
+(``median_us_per_launch``).
+
+Secondary lines (same method): the GEMV warm (one weight copy, in the MALL);
+the LM-head GEMV (N=128256, K=3072) cold (3 copies, 665 MB) and warm (one);
+the q4 embedding gather at B = 4096, 64 and 1, cold (3 tables, distinct ids)
+and warm (one table, the same ids); the two config-3 prefill GEMMs; the
+launch and read floors (an almost empty kernel; fh_read_probe reading a
+GEMV's bytes per launch, and 1 GiB); config 4 (Llama-3.2-3B shape: prefill
+and greedy decode tok/s, with greedy agreement and first-step logits against
+the CPU restatement, whose own tok/s is reported) and config 5 (8B shape,
+batch 8 at context 4096, with batch-invariance and 2-layer restatement
+logits checks).
 
 cpu_baseline: the reference arithmetic (oracle/liboracle.so: fp32 dequant,
 sequential-k fp32 accumulation, bf16 RNE) on the config-1 GEMV, on this
 host's cores, for a bounded number of calls.
+
+Single legs, for kernel traces and counters: --gemm-only, --floors-only,
+--decode-only, --batched-only.
 """
 from __future__ import annotations
 
@@ -73,8 +89,67 @@ def q4_matmul(dev, x_ptr, m, k, w_ptrs, n, y_ptr, y_dtype=_lib.BF16):
               n, 64, ctypes.c_void_p(y_ptr), y_dtype)
 
 
-def timed_graph(dev: HipDevice, enqueue, steps: int, warmup: int) -> float:
-    """Captures enqueue() as one graph; returns ms per replay over `steps`."""
+class StreamEvents:
+    """HIP event pairs recorded on the device's own stream around individual
+    graph replays that are enqueued back to back (no host wait between them),
+    so each span is one replay's GPU time."""
+
+    def __init__(self, dev: HipDevice, pairs: int):
+        self.hip = ctypes.CDLL("libamdhip64.so")
+        self.hip.hipEventCreate.argtypes = [ctypes.POINTER(ctypes.c_void_p)]
+        self.hip.hipEventRecord.argtypes = [ctypes.c_void_p, ctypes.c_void_p]
+        self.hip.hipEventElapsedTime.argtypes = [ctypes.POINTER(ctypes.c_float), ctypes.c_void_p, ctypes.c_void_p]
+        self.hip.hipEventDestroy.argtypes = [ctypes.c_void_p]
+        self.stream = ctypes.c_void_p()
+        _lib.call("fh_device_stream", dev.handle, ctypes.byref(self.stream))
+        self.events = []
+        for _ in range(2 * pairs):
+            e = ctypes.c_void_p()
+            if self.hip.hipEventCreate(ctypes.byref(e)) != 0:
+                raise RuntimeError("hipEventCreate failed")
+            self.events.append(e)
+
+    def record(self, i: int) -> None:
+        if self.hip.hipEventRecord(self.events[i], self.stream) != 0:
+            raise RuntimeError("hipEventRecord failed")
+
+    def spans_ms(self, pairs: int) -> list:
+        out = []
+        for i in range(pairs):
+            ms = ctypes.c_float()
+            if self.hip.hipEventElapsedTime(ctypes.byref(ms), self.events[2 * i], self.events[2 * i + 1]) != 0:
+                raise RuntimeError("hipEventElapsedTime failed")
+            out.append(ms.value)
+        return out
+
+    def close(self) -> None:
+        for e in self.events:
+            self.hip.hipEventDestroy(e)
+        self.events = []
+
+
+def median_replay_ms(dev: HipDevice, graph, replays: int) -> float:
+    """Median GPU time of `replays` individually timed replays of a graph."""
+    ev = StreamEvents(dev, replays)
+    try:
+        for i in range(replays):
+            ev.record(2 * i)
+            graph.launch()
+            ev.record(2 * i + 1)
+        dev.synchronize()
+        spans = sorted(ev.spans_ms(replays))
+    finally:
+        ev.close()
+    return spans[len(spans) // 2]
+
+
+MEDIAN_REPLAYS = 60
+
+
+def timed_graph(dev: HipDevice, enqueue, steps: int, warmup: int, median_replays: int = MEDIAN_REPLAYS):
+    """Captures enqueue() as one graph. Returns (ms per replay over `steps`
+    timed together, median ms of `median_replays` individually timed
+    replays)."""
     dev.capture_begin()
     enqueue()
     graph = dev.capture_end()
@@ -86,43 +161,68 @@ def timed_graph(dev: HipDevice, enqueue, steps: int, warmup: int) -> float:
         graph.launch()
     ms = dev.timer_end()
     dev.synchronize()
-    return ms / steps
+    med = median_replay_ms(dev, graph, median_replays) if median_replays else None
+    return ms / steps, med
 
 
-def bench_gemv(dev, n, k, copies, steps, warmup, seed):
+def bench_gemv(dev, n, k, copies, steps, warmup, seed, launches=None):
+    """`launches` GEMVs per replay (default one per copy), cycling through
+    `copies` distinct weight copies: cold when the copies exceed the 256 MB
+    last-level cache (MALL), warm with one copy."""
     w = Weights(dev, n, k, copies, seed)
     x = dev.storage_from_bytes(synth.bf16_normal(seed + 1, (1, k)).tobytes())
     y = dev.empty(2 * n)
+    launches = launches or copies
 
     def enqueue():
-        for p in w.ptrs:
-            q4_matmul(dev, x.ptr, 1, k, p, n, y.ptr)
+        for i in range(launches):
+            q4_matmul(dev, x.ptr, 1, k, w.ptrs[i % copies], n, y.ptr)
 
-    ms_step = timed_graph(dev, enqueue, steps, warmup)
-    per_launch_ms = ms_step / copies
+    ms_step, med_step = timed_graph(dev, enqueue, steps, warmup)
+    per_launch_ms = ms_step / launches
     gbs = gemv_bytes(1, n, k) / (per_launch_ms * 1e-3) / 1e9
-    return {"n": n, "k": k, "copies": copies, "weight_bytes_total": copies * gemv_bytes(1, n, k),
+    med_us = med_step / launches * 1e3
+    return {"n": n, "k": k, "copies": copies, "launches_per_replay": launches,
+            "distinct_weight_bytes": copies * gemv_bytes(1, n, k),
             "us_per_launch": per_launch_ms * 1e3, "GB_per_s": gbs, "frac_hbm_peak": gbs / HBM_PEAK_GBS,
-            "ms_per_step": ms_step}
+            "median_us_per_launch": med_us, "median_GB_per_s": gemv_bytes(1, n, k) / (med_us * 1e-6) / 1e9,
+            "median_over_replays": MEDIAN_REPLAYS, "ms_per_step": ms_step}
 
 
-def bench_embed(dev, batch, steps, warmup, seed):
+_TABLES: dict = {}
+
+
+def bench_embed(dev, batch, steps, warmup, seed, tables=1, reps=12):
+    """Config 2: the q4 gather of `batch` ids from a [128256, 3072] table.
+    Each replay runs `reps` gathers, gather i from table i % tables with its
+    own ids: cold with 3 tables (663 MB, more than the MALL holds), warm with
+    one table and one id set repeated."""
     rows, k = 128256, 3072
-    wq, s, b = synth.q4_weights(seed, rows, k)
-    sts = [dev.storage_from_bytes(a.tobytes()) for a in (wq, s, b)]
-    ids = dev.storage_from_bytes(synth.token_ids(seed, batch, rows).tobytes())
+    if (seed, rows, k) not in _TABLES:
+        _TABLES[(seed, rows, k)] = synth.q4_weights(seed, rows, k)
+    base = _TABLES[(seed, rows, k)]
+    tabs = []
+    for c in range(tables):
+        wq = base[0] ^ np.uint32((0x9E3779B9 * (c + 1)) & 0xFFFFFFFF) if c else base[0]
+        tabs.append([dev.storage_from_bytes(np.ascontiguousarray(a).tobytes()) for a in (wq, base[1], base[2])])
+    id_sets = [dev.storage_from_bytes(synth.token_ids(seed + (i if tables > 1 else 0), batch, rows).tobytes())
+               for i in range(reps if tables > 1 else 1)]
     out = dev.empty(batch * k * 2)
-    reps = 8
 
     def enqueue():
-        for _ in range(reps):
+        for i in range(reps):
+            sts = tabs[i % tables]
+            ids = id_sets[i % len(id_sets)]
             _lib.call("fh_q4_embed", dev.handle, *[ctypes.c_void_p(st.ptr) for st in sts], rows, k, 64,
                       ctypes.c_void_p(ids.ptr), batch, ctypes.c_void_p(out.ptr))
 
-    ms = timed_graph(dev, enqueue, steps, warmup) / reps
+    ms_step, med_step = timed_graph(dev, enqueue, steps, warmup)
+    ms, med = ms_step / reps, med_step / reps
     gbs = embed_bytes(batch, k) / (ms * 1e-3) / 1e9
-    return {"batch": batch, "us_per_launch": ms * 1e3, "GB_per_s": gbs, "frac_hbm_peak": gbs / HBM_PEAK_GBS,
-            "note": "table rows re-read across repeats may hit L2/MALL"}
+    return {"batch": batch, "tables": tables, "us_per_launch": ms * 1e3, "GB_per_s": gbs,
+            "frac_hbm_peak": gbs / HBM_PEAK_GBS, "median_us_per_launch": med * 1e3,
+            "median_GB_per_s": embed_bytes(batch, k) / (med * 1e-3) / 1e9,
+            "cache": "cold (3 tables, distinct ids per launch)" if tables > 1 else "warm (one table, same ids)"}
 
 
 def bench_gemm(dev, m, n, k, steps, warmup, seed):
@@ -135,10 +235,44 @@ def bench_gemm(dev, m, n, k, steps, warmup, seed):
         for _ in range(reps):
             q4_matmul(dev, x.ptr, m, k, w.ptrs[0], n, y.ptr)
 
-    ms = timed_graph(dev, enqueue, steps, warmup) / reps
+    ms_step, med_step = timed_graph(dev, enqueue, steps, warmup)
+    ms, med = ms_step / reps, med_step / reps
     tflops = 2.0 * m * n * k / (ms * 1e-3) / 1e12
     return {"m": m, "n": n, "k": k, "us_per_launch": ms * 1e3, "TFLOP_per_s": tflops,
-            "frac_bf16_peak": tflops / BF16_PEAK_TFLOPS}
+            "frac_bf16_peak": tflops / BF16_PEAK_TFLOPS, "median_us_per_launch": med * 1e3,
+            "median_TFLOP_per_s": 2.0 * m * n * k / (med * 1e-3) / 1e12}
+
+
+def bench_floors(dev, steps, warmup):
+    """What one launch costs before its bytes: an almost empty kernel
+    (fh_advance_positions on one word) replayed 200 times per graph, and
+    fh_read_probe (16-byte loads, nothing else) reading one config-1 GEMV's
+    worth of bytes (14,178,304) per launch over 48 distinct buffers, and a
+    1 GiB buffer per launch (the sustained read rate)."""
+    pos = dev.zeros(4)
+
+    def tiny():
+        for _ in range(200):
+            _lib.call("fh_advance_positions", dev.handle, ctypes.c_void_p(pos.ptr), 1, 1)
+
+    tiny_ms, tiny_med = timed_graph(dev, tiny, steps, warmup)
+    out = {"empty_kernel_us": tiny_ms / 200 * 1e3, "empty_kernel_median_us": tiny_med / 200 * 1e3}
+    for label, nbytes, copies in (("gemv_bytes", gemv_bytes(1, 8192, 3072) // 16 * 16, 48), ("1GiB", 1 << 30, 2)):
+        blocks = ctypes.c_uint64()
+        _lib.call("fh_read_probe_blocks", nbytes, ctypes.byref(blocks))
+        bufs = [dev.zeros(nbytes) for _ in range(copies)]
+        sink = dev.empty(blocks.value * 4)
+
+        def reads():
+            for b in bufs:
+                _lib.call("fh_read_probe", dev.handle, ctypes.c_void_p(b.ptr), nbytes, ctypes.c_void_p(sink.ptr))
+
+        ms, med = timed_graph(dev, reads, steps, warmup)
+        out[f"read_{label}"] = {"bytes_per_launch": nbytes, "buffers": copies, "us_per_launch": ms / copies * 1e3,
+                                "GB_per_s": nbytes / (ms / copies * 1e-3) / 1e9,
+                                "median_us_per_launch": med / copies * 1e3}
+        del bufs
+    return out
 
 
 def cpu_baseline(seconds: float = 12.0):
@@ -240,8 +374,45 @@ def bench_decode(dev, new_tokens: int, agreement: int, seed: int = 0):
     return out
 
 
+def config5_parity(dev, cfg, seed, depth_ids, prompt_ids, first8, max_len):
+    """Config 5's logits against two references, for sequence 0:
+    - batch invariance: the bench model's prefill logits at batch 8 against
+      the same sequence run alone at batch 1 (all 32 layers; rows of a batch
+      are independent in the reference);
+    - the restatement (oracle/llama_ref.py): a 2-layer model of the same
+      shapes at batch 8 and context 4096, its decode step's logits."""
+    from foundry_amd.llama import LlamaConfig, Q4Llama, embed_weights, final_norm_weight, layer_weights
+    from oracle import llama_ref as R  # checker only
+
+    def err(a, b):
+        a, b = np.asarray(a, np.float64), np.asarray(b, np.float64)
+        return float(np.max(np.abs(a - b)) / np.max(np.abs(b)))
+
+    d, p = depth_ids.shape[1], prompt_ids.shape[1]
+    t0 = time.perf_counter()
+    one = Q4Llama(dev, cfg, seed, max_len, max_tokens=p, batch=1)
+    one.generate(prompt_ids[:1], 1, depth=depth_ids[:1])
+    first1 = R.from_bf16(one.logits())
+    del one
+    out = {"batch_invariance_seq0_prefill_logits_err": err(first8[0], first1),
+           "batch_invariance_bit_identical_fraction": float(np.mean(first8[0] == first1))}
+    two = LlamaConfig(2, cfg.hidden, cfg.n_heads, cfg.n_kv_heads, cfg.head_dim, cfg.ffn, cfg.vocab)
+    m2 = Q4Llama(dev, two, seed, max_len, max_tokens=p, batch=depth_ids.shape[0])
+    got = m2.generate(prompt_ids, 2, depth=depth_ids)
+    step_logits = R.from_bf16(m2.logits())[0]
+    del m2
+    ref = R.RefLlama(two, embed_weights(two, seed), [layer_weights(two, seed, l) for l in range(2)],
+                     final_norm_weight(two, seed), max_len)
+    ref.forward(list(np.concatenate([depth_ids[0], prompt_ids[0]])), np.arange(d + p), batch=depth_ids.shape[0])
+    want = ref.forward([int(got[0, 0])], np.array([d + p]), batch=depth_ids.shape[0])
+    out["restatement_2_layer_decode_step_logits_err"] = err(step_logits, want)
+    out["restatement_2_layer_top5_equal"] = R.top_ids(step_logits, 5) == R.top_ids(want, 5)
+    out["s"] = time.perf_counter() - t0
+    return out
+
+
 def bench_decode_batched(dev, new_tokens: int, seed: int = 0, batch: int = 8, depth: int = 2048,
-                         prompt_len: int = 2048):
+                         prompt_len: int = 2048, parity: bool = True):
     """Config 5: Llama-3.1-8B-shaped random-init q4 decoder (32 layers,
     hidden 4096, 32/8 heads, FFN 14336, vocab 128256; the q4 table is tied as
     the reference's model requires, src/models/llama/config.rs:177-180) over
@@ -273,6 +444,7 @@ def bench_decode_batched(dev, new_tokens: int, seed: int = 0, batch: int = 8, de
     dev.timer_begin()
     model.step(prompt_ids, depth)
     prefill_ms = dev.timer_end()
+    first8 = (model.logits().astype(np.uint32) << 16).view(np.float32) if parity else None
     first = np.empty(batch, dtype=np.uint32)
     _lib.call("fh_download", dev.handle, first.ctypes.data_as(ctypes.c_void_p), ctypes.c_void_p(model.buf["next"].ptr),
               first.nbytes)
@@ -302,6 +474,7 @@ def bench_decode_batched(dev, new_tokens: int, seed: int = 0, batch: int = 8, de
         "decode_ceiling_tokens_per_s_at_peak": batch * HBM_PEAK_GBS * 1e9 / step_bytes,
         "model_build_s": build_s,
         "first_tokens": tokens[:, :4].tolist(),
+        **({"parity": config5_parity(dev, cfg, seed, depth_ids, prompt_ids, first8, max_len)} if parity else {}),
     }
 
 
@@ -315,6 +488,7 @@ def greedy_agreement(model, cfg, seed, prompt, tokens, n):
     t0 = time.perf_counter()
     layers = [layer_weights(cfg, seed, l) for l in range(cfg.n_layers)]
     ref = R.RefLlama(cfg, embed_weights(cfg, seed), layers, final_norm_weight(cfg, seed), len(prompt) + n)
+    build_s = time.perf_counter() - t0
     exp_tokens, exp_tops = ref.generate(prompt, n)
     got = tokens[:n]
     # first-step logits after the prompt, beside the token rule (random-init
@@ -335,6 +509,11 @@ def greedy_agreement(model, cfg, seed, prompt, tokens, n):
         report = R.compare_generation(got, gpu_tops, exp_tokens, exp_tops)
     report["first_step"] = first_step
     report["cpu_s"] = time.perf_counter() - t0
+    # the restatement's own speed on this host (numpy fp32, one process)
+    report["cpu_reference"] = {"threads": int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1)),
+                               "build_s": build_s, "prefill_s": ref.prefill_s,
+                               "prefill_tok_s": len(prompt) / ref.prefill_s,
+                               "decode_tok_s": (n - 1) / ref.decode_s if n > 1 else None}
     report["gpu_tokens"] = got.tolist()
     report["reference_arithmetic_tokens"] = exp_tokens.tolist()
     return report
@@ -388,13 +567,18 @@ def main() -> int:
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="also run one device copy of known size (counter calibration)")
     ap.add_argument("--decode-tokens", type=int, default=256, help="config-4 greedy steps (0 skips)")
-    ap.add_argument("--agreement", type=int, default=0,
-                    help="compare the first N config-4 tokens with the CPU reference arithmetic")
+    ap.add_argument("--agreement", type=int, default=16,
+                    help="compare the first N config-4 tokens with the CPU restatement (0 skips)")
+    ap.add_argument("--no-parity", action="store_true", help="skip config 5's logits checks")
     ap.add_argument("--decode-only", action="store_true",
                     help="only the config-4 decode (for a kernel trace of the step); prints its JSON")
     ap.add_argument("--batched-tokens", type=int, default=32,
                     help="config-5 greedy steps per sequence (8B shape, batch 8, context 4096; 0 skips)")
     ap.add_argument("--batched-only", action="store_true", help="only the config-5 run; prints its JSON")
+    ap.add_argument("--gemm-only", action="store_true",
+                    help="only the two config-3 GEMMs (for kernel traces and counters); prints their JSON")
+    ap.add_argument("--floors-only", action="store_true",
+                    help="only the launch and read floors; prints their JSON")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not supported "
@@ -404,31 +588,53 @@ def main() -> int:
     if args.calibrate_copy:
         calibrate_copy()
     dev = HipDevice(0)
-    if args.decode_only or args.batched_only:
-        d = (bench_decode(dev, max(2, args.decode_tokens), args.agreement) if args.decode_only
-             else bench_decode_batched(dev, max(2, args.batched_tokens)))
+    small = max(5, args.steps // 5)
+    if args.decode_only or args.batched_only or args.gemm_only or args.floors_only:
+        if args.decode_only:
+            d = bench_decode(dev, max(2, args.decode_tokens), args.agreement)
+        elif args.batched_only:
+            d = bench_decode_batched(dev, max(2, args.batched_tokens), parity=not args.no_parity)
+        elif args.gemm_only:
+            d = {"gemm_gate_up": bench_gemm(dev, 2048, 8192, 3072, args.steps, args.warmup, seed=7),
+                 "gemm_down": bench_gemm(dev, 2048, 3072, 8192, args.steps, args.warmup, seed=9)}
+        else:
+            d = bench_floors(dev, args.steps, args.warmup)
         dev.close()
         print(json.dumps(d), flush=True)
         return 0
     head = bench_gemv(dev, 8192, 3072, args.copies, args.steps, args.warmup, seed=1)
-    print(f"[bench] gemv 8192x3072: {head['us_per_launch']:.2f} us/launch, {head['GB_per_s']:.0f} GB/s", flush=True)
+    print(f"[bench] gemv 8192x3072: {head['us_per_launch']:.2f} us/launch, {head['GB_per_s']:.0f} GB/s "
+          f"(median {head['median_us_per_launch']:.2f} us)", flush=True)
     secondary = {}
     if not args.quick:
-        secondary["lm_head_gemv"] = bench_gemv(dev, 128256, 3072, 3, max(5, args.steps // 5), 2, seed=3)
-        print(f"[bench] lm head: {secondary['lm_head_gemv']['GB_per_s']:.0f} GB/s", flush=True)
-        secondary["embed_b4096"] = bench_embed(dev, 4096, max(5, args.steps // 5), 2, seed=5)
-        secondary["embed_b1"] = bench_embed(dev, 1, max(5, args.steps // 5), 2, seed=5)
-        print(f"[bench] embed: {secondary['embed_b4096']['GB_per_s']:.0f} GB/s", flush=True)
-        secondary["gemm_gate_up"] = bench_gemm(dev, 2048, 8192, 3072, max(5, args.steps // 5), 2, seed=7)
-        secondary["gemm_down"] = bench_gemm(dev, 2048, 3072, 8192, max(5, args.steps // 5), 2, seed=9)
-        print(f"[bench] gemm: {secondary['gemm_gate_up']['TFLOP_per_s']:.0f} TFLOP/s", flush=True)
+        secondary["gemv_warm"] = bench_gemv(dev, 8192, 3072, 1, small, 2, seed=1, launches=args.copies)
+        secondary["lm_head_gemv_cold"] = bench_gemv(dev, 128256, 3072, 3, small, 2, seed=3)
+        secondary["lm_head_gemv_warm"] = bench_gemv(dev, 128256, 3072, 1, small, 2, seed=3, launches=3)
+        print(f"[bench] gemv warm {secondary['gemv_warm']['GB_per_s']:.0f} GB/s; lm head cold "
+              f"{secondary['lm_head_gemv_cold']['GB_per_s']:.0f}, warm {secondary['lm_head_gemv_warm']['GB_per_s']:.0f} GB/s",
+              flush=True)
+        for b in (4096, 64, 1):
+            for tables, tag in ((3, "cold"), (1, "warm")):
+                secondary[f"embed_b{b}_{tag}"] = bench_embed(dev, b, small, 2, seed=5, tables=tables)
+        print(f"[bench] embed B=4096: cold {secondary['embed_b4096_cold']['GB_per_s']:.0f}, warm "
+              f"{secondary['embed_b4096_warm']['GB_per_s']:.0f} GB/s; B=64 cold "
+              f"{secondary['embed_b64_cold']['median_us_per_launch']:.2f} us", flush=True)
+        secondary["gemm_gate_up"] = bench_gemm(dev, 2048, 8192, 3072, small, 2, seed=7)
+        secondary["gemm_down"] = bench_gemm(dev, 2048, 3072, 8192, small, 2, seed=9)
+        print(f"[bench] gemm: {secondary['gemm_gate_up']['TFLOP_per_s']:.0f} / "
+              f"{secondary['gemm_down']['TFLOP_per_s']:.0f} TFLOP/s", flush=True)
+        secondary["floors"] = bench_floors(dev, small, 2)
+        f = secondary["floors"]
+        print(f"[bench] floors: empty kernel {f['empty_kernel_us']:.2f} us; read 14.2 MB "
+              f"{f['read_gemv_bytes']['us_per_launch']:.2f} us ({f['read_gemv_bytes']['GB_per_s']:.0f} GB/s); "
+              f"read 1 GiB {f['read_1GiB']['GB_per_s']:.0f} GB/s", flush=True)
     if not args.quick and args.decode_tokens > 1:
         secondary["decode_llama_3_2_3b"] = bench_decode(dev, args.decode_tokens, args.agreement)
         d = secondary["decode_llama_3_2_3b"]
         print(f"[bench] decode: {d['decode_tok_s']:.0f} tok/s ({d['decode_frac_hbm_peak']*100:.1f}% of HBM roofline), "
               f"prefill {d['prefill_tok_s']:.0f} tok/s", flush=True)
     if not args.quick and args.batched_tokens > 1:
-        secondary["decode_llama_3_1_8b_b8"] = bench_decode_batched(dev, args.batched_tokens)
+        secondary["decode_llama_3_1_8b_b8"] = bench_decode_batched(dev, args.batched_tokens, parity=not args.no_parity)
         d = secondary["decode_llama_3_1_8b_b8"]
         print(f"[bench] 8B batch 8 at context 4096: decode {d['decode_tokens_per_s']:.0f} tok/s "
               f"({d['decode_frac_hbm_peak']*100:.1f}% of HBM roofline), prefill {d['prompt_tokens_per_s']:.0f} tok/s",
@@ -443,6 +649,9 @@ def main() -> int:
                           f"(oracle/liboracle.so), {base['1_thread']['calls']} calls single-threaded; "
                           f"all {base['all_cores']['threads']} cores: {base['all_cores']['GB_per_s']:.2f} GB/s"),
                "cpu_model": model, "all_cores": base["all_cores"]}
+        dec = secondary.get("decode_llama_3_2_3b", {}).get("agreement", {}).get("cpu_reference")
+        if dec:
+            cpu["config4_restatement"] = dec
 
     per_launch_bytes = gemv_bytes(1, 8192, 3072)
     line = {
@@ -464,7 +673,9 @@ def main() -> int:
                      "frac": round(head["GB_per_s"] / HBM_PEAK_GBS, 4), "traffic": measured_traffic(),
                      "traffic_source": os.path.relpath(TRAFFIC_FILE, ROOT),
                      "algorithmic_bytes_per_launch": per_launch_bytes,
-                     "us_per_launch": head["us_per_launch"]},
+                     "us_per_launch": head["us_per_launch"],
+                     "median_us_per_launch": head["median_us_per_launch"],
+                     "median_over_replays": MEDIAN_REPLAYS},
         "cpu_baseline": cpu,
         "decode_tok_s": secondary.get("decode_llama_3_2_3b", {}).get("decode_tok_s"),
         "secondary": secondary,

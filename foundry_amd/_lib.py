@@ -141,6 +141,8 @@ SIGNATURES = {
     "fh_capture_end": [_vp, ctypes.POINTER(_vp)],
     "fh_graph_launch": [_vp, _vp],
     "fh_graph_destroy": [_vp],
+    "fh_read_probe_blocks": [ctypes.c_uint64, ctypes.POINTER(ctypes.c_uint64)],
+    "fh_read_probe": [_vp, _vp, ctypes.c_uint64, _vp],
     "fh_timer_begin": [_vp],
     "fh_timer_end": [_vp, ctypes.POINTER(ctypes.c_double)],
     "fh_q4_embed": [_vp, _vp, _vp, _vp, _i64, _i64, _i64, _vp, _i64, _vp],

@@ -122,6 +122,33 @@ int zero_fill(fh_device *dev, const char *fn, void *ptr, uint64_t nbytes) {
     });
 }
 
+// The read probe: every thread loads 4 x 16 contiguous-per-wavefront bytes
+// (all four requested before any is used) and folds them into one XOR word;
+// a block writes one word.
+constexpr uint32_t kProbeThreads = 256;
+constexpr uint32_t kProbeUnroll = 4;
+constexpr uint64_t kProbeBlockBytes = kProbeThreads * 16ull * kProbeUnroll;
+
+__global__ __launch_bounds__(kProbeThreads) void read_probe_kernel(const uint4 *__restrict__ src, uint64_t pieces,
+                                                                    uint32_t *__restrict__ out) {
+    __shared__ uint32_t red[kProbeThreads / 64];
+    const uint64_t base = static_cast<uint64_t>(blockIdx.x) * kProbeThreads * kProbeUnroll + threadIdx.x;
+    uint4 v[kProbeUnroll];
+#pragma unroll
+    for (uint32_t u = 0; u < kProbeUnroll; ++u) {
+        const uint64_t i = base + u * kProbeThreads;
+        v[u] = src[i < pieces ? i : pieces - 1];
+    }
+    uint32_t x = 0;
+#pragma unroll
+    for (uint32_t u = 0; u < kProbeUnroll; ++u) x ^= v[u].x ^ v[u].y ^ v[u].z ^ v[u].w;
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) x ^= __shfl_xor(x, off, 64);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = x;
+    __syncthreads();
+    if (threadIdx.x == 0) out[blockIdx.x] = red[0] ^ red[1] ^ red[2] ^ red[3];
+}
+
 // Frees an allocation that is no longer in dev->allocs and that no live graph
 // uses, after the work queued on the stream ends.
 static hipError_t release(fh_device *dev, uintptr_t base, size_t size) {
@@ -571,6 +598,29 @@ int fh_graph_destroy(fh_graph *graph) {
     if (err != hipSuccess) return device_error(dev, err, fn, "hipStreamSynchronize");
     if (rerr != hipSuccess) return device_error(dev, rerr, fn, "hipFree");
     return FH_OK;
+}
+
+int fh_read_probe_blocks(uint64_t nbytes, uint64_t *blocks) {
+    if (!blocks) return fail(FH_ERR_INVALID_ARGUMENT, "fh_read_probe_blocks: blocks is null");
+    *blocks = (nbytes + kProbeBlockBytes - 1) / kProbeBlockBytes;
+    return FH_OK;
+}
+
+int fh_read_probe(fh_device *dev, const void *src, uint64_t nbytes, uint32_t *out) {
+    const char *fn = "fh_read_probe";
+    if (int rc = check_usable(dev, fn)) return rc;
+    if (nbytes == 0) return FH_OK;
+    if (nbytes % 16 != 0 || reinterpret_cast<uintptr_t>(src) % 16 != 0)
+        return fail(FH_ERR_INVALID_ARGUMENT, "%s: src must be 16-byte aligned and nbytes a multiple of 16", fn);
+    const uint64_t blocks = (nbytes + kProbeBlockBytes - 1) / kProbeBlockBytes;
+    if (blocks > 0x7FFFFFFFull) return fail(FH_ERR_INDEX_TOO_LARGE, "%s: %llu bytes", fn, (unsigned long long)nbytes);
+    if (int rc = check_range(dev, src, nbytes, fn, "src")) return rc;
+    if (int rc = check_range(dev, out, blocks * 4, fn, "out")) return rc;
+    if (int rc = set_current(dev, fn)) return rc;
+    return dispatch(dev, fn, [&] {
+        hipLaunchKernelGGL(read_probe_kernel, dim3(static_cast<uint32_t>(blocks)), dim3(kProbeThreads), 0,
+                           dev->stream, static_cast<const uint4 *>(src), nbytes / 16, out);
+    });
 }
 
 int fh_timer_begin(fh_device *dev) {

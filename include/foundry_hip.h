@@ -111,7 +111,7 @@ int fh_device_stream(fh_device *dev, void **stream);
 int fh_alloc(fh_device *dev, size_t nbytes, int zero_fill, void **out);
 /* Frees an allocation of this device after the work queued on it ends.
  * A live graph retains every allocation its captured ops touched, as a
- * Metal command buffer retains its buffers (src/metal/mod.rs:288-292): the
+ * Metal command buffer retains its buffers (src/metal/mod.rs:280-282): the
  * allocation is then no longer usable by ops but stays allocated until the
  * last graph that uses it is destroyed. A free asked for while capturing is
  * carried out at fh_capture_end, on the same rule. */
@@ -153,6 +153,14 @@ int fh_graph_destroy(fh_graph *graph);
 int fh_timer_begin(fh_device *dev);
 /* Records an end event, waits for it, writes the milliseconds between the two. */
 int fh_timer_end(fh_device *dev, double *elapsed_ms);
+
+/* ---- the HBM read ceiling, for measurement: one launch that reads nbytes
+ * (16-byte aligned, a multiple of 16) in 16-byte loads, 16 KB per block,
+ * and writes one XOR word per block to out (fh_read_probe_blocks words).
+ * No counterpart in the reference (it is the roofline's measured read
+ * rate beside the quoted peak). ---- */
+int fh_read_probe_blocks(uint64_t nbytes, uint64_t *blocks);
+int fh_read_probe(fh_device *dev, const void *src, uint64_t nbytes, uint32_t *out);
 
 /* ======================================================================
  * q4 ops. Weight format (affine group quantisation):
