@@ -1,6 +1,8 @@
 """Readers for rocprofv3 output, used to build the summaries under profiles/.
 
     python -m foundry_amd.profiling stats <dir>        # kernel-trace --stats CSV
+    python -m foundry_amd.profiling trace <dir>        # per-dispatch medians from the kernel trace
+    python -m foundry_amd.profiling counters <dir> <kernel-substring>   # --pmc values per dispatch
     python -m foundry_amd.profiling traffic <fetch_dir> <write_dir> <kernel-substring>
 
 ``traffic`` takes two ``rocprofv3 --pmc`` runs of the same command, one with
@@ -35,6 +37,29 @@ def kernel_stats(directory: str):
     return sorted(out, key=lambda t: -t[3])
 
 
+def trace_medians(directory: str):
+    """[(name, grid, block, dispatches, median_us, total_ms)] from the
+    per-dispatch rows of a *_kernel_trace.csv, grouped by kernel and grid."""
+    groups = {}
+    for r in _rows(os.path.join(directory, "**", "*kernel_trace.csv")):
+        key = (r["Kernel_Name"], f'{r["Grid_Size_X"]} x {r["Grid_Size_Y"]} x {r["Grid_Size_Z"]}',
+               r["Workgroup_Size_X"])
+        groups.setdefault(key, []).append((int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3)
+    out = [(k[0], k[1], k[2], len(v), statistics.median(v), sum(v) / 1e3) for k, v in groups.items()]
+    return sorted(out, key=lambda t: -t[5])
+
+
+def counters_by_kernel(directory: str, kernel_substring: str):
+    """{(kernel, grid size): {counter: (mean value per dispatch, dispatches)}}
+    over the dispatches of the kernels whose name contains the substring."""
+    acc = {}
+    for r in _rows(os.path.join(directory, "**", "*counter_collection.csv")):
+        if kernel_substring in r["Kernel_Name"]:
+            key = (r["Kernel_Name"].split("(")[0], r["Grid_Size"])
+            acc.setdefault(key, {}).setdefault(r["Counter_Name"], []).append(float(r["Counter_Value"]))
+    return {k: {c: (statistics.mean(v), len(v)) for c, v in d.items()} for k, d in acc.items()}
+
+
 def counter_per_dispatch(directory: str, counter: str, kernel_substring: str):
     vals = [float(r["Counter_Value"]) for r in _rows(os.path.join(directory, "**", "*counter_collection.csv"))
             if r["Counter_Name"] == counter and kernel_substring in r["Kernel_Name"]]
@@ -56,6 +81,19 @@ def main(argv):
     if len(argv) >= 2 and argv[0] == "stats":
         for name, calls, avg, total in kernel_stats(argv[1]):
             print(f"| {name[:90]} | {calls} | {avg / 1e3:.2f} | {total / 1e6:.3f} |")
+        return 0
+    if len(argv) >= 2 and argv[0] == "trace":
+        print("| Kernel | grid | block | dispatches | median us | total ms |")
+        print("|---|---|---|---|---|---|")
+        for name, grid, block, n, med, total in trace_medians(argv[1]):
+            short = name.split("(")[0][:80]
+            print(f"| `{short}` | {grid} | {block} | {n} | {med:.2f} | {total:.3f} |")
+        return 0
+    if len(argv) >= 3 and argv[0] == "counters":
+        for (kernel, grid), d in sorted(counters_by_kernel(argv[1], argv[2]).items()):
+            print(f"{kernel} (grid {grid}):")
+            for name, (mean, n) in sorted(d.items()):
+                print(f"  {name}={mean:.6g} (mean of {n} dispatches)")
         return 0
     if len(argv) >= 4 and argv[0] == "traffic":
         fetch, fscale, n1 = scaled_bytes(argv[1], "FETCH_SIZE", argv[3])
