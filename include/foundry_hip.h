@@ -155,10 +155,10 @@ int fh_timer_begin(fh_device *dev);
 int fh_timer_end(fh_device *dev, double *elapsed_ms);
 
 /* ---- the HBM read ceiling, for measurement: one launch that reads nbytes
- * (16-byte aligned, a multiple of 16) in 16-byte loads, 16 KB per block,
- * and writes one XOR word per block to out (fh_read_probe_blocks words).
- * No counterpart in the reference (it is the roofline's measured read
- * rate beside the quoted peak). ---- */
+ * (16-byte aligned, a multiple of 16) in 16-byte loads, 32 KB per block,
+ * and writes one XOR word per wavefront to out (fh_read_probe_blocks gives
+ * the number of words). No counterpart in the reference (it is the
+ * roofline's measured read rate beside the quoted peak). ---- */
 int fh_read_probe_blocks(uint64_t nbytes, uint64_t *blocks);
 int fh_read_probe(fh_device *dev, const void *src, uint64_t nbytes, uint32_t *out);
 
