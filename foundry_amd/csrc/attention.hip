@@ -131,6 +131,13 @@ __device__ __forceinline__ attn_f32x4_t attn_mfma(const uint4 a, const uint4 b, 
                                                    __builtin_bit_cast(attn_bf16x8_t, b), c, 0, 0, 0);
 }
 
+// Key groups (16 keys) a scores wavefront keeps in flight.
+#ifndef FH_ATTN_SCORES_DEPTH
+#define FH_ATTN_SCORES_DEPTH 2
+#endif
+constexpr int kScoresDepth = FH_ATTN_SCORES_DEPTH;
+static_assert(kScoresDepth == 2 || kScoresDepth == 4, "a chunk's 4 groups cycle through the buffers");
+
 template <int HD, int G, bool ROPE>
 __global__ __launch_bounds__(kAttnThreads) void attn_scores_kernel(
     const uint16_t *__restrict__ q_src, const uint16_t *__restrict__ cos_tab, const uint16_t *__restrict__ sin_tab,
@@ -161,18 +168,19 @@ __global__ __launch_bounds__(kAttnThreads) void attn_scores_kernel(
     // key groups (16 keys) of this wavefront; 0 for a wavefront without chunks
     const uint32_t total = c_first < nact ? (nact - c_first + c_step - 1) / c_step * 4 : 0;
     const uint16_t *kb = k_cache + cache + 8 * quad;
-    // group f -> B fragments of its 16 keys (clamped past the context / the
-    // wavefront's last group; such values are masked or unused)
+    // group f -> B fragments of its 16 keys (clamped past the context; past
+    // the wavefront's last group, key 0's row, one line for the wavefront;
+    // such values are masked or unused)
     auto load_grp = [&](uint32_t f, uint4 (&b)[KS]) {
         const uint32_t fc = total ? (f < total ? f : total - 1) : 0;
         const uint32_t j = (c_first + (fc / 4) * c_step) * kAttnChunk + (fc % 4) * 16 + col;
-        const uint32_t jc = j < kmax ? j : (kmax ? kmax - 1 : 0);
+        const uint32_t jc = j < kmax && f < total ? j : (kmax && f < total ? kmax - 1 : 0);
 #pragma unroll
         for (int st = 0; st < KS; ++st) b[st] = *reinterpret_cast<const uint4 *>(kb + static_cast<uint64_t>(jc) * HD + 32 * st);
     };
     // Loads go out in this order, unconditionally (clamped indices): the RoPE
-    // inputs, the q fragments, then the first two key groups, so the set-up
-    // waits for its own loads only.
+    // inputs, the q fragments, then the first kScoresDepth key groups, so the
+    // set-up waits for its own loads only.
     const bool hlive = col < static_cast<uint32_t>(G);
     const uint32_t hc = hlive ? col : 0;
     uint4 a[KS];
@@ -197,9 +205,9 @@ __global__ __launch_bounds__(kAttnThreads) void attn_scores_kernel(
             a[st] = hlive ? v : make_uint4(0u, 0u, 0u, 0u);
         }
     }
-    uint4 b0[KS], b1[KS];
-    load_grp(0, b0);
-    load_grp(1, b1);
+    uint4 b[kScoresDepth][KS];  // key groups in flight
+#pragma unroll
+    for (int grp = 0; grp < kScoresDepth; ++grp) load_grp(grp, b[grp]);
     if constexpr (ROPE) {
         const bool owner = (pos / kAttnChunk) % splits == split;
         const uint4 ov = rope_apply(x4, r4, c4, s4, pp < PPH / 2);
@@ -227,20 +235,20 @@ __global__ __launch_bounds__(kAttnThreads) void attn_scores_kernel(
         const uint32_t c = c_first + (f0 / 4) * c_step;
 #pragma unroll
         for (int grp = 0; grp < 4; ++grp) {
-            uint4(&b)[KS] = grp % 2 ? b1 : b0;
+            uint4(&bg)[KS] = b[grp % kScoresDepth];
             if constexpr (ROPE) {
                 if (c * kAttnChunk + grp * 16 + col == pos) {
 #pragma unroll
-                    for (int st = 0; st < KS; ++st) b[st] = kn[4 * st];
+                    for (int st = 0; st < KS; ++st) bg[st] = kn[4 * st];
                 }
             }
-            attn_f32x4_t d = attn_mfma(a[0], b[0], attn_f32x4_t{0.f, 0.f, 0.f, 0.f});
+            attn_f32x4_t d = attn_mfma(a[0], bg[0], attn_f32x4_t{0.f, 0.f, 0.f, 0.f});
 #pragma unroll
-            for (int st = 1; st < KS; ++st) d = attn_mfma(a[st], b[st], d);
+            for (int st = 1; st < KS; ++st) d = attn_mfma(a[st], bg[st], d);
             // result lane (key col, row quad) holds heads 4 quad .. 4 quad + 3
             if (quad < static_cast<uint32_t>(NQ))
                 *reinterpret_cast<float4 *>(&sc[wave][grp * 16 + col][4 * quad]) = make_float4(d[0], d[1], d[2], d[3]);
-            load_grp(f0 + grp + 2, b);
+            load_grp(f0 + grp + kScoresDepth, bg);
         }
         __builtin_amdgcn_wave_barrier();  // this wavefront's writes before its reads
         float dv[HP];
@@ -497,11 +505,16 @@ __global__ __launch_bounds__(kAttnThreads) void attn_pv_kernel(
 // wavefront load covers 64 / (HD/8) whole key rows). Each wavefront takes
 // every 4th tile of 16 keys on its own: it computes the row's softmax
 // statistics itself, stages its tile's probabilities in its own LDS slice
-// (no block barrier in the loop) and keeps two tiles of loads in flight. The
+// (no block barrier in the loop) and keeps kPvDepth tiles of loads in flight. The
 // lanes' and wavefronts' partials are added in a fixed order. With one chunk
 // per row the result (RNE) goes to out, else the f32 partial goes to part
 // for attn_combine_kernel.
 constexpr int kPvWaveTile = 16;  // keys per wavefront tile
+// Tiles a chunked P.V wavefront keeps in flight.
+#ifndef FH_PV_DEPTH
+#define FH_PV_DEPTH 2
+#endif
+constexpr int kPvDepth = FH_PV_DEPTH;
 
 template <int HD, int G>
 __global__ __launch_bounds__(kAttnThreads) void attn_pv_chunk_kernel(
@@ -538,25 +551,27 @@ __global__ __launch_bounds__(kAttnThreads) void attn_pv_chunk_kernel(
     // entries t = lane + 64 n of its [G][16] block. Keys past k1 and tiles past
     // the wavefront's last are clamped (loads stay unconditional; the values
     // are masked or unused).
+    // Tiles past the wavefront's last read the chunk's first key (one line).
     auto load_tile = [&](uint32_t i, uint4 (&vr)[IT], float (&sr)[NSW]) {
-        const uint32_t ic = wt ? (i < wt ? i : wt - 1) : 0;
-        const uint32_t t0 = k0 + (wave + ic * kAttnWaves) * kPvWaveTile;
+        const bool live = i < wt;
+        const uint32_t t0 = k0 + (wave + (live ? i : 0) * kAttnWaves) * kPvWaveTile;
 #pragma unroll
         for (int it = 0; it < IT; ++it) {
             const uint32_t j = t0 + it * KPI + kl;
-            vr[it] = *reinterpret_cast<const uint4 *>(vb + static_cast<uint64_t>(j < k1 ? j : k1 - 1) * HD);
+            vr[it] = *reinterpret_cast<const uint4 *>(vb + static_cast<uint64_t>(live && j < k1 ? j : k0) * HD);
         }
 #pragma unroll
         for (int n = 0; n < NSW; ++n) {
             const uint32_t t = lane + n * 64;
             const uint32_t g = t / kPvWaveTile < G ? t / kPvWaveTile : G - 1, j = t0 + t % kPvWaveTile;
-            sr[n] = srow[static_cast<uint64_t>(g) * max_len + (j < k1 ? j : k1 - 1)];
+            sr[n] = srow[static_cast<uint64_t>(live ? g : 0) * max_len + (live && j < k1 ? j : k0)];
         }
     };
-    uint4 va[IT], vb2[IT];
-    float sa[NSW], sb[NSW];
-    load_tile(0, va, sa);
-    load_tile(1, vb2, sb);
+    constexpr int kDepth = kPvDepth;
+    uint4 vt[kDepth][IT];
+    float sct[kDepth][NSW];
+#pragma unroll
+    for (int q = 0; q < kDepth; ++q) load_tile(q, vt[q], sct[q]);
     // the row's softmax statistics, per wavefront (M, S the same everywhere):
     // up to 128 chunks from registers (every head's loads issued together),
     // longer rows in a loop
@@ -635,11 +650,12 @@ __global__ __launch_bounds__(kAttnThreads) void attn_pv_chunk_kernel(
         }
         __builtin_amdgcn_wave_barrier();  // reads before the next tile's writes
     };
-    for (uint32_t i = 0; i < wt; i += 2) {
-        use_tile(i, va, sa);
-        load_tile(i + 2, va, sa);
-        if (i + 1 < wt) use_tile(i + 1, vb2, sb);
-        load_tile(i + 3, vb2, sb);
+    for (uint32_t i = 0; i < wt; i += kDepth) {
+#pragma unroll
+        for (int q = 0; q < kDepth; ++q) {
+            if (i + q < wt) use_tile(i + q, vt[q], sct[q]);
+            load_tile(i + q + kDepth, vt[q], sct[q]);
+        }
     }
     // keys of one dim piece sit LPK lanes apart: add them with shuffles, then
     // the wavefronts in order through LDS

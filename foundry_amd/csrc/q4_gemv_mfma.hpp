@@ -181,19 +181,27 @@ __global__ __launch_bounds__(kMfThreads) void q4_gemv_mfma_kernel(
     auto wrow = [&](uint32_t tile, int t) { return (EPI == kEpiSiluMul && t == 1 ? n_out : 0u) + tile * 16 + col; };
     // chunk c (of this wavefront's sequence) -> operands; past the end, the
     // last chunk again (values unused)
+    // Chunks past the end, and tiles past the last of a partial round, read
+    // the first bytes of the operands instead (one line for the whole block,
+    // at hand in L1): a reload of real operands would be waited for before
+    // the last reduction. The choice is a select on uniform values, not a
+    // branch, so every wait still counts exactly.
     auto load = [&](uint32_t c, MfChunk<NT, CH> &cb) {
         const uint32_t cc = c < total ? c : total - 1;
         const uint32_t r = cc / cpt;
         const uint32_t p0 = (ks * gs) / 2 + (cc % cpt) * CH;  // first pair
         uint32_t tile = tile_of(r);
+        const bool dead = c >= total || tile >= tiles;
         tile = tile < tiles ? tile : tiles - 1;
 #pragma unroll
         for (int t = 0; t < NT; ++t) {
             const uint64_t row = wrow(tile, t);
             const uint4 *wp = reinterpret_cast<const uint4 *>(wq + row * w_ld + p0 * 16 + quarter * 4);
+            if (dead) wp = reinterpret_cast<const uint4 *>(wq);
 #pragma unroll
             for (int c2 = 0; c2 < CH; ++c2) cb.w[c2][t] = wp[c2 * 4];
             const uint16_t *sp = scales + row * sb_ld + p0 * 2, *bp = biases + row * sb_ld + p0 * 2;
+            if (dead) sp = scales, bp = biases;
             if constexpr (CH == 4) {
                 const uint4 sv = *reinterpret_cast<const uint4 *>(sp), bv = *reinterpret_cast<const uint4 *>(bp);
                 cb.s[0][t] = sv.x, cb.s[1][t] = sv.y, cb.s[2][t] = sv.z, cb.s[3][t] = sv.w;

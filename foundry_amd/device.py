@@ -258,12 +258,19 @@ class HipDevice:
                 if not w.layout.is_contiguous():
                     raise TensorError("MatmulIncompatible", "q4 weights must be contiguous")
             rows, k = x.layout.shape
-            if x.layout.strides[1] != 1 and k > 1:
-                raise TensorError("MatmulIncompatible", "x must have unit column stride")
             if x.dtype is not DType.BF16:
                 raise _lib.HipError(_lib.ERR_DTYPE, "the q4 kernels take bf16 activations")
-            x_ld = x.layout.strides[0] if rows > 1 else max(k, x.layout.strides[0])
-            _lib.call("fh_q4_matmul", self.handle, ctypes.c_void_p(x.address()), rows, k, x_ld,
+            x_ptr, x_ld = x.address(), x.layout.strides[0] if rows > 1 else max(k, x.layout.strides[0])
+            if (k > 1 and x.layout.strides[1] != 1) or (rows > 1 and x.layout.strides[0] < k):
+                # The operand rule of the reference's matmul (matmul_operand,
+                # src/metal/mod.rs:384-401): rows the kernel cannot read in
+                # place (a column stride, overlapping or broadcast rows) are
+                # copied to a contiguous [rows, k] first.
+                staged = self.empty(rows * k * 2)
+                _lib.call("fh_copy_strided", self.handle, int(x.dtype), ctypes.c_void_p(x.storage.ptr),
+                          ctypes.byref(x.layout.view()), ctypes.c_void_p(staged.ptr))
+                x_ptr, x_ld = staged.ptr, k
+            _lib.call("fh_q4_matmul", self.handle, ctypes.c_void_p(x_ptr), rows, k, x_ld,
                       ctypes.c_void_p(wq.address()), ctypes.c_void_p(s.address()),
                       ctypes.c_void_p(b.address()), shape[1], op.group, ctypes.c_void_p(out.ptr),
                       _lib.BF16 if out_dtype is DType.BF16 else _lib.F32)

@@ -279,6 +279,29 @@ def test_q4_linear_module_shapes(device, oracle):
     assert np.all(err <= bf16_ulp(y64) + 1e-5 * np.max(np.abs(y64)))
 
 
+@pytest.mark.parametrize("rows", [3, 12])  # the GEMV and the GEMM route
+def test_q4_matmul_op_stages_views_it_cannot_read_in_place(device, rows):
+    """A transposed x (column stride != 1) and a broadcast x (row stride 0)
+    are copied to contiguous rows first (the reference's matmul operand rule),
+    so they give exactly what the same rows give when stored contiguously."""
+    from foundry_amd.primitive import QuantizedMatmul
+
+    wq, s, b = synth.q4_weights(33, 96, 256)
+    w = weight(device, wq, s, b)
+    op = QuantizedMatmul(bits=4, group=64)
+    x = synth.bf16_normal(34, (rows, 256))
+    want = up(device, x, DType.BF16).apply(device, op, [w.wq, w.scales, w.biases]).to_numpy(device)
+    xt = up(device, np.ascontiguousarray(x.T), DType.BF16).permute((1, 0))
+    assert xt.layout.strides == (1, rows)
+    got = xt.apply(device, op, [w.wq, w.scales, w.biases]).to_numpy(device)
+    assert np.array_equal(got, want)
+    row = up(device, x[:1], DType.BF16).expand((rows, 256))
+    assert row.layout.strides == (0, 1)
+    got = row.apply(device, op, [w.wq, w.scales, w.biases]).to_numpy(device)
+    one = up(device, np.repeat(x[:1], rows, axis=0), DType.BF16)
+    assert np.array_equal(got, one.apply(device, op, [w.wq, w.scales, w.biases]).to_numpy(device))
+
+
 def test_foreign_and_out_of_bounds_storage_are_rejected(device):
     wq, s, b = synth.q4_weights(41, 64, 128)
     w = weight(device, wq, s, b)
