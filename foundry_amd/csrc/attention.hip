@@ -170,13 +170,15 @@ __global__ __launch_bounds__(kAttnThreads) void attn_scores_kernel(
     const uint16_t *kb = k_cache + cache + 8 * quad;
     // group f -> B fragments of its 16 keys (clamped past the context; past
     // the wavefront's last group, key 0's row, one line for the wavefront;
-    // such values are masked or unused)
+    // such values are masked or unused); each fragment is one 1 KB run of the
+    // tiled K cache (k_tile)
     auto load_grp = [&](uint32_t f, uint4 (&b)[KS]) {
         const uint32_t fc = total ? (f < total ? f : total - 1) : 0;
         const uint32_t j = (c_first + (fc / 4) * c_step) * kAttnChunk + (fc % 4) * 16 + col;
         const uint32_t jc = j < kmax && f < total ? j : (kmax && f < total ? kmax - 1 : 0);
+        const KTile t = k_tile(jc, max_len, HD);
 #pragma unroll
-        for (int st = 0; st < KS; ++st) b[st] = *reinterpret_cast<const uint4 *>(kb + static_cast<uint64_t>(jc) * HD + 32 * st);
+        for (int st = 0; st < KS; ++st) b[st] = *reinterpret_cast<const uint4 *>(kb + t.base + st * t.stride);
     };
     // Loads go out in this order, unconditionally (clamped indices): the RoPE
     // inputs, the q fragments, then the first kScoresDepth key groups, so the
@@ -216,7 +218,7 @@ __global__ __launch_bounds__(kAttnThreads) void attn_scores_kernel(
                 *reinterpret_cast<uint4 *>(&qb[hh][pp * 8]) = ov;
             } else {
                 *reinterpret_cast<uint4 *>(knew + pp * 8) = ov;
-                if (owner) *reinterpret_cast<uint4 *>(k_cache + cache + static_cast<uint64_t>(pos) * HD + pp * 8) = ov;
+                if (owner) *reinterpret_cast<uint4 *>(k_cache + cache + k_offset(pos, pp * 8, max_len, HD)) = ov;
             }
         } else if (owner && tid < (G + 2) * PPH) {
             *reinterpret_cast<uint4 *>(v_cache + cache + static_cast<uint64_t>(pos) * HD + (tid - (G + 1) * PPH) * 8) = v4;
@@ -324,8 +326,9 @@ __global__ __launch_bounds__(kAttnThreads) void attn_scores_tile_kernel(
         const uint32_t fc = f < total ? f : total - 1;
         const uint32_t j = (c_first + (fc / 4) * c_step) * kAttnChunk + (fc % 4) * 16 + col;
         const uint32_t jc = j < cmax ? j : cmax - 1;
+        const KTile t = k_tile(jc, max_len, HD);
 #pragma unroll
-        for (int st = 0; st < KS; ++st) b[st] = *reinterpret_cast<const uint4 *>(kb + static_cast<uint64_t>(jc) * HD + 32 * st);
+        for (int st = 0; st < KS; ++st) b[st] = *reinterpret_cast<const uint4 *>(kb + t.base + st * t.stride);
     };
     // A fragments: row col = (query row col / G, head col % G), dims 32 st + 8 quad
     const uint32_t qa = col / G, ha = col % G;
@@ -987,9 +990,9 @@ __global__ __launch_bounds__(kShortThreads) void attn_decode_short_kernel(
         for (int grp = 0; grp < 4; ++grp) {
             const uint32_t j = c0 + grp * 16 + col;
             const uint32_t jc = j < pos ? j : (pos ? pos - 1 : 0);
+            const KTile t = k_tile(jc, max_len, HD);
 #pragma unroll
-            for (int st = 0; st < KS; ++st)
-                b[grp][st] = *reinterpret_cast<const uint4 *>(kb + static_cast<uint64_t>(jc) * HD + 32 * st);
+            for (int st = 0; st < KS; ++st) b[grp][st] = *reinterpret_cast<const uint4 *>(kb + t.base + st * t.stride);
         }
         const uint16_t *vb = v_cache + cache + d0 + 2 * dp;
 #pragma unroll
@@ -1006,7 +1009,7 @@ __global__ __launch_bounds__(kShortThreads) void attn_decode_short_kernel(
                 *reinterpret_cast<uint4 *>(&qb[hh][pp * 8]) = ov;
             } else {
                 *reinterpret_cast<uint4 *>(knew + pp * 8) = ov;
-                if (part == 0) *reinterpret_cast<uint4 *>(k_cache + cache + static_cast<uint64_t>(pos) * HD + pp * 8) = ov;
+                if (part == 0) *reinterpret_cast<uint4 *>(k_cache + cache + k_offset(pos, pp * 8, max_len, HD)) = ov;
             }
         } else if (part == 0 && tid < (G + 2) * PPH) {
             *reinterpret_cast<uint4 *>(v_cache + cache + static_cast<uint64_t>(pos) * HD + (tid - (G + 1) * PPH) * 8) = v4;

@@ -46,6 +46,28 @@ __device__ __forceinline__ void unpack8(const uint4 v, float (&f)[8]) {
     }
 }
 
+// The K cache of one (sequence, KV head) holds max_len keys of head_dim in
+// groups of 16 keys: group g (keys 16 g .. 16 g + n_g - 1, n_g = min(16,
+// max_len - 16 g)) is n_g * head_dim contiguous elements laid out
+// [head_dim / 32][n_g][32], so dims d .. d + 7 (d a multiple of 8) of key j
+// start at 16 g * head_dim + (d / 32) * n_g * 32 + (j - 16 g) * 32 + d % 32.
+// One matrix-core B fragment (16 keys x 32 dims, 16 bytes per lane) is then a
+// single 1 KB run instead of 16 runs of 64 bytes. The V cache stays
+// [max_len][head_dim].
+struct KTile {
+    uint64_t base;    // element offset of key j's group and row within it
+    uint32_t stride;  // elements between its 32-dim blocks (n_g * 32)
+};
+__host__ __device__ __forceinline__ KTile k_tile(uint32_t j, uint32_t max_len, uint32_t head_dim) {
+    const uint32_t g = j >> 4, left = max_len - (g << 4);
+    const uint32_t n_g = left < 16u ? left : 16u;
+    return KTile{static_cast<uint64_t>(g) * 16u * head_dim + (j & 15u) * 32u, n_g * 32u};
+}
+__host__ __device__ __forceinline__ uint64_t k_offset(uint32_t j, uint32_t d, uint32_t max_len, uint32_t head_dim) {
+    const KTile t = k_tile(j, max_len, head_dim);
+    return t.base + (d >> 5) * t.stride + (d & 31u);
+}
+
 // Lane value of a DPP permutation within 16-lane rows (CDNA DPP controls:
 // 0xB1 quad_perm [1,0,3,2], 0x4E quad_perm [2,3,0,1], 0x141 row_half_mirror,
 // 0x140 row_mirror).

@@ -166,7 +166,8 @@ __global__ __launch_bounds__(256) void rope_kv_kernel(
         if (h < n_heads)
             *reinterpret_cast<uint4 *>(q_out + (static_cast<uint64_t>(t) * n_heads + h) * head_dim + p * 8) = ov;
         else
-            *reinterpret_cast<uint4 *>(k_cache + (static_cast<uint64_t>(h - n_heads) * max_len + pos) * head_dim + p * 8) = ov;
+            *reinterpret_cast<uint4 *>(k_cache + static_cast<uint64_t>(h - n_heads) * max_len * head_dim +
+                                       k_offset(pos, p * 8, max_len, head_dim)) = ov;
     }
     const uint16_t *vrow = row + rot_pieces * 8;
     for (uint32_t i = threadIdx.x; i < n_kv * ppw; i += blockDim.x) {

@@ -303,12 +303,22 @@ int fh_rms_norm(fh_device *dev, const uint16_t *x, const uint16_t *residual,
                 uint16_t *residual_out, const uint16_t *weight, int64_t rows, int64_t dim,
                 float eps, uint16_t *y);
 
+/* KV caches of the attention entry points below. One (sequence, KV head)
+ * owns max_len * head_dim elements of each cache. V is [max_len][head_dim].
+ * K holds the same keys in groups of 16: group g (keys 16 g .. 16 g + n_g -
+ * 1, n_g = min(16, max_len - 16 g)) is n_g * head_dim contiguous elements
+ * laid out [head_dim / 32][n_g][32], i.e. dim d of key j is element
+ * 16 g * head_dim + (d / 32) * n_g * 32 + (j % 16) * 32 + d % 32 of the
+ * region. The reference's StaticCache (src/nn/kv_cache.rs:41-80) keeps K as
+ * [max_len][head_dim]; the regrouping lets a matrix-core fragment of 16 keys
+ * x 32 dims be read as one 1 KB run. Sizes are unchanged. */
+
 /* apply_rotary_pos_emb (src/models/llama/rotary_emb.rs:62-85) on q and k of
  * each token, then StaticCache::update (src/nn/kv_cache.rs:41-80) of k and v
  * at the token's position. qkv: [tokens, (n_heads + 2 n_kv) * head_dim] (q
  * heads, then k heads, then v heads); cos_tab/sin_tab: [table_len, head_dim];
- * positions: device u32 [tokens]; k_cache/v_cache: [n_kv, max_len, head_dim];
- * q_out: [tokens, n_heads, head_dim]. head_dim is a multiple of 16 and every
+ * positions: device u32 [tokens]; k_cache/v_cache: n_kv regions of max_len *
+ * head_dim (K grouped as above); q_out: [tokens, n_heads, head_dim]. head_dim is a multiple of 16 and every
  * operand 16-byte aligned. A position >= max_len or >= table_len writes
  * nothing. */
 int fh_rope_kv(fh_device *dev, const uint16_t *qkv, int64_t tokens, int64_t n_heads,
@@ -326,8 +336,8 @@ int fh_attention_workspace(int64_t tokens, int64_t n_heads, int64_t n_kv, int64_
  * of its KV head (grouped-query: head h uses KV head h / (n_heads/n_kv)).
  * Scores RNE(q.k) (fp32 sums), times scale in fp32, softmax in fp32,
  * probabilities RNE to bf16 from the row's global max and sum, out =
- * RNE(sum p v). q, out: [tokens, n_heads * head_dim]; caches [n_kv, max_len,
- * head_dim]. head_dim is 64, 128 or 256 and n_heads/n_kv at most 8; tokens at
+ * RNE(sum p v). q, out: [tokens, n_heads * head_dim]; caches: n_kv regions of
+ * max_len * head_dim (K grouped as above). head_dim is 64, 128 or 256 and n_heads/n_kv at most 8; tokens at
  * most 65535. The context is split into chunks of 64 keys scored in
  * parallel, and P.V is split over head_dim, so a long context fills the
  * device. workspace: at least fh_attention_workspace() bytes of device
@@ -349,8 +359,9 @@ int fh_decode_attention_workspace(int64_t batch, int64_t n_heads, int64_t n_kv, 
  * one when max_len <= 1024 and head_dim is 64 or 128 (the workspace is then
  * not touched, but is still checked and required). qkv:
  * [batch, (n_heads + 2 n_kv) * head_dim]; cos_tab/sin_tab: [table_len,
- * head_dim]; positions: device u32 [batch]; k_cache/v_cache: [batch, n_kv,
- * max_len, head_dim] (one cache per sequence); out: [batch, n_heads *
+ * head_dim]; positions: device u32 [batch]; k_cache/v_cache: batch x n_kv
+ * regions of max_len * head_dim (one cache per sequence, K grouped as above);
+ * out: [batch, n_heads *
  * head_dim]. A position >= max_len or >= table_len writes nothing to the
  * caches and zeros to out. head_dim is 64, 128 or 256, n_heads/n_kv at most
  * 8, batch at most 65535, operands 16-byte aligned. workspace: as for
@@ -440,7 +451,8 @@ typedef struct fh_q4_weight {
 
 /* One decoder layer (LlamaDecoderLayer, src/models/llama/model.rs:47, :254-280):
  * qkv = [Wq; Wk; Wv] and gate_up = [Wgate; Wup] rows; bf16 norm weights
- * [hidden]; caches [batch, n_kv, max_len, head_dim]. */
+ * [hidden]; caches: batch x n_kv regions of max_len * head_dim (K grouped
+ * as for fh_rope_kv). */
 typedef struct fh_llama_layer {
     fh_q4_weight qkv, o, gate_up, down;
     const uint16_t *input_norm;

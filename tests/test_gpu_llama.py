@@ -18,6 +18,7 @@ import pytest
 
 from foundry_amd import _lib, synth
 from foundry_amd.device import HipDevice
+from foundry_amd.kv_layout import tile_k, untile_k
 from foundry_amd.llama import LlamaConfig, Q4Llama, embed_weights, final_norm_weight, layer_weights, rope_tables
 from oracle import llama_ref as R
 
@@ -91,7 +92,8 @@ def test_rope_kv_bit_exact(device):
     k_ref = R.RefLlama.rope(ref, xf[:, hq:hq + hk].reshape(t, c.n_kv_heads, c.head_dim), pos)
     bits = lambda a: (a.view(np.uint32) >> 16).astype(np.uint16)
     assert np.array_equal(down(device, qo, np.uint16, t * hq), bits(q_ref).ravel())
-    kcache = down(device, kc, np.uint16, c.n_kv_heads * max_len * c.head_dim).reshape(c.n_kv_heads, max_len, c.head_dim)
+    kcache = untile_k(down(device, kc, np.uint16, c.n_kv_heads * max_len * c.head_dim).reshape(c.n_kv_heads, max_len,
+                                                                                                c.head_dim))
     vcache = down(device, vc, np.uint16, c.n_kv_heads * max_len * c.head_dim).reshape(c.n_kv_heads, max_len, c.head_dim)
     assert np.array_equal(kcache[:, pos, :], bits(k_ref).transpose(1, 0, 2))
     assert np.array_equal(vcache[:, pos, :], qkv[:, hq + hk:].reshape(t, c.n_kv_heads, c.head_dim).transpose(1, 0, 2))
@@ -153,7 +155,7 @@ def assert_attention_close(got, ref, flip, what):
 def run_attention(device, q, kc, vc, pos, ws=None):
     t, n_heads, hd = q.shape
     n_kv, max_len, _ = kc.shape
-    s = [up(device, a) for a in (q, kc, vc, np.ascontiguousarray(pos, dtype=np.uint32))]
+    s = [up(device, a) for a in (q, tile_k(kc), vc, np.ascontiguousarray(pos, dtype=np.uint32))]
     nbytes = _lib.attention_workspace_bytes(t, n_heads, n_kv, hd, max_len)
     if ws is None:
         ws = device.zeros(nbytes)
@@ -248,7 +250,7 @@ def test_decode_attention(device, n_heads, n_kv, hd, batch, max_len):
         pos[1] = 0
     cos, sin = rope_tables(c, max_len)
     rc, rs = R.rope_tables(hd, c.rope_theta, (32.0, 1.0, 4.0, 8192), max_len)
-    s = [up(device, a) for a in (qkv, cos, sin, pos, kc, vc)]
+    s = [up(device, a) for a in (qkv, cos, sin, pos, tile_k(kc), vc)]
     out = device.empty(batch * n_heads * hd * 2)
     scale = float(np.float32(1) / np.sqrt(np.float32(hd), dtype=np.float32))
     nbytes = _lib.decode_attention_workspace_bytes(batch, n_heads, n_kv, hd, max_len)
@@ -258,7 +260,7 @@ def test_decode_attention(device, n_heads, n_kv, hd, batch, max_len):
               ctypes.c_void_p(s[4].ptr), ctypes.c_void_p(s[5].ptr), max_len, ctypes.c_float(scale),
               ctypes.c_void_p(ws.ptr), nbytes, ctypes.c_void_p(out.ptr))
     got = down(device, out, np.uint16, batch * n_heads * hd).reshape(batch, n_heads, hd)
-    kgot = down(device, s[4], np.uint16, kc.size).reshape(kc.shape)
+    kgot = untile_k(down(device, s[4], np.uint16, kc.size).reshape(kc.shape))
     vgot = down(device, s[5], np.uint16, vc.size).reshape(vc.shape)
     xf = R.from_bf16(qkv)
     hq, hk = n_heads * hd, n_kv * hd

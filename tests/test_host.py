@@ -249,3 +249,36 @@ def test_standard_op_output_rules():
         with pytest.raises(TensorError) as e:
             output(op, inputs)
         assert e.value.kind == kind, (op, inputs)
+
+
+# ---- the tiled K cache layout (foundry_amd/kv_layout.py, the kernels' k_tile) ----
+
+@pytest.mark.parametrize("max_len,head_dim", [(40, 64), (300, 128), (768, 128), (17, 256), (16, 32)])
+def test_k_tile_index_is_a_permutation_of_the_region(max_len, head_dim):
+    from foundry_amd.kv_layout import k_tile_index
+    idx = k_tile_index(max_len, head_dim)
+    assert idx.shape == (max_len, head_dim)
+    assert np.array_equal(np.sort(idx.ravel()), np.arange(max_len * head_dim))
+
+
+def test_k_tile_index_known_offsets_and_fragment_runs():
+    from foundry_amd.kv_layout import k_tile_index
+    # key 33 of a 40-key region (group 2, 8 keys), dim 40 (block 1, offset 8):
+    # 2 * 16 * 64 + 1 * (8 * 32) + 1 * 32 + 8
+    assert k_tile_index(40, 64)[33, 40] == 2344
+    assert k_tile_index(40, 64)[0, 0] == 0 and k_tile_index(40, 64)[0, 32] == 16 * 32
+    # a full group: the fragment of keys 16..31 x dims 64..95 is one 512-element run
+    idx = k_tile_index(64, 128)
+    run = np.sort(idx[16:32, 64:96].ravel())
+    assert np.array_equal(run, np.arange(16 * 128 + 2 * 16 * 32, 16 * 128 + 3 * 16 * 32))
+    # 8 consecutive dims of one key stay consecutive (16-byte accesses)
+    assert np.array_equal(idx[5, 24:32], np.arange(idx[5, 24], idx[5, 24] + 8))
+
+
+def test_tile_k_round_trip():
+    from foundry_amd.kv_layout import tile_k, untile_k, k_tile_index
+    k = np.arange(2 * 3 * 40 * 64, dtype=np.uint16).reshape(2, 3, 40, 64)
+    t = tile_k(k)
+    assert np.array_equal(untile_k(t), k)
+    flat = t.reshape(2, 3, -1)
+    assert flat[1, 2, k_tile_index(40, 64)[33, 40]] == k[1, 2, 33, 40]
