@@ -30,6 +30,12 @@ int rope_kv(fh_device *dev, const char *fn, const uint16_t *qkv, const float *pa
             uint64_t part_stride, int64_t tokens, int64_t n_heads, int64_t n_kv, int64_t head_dim,
             const uint16_t *cos_tab, const uint16_t *sin_tab, int64_t table_len, const uint32_t *positions,
             uint16_t *k_cache, uint16_t *v_cache, int64_t max_len, uint16_t *q_out);
+int q4_down_pack(fh_device *dev, const char *fn, const uint16_t *x, int64_t m, int64_t x_ld, const uint32_t *wq,
+                 const uint16_t *scales, const uint16_t *biases, int64_t n, int64_t k, const uint16_t *res,
+                 uint16_t *res_out, const uint16_t *norm_weight, float eps, const uint32_t *next_wq,
+                 const uint16_t *next_scales, const uint16_t *next_biases, int64_t next_n, bool *packed);
+int q4_gemv_packed(fh_device *dev, const char *fn, int64_t m, const uint32_t *wq, const uint16_t *scales,
+                   const uint16_t *biases, int64_t n, int64_t k, void *y, int y_is_f32);
 }  // namespace fh
 
 namespace {
@@ -217,10 +223,17 @@ extern "C" int fh_llama_forward(fh_device *dev, const fh_llama_model *model, int
     uint16_t *h = m.h, *h_alt = m.h2;
     const uint16_t *pending = nullptr;
     uint32_t pending_splits = 1;  // above 8 rows: K splits of the GEMM behind pending
+    // batched decode: the down projection left the next RMSNorm'd GEMV's
+    // image in the pack area (q4_down_pack) and h_alt = pending + h
+    bool packed = false;
     for (int64_t l = 0; l < m.n_layers; ++l) {
         const fh_llama_layer &L = m.layers[l];
         uint32_t qkv_splits = 1;
-        if (!fused) {
+        if (packed) {
+            FH_TRY(fh::q4_gemv_packed(dev, fn, tokens, L.qkv.wq, L.qkv.scales, L.qkv.biases, L.qkv.n, L.qkv.k,
+                                      m.qkv, 0));
+            std::swap(h, h_alt);
+        } else if (!fused) {
             FH_TRY(add_norm(dev, m, tokens, pending, pending_splits, L.input_norm));
             // one token per sequence: fh_decode_attention reads qkv itself
             if (seq_tokens > 1)
@@ -253,7 +266,18 @@ extern "C" int fh_llama_forward(fh_device *dev, const fh_llama_model *model, int
                                       w.biases, w.n, kGroup, m.act));
             std::swap(h, h_alt);
         }
-        FH_TRY(linear(dev, m.act, tokens, m.ffn, L.down, m.o));
+        packed = false;
+        if (seq_tokens == 1) {
+            // the next RMSNorm'd GEMV: the next layer's q/k/v, or the LM head
+            const bool last = l + 1 == m.n_layers;
+            const fh_q4_weight &nw = last ? m.embed : m.layers[l + 1].qkv;
+            const uint16_t *norm_w = last ? m.final_norm : m.layers[l + 1].input_norm;
+            const fh_q4_weight &w = L.down;
+            FH_TRY(fh::q4_down_pack(dev, fn, m.act, tokens, m.ffn, w.wq, w.scales, w.biases, w.n, w.k, h,
+                                    last ? nullptr : h_alt, norm_w, m.rms_norm_eps, nw.wq, nw.scales, nw.biases,
+                                    nw.n, &packed));
+        }
+        if (!packed) FH_TRY(linear(dev, m.act, tokens, m.ffn, L.down, m.o));
         pending = m.o;
     }
     // logits of each sequence's last row (src/models/llama/model.rs:112-121)
@@ -262,6 +286,9 @@ extern "C" int fh_llama_forward(fh_device *dev, const fh_llama_model *model, int
         // no layers: the embedding rows are the hidden states
         FH_TRY(norm(dev, m, tokens, nullptr, m.final_norm));
         FH_TRY(linear(dev, m.x + last, m.batch, seq_tokens * m.hidden, m.embed, m.logits));
+    } else if (packed) {
+        FH_TRY(fh::q4_gemv_packed(dev, fn, m.batch, m.embed.wq, m.embed.scales, m.embed.biases, m.embed.n,
+                                  m.embed.k, m.logits, 0));
     } else if (fused && seq_tokens == 1) {
         FH_TRY(linear_norm(dev, m, pending, h, nullptr, m.final_norm, m.batch, m.embed, m.logits));
     } else if (fused) {

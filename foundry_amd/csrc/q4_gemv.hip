@@ -81,17 +81,27 @@ void launch_q4_gemv_mfma(hipStream_t stream, uint32_t cus, int m, const GemvArgs
 }
 
 // Launches the pack kernel for m (2..8) RMSNorm rows of a (k <= kMfPackMaxK)
-// into the device's pack area.
-void launch_mf_pack(hipStream_t stream, int m, const GemvArgs &a, void *area) {
+// into the device's pack area; with part, the rows are the ranges' f32 sums
+// [ranges][m][k] instead of a.x.
+void launch_mf_pack(hipStream_t stream, int m, const GemvArgs &a, void *area, const float *part,
+                    uint32_t ranges) {
+#define FH_PACK_CASE(MM)                                                          \
+    case MM:                                                                      \
+        if (part)                                                                 \
+            launch_mf_pack_m<MM, true>(stream, a, area, part, ranges);            \
+        else                                                                      \
+            launch_mf_pack_m<MM, false>(stream, a, area, nullptr, 0);             \
+        break;
     switch (m) {
-        case 2: launch_mf_pack_m<2>(stream, a, area); break;
-        case 3: launch_mf_pack_m<3>(stream, a, area); break;
-        case 4: launch_mf_pack_m<4>(stream, a, area); break;
-        case 5: launch_mf_pack_m<5>(stream, a, area); break;
-        case 6: launch_mf_pack_m<6>(stream, a, area); break;
-        case 7: launch_mf_pack_m<7>(stream, a, area); break;
-        default: launch_mf_pack_m<8>(stream, a, area);
+        FH_PACK_CASE(2)
+        FH_PACK_CASE(3)
+        FH_PACK_CASE(4)
+        FH_PACK_CASE(5)
+        FH_PACK_CASE(6)
+        FH_PACK_CASE(7)
+        default: FH_PACK_CASE(8)
     }
+#undef FH_PACK_CASE
 }
 
 }  // namespace fh

@@ -412,32 +412,59 @@ constexpr int kMfPackThreads = 512;
 constexpr int kMfPackPieces = kMfPackMaxK / 8 / kMfPackThreads;  // 16-byte pieces per thread
 static_assert(mf_image_slots(8, kMfPackMaxK) * 16ull <= kPackAreaBytes, "the pack area holds the image of 8 rows");
 
+// K ranges a split GEMV may use (the combine's loads are issued for all).
+constexpr uint32_t kMfMaxRanges = 8;
+
 // Block m (one per x row, k <= kMfPackMaxK): h = x (+ res) (to res_out when
 // given), the row's scale = 1 / sqrt(mean(h^2) + eps) and x' = RNE(RNE(h *
 // scale) * w), RmsNorm's rounding points (src/nn/norm.rs:32-50); x' goes to
 // img as the GEMV's LDS image: fragments (mf_slot), the zero slot, a dummy
 // slot, then X [G][8] = group sums of x' (block 0 writes the zero slot and the
-// zeros of rows M..7). Sums run in a fixed order.
-template <int M>
-__global__ __launch_bounds__(kMfPackThreads) void mf_pack_kernel(const uint16_t *__restrict__ x, GemvFusion fu,
-                                                                uint32_t k, uint4 *__restrict__ img) {
-    __shared__ float part[kMfPackThreads / 64];
+// zeros of rows M..7). Sums run in a fixed order. P: 16-byte pieces per
+// thread (k <= 8 * 512 * P).
+// PARTS: x is not given; its row is formed here from the f32 partial sums of
+// a GEMV split over `ranges` K ranges ([ranges][M][k]), added in range order
+// and rounded to bf16 exactly as mf_combine_kernel would write it, so the
+// combine's launch and its round trip through memory are saved.
+template <int M, int P, bool PARTS>
+__global__ __launch_bounds__(kMfPackThreads) void mf_pack_kernel(const uint16_t *__restrict__ x,
+                                                                const float *__restrict__ part, uint32_t ranges,
+                                                                GemvFusion fu, uint32_t k, uint4 *__restrict__ img) {
+    __shared__ float red[kMfPackThreads / 64];
     const uint32_t m = blockIdx.x, ppr = k / 8, G = k / kGroup, t = threadIdx.x;
     const uint32_t lane = t & 63, wave = t >> 6;
     const bool has_res = fu.res != nullptr;
-    const uint16_t *xr = x + static_cast<uint64_t>(m) * k;
-    const uint16_t *rr = (has_res ? fu.res : x) + static_cast<uint64_t>(m) * k;  // used only with a residual
-    uint4 h[kMfPackPieces], r[kMfPackPieces], w[kMfPackPieces];
+    const uint16_t *rr = (has_res ? fu.res : fu.w) + (has_res ? static_cast<uint64_t>(m) * k : 0u);  // used only with a residual
+    uint4 h[P], r[P], w[P];
 #pragma unroll
-    for (int i = 0; i < kMfPackPieces; ++i) {
+    for (int i = 0; i < P; ++i) {
         const uint32_t c = t + i * kMfPackThreads, cc = c < ppr ? c : 0u;
-        h[i] = *reinterpret_cast<const uint4 *>(xr + cc * 8);
-        r[i] = *reinterpret_cast<const uint4 *>(rr + cc * 8);
+        if constexpr (PARTS) {
+            float4 lo[kMfMaxRanges], hi[kMfMaxRanges];
+#pragma unroll
+            for (uint32_t q = 0; q < kMfMaxRanges; ++q) {
+                const float *pp = part + (static_cast<uint64_t>(q < ranges ? q : 0u) * M + m) * k + cc * 8;
+                lo[q] = *reinterpret_cast<const float4 *>(pp);
+                hi[q] = *reinterpret_cast<const float4 *>(pp + 4);
+            }
+            float4 a = lo[0], b = hi[0];
+#pragma unroll
+            for (uint32_t q = 1; q < kMfMaxRanges; ++q)
+                if (q < ranges) {
+                    a = make_float4(a.x + lo[q].x, a.y + lo[q].y, a.z + lo[q].z, a.w + lo[q].w);
+                    b = make_float4(b.x + hi[q].x, b.y + hi[q].y, b.z + hi[q].z, b.w + hi[q].w);
+                }
+            h[i] = make_uint4(f32x2_to_bf16x2_rne(a.x, a.y), f32x2_to_bf16x2_rne(a.z, a.w),
+                              f32x2_to_bf16x2_rne(b.x, b.y), f32x2_to_bf16x2_rne(b.z, b.w));
+        } else {
+            h[i] = *reinterpret_cast<const uint4 *>(x + static_cast<uint64_t>(m) * k + cc * 8);
+        }
+        r[i] = *reinterpret_cast<const uint4 *>(rr + (has_res ? cc * 8 : 0u));
         w[i] = *reinterpret_cast<const uint4 *>(fu.w + cc * 8);
     }
     float ss = 0.f;
 #pragma unroll
-    for (int i = 0; i < kMfPackPieces; ++i) {
+    for (int i = 0; i < P; ++i) {
         const uint32_t c = t + i * kMfPackThreads;
         const bool live = c < ppr;
         if (has_res) {
@@ -455,16 +482,16 @@ __global__ __launch_bounds__(kMfPackThreads) void mf_pack_kernel(const uint16_t 
         ss += live ? sq : 0.f;
     }
     ss = wave_sum(ss);
-    if (lane == 0) part[wave] = ss;
+    if (lane == 0) red[wave] = ss;
     __syncthreads();
     float tot = 0.f;
 #pragma unroll
-    for (int i = 0; i < kMfPackThreads / 64; ++i) tot += part[i];
+    for (int i = 0; i < kMfPackThreads / 64; ++i) tot += red[i];
     const float scale = 1.0f / sqrtf(tot * fu.dim_inv + fu.eps);
     float *xs = reinterpret_cast<float *>(img + static_cast<uint64_t>(M) * ppr + 2);
     if (m == 0 && t == 0) img[static_cast<uint64_t>(M) * ppr] = make_uint4(0u, 0u, 0u, 0u);  // the zero slot
 #pragma unroll
-    for (int i = 0; i < kMfPackPieces; ++i) {
+    for (int i = 0; i < P; ++i) {
         const uint32_t c = t + i * kMfPackThreads;
         const bool live = c < ppr;
         const uint4 p = gemv_permute(gemv_pairwise(h[i], w[i], [scale](float hh, float gg) {
@@ -478,10 +505,25 @@ __global__ __launch_bounds__(kMfPackThreads) void mf_pack_kernel(const uint16_t 
         for (uint32_t j = t; j < (8 - M) * G; j += kMfPackThreads) xs[(j % G) * 8 + M + j / G] = 0.f;
 }
 
-template <int M>
-inline void launch_mf_pack_m(hipStream_t stream, const GemvArgs &a, void *area) {
-    hipLaunchKernelGGL(mf_pack_kernel<M>, dim3(M), dim3(kMfPackThreads), 0, stream, a.x, a.fu, a.k,
-                       static_cast<uint4 *>(area));
+// Pieces per thread for rows of k values.
+constexpr int mf_pack_pieces(uint32_t k) { return k <= 8u * kMfPackThreads ? 1 : k <= 16u * kMfPackThreads ? 2 : 4; }
+
+template <int M, bool PARTS>
+inline void launch_mf_pack_m(hipStream_t stream, const GemvArgs &a, void *area, const float *part,
+                             uint32_t ranges) {
+    switch (mf_pack_pieces(a.k)) {
+        case 1:
+            hipLaunchKernelGGL((mf_pack_kernel<M, 1, PARTS>), dim3(M), dim3(kMfPackThreads), 0, stream, a.x, part,
+                               ranges, a.fu, a.k, static_cast<uint4 *>(area));
+            break;
+        case 2:
+            hipLaunchKernelGGL((mf_pack_kernel<M, 2, PARTS>), dim3(M), dim3(kMfPackThreads), 0, stream, a.x, part,
+                               ranges, a.fu, a.k, static_cast<uint4 *>(area));
+            break;
+        default:
+            hipLaunchKernelGGL((mf_pack_kernel<M, 4, PARTS>), dim3(M), dim3(kMfPackThreads), 0, stream, a.x, part,
+                               ranges, a.fu, a.k, static_cast<uint4 *>(area));
+    }
 }
 
 // Picks the K split (wavefronts per task) from the weight's 16-row tiles, its

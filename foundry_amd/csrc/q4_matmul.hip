@@ -13,7 +13,8 @@ int check_q4_table(const fh_device *dev, const char *fn, const uint32_t *wq,
                    int64_t group);
 void launch_q4_gemv(hipStream_t stream, uint32_t cus, int m, const GemvArgs &a);
 void launch_q4_gemv_mfma(hipStream_t stream, uint32_t cus, int m, const GemvArgs &a);
-void launch_mf_pack(hipStream_t stream, int m, const GemvArgs &a, void *area);
+void launch_mf_pack(hipStream_t stream, int m, const GemvArgs &a, void *area, const float *part = nullptr,
+                    uint32_t ranges = 0);
 uint32_t gemv_rows_per_launch(uint32_t k, bool norm);
 void launch_q4_gemm(hipStream_t stream, uint32_t cus, const uint16_t *x, uint32_t x_ld, const uint32_t *wq,
                     const uint16_t *s, const uint16_t *b, uint32_t m, uint32_t n, uint32_t k,
@@ -28,7 +29,6 @@ constexpr int64_t kGemvMaxRows = 8;
 // RMSNorm rows), else the dot2 kernel; x, res, res_out and y advance by their
 // row strides. y_cols: columns of y per row.
 // Ranges of K a matrix-core GEMV may be split into (partial sums per range).
-constexpr uint32_t kMfMaxRanges = 8;
 // x bytes per block the range count aims at (each block stages its range of
 // every x row).
 constexpr uint32_t kMfRangeXBytes = 32 * 1024;
@@ -133,6 +133,74 @@ int launch_gemv_rows(fh_device *dev, const char *fn, int64_t m, const GemvArgs &
         if (rc) return rc;
     }
     return FH_OK;
+}
+
+// The batched decode step's down projection and the next RMSNorm'd GEMV's
+// pack as one launch less: y = x W^T runs over K ranges into the partial
+// area as fh_q4_matmul would run it, and the pack kernel then forms each row
+// of y from the ranges' sums itself (no combine launch, no y in memory),
+// adds the residual (h to res_out), normalises it with norm_weight and
+// writes the image the next GEMV (next_n rows of w.n columns) reads, the
+// same values fh_q4_matmul followed by fh_q4_matmul_rmsnorm's pack produce.
+// *packed = false (nothing launched) when the shapes do not take that route:
+// m outside 2..8, the down projection not split into K ranges, or the next
+// GEMV not taking all m rows from one image.
+int q4_down_pack(fh_device *dev, const char *fn, const uint16_t *x, int64_t m, int64_t x_ld, const uint32_t *wq,
+                 const uint16_t *scales, const uint16_t *biases, int64_t n, int64_t k, const uint16_t *res,
+                 uint16_t *res_out, const uint16_t *norm_weight, float eps, const uint32_t *next_wq,
+                 const uint16_t *next_scales, const uint16_t *next_biases, int64_t next_n, bool *packed) {
+    *packed = false;
+    if (m < 2 || m > 8 || k <= 0 || n <= 0 || n > kMfPackMaxK || x_ld > 0x7FFFFFFFll) return FH_OK;
+    GemvArgs down{x, static_cast<uint32_t>(x_ld), wq, scales, biases, static_cast<uint32_t>(n),
+                  static_cast<uint32_t>(k), nullptr, static_cast<uint32_t>(n), 1, kProNone, kEpiNone,
+                  GemvFusion{}};
+    if (!mf_eligible(static_cast<uint32_t>(m), down) || mf_rows_per_launch(down.k, 1) >= m) return FH_OK;
+    const uint32_t ranges = mf_k_ranges(dev, m, down);
+    if (ranges == 0) return FH_OK;
+    GemvArgs next{nullptr, static_cast<uint32_t>(n), next_wq, next_scales, next_biases, static_cast<uint32_t>(next_n),
+                  static_cast<uint32_t>(n), nullptr, static_cast<uint32_t>(next_n), 0, kProRmsNorm, kEpiNone,
+                  GemvFusion{}};
+    if (!mf_eligible(static_cast<uint32_t>(m), next) || mf_rows_per_launch(next.k, 1) < m) return FH_OK;
+    for (const void *p : {static_cast<const void *>(x), static_cast<const void *>(res),
+                          static_cast<const void *>(res_out), static_cast<const void *>(norm_weight)})
+        if (reinterpret_cast<uintptr_t>(p) % 16 != 0) return FH_OK;
+    if (!norm_weight || (res_out && !res)) return FH_OK;
+    const uint64_t row_bytes = static_cast<uint64_t>(m) * n * 2;
+    if (int rc = check_range(dev, x, (static_cast<uint64_t>(m - 1) * x_ld + k) * 2, fn, "x")) return rc;
+    if (res)
+        if (int rc = check_range(dev, res, row_bytes, fn, "residual")) return rc;
+    if (res_out)
+        if (int rc = check_range(dev, res_out, row_bytes, fn, "residual_out")) return rc;
+    if (int rc = check_range(dev, norm_weight, static_cast<uint64_t>(n) * 2, fn, "norm_weight")) return rc;
+    GemvArgs a = down;
+    a.k = down.k / ranges;
+    a.kranges = ranges;
+    a.y = dev->partial_area;
+    a.y_is_f32 = 1;
+    a.y_ld = down.n;
+    if (int rc = dispatch(dev, fn, [&] { launch_q4_gemv_mfma(dev->stream, dev->compute_units, static_cast<int>(m), a); }))
+        return rc;
+    GemvArgs p{};
+    p.k = static_cast<uint32_t>(n);
+    p.fu = GemvFusion{res, res_out, norm_weight, eps, 1.0f / static_cast<float>(n)};
+    if (int rc = dispatch(dev, fn, [&] {
+            launch_mf_pack(dev->stream, static_cast<int>(m), p, dev->pack_area,
+                           static_cast<const float *>(dev->partial_area), ranges);
+        }))
+        return rc;
+    *packed = true;
+    return FH_OK;
+}
+
+// The RMSNorm'd GEMV of m rows on the image q4_down_pack left in the pack
+// area (weight [n, k], k the image's row length).
+int q4_gemv_packed(fh_device *dev, const char *fn, int64_t m, const uint32_t *wq, const uint16_t *scales,
+                   const uint16_t *biases, int64_t n, int64_t k, void *y, int y_is_f32) {
+    GemvArgs a{static_cast<const uint16_t *>(dev->pack_area), static_cast<uint32_t>(k), wq, scales, biases,
+               static_cast<uint32_t>(n), static_cast<uint32_t>(k), y, static_cast<uint32_t>(n), y_is_f32,
+               kProRmsNorm, kEpiNone, GemvFusion{}};
+    if (int rc = check_range(dev, y, static_cast<uint64_t>(m) * n * (y_is_f32 ? 4 : 2), fn, "y")) return rc;
+    return dispatch(dev, fn, [&] { launch_q4_gemv_mfma(dev->stream, dev->compute_units, static_cast<int>(m), a); });
 }
 
 }  // namespace fh
