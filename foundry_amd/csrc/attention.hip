@@ -512,7 +512,10 @@ __global__ __launch_bounds__(kAttnThreads) void attn_pv_kernel(
 // lanes' and wavefronts' partials are added in a fixed order. With one chunk
 // per row the result (RNE) goes to out, else the f32 partial goes to part
 // for attn_combine_kernel.
-constexpr int kPvWaveTile = 16;  // keys per wavefront tile
+#ifndef FH_PV_WAVE_TILE
+#define FH_PV_WAVE_TILE 16
+#endif
+constexpr int kPvWaveTile = FH_PV_WAVE_TILE;  // keys per wavefront tile
 // Tiles a chunked P.V wavefront keeps in flight.
 #ifndef FH_PV_DEPTH
 #define FH_PV_DEPTH 2
