@@ -289,16 +289,84 @@ __global__ __launch_bounds__(kGemvThreads) void q4_gemv_kernel(
         // loads and the reduction would make the compiler wait for the
         // weights there.
         if (pieces <= 2 * kGemvThreads) {
+            // every piece stays in its thread's registers between the two
+            // passes (h and its norm weight), so pass 2 reads no LDS and pass
+            // 1 writes none; the arithmetic is finish()'s
             uint4 x0, r0, w0, x1, r1, w1;
-            load_round(0, x0, r0, w0);
-            load_round(kGemvThreads, x1, r1, w1);
+            auto load_round_w = [&](uint32_t t0, uint4 &xv, uint4 &rv, uint4 &wv) {
+                const uint32_t t = t0 + threadIdx.x;
+                const uint64_t o = xoff(t < pieces ? t : 0);
+                xv = *reinterpret_cast<const uint4 *>(x + o);
+                rv = fu.res ? *reinterpret_cast<const uint4 *>(fu.res + o) : make_uint4(0u, 0u, 0u, 0u);
+                wv = *reinterpret_cast<const uint4 *>(fu.w + ((t < pieces ? t : 0) % (chunks * 4)) * 8);
+            };
+            load_round_w(0, x0, r0, w0);
+            load_round_w(kGemvThreads, x1, r1, w1);
             __builtin_amdgcn_sched_barrier(0);  // keep these ahead of the weight loads
             load(group_first < groups_total ? group_first : groups_total - 1, 0, buf);
-            // both rounds are processed unconditionally (dead pieces are
-            // masked inside), so their loads cannot sink below the weights'
-            process(0, x0, r0, w0);
-            process(kGemvThreads, x1, r1, w1);
-            finish();
+            // both rounds are handled unconditionally (dead pieces are masked
+            // inside), so their loads cannot sink below the weights'
+            auto sum_round = [&](uint32_t t0, uint4 &xv, const uint4 rv) {
+                const uint32_t t = t0 + threadIdx.x;
+                const bool live = t < pieces;
+                if (fu.res) {
+                    xv = gemv_pairwise(xv, rv, [](float a, float b) { return a + b; });
+                    if (blockIdx.x == 0 && fu.res_out && live)
+                        *reinterpret_cast<uint4 *>(fu.res_out + xoff(t)) = xv;
+                }
+                if (live) {
+                    const uint32_t hv[4] = {xv.x, xv.y, xv.z, xv.w};
+                    float sq = 0.f;
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        const float lo = bf16_to_f32(hv[e] & 0xFFFFu), hi = bf16_to_f32(hv[e] >> 16);
+                        sq += lo * lo;
+                        sq += hi * hi;
+                    }
+                    const uint32_t m = t / (chunks * 4);
+#pragma unroll
+                    for (int mm = 0; mm < M; ++mm)
+                        if (mm == static_cast<int>(m)) ss[mm] += sq;
+                }
+            };
+            sum_round(0, x0, r0);
+            sum_round(kGemvThreads, x1, r1);
+            {
+                const uint32_t lane_x = threadIdx.x & 63, wave_x = threadIdx.x >> 6;
+#pragma unroll
+                for (int m = 0; m < M; ++m) {
+                    float v = ss[m];
+#pragma unroll
+                    for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
+                    if (lane_x == 0) red[wave_x][m] = v;
+                }
+            }
+            __syncthreads();
+            auto norm_round = [&](uint32_t t0, const uint4 hv, const uint4 wv) {
+                const uint32_t t = t0 + threadIdx.x;
+                const bool live = t < pieces;
+                const uint32_t m = live ? t / (chunks * 4) : 0, c = (t / 4) % chunks, wi = t % 4;
+                float tot = 0.f;
+#pragma unroll
+                for (int w = 0; w < kGemvWaves; ++w) tot += red[w][m];
+                const float scale = 1.0f / sqrtf(tot * fu.dim_inv + fu.eps);
+                float psum = 0.f;
+                if (live) {
+                    const uint4 p = gemv_permute(gemv_pairwise(hv, wv, [scale](float h, float g) {
+                        return bf16_to_f32(f32_to_bf16_rne(h * scale)) * g;
+                    }));
+                    xs[(m * 4 + wi) * chunks + c] = p;
+                    psum = ((bf16_to_f32(p.x & 0xFFFFu) + bf16_to_f32(p.y & 0xFFFFu)) +
+                            (bf16_to_f32(p.z & 0xFFFFu) + bf16_to_f32(p.w & 0xFFFFu))) +
+                           ((bf16_to_f32(p.x >> 16) + bf16_to_f32(p.y >> 16)) +
+                            (bf16_to_f32(p.z >> 16) + bf16_to_f32(p.w >> 16)));
+                }
+                psum += __shfl_xor(psum, 1, 64);
+                psum += __shfl_xor(psum, 2, 64);
+                if (live && wi == 0) xsum[m * chunks + c] = psum;
+            };
+            norm_round(0, x0, w0);
+            norm_round(kGemvThreads, x1, w1);
         } else {
             load(group_first < groups_total ? group_first : groups_total - 1, 0, buf);
             for (uint32_t t0 = 0; t0 < pieces; t0 += kGemvThreads) {
