@@ -27,6 +27,7 @@
 //   shuffles; one lane writes each output (bf16 RNE or fp32).
 #pragma once
 
+#include "decoder_common.hpp"
 #include "device.hpp"
 #include "q4_common.hpp"
 
@@ -280,8 +281,8 @@ __global__ __launch_bounds__(kGemvThreads) void q4_gemv_kernel(
                            ((bf16_to_f32(p.x >> 16) + bf16_to_f32(p.y >> 16)) +
                             (bf16_to_f32(p.z >> 16) + bf16_to_f32(p.w >> 16)));
                 }
-                psum += __shfl_xor(psum, 1, 64);
-                psum += __shfl_xor(psum, 2, 64);
+                psum += dpp_mov<0xB1>(psum);  // lane ^ 1
+                psum += dpp_mov<0x4E>(psum);  // lane ^ 2
                 if (live && wi == 0) xsum[m * chunks + c] = psum;
             }
         };
@@ -361,8 +362,8 @@ __global__ __launch_bounds__(kGemvThreads) void q4_gemv_kernel(
                            ((bf16_to_f32(p.x >> 16) + bf16_to_f32(p.y >> 16)) +
                             (bf16_to_f32(p.z >> 16) + bf16_to_f32(p.w >> 16)));
                 }
-                psum += __shfl_xor(psum, 1, 64);
-                psum += __shfl_xor(psum, 2, 64);
+                psum += dpp_mov<0xB1>(psum);  // lane ^ 1
+                psum += dpp_mov<0x4E>(psum);  // lane ^ 2
                 if (live && wi == 0) xsum[m * chunks + c] = psum;
             };
             norm_round(0, x0, w0);
