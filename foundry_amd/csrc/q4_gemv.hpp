@@ -177,10 +177,11 @@ __global__ __launch_bounds__(kGemvThreads) void q4_gemv_kernel(
             p.z = (v[wi].y & 0xFFFFu) | (v[wi].w << 16);      // (x2, x6)
             p.w = (v[wi].y >> 16) | (v[wi].w & 0xFFFF0000u);  // (x3, x7)
             xs[(m * 4 + wi) * chunks + c] = p;
-            sum += bf16_to_f32(v[wi].x & 0xFFFFu) + bf16_to_f32(v[wi].x >> 16);
-            sum += bf16_to_f32(v[wi].y & 0xFFFFu) + bf16_to_f32(v[wi].y >> 16);
-            sum += bf16_to_f32(v[wi].z & 0xFFFFu) + bf16_to_f32(v[wi].z >> 16);
-            sum += bf16_to_f32(v[wi].w & 0xFFFFu) + bf16_to_f32(v[wi].w >> 16);
+            // pair sums as dot products with (1, 1): one instruction per pair
+            sum = dot2_bf16(v[wi].x, 0x3F803F80u, sum);
+            sum = dot2_bf16(v[wi].y, 0x3F803F80u, sum);
+            sum = dot2_bf16(v[wi].z, 0x3F803F80u, sum);
+            sum = dot2_bf16(v[wi].w, 0x3F803F80u, sum);
         }
         xsum[m * chunks + c] = sum;
     };
