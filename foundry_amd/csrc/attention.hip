@@ -150,8 +150,10 @@ __global__ __launch_bounds__(kAttnThreads) void attn_scores_kernel(
     constexpr int HP = NQ * 4;        // head slots per key after the move
     static_assert(kAttnChunk == 64, "a chunk is 4 groups of 16 keys");
     static_assert(G <= 16, "query heads fit the MFMA rows");
-    __shared__ __align__(16) uint16_t qb[ROPE ? G : 1][ROPE ? HD : 8];
-    __shared__ __align__(16) uint16_t knew[ROPE ? HD : 8];
+    // rotated q heads (rows 0..G-1), the rotated new key (row G) and a row
+    // the other threads write (G + 1)
+    __shared__ __align__(16) uint16_t qb[ROPE ? G + 2 : 1][ROPE ? HD : 8];
+    __shared__ __align__(16) uint4 vpark[ROPE ? kAttnThreads : 1];
     __shared__ __align__(16) float sc[kAttnWaves][kAttnChunk][HP];  // raw dot products, lane = key
     const uint32_t tid = threadIdx.x, r = blockIdx.y, kvh = blockIdx.x / splits, split = blockIdx.x % splits;
     const uint32_t pos = positions[r];
@@ -208,20 +210,28 @@ __global__ __launch_bounds__(kAttnThreads) void attn_scores_kernel(
         }
     }
     uint4 b[kScoresDepth][KS];  // key groups in flight
+    // The key groups go out after the RoPE inputs and the new value, pinned
+    // in that order: loads return in order, so the rotation waits for its own
+    // loads only, not for the keys.
+    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int grp = 0; grp < kScoresDepth; ++grp) load_grp(grp, b[grp]);
+    __builtin_amdgcn_sched_barrier(0);
     if constexpr (ROPE) {
         const bool owner = (pos / kAttnChunk) % splits == split;
         const uint4 ov = rope_apply(x4, r4, c4, s4, pp < PPH / 2);
-        if (tid < (G + 1) * PPH) {
-            if (hh < G) {
-                *reinterpret_cast<uint4 *>(&qb[hh][pp * 8]) = ov;
-            } else {
-                *reinterpret_cast<uint4 *>(knew + pp * 8) = ov;
-                if (owner) *reinterpret_cast<uint4 *>(k_cache + cache + k_offset(pos, pp * 8, max_len, HD)) = ov;
-            }
-        } else if (owner && tid < (G + 2) * PPH) {
-            *reinterpret_cast<uint4 *>(v_cache + cache + static_cast<uint64_t>(pos) * HD + (tid - (G + 1) * PPH) * 8) = v4;
+        // Every thread writes its rotation and its value piece to LDS, uses
+        // outside any branch: with only the branches below using them, the
+        // loads would sink into those branches, behind the key loads, and
+        // their waits would drain the keys.
+        *reinterpret_cast<uint4 *>(&qb[tid < (G + 1) * PPH ? hh : G + 1][pp * 8]) = ov;
+        vpark[tid] = v4;
+        if (owner) {
+            if (tid >= G * PPH && tid < (G + 1) * PPH)
+                *reinterpret_cast<uint4 *>(k_cache + cache + k_offset(pos, pp * 8, max_len, HD)) = ov;
+            else if (tid >= (G + 1) * PPH && tid < (G + 2) * PPH)
+                *reinterpret_cast<uint4 *>(v_cache + cache + static_cast<uint64_t>(pos) * HD +
+                                           (tid - (G + 1) * PPH) * 8) = v4;
         }
         __syncthreads();
         // A fragments: head `col` (zero for col >= G), dims 32 st + 8 quad.. of each step
@@ -232,7 +242,7 @@ __global__ __launch_bounds__(kAttnThreads) void attn_scores_kernel(
         }
     }
     if (total == 0) return;  // a wavefront without chunks (no barrier follows)
-    const uint4 *kn = reinterpret_cast<const uint4 *>(knew + 8 * quad);
+    const uint4 *kn = reinterpret_cast<const uint4 *>(&qb[ROPE ? G : 0][8 * quad]);
     for (uint32_t f0 = 0; f0 < total; f0 += 4) {
         const uint32_t c = c_first + (f0 / 4) * c_step;
 #pragma unroll
@@ -576,30 +586,43 @@ __global__ __launch_bounds__(kAttnThreads) void attn_pv_chunk_kernel(
     constexpr int kDepth = kPvDepth;
     uint4 vt[kDepth][IT];
     float sct[kDepth][NSW];
-#pragma unroll
-    for (int q = 0; q < kDepth; ++q) load_tile(q, vt[q], sct[q]);
-    // the row's softmax statistics, per wavefront (M, S the same everywhere):
-    // up to 128 chunks from registers (every head's loads issued together),
-    // longer rows in a loop
+    // The row's softmax statistics, per wavefront (M, S the same everywhere).
+    // Up to 128 chunks they come from registers: every head's loads go out
+    // first (unconditional, clamped), then the first tiles, pinned in that
+    // order, so M and S wait for their own loads only (loads return in
+    // order). Past the row's chunks the values are masked by arithmetic (a
+    // select on a loaded value may become a branch around the load, whose
+    // join would drain the tiles). Longer rows loop over the statistics.
     float mg[G], sg[G];
     const float2 *st0 = stats + (static_cast<uint64_t>(r) * n_heads + h0) * nck;
-    if (nact <= 128) {
-        float2 sv[G][2];
+    const bool in_regs = nact <= 128;
+    float2 sv[G][2];
+    if (in_regs) {
 #pragma unroll
         for (int g = 0; g < G; ++g)
 #pragma unroll
             for (int n = 0; n < 2; ++n) {
                 const uint32_t cc = lane + 64 * n;
-                const float2 v = st0[static_cast<uint64_t>(g) * nck + (cc < nact ? cc : 0)];
-                sv[g][n] = cc < nact ? v : make_float2(-INFINITY, 0.f);
+                sv[g][n] = st0[static_cast<uint64_t>(g) * nck + (cc < nact ? cc : nact - 1)];
             }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int q = 0; q < kDepth; ++q) load_tile(q, vt[q], sct[q]);
+    __builtin_amdgcn_sched_barrier(0);
+    if (in_regs) {
+        float m_add[2], l_mul[2];  // 0 and 1 for the row's chunks, -inf and 0 past them
+#pragma unroll
+        for (int n = 0; n < 2; ++n) {
+            const bool live = lane + 64 * n < nact;
+            m_add[n] = live ? 0.f : -INFINITY;
+            l_mul[n] = live ? 1.f : 0.f;
+        }
 #pragma unroll
         for (int g = 0; g < G; ++g) {
-            mg[g] = wave_max(fmaxf(sv[g][0].x, sv[g][1].x));
-            float sum = 0.f;
-#pragma unroll
-            for (int n = 0; n < 2; ++n)
-                if (lane + 64 * n < nact) sum += sv[g][n].y * expf(sv[g][n].x - mg[g]);
+            const float m0 = sv[g][0].x + m_add[0], m1 = sv[g][1].x + m_add[1];
+            mg[g] = wave_max(fmaxf(m0, m1));
+            const float sum = sv[g][0].y * l_mul[0] * expf(m0 - mg[g]) + sv[g][1].y * l_mul[1] * expf(m1 - mg[g]);
             sg[g] = wave_sum(sum);
         }
     } else {
