@@ -58,16 +58,10 @@ __device__ __forceinline__ mf_f32x4_t mf_mfma(const uint4 a, const uint4 b, cons
                                                    __builtin_bit_cast(mf_bf16x8_t, b), c, 0, 0, 0);
 }
 
-// Output tiles per task: the SiLU epilogue needs the gate tile and its up tile.
-template <int EPI>
-constexpr int mf_tiles_per_task() {
-    return EPI == kEpiSiluMul ? 2 : 1;
-}
-
 // LDS bytes: staged x fragments, a zero slot and a dummy slot, group sums X
 // [G][8], the partial tiles of the K split.
-__host__ __device__ constexpr uint32_t mf_lds_bytes(uint32_t m, uint32_t k, int nt) {
-    return m * k * 2 + 32 + (k / kGroup) * 8 * 4 + kMfWaves * nt * 4 * 64 * 4;
+__host__ __device__ constexpr uint32_t mf_lds_bytes(uint32_t m, uint32_t k) {
+    return m * k * 2 + 32 + (k / kGroup) * 8 * 4 + kMfWaves * 4 * 64 * 4;
 }
 
 // 16-byte slots of the packed LDS image: fragments, the zero and dummy
@@ -78,19 +72,19 @@ __host__ __device__ constexpr uint32_t mf_image_slots(uint32_t m, uint32_t k) {
 }
 
 // Largest x row count (<= 8) whose staged copy fits the LDS budget.
-inline uint32_t mf_rows_per_launch(uint32_t k, int nt) {
+inline uint32_t mf_rows_per_launch(uint32_t k) {
     uint32_t r = 8;
-    while (r > 0 && mf_lds_bytes(r, k, nt) > kMfLdsLimit) --r;
+    while (r > 0 && mf_lds_bytes(r, k) > kMfLdsLimit) --r;
     return r;
 }
 
 // One chunk (CH group pairs) of operands as a lane holds them: 16 bytes of
 // packed words per pair, and scale / bias of the chunk's groups (one dword
 // per pair: even group low, odd group high).
-template <int NT, int CH>
+template <int CH>
 struct MfChunk {
-    uint4 w[CH][NT];
-    uint32_t s[CH][NT], b[CH][NT];
+    uint4 w[CH];
+    uint32_t s[CH], b[CH];
 };
 
 // Decodes two packed words into bf16 pairs (128 + q_t, 128 + q_{t+4}); the
@@ -142,7 +136,6 @@ __global__ __launch_bounds__(kMfThreads) void q4_gemv_mfma_kernel(
     const uint16_t *__restrict__ x, uint32_t x_ld, const uint32_t *__restrict__ wq,
     const uint16_t *__restrict__ scales, const uint16_t *__restrict__ biases, uint32_t n, uint32_t k,
     void *__restrict__ y, uint32_t y_ld, int y_is_f32, uint32_t ksplit) {
-    constexpr int NT = mf_tiles_per_task<EPI>();
     constexpr bool kPacked = PRO == kProRmsNorm;  // x: mf_pack_kernel's image of RMSNorm(x + res)
     static_assert(kMfWaves / 2 * M * 16 <= kMfThreads, "a K-split round stores one output per thread at most");
     extern __shared__ uint4 lds[];
@@ -158,13 +151,16 @@ __global__ __launch_bounds__(kMfThreads) void q4_gemv_mfma_kernel(
         biases += static_cast<uint64_t>(blockIdx.y) * G;
         y = static_cast<float *>(y) + static_cast<uint64_t>(blockIdx.y) * M * y_ld;
     }
+    // A task is one 16-column B tile: 16 weight rows, or with the SiLU
+    // epilogue 8 gate rows and their 8 up rows (n / 2 rows on), so that every
+    // variant over a weight has n / 16 tasks and spreads them alike.
     const uint32_t n_out = EPI == kEpiSiluMul ? n / 2 : n;
-    const uint32_t tiles = n_out / 16;
+    const uint32_t tiles = n / 16;
     uint4 *xa = lds;                                         // [G/2][4 j][4 q][M] fragments
     const uint32_t zero = M * wpr;                           // a zero fragment (dead A lanes)
     const uint32_t dummy = zero + 1;                         // write-only slot for dead items
     float *xsum = reinterpret_cast<float *>(lds + dummy + 1);  // [G][8]
-    float *red = xsum + G * 8;                               // [16][NT][4][64]
+    float *red = xsum + G * 8;                               // [16][4][64]
 
     const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const uint32_t col = lane & 15, quarter = lane >> 4, hi = quarter >> 1;
@@ -178,7 +174,9 @@ __global__ __launch_bounds__(kMfThreads) void q4_gemv_mfma_kernel(
     auto tile_of = [&](uint32_t r) { return (r * gridDim.x + blockIdx.x) * slots + slot; };
 
     // ---- weight operands ----
-    auto wrow = [&](uint32_t tile, int t) { return (EPI == kEpiSiluMul && t == 1 ? n_out : 0u) + tile * 16 + col; };
+    auto wrow = [&](uint32_t tile) {
+        return EPI == kEpiSiluMul ? (col < 8 ? 0u : n_out) + tile * 8 + (col & 7) : tile * 16 + col;
+    };
     // chunk c (of this wavefront's sequence) -> operands; past the end, the
     // last chunk again (values unused)
     // Chunks past the end, and tiles past the last of a partial round, read
@@ -186,37 +184,34 @@ __global__ __launch_bounds__(kMfThreads) void q4_gemv_mfma_kernel(
     // at hand in L1): a reload of real operands would be waited for before
     // the last reduction. The choice is a select on uniform values, not a
     // branch, so every wait still counts exactly.
-    auto load = [&](uint32_t c, MfChunk<NT, CH> &cb) {
+    auto load = [&](uint32_t c, MfChunk<CH> &cb) {
         const uint32_t cc = c < total ? c : total - 1;
         const uint32_t r = cc / cpt;
         const uint32_t p0 = (ks * gs) / 2 + (cc % cpt) * CH;  // first pair
         uint32_t tile = tile_of(r);
         const bool dead = c >= total || tile >= tiles;
         tile = tile < tiles ? tile : tiles - 1;
+        const uint64_t row = wrow(tile);
+        const uint4 *wp = reinterpret_cast<const uint4 *>(wq + row * w_ld + p0 * 16 + quarter * 4);
+        if (dead) wp = reinterpret_cast<const uint4 *>(wq);
 #pragma unroll
-        for (int t = 0; t < NT; ++t) {
-            const uint64_t row = wrow(tile, t);
-            const uint4 *wp = reinterpret_cast<const uint4 *>(wq + row * w_ld + p0 * 16 + quarter * 4);
-            if (dead) wp = reinterpret_cast<const uint4 *>(wq);
-#pragma unroll
-            for (int c2 = 0; c2 < CH; ++c2) cb.w[c2][t] = wp[c2 * 4];
-            const uint16_t *sp = scales + row * sb_ld + p0 * 2, *bp = biases + row * sb_ld + p0 * 2;
-            if (dead) sp = scales, bp = biases;
-            if constexpr (CH == 4) {
-                const uint4 sv = *reinterpret_cast<const uint4 *>(sp), bv = *reinterpret_cast<const uint4 *>(bp);
-                cb.s[0][t] = sv.x, cb.s[1][t] = sv.y, cb.s[2][t] = sv.z, cb.s[3][t] = sv.w;
-                cb.b[0][t] = bv.x, cb.b[1][t] = bv.y, cb.b[2][t] = bv.z, cb.b[3][t] = bv.w;
-            } else if constexpr (CH == 2) {
-                const uint2 sv = *reinterpret_cast<const uint2 *>(sp), bv = *reinterpret_cast<const uint2 *>(bp);
-                cb.s[0][t] = sv.x, cb.s[1][t] = sv.y;
-                cb.b[0][t] = bv.x, cb.b[1][t] = bv.y;
-            } else {
-                cb.s[0][t] = *reinterpret_cast<const uint32_t *>(sp);
-                cb.b[0][t] = *reinterpret_cast<const uint32_t *>(bp);
-            }
+        for (int c2 = 0; c2 < CH; ++c2) cb.w[c2] = wp[c2 * 4];
+        const uint16_t *sp = scales + row * sb_ld + p0 * 2, *bp = biases + row * sb_ld + p0 * 2;
+        if (dead) sp = scales, bp = biases;
+        if constexpr (CH == 4) {
+            const uint4 sv = *reinterpret_cast<const uint4 *>(sp), bv = *reinterpret_cast<const uint4 *>(bp);
+            cb.s[0] = sv.x, cb.s[1] = sv.y, cb.s[2] = sv.z, cb.s[3] = sv.w;
+            cb.b[0] = bv.x, cb.b[1] = bv.y, cb.b[2] = bv.z, cb.b[3] = bv.w;
+        } else if constexpr (CH == 2) {
+            const uint2 sv = *reinterpret_cast<const uint2 *>(sp), bv = *reinterpret_cast<const uint2 *>(bp);
+            cb.s[0] = sv.x, cb.s[1] = sv.y;
+            cb.b[0] = bv.x, cb.b[1] = bv.y;
+        } else {
+            cb.s[0] = *reinterpret_cast<const uint32_t *>(sp);
+            cb.b[0] = *reinterpret_cast<const uint32_t *>(bp);
         }
     };
-    MfChunk<NT, CH> buf[2];
+    MfChunk<CH> buf[2];
     // two chunks in flight, issued in buffer order (pinned) so the first
     // waits count the later loads instead of draining them
     auto prefetch = [&]() {
@@ -291,14 +286,15 @@ __global__ __launch_bounds__(kMfThreads) void q4_gemv_mfma_kernel(
     for (int j = 0; j < 4; ++j) abase[j] = alive ? xa + j * 4 * M + quarter * M + (am ^ mf_swz<M>(j)) : xa + zero;
     const uint32_t astride = alive ? 16 * M : 0;  // per pair
 
-    mf_f32x4_t acc[NT];
-#pragma unroll
-    for (int t = 0; t < NT; ++t) acc[t] = mf_f32x4_t{0.f, 0.f, 0.f, 0.f};
+    mf_f32x4_t acc = mf_f32x4_t{0.f, 0.f, 0.f, 0.f};
 
-    // the task of round r is complete: even + odd halves, the K slices, epilogue, store
+    // the task of round r is complete: even + odd halves, the K slices,
+    // epilogue, store. Output column c of a task: 16 of them, or with SiLU 8
+    // (gate in B column c, up in column c + 8).
+    constexpr uint32_t kOuts = EPI == kEpiSiluMul ? 8 : 16;
     auto finish = [&](uint32_t r) {
         auto store = [&](uint32_t m, uint32_t c, uint32_t tile, float v) {
-            const uint32_t o = m * y_ld + tile * 16 + c;  // < 2^31 (mf_eligible)
+            const uint32_t o = m * y_ld + tile * kOuts + c;  // < 2^31 (mf_eligible)
             if (y_is_f32)
                 static_cast<float *>(y)[o] = v;
             else
@@ -313,25 +309,24 @@ __global__ __launch_bounds__(kMfThreads) void q4_gemv_mfma_kernel(
                 return gsum;
             }
         };
-        float v[NT][4];
+        float v[4];
 #pragma unroll
-        for (int t = 0; t < NT; ++t)
-#pragma unroll
-            for (int i = 0; i < 4; ++i) v[t][i] = acc[t][i] + __shfl_xor(acc[t][i], 32, 64);  // lanes < 32: totals
+        for (int i = 0; i < 4; ++i) v[i] = acc[i] + __shfl_xor(acc[i], 32, 64);  // lanes < 32: totals
         if (ksplit == 1) {
             const uint32_t tile = tile_of(r);
-            if (tile < tiles && quarter < 2) {
+            float u[4];  // the up sums of the lane's gate column (SiLU)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) u[i] = EPI == kEpiSiluMul ? __shfl_xor(v[i], 8, 64) : v[i];
+            if (tile < tiles && quarter < 2 && col < kOuts) {
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
                     const uint32_t m = quarter * 4 + i;
-                    if (m < static_cast<uint32_t>(M)) store(m, col, tile, epilogue(v[0][i], v[NT - 1][i]));
+                    if (m < static_cast<uint32_t>(M)) store(m, col, tile, epilogue(v[i], u[i]));
                 }
             }
         } else {
 #pragma unroll
-            for (int t = 0; t < NT; ++t)
-#pragma unroll
-                for (int i = 0; i < 4; ++i) red[((wave * NT + t) * 4 + i) * 64 + lane] = v[t][i];
+            for (int i = 0; i < 4; ++i) red[(wave * 4 + i) * 64 + lane] = v[i];
             __syncthreads();
             // slots * M * 16 <= kMfThreads: one output per thread at most, and
             // no store loop (a store loop inside the main loop would make every
@@ -341,13 +336,11 @@ __global__ __launch_bounds__(kMfThreads) void q4_gemv_mfma_kernel(
                 const uint32_t sl = e / (M * 16), m = (e / 16) % M, c = e % 16;
                 const uint32_t tile = (r * gridDim.x + blockIdx.x) * slots + sl;
                 const uint32_t i = m & 3, ln = (m >> 2) * 16 + c;
-                float sum[NT];
-#pragma unroll
-                for (int t = 0; t < NT; ++t) {
-                    sum[t] = 0.f;
-                    for (uint32_t s = 0; s < ksplit; ++s) sum[t] += red[(((sl * ksplit + s) * NT + t) * 4 + i) * 64 + ln];
-                }
-                if (tile < tiles) store(m, c, tile, epilogue(sum[0], sum[NT - 1]));
+                float sum = 0.f, usum = 0.f;
+                for (uint32_t s = 0; s < ksplit; ++s) sum += red[((sl * ksplit + s) * 4 + i) * 64 + ln];
+                if constexpr (EPI == kEpiSiluMul)
+                    for (uint32_t s = 0; s < ksplit; ++s) usum += red[((sl * ksplit + s) * 4 + i) * 64 + ln + 8];
+                if (tile < tiles && c < kOuts) store(m, c, tile, epilogue(sum, usum));
             }
             __syncthreads();
         }
@@ -370,31 +363,27 @@ __global__ __launch_bounds__(kMfThreads) void q4_gemv_mfma_kernel(
                 uint4 a[4];
 #pragma unroll
                 for (int j = 0; j < 4; ++j) a[j] = abase[j][p * astride];
-#pragma unroll
-                for (int t = 0; t < NT; ++t) {
-                    const uint4 wv = buf[d].w[c2][t];
-                    uint4 b0, b1, b2, b3;
-                    mf_decode2(wv.x, wv.y, magic, b0, b1);
-                    mf_decode2(wv.z, wv.w, magic, b2, b3);
-                    mf_f32x4_t dv = mf_mfma(a[0], b0, mf_f32x4_t{0.f, 0.f, 0.f, 0.f});
-                    dv = mf_mfma(a[1], b1, dv);
-                    dv = mf_mfma(a[2], b2, dv);
-                    dv = mf_mfma(a[3], b3, dv);
-                    const uint32_t sb = hi ? buf[d].s[c2][t] >> 16 : buf[d].s[c2][t] & 0xFFFFu;
-                    const uint32_t bb = hi ? buf[d].b[c2][t] >> 16 : buf[d].b[c2][t] & 0xFFFFu;
-                    const float s = bf16_to_f32(sb);
-                    const float bc = fmaf(-128.f, s, bf16_to_f32(bb));
-                    acc[t][0] = fmaf(bc, xv.x, fmaf(s, dv[0], acc[t][0]));
-                    acc[t][1] = fmaf(bc, xv.y, fmaf(s, dv[1], acc[t][1]));
-                    acc[t][2] = fmaf(bc, xv.z, fmaf(s, dv[2], acc[t][2]));
-                    acc[t][3] = fmaf(bc, xv.w, fmaf(s, dv[3], acc[t][3]));
-                }
+                const uint4 wv = buf[d].w[c2];
+                uint4 b0, b1, b2, b3;
+                mf_decode2(wv.x, wv.y, magic, b0, b1);
+                mf_decode2(wv.z, wv.w, magic, b2, b3);
+                mf_f32x4_t dv = mf_mfma(a[0], b0, mf_f32x4_t{0.f, 0.f, 0.f, 0.f});
+                dv = mf_mfma(a[1], b1, dv);
+                dv = mf_mfma(a[2], b2, dv);
+                dv = mf_mfma(a[3], b3, dv);
+                const uint32_t sb = hi ? buf[d].s[c2] >> 16 : buf[d].s[c2] & 0xFFFFu;
+                const uint32_t bb = hi ? buf[d].b[c2] >> 16 : buf[d].b[c2] & 0xFFFFu;
+                const float s = bf16_to_f32(sb);
+                const float bc = fmaf(-128.f, s, bf16_to_f32(bb));
+                acc[0] = fmaf(bc, xv.x, fmaf(s, dv[0], acc[0]));
+                acc[1] = fmaf(bc, xv.y, fmaf(s, dv[1], acc[1]));
+                acc[2] = fmaf(bc, xv.z, fmaf(s, dv[2], acc[2]));
+                acc[3] = fmaf(bc, xv.w, fmaf(s, dv[3], acc[3]));
             }
             load(c0 + d + 2, buf[d]);
             if (cc == cpt - 1 && cr < rounds) {  // uniform across the block
                 finish(cr);
-#pragma unroll
-                for (int t = 0; t < NT; ++t) acc[t] = mf_f32x4_t{0.f, 0.f, 0.f, 0.f};
+                acc = mf_f32x4_t{0.f, 0.f, 0.f, 0.f};
             }
             if (++cc == cpt) {
                 cc = 0;
@@ -555,13 +544,12 @@ inline uint32_t pick_mf_split(uint32_t weight_tiles, uint32_t groups, uint32_t c
 template <int M, int PRO, int EPI, int CH>
 inline void launch_gemv_mfma_t(hipStream_t stream, uint32_t cus, const GemvArgs &a, uint32_t ksplit) {
     auto kernel = q4_gemv_mfma_kernel<M, PRO, EPI, CH>;
-    const uint32_t lds = mf_lds_bytes(M, a.k, mf_tiles_per_task<EPI>());
+    const uint32_t lds = mf_lds_bytes(M, a.k);
     int per_cu = 0;
     if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, kMfThreads, lds) != hipSuccess || per_cu < 1)
         per_cu = 1;
-    const uint32_t n_out = EPI == kEpiSiluMul ? a.n / 2 : a.n;
     const uint32_t slots = kMfWaves / ksplit;
-    const uint32_t need = (n_out / 16 + slots - 1) / slots;
+    const uint32_t need = (a.n / 16 + slots - 1) / slots;
     const uint32_t ranges = a.kranges > 1 ? a.kranges : 1;
     const uint32_t cap = (cus / ranges > 0 ? cus / ranges : 1) * static_cast<uint32_t>(per_cu);
     hipLaunchKernelGGL(kernel, dim3(need < cap ? need : cap, a.kranges > 1 ? a.kranges : 1), dim3(kMfThreads), lds,
@@ -573,15 +561,13 @@ inline void launch_gemv_mfma_t(hipStream_t stream, uint32_t cus, const GemvArgs 
 // at least 2 x rows staged per launch (the caller splits larger m), and with
 // RMSNorm rows the pack area can hold.
 inline bool mf_eligible(uint32_t m, const GemvArgs &a) {
-    const uint32_t n_out = a.epi == kEpiSiluMul ? a.n / 2 : a.n;
-    if (m < 2 || m > 8 || a.k == 0 || a.k % (kGroup * 4) != 0 || n_out == 0 || n_out % 16 != 0 ||
-        a.x_ld % 8 != 0)
+    if (m < 2 || m > 8 || a.k == 0 || a.k % (kGroup * 4) != 0 || a.n == 0 || a.n % 16 != 0 || a.x_ld % 8 != 0)
         return false;
     if ((reinterpret_cast<uintptr_t>(a.wq) | reinterpret_cast<uintptr_t>(a.s) | reinterpret_cast<uintptr_t>(a.b)) & 15u)
         return false;
     if (a.pro == kProRmsNorm && a.k > kMfPackMaxK) return false;  // the pack area's row limit
     if (static_cast<uint64_t>(m) * a.y_ld >= (1ull << 31)) return false;  // 32-bit output offsets
-    return mf_rows_per_launch(a.k, a.epi == kEpiSiluMul ? 2 : 1) >= 2;
+    return mf_rows_per_launch(a.k) >= 2;
 }
 
 // Defined in q4_gemv_m<M>.hip.
@@ -604,13 +590,12 @@ inline void launch_gemv_mfma_dispatch(hipStream_t stream, uint32_t cus, const Ge
     const uint32_t ranges_ = a.kranges > 1 ? a.kranges : 1;
     const uint32_t cap = cus / ranges_ > 0 ? cus / ranges_ : 1;
     const uint32_t slots = kMfWaves / ksplit;
-    const uint32_t task_tiles = (a.epi == kEpiSiluMul ? a.n / 2 : a.n) / 16;
+    const uint32_t task_tiles = a.n / 16;
     const uint32_t need = (task_tiles + slots - 1) / slots;
     const uint32_t blocks = need < cap ? need : cap;
     const uint32_t rounds = (task_tiles + blocks * slots - 1) / (blocks * slots);
     int ch = 1;
     for (const int c : {4, 2, 1}) {
-        if (c == 4 && a.epi == kEpiSiluMul) continue;
         if (gs % (2 * c) != 0) continue;
         const uint32_t total = rounds * (gs / (2 * c));
         if (total % 2 == 0 || total >= 5) {
@@ -625,14 +610,8 @@ inline void launch_gemv_mfma_dispatch(hipStream_t stream, uint32_t cus, const Ge
         else launch_gemv_mfma_t<M, P, E, 1>(stream, cus, a, ksplit);                        \
     } while (0)
     if (a.epi == kEpiSiluMul) {
-        // (the 4-pair width is never taken with two tiles of buffers)
-        if (a.pro == kProRmsNorm) {
-            if (ch == 1) launch_gemv_mfma_t<M, kProRmsNorm, kEpiSiluMul, 1>(stream, cus, a, ksplit);
-            else launch_gemv_mfma_t<M, kProRmsNorm, kEpiSiluMul, 2>(stream, cus, a, ksplit);
-        } else {
-            if (ch == 1) launch_gemv_mfma_t<M, kProNone, kEpiSiluMul, 1>(stream, cus, a, ksplit);
-            else launch_gemv_mfma_t<M, kProNone, kEpiSiluMul, 2>(stream, cus, a, ksplit);
-        }
+        if (a.pro == kProRmsNorm) FH_MF_LAUNCH(kProRmsNorm, kEpiSiluMul);
+        else FH_MF_LAUNCH(kProNone, kEpiSiluMul);
     } else if (a.pro == kProRmsNorm) {
         FH_MF_LAUNCH(kProRmsNorm, kEpiNone);
     } else {

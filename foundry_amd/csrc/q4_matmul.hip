@@ -77,7 +77,7 @@ static uint32_t mf_k_ranges(fh_device *dev, int64_t m, const GemvArgs &a) {
             if (pass == 0 && static_cast<uint64_t>(kp) * m * 2 > kMfRangeXBytes) continue;
             if (static_cast<uint64_t>(r) * m * a.n * 4 > kPartialAreaBytes) continue;
             const uint32_t cus = dev->compute_units / r > 0 ? dev->compute_units / r : 1;
-            if (mf_rows_per_launch(kp, 1) >= m && pick_mf_split(a.n / 16, kp / kGroup, cus) != 0) return r;
+            if (mf_rows_per_launch(kp) >= m && pick_mf_split(a.n / 16, kp / kGroup, cus) != 0) return r;
         }
     }
     return 0;
@@ -85,7 +85,7 @@ static uint32_t mf_k_ranges(fh_device *dev, int64_t m, const GemvArgs &a) {
 
 int launch_gemv_rows(fh_device *dev, const char *fn, int64_t m, const GemvArgs &base, int64_t y_cols) {
     const bool mf = m >= 2 && mf_eligible(static_cast<uint32_t>(m), base);
-    const int64_t per = mf ? mf_rows_per_launch(base.k, base.epi == kEpiSiluMul ? 2 : 1)
+    const int64_t per = mf ? mf_rows_per_launch(base.k)
                            : gemv_rows_per_launch(base.k, base.pro == kProRmsNorm);
     if (mf && per < m) {
         // all rows over K ranges instead of row groups over all of K: the
@@ -154,13 +154,13 @@ int q4_down_pack(fh_device *dev, const char *fn, const uint16_t *x, int64_t m, i
     GemvArgs down{x, static_cast<uint32_t>(x_ld), wq, scales, biases, static_cast<uint32_t>(n),
                   static_cast<uint32_t>(k), nullptr, static_cast<uint32_t>(n), 1, kProNone, kEpiNone,
                   GemvFusion{}};
-    if (!mf_eligible(static_cast<uint32_t>(m), down) || mf_rows_per_launch(down.k, 1) >= m) return FH_OK;
+    if (!mf_eligible(static_cast<uint32_t>(m), down) || mf_rows_per_launch(down.k) >= m) return FH_OK;
     const uint32_t ranges = mf_k_ranges(dev, m, down);
     if (ranges == 0) return FH_OK;
     GemvArgs next{nullptr, static_cast<uint32_t>(n), next_wq, next_scales, next_biases, static_cast<uint32_t>(next_n),
                   static_cast<uint32_t>(n), nullptr, static_cast<uint32_t>(next_n), 0, kProRmsNorm, kEpiNone,
                   GemvFusion{}};
-    if (!mf_eligible(static_cast<uint32_t>(m), next) || mf_rows_per_launch(next.k, 1) < m) return FH_OK;
+    if (!mf_eligible(static_cast<uint32_t>(m), next) || mf_rows_per_launch(next.k) < m) return FH_OK;
     for (const void *p : {static_cast<const void *>(x), static_cast<const void *>(res),
                           static_cast<const void *>(res_out), static_cast<const void *>(norm_weight)})
         if (reinterpret_cast<uintptr_t>(p) % 16 != 0) return FH_OK;
