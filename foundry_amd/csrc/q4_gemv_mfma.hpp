@@ -60,8 +60,16 @@ __device__ __forceinline__ mf_f32x4_t mf_mfma(const uint4 a, const uint4 b, cons
 
 // LDS bytes: staged x fragments, a zero slot and a dummy slot, group sums X
 // [G][8], the partial tiles of the K split.
+constexpr uint32_t kMfRedBytes = kMfWaves * 4 * 64 * 4;
 __host__ __device__ constexpr uint32_t mf_lds_bytes(uint32_t m, uint32_t k) {
-    return m * k * 2 + 32 + (k / kGroup) * 8 * 4 + kMfWaves * 4 * 64 * 4;
+    return m * k * 2 + 32 + (k / kGroup) * 8 * 4 + kMfRedBytes;
+}
+
+// Areas for the K split's partial tiles: two when LDS has room (rounds
+// alternate between them, so a round needs one block barrier instead of
+// two), else one.
+__host__ __device__ constexpr uint32_t mf_red_areas(uint32_t m, uint32_t k) {
+    return mf_lds_bytes(m, k) + kMfRedBytes <= kMfLdsLimit ? 2u : 1u;
 }
 
 // 16-byte slots of the packed LDS image: fragments, the zero and dummy
@@ -160,7 +168,8 @@ __global__ __launch_bounds__(kMfThreads) void q4_gemv_mfma_kernel(
     const uint32_t zero = M * wpr;                           // a zero fragment (dead A lanes)
     const uint32_t dummy = zero + 1;                         // write-only slot for dead items
     float *xsum = reinterpret_cast<float *>(lds + dummy + 1);  // [G][8]
-    float *red = xsum + G * 8;                               // [16][4][64]
+    float *red = xsum + G * 8;                               // [areas][16][4][64]
+    const uint32_t red_areas = mf_red_areas(M, k);
 
     const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const uint32_t col = lane & 15, quarter = lane >> 4, hi = quarter >> 1;
@@ -325,8 +334,11 @@ __global__ __launch_bounds__(kMfThreads) void q4_gemv_mfma_kernel(
                 }
             }
         } else {
+            // round r's area; with two, round r + 2 writes this one only after
+            // every thread has passed round r + 1's barrier, i.e. after its reads
+            float *rd = red + (red_areas == 2 ? (r & 1u) * (kMfRedBytes / 4) : 0u);
 #pragma unroll
-            for (int i = 0; i < 4; ++i) red[(wave * 4 + i) * 64 + lane] = v[i];
+            for (int i = 0; i < 4; ++i) rd[(wave * 4 + i) * 64 + lane] = v[i];
             __syncthreads();
             // slots * M * 16 <= kMfThreads: one output per thread at most, and
             // no store loop (a store loop inside the main loop would make every
@@ -337,12 +349,12 @@ __global__ __launch_bounds__(kMfThreads) void q4_gemv_mfma_kernel(
                 const uint32_t tile = (r * gridDim.x + blockIdx.x) * slots + sl;
                 const uint32_t i = m & 3, ln = (m >> 2) * 16 + c;
                 float sum = 0.f, usum = 0.f;
-                for (uint32_t s = 0; s < ksplit; ++s) sum += red[((sl * ksplit + s) * 4 + i) * 64 + ln];
+                for (uint32_t s = 0; s < ksplit; ++s) sum += rd[((sl * ksplit + s) * 4 + i) * 64 + ln];
                 if constexpr (EPI == kEpiSiluMul)
-                    for (uint32_t s = 0; s < ksplit; ++s) usum += red[((sl * ksplit + s) * 4 + i) * 64 + ln + 8];
+                    for (uint32_t s = 0; s < ksplit; ++s) usum += rd[((sl * ksplit + s) * 4 + i) * 64 + ln + 8];
                 if (tile < tiles && c < kOuts) store(m, c, tile, epilogue(sum, usum));
             }
-            __syncthreads();
+            if (red_areas == 1) __syncthreads();
         }
     };
 
@@ -544,7 +556,7 @@ inline uint32_t pick_mf_split(uint32_t weight_tiles, uint32_t groups, uint32_t c
 template <int M, int PRO, int EPI, int CH>
 inline void launch_gemv_mfma_t(hipStream_t stream, uint32_t cus, const GemvArgs &a, uint32_t ksplit) {
     auto kernel = q4_gemv_mfma_kernel<M, PRO, EPI, CH>;
-    const uint32_t lds = mf_lds_bytes(M, a.k);
+    const uint32_t lds = mf_lds_bytes(M, a.k) + (mf_red_areas(M, a.k) - 1) * kMfRedBytes;
     int per_cu = 0;
     if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, kMfThreads, lds) != hipSuccess || per_cu < 1)
         per_cu = 1;
