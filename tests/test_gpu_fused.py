@@ -11,7 +11,10 @@ Bars:
   partials are added in another order, so g or u can differ by one bf16 ulp;
   the bar is then 99% identical and every output within 2^-7 of its row's
   largest magnitude (one ulp of g or u moves silu(g) * u by about that much;
-  near zero that is many ulps of the output itself).
+  near zero that is many ulps of the output itself). From 2 rows both run
+  the matrix-core GEMV with the same K split: a task there is 16 weight rows,
+  or 8 gate rows and their 8 up rows, so f need only be a multiple of 8
+  (f = 1000 below).
 - fh_q4_matmul_rmsnorm: the prologue sums h^2 in another order than
   fh_rms_norm, and sums each staged chunk of x in pairs, so a normalised value
   or a chunk sum can differ in its last bit. Bars: the fp32 output within 2e-3
@@ -100,8 +103,8 @@ def test_matmul_rmsnorm(device, oracle, m, k, with_res):
     assert np.mean(unfused == outs[_lib.BF16]) >= 0.99
 
 
-@pytest.mark.parametrize("m,k,f,same_shape", [(1, 3072, 8192, True), (4, 3072, 8192, True), (8, 4096, 1000, False),
-                                              (2, 256, 64, True)])
+@pytest.mark.parametrize("m,k,f,same_shape", [(1, 3072, 8192, True), (4, 3072, 8192, True), (8, 4096, 1000, True),
+                                              (1, 4096, 8192, False), (2, 256, 64, True)])
 def test_gate_up_silu(device, m, k, f, same_shape):
     x = synth.bf16_normal(70 + m, (m, k))
     _, w = q4(device, 80 + m, 2 * f, k)
