@@ -36,9 +36,9 @@
 //   over each row's chunks in another fixed order).
 //   Every output element is a sum in a fixed order, so results do not
 //   change from run to run.
-// splits, slices and chunks make rows * n_kv * (blocks per pair) about
-// kAttnTargetBlocks: decode spreads one row over many CUs, prefill keeps one
-// block per (row, KV head).
+// splits and slices make rows * n_kv * (blocks per pair) about
+// kAttnTargetBlocks, chunks about kPvTargetBlocks: decode spreads one row
+// over many CUs, prefill keeps one block per (row, KV head).
 // Decode over a cache of at most 1024 positions (head_dim 64 or 128) runs
 // instead as ONE launch, attn_decode_short_kernel: each block scores all of
 // its KV head's keys itself (16 wavefronts, a chunk each), meets the chunks'
@@ -61,6 +61,13 @@ constexpr int kAttnMaxGroup = 8;
 #define FH_ATTN_TARGET_BLOCKS 1024
 #endif
 constexpr uint64_t kAttnTargetBlocks = FH_ATTN_TARGET_BLOCKS;
+// The chunked P.V aims at fewer, longer blocks: each block first gathers
+// the row's softmax statistics, and its partials are added by the combine
+// pass (config-5 decode attention 37.3 -> 36.1 us per call against 1024).
+#ifndef FH_PV_TARGET_BLOCKS
+#define FH_PV_TARGET_BLOCKS 512
+#endif
+constexpr uint64_t kPvTargetBlocks = FH_PV_TARGET_BLOCKS;
 
 // Workspace: per-chunk softmax statistics [rows][n_heads][nck] float2, then
 // the scores [rows][n_heads][max_len] f32, then (chunked P.V) the partial
@@ -98,7 +105,8 @@ static AttnLayout attn_layout(uint64_t rows, uint64_t n_heads, uint64_t n_kv, ui
     a.chunks = a.chunk_keys = 0;
     if (blocks * max_len >= kPvChunkedMinKeys) {
         const uint64_t tiles = (max_len + kPvTile - 1) / kPvTile;
-        uint64_t chunks = want < tiles ? want : tiles;
+        const uint64_t want_pv = blocks ? (kPvTargetBlocks + blocks - 1) / blocks : 1;
+        uint64_t chunks = want_pv < tiles ? want_pv : tiles;
         if (chunks == 0) chunks = 1;
         a.chunk_keys = (tiles + chunks - 1) / chunks * kPvTile;
         a.chunks = (max_len + a.chunk_keys - 1) / a.chunk_keys;
