@@ -33,11 +33,11 @@
 //   projection) run over K ranges: blockIdx.y picks the range, each block
 //   stages that range of x, and the f32 partial tiles go to the device's
 //   partial area for mf_combine_kernel (q4_matmul.hip) to add in order.
-// - Work: blocks of 16 wavefronts, persistent; a task is one output tile
-//   (gate and up tiles together for the SiLU epilogue) over a K slice; S
-//   wavefronts split K (S = 1..16) and add their partial tiles in LDS in a
-//   fixed order, so the result is deterministic and the same for every
-//   variant over one weight.
+// - Work: blocks of 16 wavefronts, persistent; a task is one 16-column B
+//   tile (16 weight rows, or 8 gate rows and their 8 up rows for the SiLU
+//   epilogue) over a K slice; S wavefronts split K (S = 1..16) and add their
+//   partial tiles in LDS in a fixed order, so the result is deterministic
+//   and the same for every variant over one weight.
 #pragma once
 
 #include "decoder_common.hpp"
@@ -569,7 +569,8 @@ inline void launch_gemv_mfma_t(hipStream_t stream, uint32_t cus, const GemvArgs 
 }
 
 // Whether the matrix-core GEMV takes this launch of 2..8 rows: k a multiple of
-// 256 with a K split for it, 16-row output tiles, 16-byte aligned operands,
+// 256 with a K split for it, n a multiple of 16 (whole B tiles; with SiLU
+// [gate; up] rows, so 8 outputs per tile), 16-byte aligned operands,
 // at least 2 x rows staged per launch (the caller splits larger m), and with
 // RMSNorm rows the pack area can hold.
 inline bool mf_eligible(uint32_t m, const GemvArgs &a) {
@@ -588,7 +589,7 @@ void launch_gemv_mfma_m(hipStream_t stream, uint32_t cus, const GemvArgs &a);
 
 // Chunk width: 4 group pairs when each wavefront's slice allows it (one
 // 16-byte scale and one bias load per 8 groups), else 2, else 1, at most
-// half the slice; the SiLU variant takes at most 2 (two tiles of buffers).
+// half the slice.
 template <int M>
 inline void launch_gemv_mfma_dispatch(hipStream_t stream, uint32_t cus, const GemvArgs &a) {
     const uint32_t groups = a.k / kGroup;
