@@ -33,7 +33,10 @@
 
 namespace fh {
 
-constexpr int kGemvThreads = 256;
+#ifndef FH_GEMV_THREADS
+#define FH_GEMV_THREADS 256
+#endif
+constexpr int kGemvThreads = FH_GEMV_THREADS;
 constexpr int kGemvWaves = kGemvThreads / 64;
 // Dynamic LDS one block may use for staged x (bytes).
 constexpr uint32_t kGemvLdsLimit = 64 * 1024;
