@@ -19,8 +19,9 @@
 // so a K or V row is read once for the group:
 //   attn_scores_kernel, block (KV head, split, row): chunks of kAttnChunk keys
 //     dealt round-robin to the split blocks and their wavefronts;
-//     s_j = RNE(q.k_j) * scale from matrix-core dot products, written to the
-//     workspace with each chunk's (m_c = max s_j, l_c = sum exp(s_j - m_c)).
+//     s_j = RNE(q.k_j) * scale from matrix-core dot products; RNE(q.k_j)
+//     goes to the workspace (bf16) with each chunk's (m_c = max s_j, l_c =
+//     sum exp(s_j - m_c)).
 //     Decode uses it; fh_attention uses attn_scores_tile_kernel, the same
 //     per row but with a block serving a tile of 16 / G query rows, so that
 //     every key it loads serves the whole tile.
@@ -70,7 +71,8 @@ constexpr uint64_t kAttnTargetBlocks = FH_ATTN_TARGET_BLOCKS;
 constexpr uint64_t kPvTargetBlocks = FH_PV_TARGET_BLOCKS;
 
 // Workspace: per-chunk softmax statistics [rows][n_heads][nck] float2, then
-// the scores [rows][n_heads][max_len] f32, then (chunked P.V) the partial
+// the scores [rows][n_heads][max_len] as bf16 RNE(q.k) (score_of forms
+// RNE(q.k) * scale), then (chunked P.V) the partial
 // outputs [rows][n_kv][chunks][G][head_dim] f32. splits: blocks per (row, KV
 // head) of the scores kernel. P.V runs one of two ways:
 //   sliced: blocks per (row, KV head) = slices, each over head_dim / slices
@@ -101,7 +103,7 @@ static AttnLayout attn_layout(uint64_t rows, uint64_t n_heads, uint64_t n_kv, ui
     a.slices = 1;
     while (a.slices * 2 <= want && head_dim / (a.slices * 2) >= 16) a.slices *= 2;
     a.scores = round_up(rows * n_heads * a.nck * 8);
-    a.part = a.scores + round_up(rows * n_heads * max_len * 4);
+    a.part = a.scores + round_up(rows * n_heads * max_len * 2);
     a.chunks = a.chunk_keys = 0;
     if (blocks * max_len >= kPvChunkedMinKeys) {
         const uint64_t tiles = (max_len + kPvTile - 1) / kPvTile;
@@ -139,6 +141,12 @@ __device__ __forceinline__ attn_f32x4_t attn_mfma(const uint4 a, const uint4 b, 
                                                    __builtin_bit_cast(attn_bf16x8_t, b), c, 0, 0, 0);
 }
 
+// The workspace keeps each score as the bf16 RNE(q.k); s = RNE(q.k) * scale
+// is re-formed where it is used, as one rounded multiply (never contracted
+// into a following subtraction), so it equals the value the scores kernels
+// computed.
+__device__ __forceinline__ float score_of(uint16_t qk, float scale) { return __fmul_rn(bf(qk), scale); }
+
 // Key groups (16 keys) a scores wavefront keeps in flight.
 #ifndef FH_ATTN_SCORES_DEPTH
 #define FH_ATTN_SCORES_DEPTH 2
@@ -151,7 +159,7 @@ __global__ __launch_bounds__(kAttnThreads) void attn_scores_kernel(
     const uint16_t *__restrict__ q_src, const uint16_t *__restrict__ cos_tab, const uint16_t *__restrict__ sin_tab,
     const uint32_t *__restrict__ positions, uint32_t pos_limit, uint16_t *__restrict__ k_cache,
     uint16_t *__restrict__ v_cache, uint64_t row_stride, uint32_t n_heads, uint32_t n_kv, uint32_t max_len,
-    uint32_t nck, uint32_t splits, float scale, float *__restrict__ scores, float2 *__restrict__ stats) {
+    uint32_t nck, uint32_t splits, float scale, uint16_t *__restrict__ scores, float2 *__restrict__ stats) {
     constexpr int KS = HD / 32;       // MFMA k steps per key group
     constexpr uint32_t PPH = HD / 8;  // 8-dim pieces per head
     constexpr int NQ = (G + 3) / 4;   // 16-lane rows of the results holding live heads
@@ -283,11 +291,12 @@ __global__ __launch_bounds__(kAttnThreads) void attn_scores_kernel(
         const uint32_t j = c * kAttnChunk + lane;
 #pragma unroll
         for (int h = 0; h < G; ++h) {
-            const float sv = j < ctx ? bf(rne(dv[h])) * scale : -INFINITY;
+            const uint16_t qk = rne(dv[h]);
+            const float sv = j < ctx ? bf(qk) * scale : -INFINITY;
             const float m = wave_max(sv);
             const float l = wave_sum(expf(sv - m));
             const uint64_t hrow = static_cast<uint64_t>(r) * n_heads + h0 + h;
-            if (j < ctx) scores[hrow * max_len + j] = sv;
+            if (j < ctx) scores[hrow * max_len + j] = qk;
             if (lane == 0) stats[hrow * nck + c] = make_float2(m, l);
         }
     }
@@ -306,7 +315,7 @@ template <int HD, int G>
 __global__ __launch_bounds__(kAttnThreads) void attn_scores_tile_kernel(
     const uint16_t *__restrict__ q, const uint32_t *__restrict__ positions, uint32_t rows,
     const uint16_t *__restrict__ k_cache, uint32_t n_heads, uint32_t max_len, uint32_t nck, uint32_t splits,
-    float scale, float *__restrict__ scores, float2 *__restrict__ stats) {
+    float scale, uint16_t *__restrict__ scores, float2 *__restrict__ stats) {
     constexpr int KS = HD / 32;             // MFMA k steps per key group
     constexpr uint32_t QR = 16 / G;         // query rows per tile
     constexpr uint32_t LIVE = QR * G;       // live A rows
@@ -363,7 +372,8 @@ __global__ __launch_bounds__(kAttnThreads) void attn_scores_tile_kernel(
     load_grp(1, b1);
     for (uint32_t f0 = 0; f0 < total; f0 += 4) {
         const uint32_t c = c_first + (f0 / 4) * c_step;
-        float sv[4][4];  // [group][i]: result row quad * 4 + i, key c * 64 + group * 16 + col
+        float sv[4][4];      // [group][i]: result row quad * 4 + i, key c * 64 + group * 16 + col
+        uint16_t qk[4][4];   // RNE(q.k) of the same entries, the stored form
 #pragma unroll
         for (int grp = 0; grp < 4; ++grp) {
             uint4(&b)[KS] = grp % 2 ? b1 : b0;
@@ -372,7 +382,10 @@ __global__ __launch_bounds__(kAttnThreads) void attn_scores_tile_kernel(
 #pragma unroll
             for (int st = 1; st < KS; ++st) d = attn_mfma(a[st], b[st], d);
 #pragma unroll
-            for (int i = 0; i < 4; ++i) sv[grp][i] = j < ctxr[i] ? bf(rne(d[i])) * scale : -INFINITY;
+            for (int i = 0; i < 4; ++i) {
+                qk[grp][i] = rne(d[i]);
+                sv[grp][i] = j < ctxr[i] ? bf(qk[grp][i]) * scale : -INFINITY;
+            }
             load_grp(f0 + grp + 2, b);
         }
         // per result row: (max, sum of exp) over the chunk's 64 keys
@@ -383,10 +396,10 @@ __global__ __launch_bounds__(kAttnThreads) void attn_scores_tile_kernel(
             const uint32_t rr = quad * 4 + i;
             if (rr < LIVE && c * kAttnChunk < ctxr[i]) {  // the row is live and reaches this chunk
                 const uint64_t hrow = static_cast<uint64_t>(r0 + rr / G) * n_heads + h0 + rr % G;
-                float *srow = scores + hrow * max_len + c * kAttnChunk + col;
+                uint16_t *srow = scores + hrow * max_len + c * kAttnChunk + col;
 #pragma unroll
                 for (int grp = 0; grp < 4; ++grp)
-                    if (c * kAttnChunk + grp * 16 + col < ctxr[i]) srow[grp * 16] = sv[grp][i];
+                    if (c * kAttnChunk + grp * 16 + col < ctxr[i]) srow[grp * 16] = qk[grp][i];
                 if (col == 0) stats[hrow * nck + c] = make_float2(m, l);
             }
         }
@@ -408,7 +421,7 @@ template <int G, int P>
 __global__ __launch_bounds__(kAttnThreads) void attn_pv_kernel(
     const uint16_t *__restrict__ v_cache, uint64_t row_stride, const uint32_t *__restrict__ positions,
     uint32_t pos_limit, uint32_t n_heads, uint32_t n_kv, uint32_t head_dim, uint32_t max_len, uint32_t nck,
-    uint32_t slices, const float *__restrict__ scores, const float2 *__restrict__ stats,
+    uint32_t slices, float scale, const uint16_t *__restrict__ scores, const float2 *__restrict__ stats,
     uint16_t *__restrict__ out) {
     using S = PvShape<P>;
     __shared__ float p[G][S::kTile];
@@ -427,9 +440,10 @@ __global__ __launch_bounds__(kAttnThreads) void attn_pv_kernel(
     const uint32_t wave = tid >> 6, lane = tid & 63, q = tid % P, s = tid / P;
     const uint16_t *vb = v_cache + static_cast<uint64_t>(r) * row_stride + static_cast<uint64_t>(kvh) * max_len * head_dim +
                          d0 + 2 * q;
-    const float *srow = scores + (static_cast<uint64_t>(r) * n_heads + h0) * max_len;
-    // A tile: V of keys t0 + s + k * slots (this thread's dims) and the raw
-    // scores of entries i = tid + n * 256 of the tile's [G][kTile] block.
+    const uint16_t *srow = scores + (static_cast<uint64_t>(r) * n_heads + h0) * max_len;
+    // A tile: V of keys t0 + s + k * slots (this thread's dims) and the
+    // scores s_j = RNE(q.k_j) * scale of entries i = tid + n * 256 of the
+    // tile's [G][kTile] block.
     constexpr int NS = (G * S::kTile + kAttnThreads - 1) / kAttnThreads;
     auto load_tile = [&](uint32_t t0, uint32_t (&vr)[S::kLoads], float (&sr)[NS]) {
 #pragma unroll
@@ -440,7 +454,7 @@ __global__ __launch_bounds__(kAttnThreads) void attn_pv_kernel(
 #pragma unroll
         for (int n = 0; n < NS; ++n) {
             const uint32_t i = tid + n * kAttnThreads, g = i / S::kTile, j = t0 + i % S::kTile;
-            sr[n] = i < G * S::kTile && j < ctx ? srow[static_cast<uint64_t>(g) * max_len + j] : 0.f;
+            sr[n] = i < G * S::kTile && j < ctx ? score_of(srow[static_cast<uint64_t>(g) * max_len + j], scale) : 0.f;
         }
     };
     uint32_t vr[S::kLoads];
@@ -544,7 +558,7 @@ template <int HD, int G>
 __global__ __launch_bounds__(kAttnThreads) void attn_pv_chunk_kernel(
     const uint16_t *__restrict__ v_cache, uint64_t row_stride, const uint32_t *__restrict__ positions,
     uint32_t pos_limit, uint32_t n_heads, uint32_t n_kv, uint32_t max_len, uint32_t nck, uint32_t chunks,
-    uint32_t chunk_keys, const float *__restrict__ scores, const float2 *__restrict__ stats,
+    uint32_t chunk_keys, float scale, const uint16_t *__restrict__ scores, const float2 *__restrict__ stats,
     uint16_t *__restrict__ out, float *__restrict__ part) {
     constexpr int LPK = HD / 8, KPI = 64 / LPK;  // lanes per key, keys per load
     constexpr int IT = kPvWaveTile / KPI;        // V loads per lane per tile
@@ -570,7 +584,7 @@ __global__ __launch_bounds__(kAttnThreads) void attn_pv_chunk_kernel(
     const uint32_t wt = nt > wave ? (nt - wave + kAttnWaves - 1) / kAttnWaves : 0;  // this wavefront's
     const uint16_t *vb = v_cache + static_cast<uint64_t>(r) * row_stride + static_cast<uint64_t>(kvh) * max_len * HD +
                          dp * 8;
-    const float *srow = scores + (static_cast<uint64_t>(r) * n_heads + h0) * max_len;
+    const uint16_t *srow = scores + (static_cast<uint64_t>(r) * n_heads + h0) * max_len;
     // Tile i of this wavefront: its V rows for this lane, and the scores of
     // entries t = lane + 64 n of its [G][16] block. Keys past k1 and tiles past
     // the wavefront's last are clamped (loads stay unconditional; the values
@@ -588,7 +602,7 @@ __global__ __launch_bounds__(kAttnThreads) void attn_pv_chunk_kernel(
         for (int n = 0; n < NSW; ++n) {
             const uint32_t t = lane + n * 64;
             const uint32_t g = t / kPvWaveTile < G ? t / kPvWaveTile : G - 1, j = t0 + t % kPvWaveTile;
-            sr[n] = srow[static_cast<uint64_t>(live ? g : 0) * max_len + (live && j < k1 ? j : k0)];
+            sr[n] = score_of(srow[static_cast<uint64_t>(live ? g : 0) * max_len + (live && j < k1 ? j : k0)], scale);
         }
     };
     constexpr int kDepth = kPvDepth;
@@ -738,7 +752,7 @@ template <int HD, int G>
 __global__ __launch_bounds__(kAttnThreads) void attn_pv_tile_kernel(
     const uint16_t *__restrict__ v_cache, const uint32_t *__restrict__ positions, uint32_t rows, uint32_t n_heads,
     uint32_t n_kv, uint32_t max_len, uint32_t nck, uint32_t chunks, uint32_t chunk_keys,
-    const float *__restrict__ scores, const float2 *__restrict__ stats, uint16_t *__restrict__ out,
+    float scale, const uint16_t *__restrict__ scores, const float2 *__restrict__ stats, uint16_t *__restrict__ out,
     float *__restrict__ part) {
     constexpr uint32_t R = 16 / G, LIVE = R * G;
     constexpr int DT = HD / 16;  // 16-dim tiles of the output
@@ -784,7 +798,7 @@ __global__ __launch_bounds__(kAttnThreads) void attn_pv_tile_kernel(
     }
     sloc += __shfl_xor(sloc, 16, 64);
     const float srow_sum = sloc + __shfl_xor(sloc, 32, 64);
-    const float *srow = scores + hrow * max_len;
+    const uint16_t *srow = scores + hrow * max_len;
     const uint32_t kend_a = alive ? (k0 + chunk_keys < ctx_a ? k0 + chunk_keys : ctx_a) : 0u;  // this row's keys end
     // V: lane (key octet j, piece pv) loads keys 8 j .. 8 j + 7 of a step, dims 8 pv .. 8 pv + 7
     const uint32_t vj = lane >> 4, pv = lane & 15;
@@ -803,7 +817,7 @@ __global__ __launch_bounds__(kAttnThreads) void attn_pv_tile_kernel(
         const uint32_t sc = s < nsteps ? s : nsteps - 1;
         const uint32_t kb = k0 + sc * 32 + 8 * quad;
 #pragma unroll
-        for (int e = 0; e < 8; ++e) sv[e] = srow[kb + e < kend ? kb + e : k0];
+        for (int e = 0; e < 8; ++e) sv[e] = score_of(srow[kb + e < kend ? kb + e : k0], scale);
     };
     attn_f32x4_t acc[DT];
 #pragma unroll
@@ -1192,17 +1206,17 @@ struct AttnArgs {
 
 template <int G, int P>
 static void launch_pv(hipStream_t stream, uint32_t rows, const AttnLayout &a, const AttnArgs &x, uint32_t head_dim,
-                      const float *scores, const float2 *stats) {
+                      const uint16_t *scores, const float2 *stats) {
     const dim3 grid(static_cast<uint32_t>(x.n_kv * a.slices), rows);
     hipLaunchKernelGGL((attn_pv_kernel<G, P>), grid, dim3(kAttnThreads), 0, stream, x.v_cache, x.row_stride,
                        x.positions, x.pos_limit, x.n_heads, x.n_kv, head_dim, x.max_len,
-                       static_cast<uint32_t>(a.nck), static_cast<uint32_t>(a.slices), scores, stats, x.out);
+                       static_cast<uint32_t>(a.nck), static_cast<uint32_t>(a.slices), x.scale, scores, stats, x.out);
 }
 
 template <int HD, int G, bool ROPE>
 static void launch_attention(hipStream_t stream, uint32_t rows, const AttnLayout &a, const AttnArgs &x) {
     auto *stats = reinterpret_cast<float2 *>(x.ws);
-    auto *scores = reinterpret_cast<float *>(x.ws + a.scores);
+    auto *scores = reinterpret_cast<uint16_t *>(x.ws + a.scores);
     if constexpr (ROPE) {
         const dim3 grid(static_cast<uint32_t>(x.n_kv * a.splits), rows);
         hipLaunchKernelGGL((attn_scores_kernel<HD, G, ROPE>), grid, dim3(kAttnThreads), 0, stream, x.q_src,
@@ -1231,7 +1245,7 @@ static void launch_attention(hipStream_t stream, uint32_t rows, const AttnLayout
         float *part = reinterpret_cast<float *>(x.ws + a.part);
         hipLaunchKernelGGL((attn_pv_tile_kernel<HD, G>), dim3(x.n_kv * chunks, tiles), dim3(kAttnThreads), 0, stream,
                            x.v_cache, x.positions, rows, x.n_heads, x.n_kv, x.max_len, static_cast<uint32_t>(a.nck),
-                           chunks, ck, scores, stats, x.out, part);
+                           chunks, ck, x.scale, scores, stats, x.out, part);
         if (chunks > 1)
             hipLaunchKernelGGL(attn_combine_kernel, dim3((G * HD + kCombineOuts - 1) / kCombineOuts, x.n_kv, rows),
                                dim3(kAttnThreads), 0, stream, x.positions, x.pos_limit, x.n_heads, x.n_kv,
@@ -1243,7 +1257,7 @@ static void launch_attention(hipStream_t stream, uint32_t rows, const AttnLayout
         float *part = reinterpret_cast<float *>(x.ws + a.part);
         hipLaunchKernelGGL((attn_pv_chunk_kernel<HD, G>), dim3(x.n_kv * chunks, rows), dim3(kAttnThreads), 0, stream,
                            x.v_cache, x.row_stride, x.positions, x.pos_limit, x.n_heads, x.n_kv, x.max_len,
-                           static_cast<uint32_t>(a.nck), chunks, ck, scores, stats, x.out, part);
+                           static_cast<uint32_t>(a.nck), chunks, ck, x.scale, scores, stats, x.out, part);
         if (chunks > 1)
             hipLaunchKernelGGL(attn_combine_kernel, dim3((G * HD + kCombineOuts - 1) / kCombineOuts, x.n_kv, rows),
                                dim3(kAttnThreads), 0, stream, x.positions, x.pos_limit, x.n_heads, x.n_kv,
