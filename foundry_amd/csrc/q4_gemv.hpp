@@ -505,6 +505,9 @@ struct GemvArgs {
     // rows hold kranges of them (0 or 1: k is the whole row); y then takes
     // f32 partial sums [kranges][rows][y_ld]
     uint32_t kranges = 0;
+    // the scales and biases interleaved per group pair (fh_q4_interleave),
+    // or null; read by the matrix-core GEMV where it has a form for them
+    const uint32_t *sb = nullptr;
 };
 
 template <int M, int L, int CPL, bool FULL, int PRO, int EPI>

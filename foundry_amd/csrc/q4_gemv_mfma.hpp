@@ -22,6 +22,9 @@
 // - Scale and bias load 2*CH groups per instruction; weight loads run two
 //   chunks (CH group pairs each) ahead of the MFMAs, across task boundaries,
 //   with clamped (never guarded) addresses, so every wait counts exactly.
+//   With SB the scales and biases come interleaved per group pair (the two
+//   scale halves, then the two bias halves: fh_q4_interleave's layout), so
+//   one load brings a chunk's scales and biases together (CH <= 2).
 // - Every block stages all of x in LDS. Plain x: the prologue loads it in
 //   1 KB runs and permutes it into fragments. With RMSNorm (fh_q4_matmul_
 //   rmsnorm, fh_q4_gate_up_silu) a separate pack kernel normalises x once
@@ -139,24 +142,29 @@ __device__ __forceinline__ uint32_t mf_slot(uint32_t m, uint32_t c) {
 
 // M: x rows (1..8). CH: group pairs per chunk (1, 2 or 4). ksplit:
 // wavefronts per task (divides 16; k / 64 / ksplit is a multiple of 2 * CH).
-template <int M, int PRO, int EPI, int CH>
+// SB: scale and bias are read from sbi (dword 2p of a row: the scales of
+// groups 2p and 2p + 1, dword 2p + 1: their biases), not scales / biases.
+template <int M, int PRO, int EPI, int CH, bool SB>
 __global__ __launch_bounds__(kMfThreads) void q4_gemv_mfma_kernel(
     const uint16_t *__restrict__ x, uint32_t x_ld, const uint32_t *__restrict__ wq,
-    const uint16_t *__restrict__ scales, const uint16_t *__restrict__ biases, uint32_t n, uint32_t k,
-    void *__restrict__ y, uint32_t y_ld, int y_is_f32, uint32_t ksplit) {
+    const uint16_t *__restrict__ scales, const uint16_t *__restrict__ biases, const uint32_t *__restrict__ sbi,
+    uint32_t n, uint32_t k, void *__restrict__ y, uint32_t y_ld, int y_is_f32, uint32_t ksplit) {
     constexpr bool kPacked = PRO == kProRmsNorm;  // x: mf_pack_kernel's image of RMSNorm(x + res)
     static_assert(kMfWaves / 2 * M * 16 <= kMfThreads, "a K-split round stores one output per thread at most");
+    static_assert(!SB || CH <= 2, "interleaved scale/bias: one load per chunk of at most 2 pairs");
     extern __shared__ uint4 lds[];
     const uint32_t G = k / kGroup;
     const uint32_t wpr = k / 8;  // packed words per row of the K range (x fragments)
     // K range blockIdx.y of gridDim.y: weight rows hold all of them; y takes
-    // this range's f32 partial sums at [blockIdx.y][M][y_ld]
+    // this range's f32 partial sums at [blockIdx.y][M][y_ld]. A row has
+    // sb_ld scales, sb_ld biases, or sb_ld interleaved dwords.
     const uint32_t w_ld = wpr * gridDim.y, sb_ld = G * gridDim.y;
     if (gridDim.y > 1) {
         x += static_cast<uint64_t>(blockIdx.y) * k;
         wq += static_cast<uint64_t>(blockIdx.y) * wpr;
         scales += static_cast<uint64_t>(blockIdx.y) * G;
         biases += static_cast<uint64_t>(blockIdx.y) * G;
+        sbi += static_cast<uint64_t>(blockIdx.y) * G;
         y = static_cast<float *>(y) + static_cast<uint64_t>(blockIdx.y) * M * y_ld;
     }
     // A task is one 16-column B tile: 16 weight rows, or with the SiLU
@@ -207,7 +215,14 @@ __global__ __launch_bounds__(kMfThreads) void q4_gemv_mfma_kernel(
         for (int c2 = 0; c2 < CH; ++c2) cb.w[c2] = wp[c2 * 4];
         const uint16_t *sp = scales + row * sb_ld + p0 * 2, *bp = biases + row * sb_ld + p0 * 2;
         if (dead) sp = scales, bp = biases;
-        if constexpr (CH == 4) {
+        const uint32_t *ip = dead ? sbi : sbi + row * sb_ld + p0 * 2;
+        if constexpr (SB && CH == 2) {
+            const uint4 v = *reinterpret_cast<const uint4 *>(ip);
+            cb.s[0] = v.x, cb.b[0] = v.y, cb.s[1] = v.z, cb.b[1] = v.w;
+        } else if constexpr (SB) {
+            const uint2 v = *reinterpret_cast<const uint2 *>(ip);
+            cb.s[0] = v.x, cb.b[0] = v.y;
+        } else if constexpr (CH == 4) {
             const uint4 sv = *reinterpret_cast<const uint4 *>(sp), bv = *reinterpret_cast<const uint4 *>(bp);
             cb.s[0] = sv.x, cb.s[1] = sv.y, cb.s[2] = sv.z, cb.s[3] = sv.w;
             cb.b[0] = bv.x, cb.b[1] = bv.y, cb.b[2] = bv.z, cb.b[3] = bv.w;
@@ -553,9 +568,9 @@ inline uint32_t pick_mf_split(uint32_t weight_tiles, uint32_t groups, uint32_t c
     return best_s;
 }
 
-template <int M, int PRO, int EPI, int CH>
+template <int M, int PRO, int EPI, int CH, bool SB>
 inline void launch_gemv_mfma_t(hipStream_t stream, uint32_t cus, const GemvArgs &a, uint32_t ksplit) {
-    auto kernel = q4_gemv_mfma_kernel<M, PRO, EPI, CH>;
+    auto kernel = q4_gemv_mfma_kernel<M, PRO, EPI, CH, SB>;
     const uint32_t lds = mf_lds_bytes(M, a.k) + (mf_red_areas(M, a.k) - 1) * kMfRedBytes;
     int per_cu = 0;
     if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, kMfThreads, lds) != hipSuccess || per_cu < 1)
@@ -565,7 +580,7 @@ inline void launch_gemv_mfma_t(hipStream_t stream, uint32_t cus, const GemvArgs 
     const uint32_t ranges = a.kranges > 1 ? a.kranges : 1;
     const uint32_t cap = (cus / ranges > 0 ? cus / ranges : 1) * static_cast<uint32_t>(per_cu);
     hipLaunchKernelGGL(kernel, dim3(need < cap ? need : cap, a.kranges > 1 ? a.kranges : 1), dim3(kMfThreads), lds,
-                       stream, a.x, a.x_ld, a.wq, a.s, a.b, a.n, a.k, a.y, a.y_ld, a.y_is_f32, ksplit);
+                       stream, a.x, a.x_ld, a.wq, a.s, a.b, a.sb, a.n, a.k, a.y, a.y_ld, a.y_is_f32, ksplit);
 }
 
 // Whether the matrix-core GEMV takes this launch of 2..8 rows: k a multiple of
@@ -576,7 +591,8 @@ inline void launch_gemv_mfma_t(hipStream_t stream, uint32_t cus, const GemvArgs 
 inline bool mf_eligible(uint32_t m, const GemvArgs &a) {
     if (m < 2 || m > 8 || a.k == 0 || a.k % (kGroup * 4) != 0 || a.n == 0 || a.n % 16 != 0 || a.x_ld % 8 != 0)
         return false;
-    if ((reinterpret_cast<uintptr_t>(a.wq) | reinterpret_cast<uintptr_t>(a.s) | reinterpret_cast<uintptr_t>(a.b)) & 15u)
+    if ((reinterpret_cast<uintptr_t>(a.wq) | reinterpret_cast<uintptr_t>(a.s) | reinterpret_cast<uintptr_t>(a.b) |
+         reinterpret_cast<uintptr_t>(a.sb)) & 15u)
         return false;
     if (a.pro == kProRmsNorm && a.k > kMfPackMaxK) return false;  // the pack area's row limit
     if (static_cast<uint64_t>(m) * a.y_ld >= (1ull << 31)) return false;  // 32-bit output offsets
@@ -589,7 +605,10 @@ void launch_gemv_mfma_m(hipStream_t stream, uint32_t cus, const GemvArgs &a);
 
 // Chunk width: 4 group pairs when each wavefront's slice allows it (one
 // 16-byte scale and one bias load per 8 groups), else 2, else 1, at most
-// half the slice.
+// half the slice. Interleaved scales and biases (a.sb) are read at 2 and 1
+// pairs per chunk, for the prologue / epilogue pairs of the decoder's GEMVs.
+// At 4 pairs the separate arrays take two loads as well, and two loads from
+// the interleaved table measured slower (config-5 decode 2,611 -> 2,596 tok/s).
 template <int M>
 inline void launch_gemv_mfma_dispatch(hipStream_t stream, uint32_t cus, const GemvArgs &a) {
     const uint32_t groups = a.k / kGroup;
@@ -616,19 +635,24 @@ inline void launch_gemv_mfma_dispatch(hipStream_t stream, uint32_t cus, const Ge
             break;
         }
     }
-#define FH_MF_LAUNCH(P, E)                                                                 \
-    do {                                                                                   \
-        if (ch == 4) launch_gemv_mfma_t<M, P, E, 4>(stream, cus, a, ksplit);                \
-        else if (ch == 2) launch_gemv_mfma_t<M, P, E, 2>(stream, cus, a, ksplit);           \
-        else launch_gemv_mfma_t<M, P, E, 1>(stream, cus, a, ksplit);                        \
+    const bool sb = a.sb != nullptr;
+#define FH_MF_LAUNCH(P, E, S)                                                                      \
+    do {                                                                                           \
+        if (ch == 4) launch_gemv_mfma_t<M, P, E, 4, false>(stream, cus, a, ksplit);                 \
+        else if (ch == 2 && S && sb) launch_gemv_mfma_t<M, P, E, 2, S>(stream, cus, a, ksplit);      \
+        else if (ch == 2) launch_gemv_mfma_t<M, P, E, 2, false>(stream, cus, a, ksplit);            \
+        else if (S && sb) launch_gemv_mfma_t<M, P, E, 1, S>(stream, cus, a, ksplit);                \
+        else launch_gemv_mfma_t<M, P, E, 1, false>(stream, cus, a, ksplit);                         \
     } while (0)
+    // (no interleaved form of the SiLU epilogue without RMSNorm: the decoder
+    // does not run it)
     if (a.epi == kEpiSiluMul) {
-        if (a.pro == kProRmsNorm) FH_MF_LAUNCH(kProRmsNorm, kEpiSiluMul);
-        else FH_MF_LAUNCH(kProNone, kEpiSiluMul);
+        if (a.pro == kProRmsNorm) FH_MF_LAUNCH(kProRmsNorm, kEpiSiluMul, true);
+        else FH_MF_LAUNCH(kProNone, kEpiSiluMul, false);
     } else if (a.pro == kProRmsNorm) {
-        FH_MF_LAUNCH(kProRmsNorm, kEpiNone);
+        FH_MF_LAUNCH(kProRmsNorm, kEpiNone, true);
     } else {
-        FH_MF_LAUNCH(kProNone, kEpiNone);
+        FH_MF_LAUNCH(kProNone, kEpiNone, true);
     }
 #undef FH_MF_LAUNCH
 }

@@ -146,20 +146,23 @@ int launch_gemv_rows(fh_device *dev, const char *fn, int64_t m, const GemvArgs &
 // m outside 2..8, the down projection not split into K ranges, or the next
 // GEMV not taking all m rows from one image.
 int q4_down_pack(fh_device *dev, const char *fn, const uint16_t *x, int64_t m, int64_t x_ld, const uint32_t *wq,
-                 const uint16_t *scales, const uint16_t *biases, int64_t n, int64_t k, const uint16_t *res,
-                 uint16_t *res_out, const uint16_t *norm_weight, float eps, const uint32_t *next_wq,
-                 const uint16_t *next_scales, const uint16_t *next_biases, int64_t next_n, bool *packed) {
+                 const uint16_t *scales, const uint16_t *biases, const uint32_t *sb, int64_t n, int64_t k,
+                 const uint16_t *res, uint16_t *res_out, const uint16_t *norm_weight, float eps,
+                 const uint32_t *next_wq, const uint16_t *next_scales, const uint16_t *next_biases,
+                 const uint32_t *next_sb, int64_t next_n, bool *packed) {
     *packed = false;
     if (m < 2 || m > 8 || k <= 0 || n <= 0 || n > kMfPackMaxK || x_ld > 0x7FFFFFFFll) return FH_OK;
     GemvArgs down{x, static_cast<uint32_t>(x_ld), wq, scales, biases, static_cast<uint32_t>(n),
                   static_cast<uint32_t>(k), nullptr, static_cast<uint32_t>(n), 1, kProNone, kEpiNone,
                   GemvFusion{}};
+    down.sb = sb;
     if (!mf_eligible(static_cast<uint32_t>(m), down) || mf_rows_per_launch(down.k) >= m) return FH_OK;
     const uint32_t ranges = mf_k_ranges(dev, m, down);
     if (ranges == 0) return FH_OK;
     GemvArgs next{nullptr, static_cast<uint32_t>(n), next_wq, next_scales, next_biases, static_cast<uint32_t>(next_n),
                   static_cast<uint32_t>(n), nullptr, static_cast<uint32_t>(next_n), 0, kProRmsNorm, kEpiNone,
                   GemvFusion{}};
+    next.sb = next_sb;
     if (!mf_eligible(static_cast<uint32_t>(m), next) || mf_rows_per_launch(next.k) < m) return FH_OK;
     for (const void *p : {static_cast<const void *>(x), static_cast<const void *>(res),
                           static_cast<const void *>(res_out), static_cast<const void *>(norm_weight)})
@@ -195,25 +198,34 @@ int q4_down_pack(fh_device *dev, const char *fn, const uint16_t *x, int64_t m, i
 // The RMSNorm'd GEMV of m rows on the image q4_down_pack left in the pack
 // area (weight [n, k], k the image's row length).
 int q4_gemv_packed(fh_device *dev, const char *fn, int64_t m, const uint32_t *wq, const uint16_t *scales,
-                   const uint16_t *biases, int64_t n, int64_t k, void *y, int y_is_f32) {
+                   const uint16_t *biases, const uint32_t *sb, int64_t n, int64_t k, void *y, int y_is_f32) {
     GemvArgs a{static_cast<const uint16_t *>(dev->pack_area), static_cast<uint32_t>(k), wq, scales, biases,
                static_cast<uint32_t>(n), static_cast<uint32_t>(k), y, static_cast<uint32_t>(n), y_is_f32,
                kProRmsNorm, kEpiNone, GemvFusion{}};
+    a.sb = sb;
     if (int rc = check_range(dev, y, static_cast<uint64_t>(m) * n * (y_is_f32 ? 4 : 2), fn, "y")) return rc;
     return dispatch(dev, fn, [&] { launch_q4_gemv_mfma(dev->stream, dev->compute_units, static_cast<int>(m), a); });
 }
 
-}  // namespace fh
+// The interleaved scale/bias table of an n x k weight (fh_q4_interleave):
+// null, or 16-byte aligned n * k / 64 dwords with k a multiple of 128.
+int check_sb(fh_device *dev, const char *fn, const uint32_t *sb, int64_t n, int64_t k) {
+    if (sb == nullptr) return FH_OK;
+    if (k % (2 * kGroup) != 0 || reinterpret_cast<uintptr_t>(sb) % 16 != 0)
+        return fail(FH_ERR_INVALID_ARGUMENT,
+                    "%s: an interleaved scale/bias table needs k %% 128 == 0 (k=%lld) and 16-byte alignment", fn,
+                    (long long)k);
+    return check_range(dev, sb, static_cast<uint64_t>(n) * (k / kGroup) * 4, fn, "interleaved scale/bias");
+}
 
-using namespace fh;
-
-extern "C" int fh_q4_matmul(fh_device *dev, const uint16_t *x, int64_t m, int64_t k,
-                            int64_t x_ld, const uint32_t *wq, const uint16_t *scales,
-                            const uint16_t *biases, int64_t n, int64_t group, void *y,
-                            int y_dtype) {
+// fh_q4_matmul with the weight's optional interleaved scale/bias table.
+int q4_matmul(fh_device *dev, const uint16_t *x, int64_t m, int64_t k, int64_t x_ld, const uint32_t *wq,
+              const uint16_t *scales, const uint16_t *biases, const uint32_t *sb, int64_t n, int64_t group, void *y,
+              int y_dtype) {
     const char *fn = "fh_q4_matmul";
     if (int rc = check_usable(dev, fn)) return rc;
     if (int rc = check_q4_table(dev, fn, wq, scales, biases, n, k, group)) return rc;
+    if (int rc = check_sb(dev, fn, sb, n, k)) return rc;
     if (m < 0) return fail(FH_ERR_INVALID_ARGUMENT, "%s: m=%lld", fn, (long long)m);
     if (m > 65535ll * 128) return fail(FH_ERR_INDEX_TOO_LARGE, "%s: m > 65535*128 rows", fn);
     if (y_dtype != FH_BF16 && y_dtype != FH_F32)
@@ -244,12 +256,24 @@ extern "C" int fh_q4_matmul(fh_device *dev, const uint16_t *x, int64_t m, int64_
             return fail(FH_ERR_UNSUPPORTED, "%s: k=%lld is too large for the GEMV's LDS stage", fn,
                         (long long)k);
         GemvArgs a{x, ld32, wq, scales, biases, n32, k32, y, n32, y_is_f32, kProNone, kEpiNone, GemvFusion{}};
+        a.sb = sb;
         return launch_gemv_rows(dev, fn, m, a, n);
     }
     return dispatch(dev, fn, [&] {
         launch_q4_gemm(dev->stream, dev->compute_units, x, ld32, wq, scales, biases, static_cast<uint32_t>(m), n32,
                        k32, y, y_is_f32, dev->partial_area);
     });
+}
+
+}  // namespace fh
+
+using namespace fh;
+
+extern "C" int fh_q4_matmul(fh_device *dev, const uint16_t *x, int64_t m, int64_t k,
+                            int64_t x_ld, const uint32_t *wq, const uint16_t *scales,
+                            const uint16_t *biases, int64_t n, int64_t group, void *y,
+                            int y_dtype) {
+    return q4_matmul(dev, x, m, k, x_ld, wq, scales, biases, nullptr, n, group, y, y_dtype);
 }
 
 namespace {
@@ -315,12 +339,16 @@ int check_norm_operands(fh_device *dev, const char *fn, const uint16_t *x, const
 
 }  // namespace
 
-extern "C" int fh_q4_matmul_rmsnorm(fh_device *dev, const uint16_t *x, const uint16_t *residual,
-                                    uint16_t *residual_out, const uint16_t *norm_weight, float eps, int64_t m,
-                                    int64_t k, const uint32_t *wq, const uint16_t *scales,
-                                    const uint16_t *biases, int64_t n, int64_t group, void *y, int y_dtype) {
+namespace fh {
+
+// fh_q4_matmul_rmsnorm with the weight's optional interleaved scale/bias table.
+int q4_matmul_rmsnorm(fh_device *dev, const uint16_t *x, const uint16_t *residual, uint16_t *residual_out,
+                      const uint16_t *norm_weight, float eps, int64_t m, int64_t k, const uint32_t *wq,
+                      const uint16_t *scales, const uint16_t *biases, const uint32_t *sb, int64_t n, int64_t group,
+                      void *y, int y_dtype) {
     const char *fn = "fh_q4_matmul_rmsnorm";
     if (int rc = check_fused(dev, fn, m, k, wq, scales, biases, n, group, y, y_dtype, n, true)) return rc;
+    if (int rc = check_sb(dev, fn, sb, n, k)) return rc;
     if (!norm_weight) return fail(FH_ERR_INVALID_ARGUMENT, "%s: null norm weight", fn);
     if (int rc = check_norm_operands(dev, fn, x, residual, residual_out, norm_weight, m, k)) return rc;
     if (m == 0 || n == 0) return FH_OK;
@@ -328,26 +356,86 @@ extern "C" int fh_q4_matmul_rmsnorm(fh_device *dev, const uint16_t *x, const uin
     // empty rows: h and the normalised x are empty, y = x' W^T is zeros
     if (k == 0) return zero_fill(dev, fn, y, static_cast<uint64_t>(m) * n * (y_dtype == FH_F32 ? 4 : 2));
     const uint32_t k32 = static_cast<uint32_t>(k), n32 = static_cast<uint32_t>(n);
-    const GemvArgs a{x, k32, wq, scales, biases, n32, k32, y, n32, y_dtype == FH_F32, kProRmsNorm, kEpiNone,
-                     GemvFusion{residual, residual_out, norm_weight, eps, 1.0f / static_cast<float>(k)}};
+    GemvArgs a{x, k32, wq, scales, biases, n32, k32, y, n32, y_dtype == FH_F32, kProRmsNorm, kEpiNone,
+               GemvFusion{residual, residual_out, norm_weight, eps, 1.0f / static_cast<float>(k)}};
+    a.sb = sb;
     return launch_gemv_rows(dev, fn, m, a, n);
 }
 
-extern "C" int fh_q4_gate_up_silu(fh_device *dev, const uint16_t *x, const uint16_t *residual,
-                                  uint16_t *residual_out, const uint16_t *norm_weight, float eps, int64_t m,
-                                  int64_t k, const uint32_t *wq, const uint16_t *scales, const uint16_t *biases,
-                                  int64_t n, int64_t group, uint16_t *act) {
+// fh_q4_gate_up_silu with the weight's optional interleaved scale/bias table.
+int q4_gate_up_silu(fh_device *dev, const uint16_t *x, const uint16_t *residual, uint16_t *residual_out,
+                    const uint16_t *norm_weight, float eps, int64_t m, int64_t k, const uint32_t *wq,
+                    const uint16_t *scales, const uint16_t *biases, const uint32_t *sb, int64_t n, int64_t group,
+                    uint16_t *act) {
     const char *fn = "fh_q4_gate_up_silu";
     if (n % 2 != 0) return fail(FH_ERR_INVALID_ARGUMENT, "%s: n=%lld is not [gate; up] rows", fn, (long long)n);
     const bool norm = norm_weight != nullptr;
     if (int rc = check_fused(dev, fn, m, k, wq, scales, biases, n, group, act, FH_BF16, n / 2, norm)) return rc;
+    if (int rc = check_sb(dev, fn, sb, n, k)) return rc;
     if (int rc = check_norm_operands(dev, fn, x, residual, residual_out, norm_weight, m, k)) return rc;
     if (m == 0 || n == 0) return FH_OK;
     if (int rc = set_current(dev, fn)) return rc;
     // empty rows: gate and up are zeros, and RNE(RNE(silu(0)) * 0) = 0
     if (k == 0) return zero_fill(dev, fn, act, static_cast<uint64_t>(m) * (n / 2) * 2);
     const uint32_t k32 = static_cast<uint32_t>(k), n32 = static_cast<uint32_t>(n);
-    const GemvArgs a{x, k32, wq, scales, biases, n32, k32, act, n32 / 2, 0, norm ? kProRmsNorm : kProNone,
-                     kEpiSiluMul, GemvFusion{residual, residual_out, norm_weight, eps, 1.0f / static_cast<float>(k)}};
+    GemvArgs a{x, k32, wq, scales, biases, n32, k32, act, n32 / 2, 0, norm ? kProRmsNorm : kProNone,
+               kEpiSiluMul, GemvFusion{residual, residual_out, norm_weight, eps, 1.0f / static_cast<float>(k)}};
+    a.sb = sb;
     return launch_gemv_rows(dev, fn, m, a, n / 2);
+}
+
+// Writes sb[r][2p] = the scales of groups 2p, 2p + 1 of row r (low half:
+// group 2p) and sb[r][2p + 1] = their biases, i.e. dword i of the scales
+// and of the biases (viewed as dword arrays) go to dwords 2i and 2i + 1.
+__global__ __launch_bounds__(256) void q4_interleave_kernel(const uint32_t *__restrict__ s,
+                                                            const uint32_t *__restrict__ b, uint64_t pairs,
+                                                            uint2 *__restrict__ sb) {
+    for (uint64_t i = static_cast<uint64_t>(blockIdx.x) * 256 + threadIdx.x; i < pairs;
+         i += static_cast<uint64_t>(gridDim.x) * 256)
+        sb[i] = make_uint2(s[i], b[i]);
+}
+
+}  // namespace fh
+
+extern "C" int fh_q4_matmul_rmsnorm(fh_device *dev, const uint16_t *x, const uint16_t *residual,
+                                    uint16_t *residual_out, const uint16_t *norm_weight, float eps, int64_t m,
+                                    int64_t k, const uint32_t *wq, const uint16_t *scales,
+                                    const uint16_t *biases, int64_t n, int64_t group, void *y, int y_dtype) {
+    return q4_matmul_rmsnorm(dev, x, residual, residual_out, norm_weight, eps, m, k, wq, scales, biases, nullptr, n,
+                             group, y, y_dtype);
+}
+
+extern "C" int fh_q4_gate_up_silu(fh_device *dev, const uint16_t *x, const uint16_t *residual,
+                                  uint16_t *residual_out, const uint16_t *norm_weight, float eps, int64_t m,
+                                  int64_t k, const uint32_t *wq, const uint16_t *scales, const uint16_t *biases,
+                                  int64_t n, int64_t group, uint16_t *act) {
+    return q4_gate_up_silu(dev, x, residual, residual_out, norm_weight, eps, m, k, wq, scales, biases, nullptr, n,
+                           group, act);
+}
+
+extern "C" int fh_q4_interleave(fh_device *dev, const uint16_t *scales, const uint16_t *biases, int64_t n,
+                                int64_t k, int64_t group, uint32_t *sb) {
+    const char *fn = "fh_q4_interleave";
+    if (int rc = check_usable(dev, fn)) return rc;
+    if (n < 0 || k < 0) return fail(FH_ERR_INVALID_ARGUMENT, "%s: negative shape n=%lld k=%lld", fn, (long long)n,
+                                    (long long)k);
+    if (group != kGroup)
+        return fail(FH_ERR_UNSUPPORTED, "%s: group %lld; the kernels implement group 64", fn, (long long)group);
+    if (k % (2 * kGroup) != 0)
+        return fail(FH_ERR_INVALID_ARGUMENT, "%s: k=%lld is not a multiple of two groups (128)", fn, (long long)k);
+    if ((reinterpret_cast<uintptr_t>(scales) | reinterpret_cast<uintptr_t>(biases)) % 4 != 0 ||
+        reinterpret_cast<uintptr_t>(sb) % 16 != 0)
+        return fail(FH_ERR_INVALID_ARGUMENT, "%s: scales and biases must be 4-byte aligned, sb 16-byte aligned", fn);
+    const uint64_t pairs = static_cast<uint64_t>(n) * (k / kGroup) / 2;
+    if (pairs == 0) return FH_OK;
+    if (int rc = check_range(dev, scales, pairs * 4, fn, "scales")) return rc;
+    if (int rc = check_range(dev, biases, pairs * 4, fn, "biases")) return rc;
+    if (int rc = check_range(dev, sb, pairs * 8, fn, "sb")) return rc;
+    if (int rc = set_current(dev, fn)) return rc;
+    const uint64_t blocks = (pairs + 255) / 256;
+    return dispatch(dev, fn, [&] {
+        hipLaunchKernelGGL(q4_interleave_kernel, dim3(blocks < 65536 ? blocks : 65536), dim3(256), 0, dev->stream,
+                           reinterpret_cast<const uint32_t *>(scales), reinterpret_cast<const uint32_t *>(biases),
+                           pairs, reinterpret_cast<uint2 *>(sb));
+    });
 }

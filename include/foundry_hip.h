@@ -413,6 +413,18 @@ int fh_q4_gate_up_silu(fh_device *dev, const uint16_t *x, const uint16_t *residu
                        int64_t k, const uint32_t *wq, const uint16_t *scales, const uint16_t *biases,
                        int64_t n, int64_t group, uint16_t *act);
 
+/* A load-time copy of a q4 weight's scales and biases, interleaved per group
+ * pair: sb (u32 [n, k / 64], 16-byte aligned) gets at dword 2p of row r the
+ * scales of groups 2p and 2p + 1 (group 2p in the low half) and at dword
+ * 2p + 1 their biases. fh_q4_weight.sb takes it; the 2..8-row decode GEMV of
+ * fh_llama_forward then reads a chunk's scales and biases with one load
+ * instead of two (the same values: results are unchanged). No counterpart in
+ * the reference (its Linear reads the separate scales / biases tensors,
+ * src/nn/linear.rs:22-35); a data layout of this library's decoder.
+ * group = 64, k a multiple of 128. */
+int fh_q4_interleave(fh_device *dev, const uint16_t *scales, const uint16_t *biases, int64_t n,
+                     int64_t k, int64_t group, uint32_t *sb);
+
 /* LlamaMlp's act_fn(gate) * up (src/models/llama/mlp.rs:49-58, Silu at
  * src/nn/activation.rs:19-28): gate_up row = [gate (f) | up (f)],
  * out = RNE(RNE(g / (1 + exp(-g))) * u), out: [rows, f]. */
@@ -440,13 +452,16 @@ int fh_advance_positions(fh_device *dev, uint32_t *positions, int64_t n, int64_t
  * by per-call host overhead.
  * ====================================================================== */
 
-/* A q4 weight: n rows of k columns (group 64), as fh_q4_matmul takes it. */
+/* A q4 weight: n rows of k columns (group 64), as fh_q4_matmul takes it.
+ * sb: null, or fh_q4_interleave's copy of scales / biases, which the
+ * batched decode GEMVs (2..8 rows) then read instead. */
 typedef struct fh_q4_weight {
     const uint32_t *wq;
     const uint16_t *scales;
     const uint16_t *biases;
     int64_t n;
     int64_t k;
+    const uint32_t *sb;
 } fh_q4_weight;
 
 /* One decoder layer (LlamaDecoderLayer, src/models/llama/model.rs:47, :254-280):

@@ -564,6 +564,77 @@ def test_llama_forward_equals_the_op_sequence(device, batch, t):
         assert np.array_equal(got, exp), f"{what}: {np.count_nonzero(got != exp)} of {got.size} differ"
 
 
+def test_q4_interleave_layout(device):
+    """fh_q4_interleave: dword 2p of a row holds the scales of groups 2p and
+    2p + 1 (group 2p in the low half), dword 2p + 1 their biases; shapes it
+    cannot lay out are rejected."""
+    rng = np.random.default_rng(7)
+    n, k = 37, 384  # 6 groups a row
+    s = rng.integers(0, 1 << 16, (n, k // 64), dtype=np.uint16)
+    b = rng.integers(0, 1 << 16, (n, k // 64), dtype=np.uint16)
+    ds, db, sb = up(device, s), up(device, b), device.empty(n * (k // 64) * 4)
+    _lib.call("fh_q4_interleave", device.handle, ctypes.c_void_p(ds.ptr), ctypes.c_void_p(db.ptr), n, k, 64,
+              ctypes.c_void_p(sb.ptr))
+    got = down(device, sb, np.uint32, n * (k // 64)).reshape(n, k // 64)
+    g = np.arange(k // 64 // 2)
+    assert np.array_equal(got[:, 2 * g] & 0xFFFF, s[:, 2 * g]) and np.array_equal(got[:, 2 * g] >> 16, s[:, 2 * g + 1])
+    assert np.array_equal(got[:, 2 * g + 1] & 0xFFFF, b[:, 2 * g])
+    assert np.array_equal(got[:, 2 * g + 1] >> 16, b[:, 2 * g + 1])
+    with pytest.raises(_lib.HipError, match="multiple of two groups"):
+        _lib.call("fh_q4_interleave", device.handle, ctypes.c_void_p(ds.ptr), ctypes.c_void_p(db.ptr), n, 320, 64,
+                  ctypes.c_void_p(sb.ptr))
+    with pytest.raises(_lib.HipError, match="group 32"):
+        _lib.call("fh_q4_interleave", device.handle, ctypes.c_void_p(ds.ptr), ctypes.c_void_p(db.ptr), n, k, 32,
+                  ctypes.c_void_p(sb.ptr))
+    with pytest.raises(_lib.HipError, match="sb"):  # a table larger than its storage
+        _lib.call("fh_q4_interleave", device.handle, ctypes.c_void_p(ds.ptr), ctypes.c_void_p(db.ptr), n, k, 64,
+                  ctypes.c_void_p(sb.ptr + 16))
+
+
+# 8B-shaped layers: at 2..8 rows the q/k/v and gate/up GEMVs read two group
+# pairs per chunk, o one, the down projection runs over K ranges into the
+# next layer's RMSNorm image
+WIDE = LlamaConfig(n_layers=2, hidden=4096, n_heads=32, n_kv_heads=8, head_dim=128, ffn=14336, vocab=1000)
+
+
+@pytest.mark.parametrize("cfg,batch", [(TINY, 2), (TINY, 5), (WIDE, 3), (WIDE, 8)])
+def test_interleaved_scale_bias_tables_change_no_result(device, cfg, batch):
+    """Decode steps of `batch` sequences with the interleaved scale/bias
+    tables (fh_q4_interleave, read by the batched GEMVs) and without give
+    bit-identical logits and ids: the tables only change how the kernels
+    load the same values."""
+    ids = synth.token_ids(5, batch * 3, cfg.vocab).reshape(batch, 3).astype(np.uint32)
+    out = []
+    for interleave in (True, False):
+        model = Q4Llama(device, cfg, 2, 16, max_tokens=1, batch=batch, interleave=interleave)
+        assert (model.layers[0]["qkv"].sb is not None) == interleave
+        got = []
+        for pos in range(3):
+            model.step(ids[:, pos:pos + 1], pos)
+            got.append((down(device, model.buf["logits"], np.uint16, batch * cfg.vocab),
+                        down(device, model.buf["next"], np.uint32, batch)))
+        out.append(got)
+        del model
+    for pos, ((la, na), (lb, nb)) in enumerate(zip(*out)):
+        assert np.array_equal(la, lb), f"step {pos}: {np.count_nonzero(la != lb)} logits differ"
+        assert np.array_equal(na, nb)
+
+
+def test_llama_forward_checks_the_interleaved_tables(device):
+    """A misaligned or short interleaved table is rejected before any work."""
+    model = Q4Llama(device, TINY, 1, 16, max_tokens=4, batch=2)
+    b = model.buf
+    sb = model._layer_table[1].gate_up.sb
+    model._layer_table[1].gate_up.sb = sb + 8
+    with pytest.raises(_lib.HipError, match="16-byte alignment"):
+        model._forward(1, b["ids"], b["positions"])
+    model._layer_table[1].gate_up.sb = sb + 16
+    with pytest.raises(_lib.HipError, match="interleaved scale/bias"):
+        model._forward(1, b["ids"], b["positions"])
+    model._layer_table[1].gate_up.sb = sb
+    model.step(np.ones((2, 1), np.uint32), 0)
+
+
 def test_append_token_rows(device):
     """fh_append_token logs each sequence's token at its own position; a
     position before base or past capacity writes nothing."""
