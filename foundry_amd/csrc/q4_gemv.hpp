@@ -111,11 +111,14 @@ struct GemvChunks {
 
 // FULL: every lane's CPL chunks exist (k is a multiple of 32*CPL*L), so the
 // loads need no per-chunk guard and share one address with immediate offsets.
-template <int M, int L, int CPL, bool FULL, int PRO, int EPI>
+// SB: a chunk's scale and bias come from sbi, the table interleaved per group
+// pair (dword 2p of a row: scales of groups 2p, 2p + 1; dword 2p + 1: their
+// biases), one 8-byte load instead of two 2-byte loads.
+template <int M, int L, int CPL, bool FULL, int PRO, int EPI, bool SB>
 __global__ __launch_bounds__(kGemvThreads) void q4_gemv_kernel(
     const uint16_t *__restrict__ x, uint32_t x_ld, const uint32_t *__restrict__ wq,
-    const uint16_t *__restrict__ scales, const uint16_t *__restrict__ biases, uint32_t n,
-    uint32_t k, void *__restrict__ y, uint32_t y_ld, int y_is_f32, GemvFusion fu) {
+    const uint16_t *__restrict__ scales, const uint16_t *__restrict__ biases, const uint32_t *__restrict__ sbi,
+    uint32_t n, uint32_t k, void *__restrict__ y, uint32_t y_ld, int y_is_f32, GemvFusion fu) {
     constexpr uint32_t kRowsPerWave = 64 / L;
     static_assert(EPI == kEpiNone || kRowsPerWave >= 2, "the SiLU epilogue pairs rows within a wavefront");
     // rows of one wavefront that produce outputs: with kEpiSiluMul, gate rows
@@ -154,13 +157,23 @@ __global__ __launch_bounds__(kGemvThreads) void q4_gemv_kernel(
         const uint4 *wrow = reinterpret_cast<const uint4 *>(wq + row_c * (k / 8)) + c0;
         const uint16_t *srow = scales + row_c * (k / kGroup);
         const uint16_t *brow = biases + row_c * (k / kGroup);
+        const uint2 *irow = reinterpret_cast<const uint2 *>(sbi + row_c * (k / kGroup));
 #pragma unroll
         for (int u = 0; u < CPL; ++u) {
             const uint32_t c = c0 + u * L;
             if (FULL || c < chunks) {
                 buf.w[u] = wrow[u * L];
-                buf.s[u] = srow[c / 2];
-                buf.b[u] = brow[c / 2];
+                if constexpr (SB) {
+                    // group c / 2 is half (c / 2) & 1 of pair c / 4 (the bf16
+                    // conversion takes the low half)
+                    const uint2 v = irow[c / 4];
+                    const uint32_t sh = (c & 2u) * 8u;
+                    buf.s[u] = v.x >> sh;
+                    buf.b[u] = v.y >> sh;
+                } else {
+                    buf.s[u] = srow[c / 2];
+                    buf.b[u] = brow[c / 2];
+                }
             }
         }
     };
@@ -510,28 +523,37 @@ struct GemvArgs {
     const uint32_t *sb = nullptr;
 };
 
-template <int M, int L, int CPL, bool FULL, int PRO, int EPI>
+template <int M, int L, int CPL, bool FULL, int PRO, int EPI, bool SB>
 inline void launch_gemv_full(hipStream_t stream, uint32_t cus, const GemvArgs &a) {
     constexpr uint32_t kRowsPerWave = 64 / L;
     constexpr uint32_t kOutRows = EPI == kEpiSiluMul ? kRowsPerWave / 2 : kRowsPerWave;
-    auto kernel = q4_gemv_kernel<M, L, CPL, FULL, PRO, EPI>;
+    auto kernel = q4_gemv_kernel<M, L, CPL, FULL, PRO, EPI, SB>;
     const uint32_t lds = gemv_lds_bytes(M, a.k, PRO == kProRmsNorm);
     const uint32_t n_out = EPI == kEpiSiluMul ? a.n / 2 : a.n;
     const uint32_t groups = (n_out + kOutRows - 1) / kOutRows;
     const uint32_t need = (groups + kGemvWaves - 1) / kGemvWaves;
     const uint32_t cap = cus * resident_blocks(kernel, lds);
     const uint32_t blocks = need < cap ? need : cap;
-    hipLaunchKernelGGL(kernel, dim3(blocks), dim3(kGemvThreads), lds, stream, a.x, a.x_ld, a.wq, a.s, a.b, a.n,
-                       a.k, a.y, a.y_ld, a.y_is_f32, a.fu);
+    hipLaunchKernelGGL(kernel, dim3(blocks), dim3(kGemvThreads), lds, stream, a.x, a.x_ld, a.wq, a.s, a.b, a.sb,
+                       a.n, a.k, a.y, a.y_ld, a.y_is_f32, a.fu);
 }
 
+// The interleaved scale/bias table (a.sb) is read by the one-row
+// single-segment kernels, the decoder's batch-1 step.
 template <int M, int L, int CPL, int PRO, int EPI>
 inline void launch_gemv_fused(hipStream_t stream, uint32_t cus, const GemvArgs &a) {
     const uint32_t chunks = a.k / 32;
-    if (chunks > 0 && chunks % (CPL * L) == 0)
-        launch_gemv_full<M, L, CPL, true, PRO, EPI>(stream, cus, a);
-    else
-        launch_gemv_full<M, L, CPL, false, PRO, EPI>(stream, cus, a);
+    if (chunks > 0 && chunks % (CPL * L) == 0) {
+        if constexpr (M == 1) {
+            if (a.sb != nullptr && (reinterpret_cast<uintptr_t>(a.sb) & 7u) == 0 && a.k % (2 * kGroup) == 0) {
+                launch_gemv_full<M, L, CPL, true, PRO, EPI, true>(stream, cus, a);
+                return;
+            }
+        }
+        launch_gemv_full<M, L, CPL, true, PRO, EPI, false>(stream, cus, a);
+    } else {
+        launch_gemv_full<M, L, CPL, false, PRO, EPI, false>(stream, cus, a);
+    }
 }
 
 template <int M, int L, int CPL>

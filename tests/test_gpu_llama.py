@@ -595,9 +595,12 @@ def test_q4_interleave_layout(device):
 # pairs per chunk, o one, the down projection runs over K ranges into the
 # next layer's RMSNorm image
 WIDE = LlamaConfig(n_layers=2, hidden=4096, n_heads=32, n_kv_heads=8, head_dim=128, ffn=14336, vocab=1000)
+# 3B-shaped layers: at one row the dot2 GEMV's single-segment shapes (32 x 3,
+# 16 x 6, 64 x 4 lanes x chunks) read the interleaved table
+C4ISH = LlamaConfig(n_layers=1, hidden=3072, n_heads=24, n_kv_heads=8, head_dim=128, ffn=8192, vocab=1024)
 
 
-@pytest.mark.parametrize("cfg,batch", [(TINY, 2), (TINY, 5), (WIDE, 3), (WIDE, 8)])
+@pytest.mark.parametrize("cfg,batch", [(TINY, 2), (TINY, 5), (WIDE, 3), (WIDE, 8), (WIDE, 1), (C4ISH, 1)])
 def test_interleaved_scale_bias_tables_change_no_result(device, cfg, batch):
     """Decode steps of `batch` sequences with the interleaved scale/bias
     tables (fh_q4_interleave, read by the batched GEMVs) and without give
