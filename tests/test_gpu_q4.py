@@ -171,6 +171,28 @@ def test_embed_config2_full_table(device, oracle, batch, _config2_table):
     assert np.array_equal(out[0], oracle.q4_embed(wq, s, b, ids))
 
 
+@pytest.mark.parametrize("k", [3072, 4096])
+def test_gather_wave_rows_specials_and_tails(device, oracle, k):
+    """The row-per-wavefront gather (k = 3072, 4096; at least 4 rows per CU):
+    special scale and bias values (zeros, infinities, NaNs, denormals) bit for
+    bit, 1029 ids (a partial last block) with ids past the table, and the
+    materialised dequant of the same 1100-row table; then 13 ids of the same
+    table (the per-word kernel of small batches)."""
+    specials = np.array([0x0000, 0x8000, 0x7F80, 0xFF80, 0x7FC0, 0x7F81, 0x0001, 0x7F7F, 0x3C80, 0xBC80,
+                         0x4700, 0xC2F0, 0x3B83, 0x0080, 0x8001, 0x3F80], dtype=np.uint16)
+    rows, g = 1100, k // 64
+    wq, s, b = synth.q4_weights(17 + k, rows, k)
+    s[::3] = specials[np.arange(rows * g).reshape(rows, g)[::3] % 16]
+    b[1::4] = specials[(np.arange(rows * g).reshape(rows, g)[1::4] * 7 + 3) % 16]
+    assert_bf16_identical(dev_dequant(device, wq, s, b), oracle.q4_dequant_bf16(wq, s, b))
+    ids = (synth.token_ids(k, 1029, 1200) % 1200).astype(np.uint32)
+    ids[:5] = [0, rows - 1, rows, 2**32 - 1, 7]
+    w = weight(device, wq, s, b)
+    for sel in (ids, ids[:13]):
+        out = Q4Embedding(w).forward(device, up(device, sel.reshape(1, -1), DType.U32))
+        assert_bf16_identical(out.to_numpy(device)[0], oracle.q4_embed(wq, s, b, sel))
+
+
 @pytest.fixture(scope="module")
 def _config2_table(device):
     wq, s, b = synth.q4_weights(2, 128256, 3072)
