@@ -67,7 +67,7 @@ class Profile(ctypes.Structure):
 class Q4Weight(ctypes.Structure):
     """fh_q4_weight."""
     _fields_ = [("wq", ctypes.c_void_p), ("scales", ctypes.c_void_p), ("biases", ctypes.c_void_p),
-                ("n", ctypes.c_int64), ("k", ctypes.c_int64), ("sb", ctypes.c_void_p)]
+                ("n", ctypes.c_int64), ("k", ctypes.c_int64), ("sb", ctypes.c_void_p), ("wt", ctypes.c_void_p)]
 
 
 class LlamaLayer(ctypes.Structure):
@@ -162,6 +162,7 @@ SIGNATURES = {
                              _vp, _int],
     "fh_q4_gate_up_silu": [_vp, _vp, _vp, _vp, _vp, ctypes.c_float, _i64, _i64, _vp, _vp, _vp, _i64, _i64, _vp],
     "fh_q4_interleave": [_vp, _vp, _vp, _i64, _i64, _i64, _vp],
+    "fh_q4_tile": [_vp, _vp, _i64, _i64, _i64, _int, _vp],
     "fh_silu_mul": [_vp, _vp, _i64, _i64, _vp],
     "fh_argmax": [_vp, _vp, _i64, _i64, _vp],
     "fh_advance_positions": [_vp, _vp, _i64, _i64],

@@ -31,24 +31,26 @@ int rope_kv(fh_device *dev, const char *fn, const uint16_t *qkv, const float *pa
             const uint16_t *cos_tab, const uint16_t *sin_tab, int64_t table_len, const uint32_t *positions,
             uint16_t *k_cache, uint16_t *v_cache, int64_t max_len, uint16_t *q_out);
 int q4_down_pack(fh_device *dev, const char *fn, const uint16_t *x, int64_t m, int64_t x_ld, const uint32_t *wq,
-                 const uint16_t *scales, const uint16_t *biases, const uint32_t *sb, int64_t n, int64_t k,
-                 const uint16_t *res, uint16_t *res_out, const uint16_t *norm_weight, float eps,
+                 const uint16_t *scales, const uint16_t *biases, const uint32_t *sb, const uint32_t *wt, int64_t n,
+                 int64_t k, const uint16_t *res, uint16_t *res_out, const uint16_t *norm_weight, float eps,
                  const uint32_t *next_wq, const uint16_t *next_scales, const uint16_t *next_biases,
-                 const uint32_t *next_sb, int64_t next_n, bool *packed);
+                 const uint32_t *next_sb, const uint32_t *next_wt, int64_t next_n, bool *packed);
 int q4_gemv_packed(fh_device *dev, const char *fn, int64_t m, const uint32_t *wq, const uint16_t *scales,
-                   const uint16_t *biases, const uint32_t *sb, int64_t n, int64_t k, void *y, int y_is_f32);
+                   const uint16_t *biases, const uint32_t *sb, const uint32_t *wt, int64_t n, int64_t k, void *y,
+                   int y_is_f32);
 int check_sb(fh_device *dev, const char *fn, const uint32_t *sb, int64_t n, int64_t k);
+int check_wt(fh_device *dev, const char *fn, const uint32_t *wt, const uint32_t *sb, int64_t n, int64_t k);
 int q4_matmul(fh_device *dev, const uint16_t *x, int64_t m, int64_t k, int64_t x_ld, const uint32_t *wq,
-              const uint16_t *scales, const uint16_t *biases, const uint32_t *sb, int64_t n, int64_t group, void *y,
-              int y_dtype);
+              const uint16_t *scales, const uint16_t *biases, const uint32_t *sb, const uint32_t *wt, int64_t n,
+              int64_t group, void *y, int y_dtype);
 int q4_matmul_rmsnorm(fh_device *dev, const uint16_t *x, const uint16_t *residual, uint16_t *residual_out,
                       const uint16_t *norm_weight, float eps, int64_t m, int64_t k, const uint32_t *wq,
-                      const uint16_t *scales, const uint16_t *biases, const uint32_t *sb, int64_t n, int64_t group,
-                      void *y, int y_dtype);
+                      const uint16_t *scales, const uint16_t *biases, const uint32_t *sb, const uint32_t *wt,
+                      int64_t n, int64_t group, void *y, int y_dtype);
 int q4_gate_up_silu(fh_device *dev, const uint16_t *x, const uint16_t *residual, uint16_t *residual_out,
                     const uint16_t *norm_weight, float eps, int64_t m, int64_t k, const uint32_t *wq,
-                    const uint16_t *scales, const uint16_t *biases, const uint32_t *sb, int64_t n, int64_t group,
-                    uint16_t *act);
+                    const uint16_t *scales, const uint16_t *biases, const uint32_t *sb, const uint32_t *wt,
+                    int64_t n, int64_t group, uint16_t *act);
 }  // namespace fh
 
 namespace {
@@ -96,24 +98,31 @@ int check_model(const char *fn, const fh_llama_model &m, int64_t seq_tokens) {
     return FH_OK;
 }
 
-// Every interleaved scale/bias table the model gives (fh_q4_weight.sb),
-// before any work is issued: the GEMVs that read one get it unchecked.
+// Every interleaved scale/bias table and tiled word copy the model gives
+// (fh_q4_weight.sb, .wt), before any work is issued: the GEMVs that read
+// one get it unchecked.
 int check_sb_tables(fh_device *d, const char *fn, const fh_llama_model &m) {
     FH_TRY(fh::check_sb(d, fn, m.embed.sb, m.embed.n, m.embed.k));
+    FH_TRY(fh::check_wt(d, fn, m.embed.wt, m.embed.sb, m.embed.n, m.embed.k));
     for (int64_t l = 0; l < m.n_layers; ++l)
-        for (const fh_q4_weight *w : {&m.layers[l].qkv, &m.layers[l].o, &m.layers[l].gate_up, &m.layers[l].down})
+        for (const fh_q4_weight *w : {&m.layers[l].qkv, &m.layers[l].o, &m.layers[l].gate_up, &m.layers[l].down}) {
             FH_TRY(fh::check_sb(d, fn, w->sb, w->n, w->k));
+            FH_TRY(fh::check_wt(d, fn, w->wt, w->sb, w->n, w->k));
+            if (w->wt != nullptr && w == &m.layers[l].gate_up && w->n % 32 != 0)
+                return fail(FH_ERR_INVALID_ARGUMENT, "%s: layer %lld gate_up: tiled words need n %% 32 == 0", fn,
+                            (long long)l);
+        }
     return FH_OK;
 }
 
 int linear(fh_device *d, const uint16_t *x, int64_t rows, int64_t x_ld, const fh_q4_weight &w, uint16_t *y) {
-    return fh::q4_matmul(d, x, rows, w.k, x_ld, w.wq, w.scales, w.biases, w.sb, w.n, kGroup, y, FH_BF16);
+    return fh::q4_matmul(d, x, rows, w.k, x_ld, w.wq, w.scales, w.biases, w.sb, w.wt, w.n, kGroup, y, FH_BF16);
 }
 
 int linear_norm(fh_device *d, const fh_llama_model &m, const uint16_t *x, const uint16_t *res, uint16_t *res_out,
                 const uint16_t *weight, int64_t rows, const fh_q4_weight &w, uint16_t *y) {
     return fh::q4_matmul_rmsnorm(d, x, res, res_out, weight, m.rms_norm_eps, rows, w.k, w.wq, w.scales, w.biases,
-                                 w.sb, w.n, kGroup, y, FH_BF16);
+                                 w.sb, w.wt, w.n, kGroup, y, FH_BF16);
 }
 
 // x = rms_norm(h [+ pending]); h updated in place when pending is given.
@@ -185,7 +194,9 @@ int add_norm(fh_device *d, const fh_llama_model &m, int64_t rows, const uint16_t
 int linear_silu(fh_device *d, const fh_llama_model &m, int64_t rows, const fh_q4_weight &w) {
     const char *fn = "fh_llama_forward";
     if (m.ffn % 8 != 0 || !aligned16(m.act)) {
-        FH_TRY(linear(d, m.x, rows, m.hidden, w, m.gate_up));
+        fh_q4_weight plain = w;
+        plain.wt = nullptr;  // gate/up's tiled words are in the SiLU pairing, not row order
+        FH_TRY(linear(d, m.x, rows, m.hidden, plain, m.gate_up));
         return fh_silu_mul(d, m.gate_up, rows, m.ffn, m.act);
     }
     FH_TRY(check_gemm(d, fn, m.x, rows, m.hidden, w, m.gate_up));
@@ -254,8 +265,8 @@ extern "C" int fh_llama_forward(fh_device *dev, const fh_llama_model *model, int
         const fh_llama_layer &L = m.layers[l];
         uint32_t qkv_splits = 1;
         if (packed) {
-            FH_TRY(fh::q4_gemv_packed(dev, fn, tokens, L.qkv.wq, L.qkv.scales, L.qkv.biases, L.qkv.sb, L.qkv.n,
-                                      L.qkv.k, m.qkv, 0));
+            FH_TRY(fh::q4_gemv_packed(dev, fn, tokens, L.qkv.wq, L.qkv.scales, L.qkv.biases, L.qkv.sb, L.qkv.wt,
+                                      L.qkv.n, L.qkv.k, m.qkv, 0));
             std::swap(h, h_alt);
         } else if (!fused) {
             FH_TRY(add_norm(dev, m, tokens, pending, pending_splits, L.input_norm));
@@ -287,7 +298,7 @@ extern "C" int fh_llama_forward(fh_device *dev, const fh_llama_model *model, int
             // act = silu_mul(rms_norm(o + h) [Wgate; Wup]^T) in one GEMV
             const fh_q4_weight &w = L.gate_up;
             FH_TRY(fh::q4_gate_up_silu(dev, m.o, h, h_alt, L.post_norm, m.rms_norm_eps, tokens, w.k, w.wq,
-                                       w.scales, w.biases, w.sb, w.n, kGroup, m.act));
+                                       w.scales, w.biases, w.sb, w.wt, w.n, kGroup, m.act));
             std::swap(h, h_alt);
         }
         packed = false;
@@ -297,9 +308,9 @@ extern "C" int fh_llama_forward(fh_device *dev, const fh_llama_model *model, int
             const fh_q4_weight &nw = last ? m.embed : m.layers[l + 1].qkv;
             const uint16_t *norm_w = last ? m.final_norm : m.layers[l + 1].input_norm;
             const fh_q4_weight &w = L.down;
-            FH_TRY(fh::q4_down_pack(dev, fn, m.act, tokens, m.ffn, w.wq, w.scales, w.biases, w.sb, w.n, w.k, h,
-                                    last ? nullptr : h_alt, norm_w, m.rms_norm_eps, nw.wq, nw.scales, nw.biases,
-                                    nw.sb, nw.n, &packed));
+            FH_TRY(fh::q4_down_pack(dev, fn, m.act, tokens, m.ffn, w.wq, w.scales, w.biases, w.sb, w.wt, w.n, w.k,
+                                    h, last ? nullptr : h_alt, norm_w, m.rms_norm_eps, nw.wq, nw.scales, nw.biases,
+                                    nw.sb, nw.wt, nw.n, &packed));
         }
         if (!packed) FH_TRY(linear(dev, m.act, tokens, m.ffn, L.down, m.o));
         pending = m.o;
@@ -312,7 +323,7 @@ extern "C" int fh_llama_forward(fh_device *dev, const fh_llama_model *model, int
         FH_TRY(linear(dev, m.x + last, m.batch, seq_tokens * m.hidden, m.embed, m.logits));
     } else if (packed) {
         FH_TRY(fh::q4_gemv_packed(dev, fn, m.batch, m.embed.wq, m.embed.scales, m.embed.biases, m.embed.sb,
-                                  m.embed.n, m.embed.k, m.logits, 0));
+                                  m.embed.wt, m.embed.n, m.embed.k, m.logits, 0));
     } else if (fused && seq_tokens == 1) {
         FH_TRY(linear_norm(dev, m, pending, h, nullptr, m.final_norm, m.batch, m.embed, m.logits));
     } else if (fused) {

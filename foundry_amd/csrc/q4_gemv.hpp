@@ -521,6 +521,10 @@ struct GemvArgs {
     // the scales and biases interleaved per group pair (fh_q4_interleave),
     // or null; read by the matrix-core GEMV where it has a form for them
     const uint32_t *sb = nullptr;
+    // the words tiled in the matrix-core GEMV's task order (fh_q4_tile;
+    // [gate; up] weights with the SiLU pairing), or null; read together with
+    // sb by the matrix-core GEMV
+    const uint32_t *wt = nullptr;
 };
 
 template <int M, int L, int CPL, bool FULL, int PRO, int EPI, bool SB>

@@ -22,9 +22,12 @@
 // - Scale and bias load 2*CH groups per instruction; weight loads run two
 //   chunks (CH group pairs each) ahead of the MFMAs, across task boundaries,
 //   with clamped (never guarded) addresses, so every wait counts exactly.
-//   With SB the scales and biases come interleaved per group pair (the two
-//   scale halves, then the two bias halves: fh_q4_interleave's layout), so
-//   one load brings a chunk's scales and biases together (CH <= 2).
+//   With kLaySb the scales and biases come interleaved per group pair (the
+//   two scale halves, then the two bias halves: fh_q4_interleave's layout),
+//   so one load brings a chunk's scales and biases together (CH <= 2). With
+//   kLayTiled the words come from fh_q4_tile's copy, where the 16 rows of a
+//   task's B tile hold each group pair's 64 bytes side by side: a wavefront
+//   load then reads one contiguous KiB instead of 16 rows x 64 bytes.
 // - Every block stages all of x in LDS. Plain x: the prologue loads it in
 //   1 KB runs and permutes it into fragments. With RMSNorm (fh_q4_matmul_
 //   rmsnorm, fh_q4_gate_up_silu) a separate pack kernel normalises x once
@@ -142,14 +145,21 @@ __device__ __forceinline__ uint32_t mf_slot(uint32_t m, uint32_t c) {
 
 // M: x rows (1..8). CH: group pairs per chunk (1, 2 or 4). ksplit:
 // wavefronts per task (divides 16; k / 64 / ksplit is a multiple of 2 * CH).
-// SB: scale and bias are read from sbi (dword 2p of a row: the scales of
+// LAY: operand layouts, a set of the bits below.
+// kLaySb: scale and bias are read from sbi (dword 2p of a row: the scales of
 // groups 2p and 2p + 1, dword 2p + 1: their biases), not scales / biases.
-template <int M, int PRO, int EPI, int CH, bool SB>
+// kLayTiled: the words are read from wt (fh_q4_tile: [task tile][group pair
+// of the whole row][16 B-tile columns][16 words]), not wq.
+constexpr int kLaySb = 1, kLayTiled = 2;
+
+template <int M, int PRO, int EPI, int CH, int LAY>
 __global__ __launch_bounds__(kMfThreads) void q4_gemv_mfma_kernel(
     const uint16_t *__restrict__ x, uint32_t x_ld, const uint32_t *__restrict__ wq,
     const uint16_t *__restrict__ scales, const uint16_t *__restrict__ biases, const uint32_t *__restrict__ sbi,
-    uint32_t n, uint32_t k, void *__restrict__ y, uint32_t y_ld, int y_is_f32, uint32_t ksplit) {
+    const uint32_t *__restrict__ wt, uint32_t n, uint32_t k, void *__restrict__ y, uint32_t y_ld, int y_is_f32,
+    uint32_t ksplit) {
     constexpr bool kPacked = PRO == kProRmsNorm;  // x: mf_pack_kernel's image of RMSNorm(x + res)
+    constexpr bool SB = (LAY & kLaySb) != 0, TILED = (LAY & kLayTiled) != 0;
     static_assert(kMfWaves / 2 * M * 16 <= kMfThreads, "a K-split round stores one output per thread at most");
     static_assert(!SB || CH <= 2, "interleaved scale/bias: one load per chunk of at most 2 pairs");
     extern __shared__ uint4 lds[];
@@ -159,6 +169,8 @@ __global__ __launch_bounds__(kMfThreads) void q4_gemv_mfma_kernel(
     // this range's f32 partial sums at [blockIdx.y][M][y_ld]. A row has
     // sb_ld scales, sb_ld biases, or sb_ld interleaved dwords.
     const uint32_t w_ld = wpr * gridDim.y, sb_ld = G * gridDim.y;
+    // tiled words: group pairs per whole row, and this range's first pair
+    const uint32_t wt_pairs = w_ld / 16, wt_p0 = blockIdx.y * (G / 2);
     if (gridDim.y > 1) {
         x += static_cast<uint64_t>(blockIdx.y) * k;
         wq += static_cast<uint64_t>(blockIdx.y) * wpr;
@@ -209,10 +221,19 @@ __global__ __launch_bounds__(kMfThreads) void q4_gemv_mfma_kernel(
         const bool dead = c >= total || tile >= tiles;
         tile = tile < tiles ? tile : tiles - 1;
         const uint64_t row = wrow(tile);
-        const uint4 *wp = reinterpret_cast<const uint4 *>(wq + row * w_ld + p0 * 16 + quarter * 4);
-        if (dead) wp = reinterpret_cast<const uint4 *>(wq);
+        if constexpr (TILED) {
+            // pair p of tile t: 1 KiB at ((t * pairs + p) * 16) * 16 words, column col at 16 col
+            const uint4 *wp = reinterpret_cast<const uint4 *>(
+                wt + ((static_cast<uint64_t>(tile) * wt_pairs + wt_p0 + p0) * 16 + col) * 16 + quarter * 4);
+            if (dead) wp = reinterpret_cast<const uint4 *>(wt);
 #pragma unroll
-        for (int c2 = 0; c2 < CH; ++c2) cb.w[c2] = wp[c2 * 4];
+            for (int c2 = 0; c2 < CH; ++c2) cb.w[c2] = wp[c2 * 64];
+        } else {
+            const uint4 *wp = reinterpret_cast<const uint4 *>(wq + row * w_ld + p0 * 16 + quarter * 4);
+            if (dead) wp = reinterpret_cast<const uint4 *>(wq);
+#pragma unroll
+            for (int c2 = 0; c2 < CH; ++c2) cb.w[c2] = wp[c2 * 4];
+        }
         const uint16_t *sp = scales + row * sb_ld + p0 * 2, *bp = biases + row * sb_ld + p0 * 2;
         if (dead) sp = scales, bp = biases;
         const uint32_t *ip = dead ? sbi : sbi + row * sb_ld + p0 * 2;
@@ -568,9 +589,9 @@ inline uint32_t pick_mf_split(uint32_t weight_tiles, uint32_t groups, uint32_t c
     return best_s;
 }
 
-template <int M, int PRO, int EPI, int CH, bool SB>
+template <int M, int PRO, int EPI, int CH, int LAY>
 inline void launch_gemv_mfma_t(hipStream_t stream, uint32_t cus, const GemvArgs &a, uint32_t ksplit) {
-    auto kernel = q4_gemv_mfma_kernel<M, PRO, EPI, CH, SB>;
+    auto kernel = q4_gemv_mfma_kernel<M, PRO, EPI, CH, LAY>;
     const uint32_t lds = mf_lds_bytes(M, a.k) + (mf_red_areas(M, a.k) - 1) * kMfRedBytes;
     int per_cu = 0;
     if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, kMfThreads, lds) != hipSuccess || per_cu < 1)
@@ -580,7 +601,28 @@ inline void launch_gemv_mfma_t(hipStream_t stream, uint32_t cus, const GemvArgs 
     const uint32_t ranges = a.kranges > 1 ? a.kranges : 1;
     const uint32_t cap = (cus / ranges > 0 ? cus / ranges : 1) * static_cast<uint32_t>(per_cu);
     hipLaunchKernelGGL(kernel, dim3(need < cap ? need : cap, a.kranges > 1 ? a.kranges : 1), dim3(kMfThreads), lds,
-                       stream, a.x, a.x_ld, a.wq, a.s, a.b, a.sb, a.n, a.k, a.y, a.y_ld, a.y_is_f32, ksplit);
+                       stream, a.x, a.x_ld, a.wq, a.s, a.b, a.sb, a.wt, a.n, a.k, a.y, a.y_ld, a.y_is_f32, ksplit);
+}
+
+// Launches chunk width C with operand layouts `lay` (LAYS: the layouts other
+// than the plain one are built for this prologue / epilogue pair). Four-pair
+// chunks read the separate scale and bias arrays (two loads either way).
+template <int M, int P, int E, int C, bool LAYS>
+inline void launch_gemv_mfma_lay(hipStream_t stream, uint32_t cus, const GemvArgs &a, uint32_t ksplit, int lay) {
+    if constexpr (LAYS) {
+        constexpr int sb = C == 4 ? 0 : kLaySb;
+        if (lay == (kLaySb | kLayTiled)) return launch_gemv_mfma_t<M, P, E, C, sb | kLayTiled>(stream, cus, a, ksplit);
+        if (lay == kLaySb) return launch_gemv_mfma_t<M, P, E, C, sb>(stream, cus, a, ksplit);
+    }
+    launch_gemv_mfma_t<M, P, E, C, 0>(stream, cus, a, ksplit);
+}
+
+template <int M, int P, int E, bool LAYS>
+inline void launch_gemv_mfma_ch(hipStream_t stream, uint32_t cus, const GemvArgs &a, uint32_t ksplit, int ch,
+                                int lay) {
+    if (ch == 4) launch_gemv_mfma_lay<M, P, E, 4, LAYS>(stream, cus, a, ksplit, lay);
+    else if (ch == 2) launch_gemv_mfma_lay<M, P, E, 2, LAYS>(stream, cus, a, ksplit, lay);
+    else launch_gemv_mfma_lay<M, P, E, 1, LAYS>(stream, cus, a, ksplit, lay);
 }
 
 // Whether the matrix-core GEMV takes this launch of 2..8 rows: k a multiple of
@@ -592,7 +634,7 @@ inline bool mf_eligible(uint32_t m, const GemvArgs &a) {
     if (m < 2 || m > 8 || a.k == 0 || a.k % (kGroup * 4) != 0 || a.n == 0 || a.n % 16 != 0 || a.x_ld % 8 != 0)
         return false;
     if ((reinterpret_cast<uintptr_t>(a.wq) | reinterpret_cast<uintptr_t>(a.s) | reinterpret_cast<uintptr_t>(a.b) |
-         reinterpret_cast<uintptr_t>(a.sb)) & 15u)
+         reinterpret_cast<uintptr_t>(a.sb) | reinterpret_cast<uintptr_t>(a.wt)) & 15u)
         return false;
     if (a.pro == kProRmsNorm && a.k > kMfPackMaxK) return false;  // the pack area's row limit
     if (static_cast<uint64_t>(m) * a.y_ld >= (1ull << 31)) return false;  // 32-bit output offsets
@@ -609,6 +651,7 @@ void launch_gemv_mfma_m(hipStream_t stream, uint32_t cus, const GemvArgs &a);
 // pairs per chunk, for the prologue / epilogue pairs of the decoder's GEMVs.
 // At 4 pairs the separate arrays take two loads as well, and two loads from
 // the interleaved table measured slower (config-5 decode 2,611 -> 2,596 tok/s).
+// Tiled words (a.wt) are read at every width.
 template <int M>
 inline void launch_gemv_mfma_dispatch(hipStream_t stream, uint32_t cus, const GemvArgs &a) {
     const uint32_t groups = a.k / kGroup;
@@ -635,26 +678,19 @@ inline void launch_gemv_mfma_dispatch(hipStream_t stream, uint32_t cus, const Ge
             break;
         }
     }
-    const bool sb = a.sb != nullptr;
-#define FH_MF_LAUNCH(P, E, S)                                                                      \
-    do {                                                                                           \
-        if (ch == 4) launch_gemv_mfma_t<M, P, E, 4, false>(stream, cus, a, ksplit);                 \
-        else if (ch == 2 && S && sb) launch_gemv_mfma_t<M, P, E, 2, S>(stream, cus, a, ksplit);      \
-        else if (ch == 2) launch_gemv_mfma_t<M, P, E, 2, false>(stream, cus, a, ksplit);            \
-        else if (S && sb) launch_gemv_mfma_t<M, P, E, 1, S>(stream, cus, a, ksplit);                \
-        else launch_gemv_mfma_t<M, P, E, 1, false>(stream, cus, a, ksplit);                         \
-    } while (0)
-    // (no interleaved form of the SiLU epilogue without RMSNorm: the decoder
-    // does not run it)
+    // operand layouts given: the tiled words only with the interleaved
+    // scales and biases (fh_llama_forward's weights carry both or neither);
+    // no interleaved or tiled form of the SiLU epilogue without RMSNorm (the
+    // decoder does not run it)
+    const int lay = a.sb == nullptr ? 0 : a.wt == nullptr ? kLaySb : kLaySb | kLayTiled;
     if (a.epi == kEpiSiluMul) {
-        if (a.pro == kProRmsNorm) FH_MF_LAUNCH(kProRmsNorm, kEpiSiluMul, true);
-        else FH_MF_LAUNCH(kProNone, kEpiSiluMul, false);
+        if (a.pro == kProRmsNorm) launch_gemv_mfma_ch<M, kProRmsNorm, kEpiSiluMul, true>(stream, cus, a, ksplit, ch, lay);
+        else launch_gemv_mfma_ch<M, kProNone, kEpiSiluMul, false>(stream, cus, a, ksplit, ch, 0);
     } else if (a.pro == kProRmsNorm) {
-        FH_MF_LAUNCH(kProRmsNorm, kEpiNone, true);
+        launch_gemv_mfma_ch<M, kProRmsNorm, kEpiNone, true>(stream, cus, a, ksplit, ch, lay);
     } else {
-        FH_MF_LAUNCH(kProNone, kEpiNone, true);
+        launch_gemv_mfma_ch<M, kProNone, kEpiNone, true>(stream, cus, a, ksplit, ch, lay);
     }
-#undef FH_MF_LAUNCH
 }
 
 }  // namespace fh

@@ -146,16 +146,17 @@ int launch_gemv_rows(fh_device *dev, const char *fn, int64_t m, const GemvArgs &
 // m outside 2..8, the down projection not split into K ranges, or the next
 // GEMV not taking all m rows from one image.
 int q4_down_pack(fh_device *dev, const char *fn, const uint16_t *x, int64_t m, int64_t x_ld, const uint32_t *wq,
-                 const uint16_t *scales, const uint16_t *biases, const uint32_t *sb, int64_t n, int64_t k,
-                 const uint16_t *res, uint16_t *res_out, const uint16_t *norm_weight, float eps,
+                 const uint16_t *scales, const uint16_t *biases, const uint32_t *sb, const uint32_t *wt, int64_t n,
+                 int64_t k, const uint16_t *res, uint16_t *res_out, const uint16_t *norm_weight, float eps,
                  const uint32_t *next_wq, const uint16_t *next_scales, const uint16_t *next_biases,
-                 const uint32_t *next_sb, int64_t next_n, bool *packed) {
+                 const uint32_t *next_sb, const uint32_t *next_wt, int64_t next_n, bool *packed) {
     *packed = false;
     if (m < 2 || m > 8 || k <= 0 || n <= 0 || n > kMfPackMaxK || x_ld > 0x7FFFFFFFll) return FH_OK;
     GemvArgs down{x, static_cast<uint32_t>(x_ld), wq, scales, biases, static_cast<uint32_t>(n),
                   static_cast<uint32_t>(k), nullptr, static_cast<uint32_t>(n), 1, kProNone, kEpiNone,
                   GemvFusion{}};
     down.sb = sb;
+    down.wt = wt;
     if (!mf_eligible(static_cast<uint32_t>(m), down) || mf_rows_per_launch(down.k) >= m) return FH_OK;
     const uint32_t ranges = mf_k_ranges(dev, m, down);
     if (ranges == 0) return FH_OK;
@@ -163,6 +164,7 @@ int q4_down_pack(fh_device *dev, const char *fn, const uint16_t *x, int64_t m, i
                   static_cast<uint32_t>(n), nullptr, static_cast<uint32_t>(next_n), 0, kProRmsNorm, kEpiNone,
                   GemvFusion{}};
     next.sb = next_sb;
+    next.wt = next_wt;
     if (!mf_eligible(static_cast<uint32_t>(m), next) || mf_rows_per_launch(next.k) < m) return FH_OK;
     for (const void *p : {static_cast<const void *>(x), static_cast<const void *>(res),
                           static_cast<const void *>(res_out), static_cast<const void *>(norm_weight)})
@@ -198,11 +200,13 @@ int q4_down_pack(fh_device *dev, const char *fn, const uint16_t *x, int64_t m, i
 // The RMSNorm'd GEMV of m rows on the image q4_down_pack left in the pack
 // area (weight [n, k], k the image's row length).
 int q4_gemv_packed(fh_device *dev, const char *fn, int64_t m, const uint32_t *wq, const uint16_t *scales,
-                   const uint16_t *biases, const uint32_t *sb, int64_t n, int64_t k, void *y, int y_is_f32) {
+                   const uint16_t *biases, const uint32_t *sb, const uint32_t *wt, int64_t n, int64_t k, void *y,
+                   int y_is_f32) {
     GemvArgs a{static_cast<const uint16_t *>(dev->pack_area), static_cast<uint32_t>(k), wq, scales, biases,
                static_cast<uint32_t>(n), static_cast<uint32_t>(k), y, static_cast<uint32_t>(n), y_is_f32,
                kProRmsNorm, kEpiNone, GemvFusion{}};
     a.sb = sb;
+    a.wt = wt;
     if (int rc = check_range(dev, y, static_cast<uint64_t>(m) * n * (y_is_f32 ? 4 : 2), fn, "y")) return rc;
     return dispatch(dev, fn, [&] { launch_q4_gemv_mfma(dev->stream, dev->compute_units, static_cast<int>(m), a); });
 }
@@ -218,14 +222,30 @@ int check_sb(fh_device *dev, const char *fn, const uint32_t *sb, int64_t n, int6
     return check_range(dev, sb, static_cast<uint64_t>(n) * (k / kGroup) * 4, fn, "interleaved scale/bias");
 }
 
-// fh_q4_matmul with the weight's optional interleaved scale/bias table.
+// The tiled words of an n x k weight (fh_q4_tile): null, or 16-byte aligned
+// n * k / 8 words, n a multiple of 16 and k of 128; only with an
+// interleaved scale/bias table.
+int check_wt(fh_device *dev, const char *fn, const uint32_t *wt, const uint32_t *sb, int64_t n, int64_t k) {
+    if (wt == nullptr) return FH_OK;
+    if (sb == nullptr)
+        return fail(FH_ERR_INVALID_ARGUMENT, "%s: tiled words need the interleaved scale/bias table too", fn);
+    if (n % 16 != 0 || k % (2 * kGroup) != 0 || reinterpret_cast<uintptr_t>(wt) % 16 != 0)
+        return fail(FH_ERR_INVALID_ARGUMENT,
+                    "%s: tiled words need n %% 16 == 0 (n=%lld), k %% 128 == 0 (k=%lld) and 16-byte alignment", fn,
+                    (long long)n, (long long)k);
+    return check_range(dev, wt, static_cast<uint64_t>(n) * (k / 8) * 4, fn, "tiled words");
+}
+
+// fh_q4_matmul with the weight's optional interleaved scale/bias table and
+// tiled words (the words in plain row order).
 int q4_matmul(fh_device *dev, const uint16_t *x, int64_t m, int64_t k, int64_t x_ld, const uint32_t *wq,
-              const uint16_t *scales, const uint16_t *biases, const uint32_t *sb, int64_t n, int64_t group, void *y,
-              int y_dtype) {
+              const uint16_t *scales, const uint16_t *biases, const uint32_t *sb, const uint32_t *wt, int64_t n,
+              int64_t group, void *y, int y_dtype) {
     const char *fn = "fh_q4_matmul";
     if (int rc = check_usable(dev, fn)) return rc;
     if (int rc = check_q4_table(dev, fn, wq, scales, biases, n, k, group)) return rc;
     if (int rc = check_sb(dev, fn, sb, n, k)) return rc;
+    if (int rc = check_wt(dev, fn, wt, sb, n, k)) return rc;
     if (m < 0) return fail(FH_ERR_INVALID_ARGUMENT, "%s: m=%lld", fn, (long long)m);
     if (m > 65535ll * 128) return fail(FH_ERR_INDEX_TOO_LARGE, "%s: m > 65535*128 rows", fn);
     if (y_dtype != FH_BF16 && y_dtype != FH_F32)
@@ -257,6 +277,7 @@ int q4_matmul(fh_device *dev, const uint16_t *x, int64_t m, int64_t k, int64_t x
                         (long long)k);
         GemvArgs a{x, ld32, wq, scales, biases, n32, k32, y, n32, y_is_f32, kProNone, kEpiNone, GemvFusion{}};
         a.sb = sb;
+        a.wt = wt;
         return launch_gemv_rows(dev, fn, m, a, n);
     }
     return dispatch(dev, fn, [&] {
@@ -273,7 +294,7 @@ extern "C" int fh_q4_matmul(fh_device *dev, const uint16_t *x, int64_t m, int64_
                             int64_t x_ld, const uint32_t *wq, const uint16_t *scales,
                             const uint16_t *biases, int64_t n, int64_t group, void *y,
                             int y_dtype) {
-    return q4_matmul(dev, x, m, k, x_ld, wq, scales, biases, nullptr, n, group, y, y_dtype);
+    return q4_matmul(dev, x, m, k, x_ld, wq, scales, biases, nullptr, nullptr, n, group, y, y_dtype);
 }
 
 namespace {
@@ -341,14 +362,16 @@ int check_norm_operands(fh_device *dev, const char *fn, const uint16_t *x, const
 
 namespace fh {
 
-// fh_q4_matmul_rmsnorm with the weight's optional interleaved scale/bias table.
+// fh_q4_matmul_rmsnorm with the weight's optional interleaved scale/bias
+// table and tiled words (plain row order).
 int q4_matmul_rmsnorm(fh_device *dev, const uint16_t *x, const uint16_t *residual, uint16_t *residual_out,
                       const uint16_t *norm_weight, float eps, int64_t m, int64_t k, const uint32_t *wq,
-                      const uint16_t *scales, const uint16_t *biases, const uint32_t *sb, int64_t n, int64_t group,
-                      void *y, int y_dtype) {
+                      const uint16_t *scales, const uint16_t *biases, const uint32_t *sb, const uint32_t *wt,
+                      int64_t n, int64_t group, void *y, int y_dtype) {
     const char *fn = "fh_q4_matmul_rmsnorm";
     if (int rc = check_fused(dev, fn, m, k, wq, scales, biases, n, group, y, y_dtype, n, true)) return rc;
     if (int rc = check_sb(dev, fn, sb, n, k)) return rc;
+    if (int rc = check_wt(dev, fn, wt, sb, n, k)) return rc;
     if (!norm_weight) return fail(FH_ERR_INVALID_ARGUMENT, "%s: null norm weight", fn);
     if (int rc = check_norm_operands(dev, fn, x, residual, residual_out, norm_weight, m, k)) return rc;
     if (m == 0 || n == 0) return FH_OK;
@@ -359,19 +382,25 @@ int q4_matmul_rmsnorm(fh_device *dev, const uint16_t *x, const uint16_t *residua
     GemvArgs a{x, k32, wq, scales, biases, n32, k32, y, n32, y_dtype == FH_F32, kProRmsNorm, kEpiNone,
                GemvFusion{residual, residual_out, norm_weight, eps, 1.0f / static_cast<float>(k)}};
     a.sb = sb;
+    a.wt = wt;
     return launch_gemv_rows(dev, fn, m, a, n);
 }
 
-// fh_q4_gate_up_silu with the weight's optional interleaved scale/bias table.
+// fh_q4_gate_up_silu with the weight's optional interleaved scale/bias table
+// and tiled words (in the SiLU pairing: fh_q4_tile with silu_pairs = 1).
 int q4_gate_up_silu(fh_device *dev, const uint16_t *x, const uint16_t *residual, uint16_t *residual_out,
                     const uint16_t *norm_weight, float eps, int64_t m, int64_t k, const uint32_t *wq,
-                    const uint16_t *scales, const uint16_t *biases, const uint32_t *sb, int64_t n, int64_t group,
-                    uint16_t *act) {
+                    const uint16_t *scales, const uint16_t *biases, const uint32_t *sb, const uint32_t *wt,
+                    int64_t n, int64_t group, uint16_t *act) {
     const char *fn = "fh_q4_gate_up_silu";
     if (n % 2 != 0) return fail(FH_ERR_INVALID_ARGUMENT, "%s: n=%lld is not [gate; up] rows", fn, (long long)n);
     const bool norm = norm_weight != nullptr;
     if (int rc = check_fused(dev, fn, m, k, wq, scales, biases, n, group, act, FH_BF16, n / 2, norm)) return rc;
     if (int rc = check_sb(dev, fn, sb, n, k)) return rc;
+    if (int rc = check_wt(dev, fn, wt, sb, n, k)) return rc;
+    if (wt != nullptr && n % 32 != 0)
+        return fail(FH_ERR_INVALID_ARGUMENT, "%s: tiled [gate; up] words need n %% 32 == 0 (n=%lld)", fn,
+                    (long long)n);
     if (int rc = check_norm_operands(dev, fn, x, residual, residual_out, norm_weight, m, k)) return rc;
     if (m == 0 || n == 0) return FH_OK;
     if (int rc = set_current(dev, fn)) return rc;
@@ -381,7 +410,26 @@ int q4_gate_up_silu(fh_device *dev, const uint16_t *x, const uint16_t *residual,
     GemvArgs a{x, k32, wq, scales, biases, n32, k32, act, n32 / 2, 0, norm ? kProRmsNorm : kProNone,
                kEpiSiluMul, GemvFusion{residual, residual_out, norm_weight, eps, 1.0f / static_cast<float>(k)}};
     a.sb = sb;
+    a.wt = wt;
     return launch_gemv_rows(dev, fn, m, a, n / 2);
+}
+
+// Tiled words: uint4 d of wt is words 4 (d % 4) .. + 3 of group pair p of
+// weight row r, for d = ((t * pairs + p) * 16 + c) * 4 + d % 4 and r the
+// row of column c in task tile t (c < 8 with the SiLU pairing: gate row
+// 8 t + c, else up row n / 2 + 8 t + c - 8; plain: 16 t + c).
+__global__ __launch_bounds__(256) void q4_tile_kernel(const uint4 *__restrict__ wq, uint32_t n, uint32_t pairs,
+                                                      int silu_pairs, uint4 *__restrict__ wt) {
+    const uint64_t total = static_cast<uint64_t>(n) * pairs * 4;
+    for (uint64_t d = static_cast<uint64_t>(blockIdx.x) * 256 + threadIdx.x; d < total;
+         d += static_cast<uint64_t>(gridDim.x) * 256) {
+        const uint32_t q = d % 4, c = (d / 4) % 16;
+        const uint64_t tp = d / 64;
+        const uint32_t p = tp % pairs;
+        const uint32_t t = static_cast<uint32_t>(tp / pairs);
+        const uint32_t r = silu_pairs ? (c < 8 ? 8 * t + c : n / 2 + 8 * t + c - 8) : 16 * t + c;
+        wt[d] = wq[(static_cast<uint64_t>(r) * pairs + p) * 4 + q];
+    }
 }
 
 // Writes sb[r][2p] = the scales of groups 2p, 2p + 1 of row r (low half:
@@ -401,16 +449,16 @@ extern "C" int fh_q4_matmul_rmsnorm(fh_device *dev, const uint16_t *x, const uin
                                     uint16_t *residual_out, const uint16_t *norm_weight, float eps, int64_t m,
                                     int64_t k, const uint32_t *wq, const uint16_t *scales,
                                     const uint16_t *biases, int64_t n, int64_t group, void *y, int y_dtype) {
-    return q4_matmul_rmsnorm(dev, x, residual, residual_out, norm_weight, eps, m, k, wq, scales, biases, nullptr, n,
-                             group, y, y_dtype);
+    return q4_matmul_rmsnorm(dev, x, residual, residual_out, norm_weight, eps, m, k, wq, scales, biases, nullptr,
+                             nullptr, n, group, y, y_dtype);
 }
 
 extern "C" int fh_q4_gate_up_silu(fh_device *dev, const uint16_t *x, const uint16_t *residual,
                                   uint16_t *residual_out, const uint16_t *norm_weight, float eps, int64_t m,
                                   int64_t k, const uint32_t *wq, const uint16_t *scales, const uint16_t *biases,
                                   int64_t n, int64_t group, uint16_t *act) {
-    return q4_gate_up_silu(dev, x, residual, residual_out, norm_weight, eps, m, k, wq, scales, biases, nullptr, n,
-                           group, act);
+    return q4_gate_up_silu(dev, x, residual, residual_out, norm_weight, eps, m, k, wq, scales, biases, nullptr,
+                           nullptr, n, group, act);
 }
 
 extern "C" int fh_q4_interleave(fh_device *dev, const uint16_t *scales, const uint16_t *biases, int64_t n,
@@ -437,5 +485,33 @@ extern "C" int fh_q4_interleave(fh_device *dev, const uint16_t *scales, const ui
         hipLaunchKernelGGL(q4_interleave_kernel, dim3(blocks < 65536 ? blocks : 65536), dim3(256), 0, dev->stream,
                            reinterpret_cast<const uint32_t *>(scales), reinterpret_cast<const uint32_t *>(biases),
                            pairs, reinterpret_cast<uint2 *>(sb));
+    });
+}
+
+extern "C" int fh_q4_tile(fh_device *dev, const uint32_t *wq, int64_t n, int64_t k, int64_t group, int silu_pairs,
+                          uint32_t *wt) {
+    const char *fn = "fh_q4_tile";
+    if (int rc = check_usable(dev, fn)) return rc;
+    if (n < 0 || k < 0)
+        return fail(FH_ERR_INVALID_ARGUMENT, "%s: negative shape n=%lld k=%lld", fn, (long long)n, (long long)k);
+    if (group != kGroup)
+        return fail(FH_ERR_UNSUPPORTED, "%s: group %lld; the kernels implement group 64", fn, (long long)group);
+    if (n % (silu_pairs ? 32 : 16) != 0 || k % (2 * kGroup) != 0)
+        return fail(FH_ERR_INVALID_ARGUMENT, "%s: n=%lld must be a multiple of %d and k=%lld of 128", fn, (long long)n,
+                    silu_pairs ? 32 : 16, (long long)k);
+    if (n > 0x7FFFFFFFll || k > 0x7FFFFFFFll) return fail(FH_ERR_INDEX_TOO_LARGE, "%s: n or k exceeds 2^31-1", fn);
+    if ((reinterpret_cast<uintptr_t>(wq) | reinterpret_cast<uintptr_t>(wt)) % 16 != 0)
+        return fail(FH_ERR_INVALID_ARGUMENT, "%s: wq and wt must be 16-byte aligned", fn);
+    const uint64_t bytes = static_cast<uint64_t>(n) * (k / 8) * 4;
+    if (bytes == 0) return FH_OK;
+    if (int rc = check_range(dev, wq, bytes, fn, "wq")) return rc;
+    if (int rc = check_range(dev, wt, bytes, fn, "wt")) return rc;
+    if (overlaps(wq, bytes, wt, bytes)) return fail(FH_ERR_INVALID_ARGUMENT, "%s: wt overlaps wq", fn);
+    if (int rc = set_current(dev, fn)) return rc;
+    const uint64_t blocks = (bytes / 16 + 255) / 256;
+    return dispatch(dev, fn, [&] {
+        hipLaunchKernelGGL(q4_tile_kernel, dim3(blocks < 65536 ? blocks : 65536), dim3(256), 0, dev->stream,
+                           reinterpret_cast<const uint4 *>(wq), static_cast<uint32_t>(n),
+                           static_cast<uint32_t>(k / kGroup / 2), silu_pairs, reinterpret_cast<uint4 *>(wt));
     });
 }

@@ -196,20 +196,27 @@ def rope_tables(cfg: LlamaConfig, length: int):
 
 
 class _Q4:
-    """A q4 weight triplet on the device, and with ``interleave`` (k a
-    multiple of 128) fh_q4_interleave's copy of its scales and biases, which
-    the batched decode GEMVs read instead (same values, one load per chunk)."""
+    """A q4 weight triplet on the device. With ``interleave`` (k a multiple
+    of 128) also fh_q4_interleave's copy of its scales and biases, and with
+    ``tile`` (n a multiple of 16, 32 for ``silu_pairs``) fh_q4_tile's copy of
+    its words, both read by the batched decode GEMVs instead of the triplet
+    (the same values: results do not change)."""
 
-    def __init__(self, dev: HipDevice, wq: np.ndarray, s: np.ndarray, b: np.ndarray, interleave: bool = True):
+    def __init__(self, dev: HipDevice, wq: np.ndarray, s: np.ndarray, b: np.ndarray, interleave: bool = True,
+                 tile: bool = False, silu_pairs: bool = False):
         self.n, self.k = wq.shape[0], wq.shape[1] * 8
         self.wq = dev.storage_from_bytes(np.ascontiguousarray(wq).tobytes())
         self.s = dev.storage_from_bytes(np.ascontiguousarray(s).tobytes())
         self.b = dev.storage_from_bytes(np.ascontiguousarray(b).tobytes())
-        self.sb = None
+        self.sb = self.wt = None
         if interleave and self.k % (2 * GROUP) == 0 and self.n > 0:
             self.sb = dev.empty(self.n * (self.k // GROUP) * 4)
             _lib.call("fh_q4_interleave", dev.handle, ctypes.c_void_p(self.s.ptr), ctypes.c_void_p(self.b.ptr),
                       self.n, self.k, GROUP, ctypes.c_void_p(self.sb.ptr))
+            if tile and self.n % (32 if silu_pairs else 16) == 0:
+                self.wt = dev.empty(self.n * self.k // 2)
+                _lib.call("fh_q4_tile", dev.handle, ctypes.c_void_p(self.wq.ptr), self.n, self.k, GROUP,
+                          int(silu_pairs), ctypes.c_void_p(self.wt.ptr))
 
 
 def layer_weights(cfg: LlamaConfig, seed: int, layer: int, centre: float = 8.0):
@@ -269,8 +276,10 @@ class Q4Llama:
         see layer_weights), or read from `weights` (a
         foundry_amd.weights.Weights of q4 triplets; see from_checkpoint).
         `interleave`: also keep each weight's scales and biases interleaved
-        (fh_q4_interleave, 1/8 more weight memory) for the batched decode
-        GEMVs; the results are the same either way."""
+        (fh_q4_interleave, 1/8 more weight memory) and, for batch 2..8, its
+        words tiled in the batched GEMV's task order (fh_q4_tile, twice the
+        weight memory) for the batched decode GEMVs; the results are the same
+        either way."""
         self.dev, self.cfg, self.max_len = dev, cfg, max_len
         if max_len > cfg.max_position_embeddings:
             raise ValueError("max_len exceeds max_position_embeddings")
@@ -288,14 +297,16 @@ class Q4Llama:
             src_embed, src_layer, src_norm = (lambda: embed_weights(cfg, seed, centre),
                                               lambda l: layer_weights(cfg, seed, l, centre),
                                               lambda: final_norm_weight(cfg, seed))
-        self.embed = _Q4(dev, *src_embed(), interleave=interleave)
+        tile = interleave and 2 <= self.batch <= 8  # the batched GEMVs read tiled words
+        self.embed = _Q4(dev, *src_embed(), interleave=interleave, tile=tile)
         self.layers = []
         for layer in range(cfg.n_layers):
             w = src_layer(layer)
             self.layers.append({
-                "qkv": _Q4(dev, *w["qkv"], interleave=interleave), "o": _Q4(dev, *w["o"], interleave=interleave),
-                "gate_up": _Q4(dev, *w["gate_up"], interleave=interleave),
-                "down": _Q4(dev, *w["down"], interleave=interleave),
+                "qkv": _Q4(dev, *w["qkv"], interleave=interleave, tile=tile),
+                "o": _Q4(dev, *w["o"], interleave=interleave, tile=tile),
+                "gate_up": _Q4(dev, *w["gate_up"], interleave=interleave, tile=tile, silu_pairs=True),
+                "down": _Q4(dev, *w["down"], interleave=interleave, tile=tile),
                 "input_norm": dev.storage_from_bytes(w["input_norm"].tobytes()),
                 "post_norm": dev.storage_from_bytes(w["post_norm"].tobytes()),
                 "k_cache": dev.zeros(self.batch * self.seq_bytes),
@@ -338,7 +349,8 @@ class Q4Llama:
         c, b = self.cfg, self.buf
 
         def q4(w: _Q4) -> _lib.Q4Weight:
-            return _lib.Q4Weight(w.wq.ptr, w.s.ptr, w.b.ptr, w.n, w.k, w.sb.ptr if w.sb is not None else None)
+            return _lib.Q4Weight(w.wq.ptr, w.s.ptr, w.b.ptr, w.n, w.k, w.sb.ptr if w.sb is not None else None,
+                                 w.wt.ptr if w.wt is not None else None)
 
         self._layer_table = (_lib.LlamaLayer * len(self.layers))(*[
             _lib.LlamaLayer(q4(L["qkv"]), q4(L["o"]), q4(L["gate_up"]), q4(L["down"]), L["input_norm"].ptr,

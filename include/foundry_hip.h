@@ -425,6 +425,22 @@ int fh_q4_gate_up_silu(fh_device *dev, const uint16_t *x, const uint16_t *residu
 int fh_q4_interleave(fh_device *dev, const uint16_t *scales, const uint16_t *biases, int64_t n,
                      int64_t k, int64_t group, uint32_t *sb);
 
+/* A load-time copy of a q4 weight's packed words in the batched decode
+ * GEMV's task order: wt (u32, n * k / 8 words, 16-byte aligned) holds, for
+ * task tile t, group pair p and column c < 16, the 16 words of pair p of
+ * weight row r(t, c) at words ((t * k / 128 + p) * 16 + c) * 16. r(t, c) =
+ * 16 t + c, or with silu_pairs (a [gate; up] weight of n = 2f rows) the gate
+ * row 8 t + c for c < 8 and the up row f + 8 t + c - 8. fh_q4_weight.wt
+ * takes it (silu_pairs = 1 for the gate/up weight, 0 for the others); the
+ * 2..8-row GEMVs of fh_llama_forward then read one contiguous KiB per
+ * wavefront load instead of 16 rows x 64 bytes (the same values: results
+ * are unchanged). No counterpart in the reference (its Linear reads the
+ * packed tensor as stored, src/nn/linear.rs:22-35); a data layout of this
+ * library's decoder. group = 64; n a multiple of 16 (32 with silu_pairs),
+ * k of 128; wt must not overlap wq. */
+int fh_q4_tile(fh_device *dev, const uint32_t *wq, int64_t n, int64_t k, int64_t group, int silu_pairs,
+               uint32_t *wt);
+
 /* LlamaMlp's act_fn(gate) * up (src/models/llama/mlp.rs:49-58, Silu at
  * src/nn/activation.rs:19-28): gate_up row = [gate (f) | up (f)],
  * out = RNE(RNE(g / (1 + exp(-g))) * u), out: [rows, f]. */
@@ -454,7 +470,10 @@ int fh_advance_positions(fh_device *dev, uint32_t *positions, int64_t n, int64_t
 
 /* A q4 weight: n rows of k columns (group 64), as fh_q4_matmul takes it.
  * sb: null, or fh_q4_interleave's copy of scales / biases, which the
- * batched decode GEMVs (2..8 rows) then read instead. */
+ * batched decode GEMVs (2..8 rows) then read instead. wt: null, or (with sb)
+ * fh_q4_tile's copy of the words, built with silu_pairs = 1 for gate_up and
+ * 0 for the other weights, which the batched decode GEMVs read instead of
+ * wq. */
 typedef struct fh_q4_weight {
     const uint32_t *wq;
     const uint16_t *scales;
@@ -462,6 +481,7 @@ typedef struct fh_q4_weight {
     int64_t n;
     int64_t k;
     const uint32_t *sb;
+    const uint32_t *wt;
 } fh_q4_weight;
 
 /* One decoder layer (LlamaDecoderLayer, src/models/llama/model.rs:47, :254-280):

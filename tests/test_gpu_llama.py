@@ -591,6 +591,28 @@ def test_q4_interleave_layout(device):
                   ctypes.c_void_p(sb.ptr + 16))
 
 
+@pytest.mark.parametrize("n,k,silu", [(48, 256, False), (64, 384, True)])
+def test_q4_tile_layout(device, n, k, silu):
+    """fh_q4_tile: words ((t * k/128 + p) * 16 + c) * 16 .. + 15 are the 16
+    words of group pair p of row r(t, c) (16 t + c, or with the SiLU pairing
+    gate row 8 t + c / up row n/2 + 8 t + c - 8); shapes it cannot lay out
+    are rejected."""
+    rng = np.random.default_rng(n + k)
+    wq = rng.integers(0, 2**32, (n, k // 8), dtype=np.uint32)
+    src, wt = up(device, wq), device.empty(n * k // 2)
+    _lib.call("fh_q4_tile", device.handle, ctypes.c_void_p(src.ptr), n, k, 64, int(silu), ctypes.c_void_p(wt.ptr))
+    got = down(device, wt, np.uint32, n * k // 8).reshape(n // 16, k // 128, 16, 16)
+    c = np.arange(16)
+    for t in range(n // 16):
+        rows = np.where(c < 8, 8 * t + c, n // 2 + 8 * t + c - 8) if silu else 16 * t + c
+        want = wq[rows].reshape(16, k // 128, 16).transpose(1, 0, 2)
+        assert np.array_equal(got[t], want), f"tile {t}"
+    with pytest.raises(_lib.HipError, match="multiple of 32"):
+        _lib.call("fh_q4_tile", device.handle, ctypes.c_void_p(src.ptr), 48, k, 64, 1, ctypes.c_void_p(wt.ptr))
+    with pytest.raises(_lib.HipError, match="overlaps"):
+        _lib.call("fh_q4_tile", device.handle, ctypes.c_void_p(src.ptr), n, k, 64, 0, ctypes.c_void_p(src.ptr))
+
+
 # 8B-shaped layers: at 2..8 rows the q/k/v and gate/up GEMVs read two group
 # pairs per chunk, o one, the down projection runs over K ranges into the
 # next layer's RMSNorm image
@@ -603,14 +625,15 @@ C4ISH = LlamaConfig(n_layers=1, hidden=3072, n_heads=24, n_kv_heads=8, head_dim=
 @pytest.mark.parametrize("cfg,batch", [(TINY, 2), (TINY, 5), (WIDE, 3), (WIDE, 8), (WIDE, 1), (C4ISH, 1)])
 def test_interleaved_scale_bias_tables_change_no_result(device, cfg, batch):
     """Decode steps of `batch` sequences with the interleaved scale/bias
-    tables (fh_q4_interleave, read by the batched GEMVs) and without give
-    bit-identical logits and ids: the tables only change how the kernels
-    load the same values."""
+    tables (fh_q4_interleave) and, at batch 2..8, the tiled words (fh_q4_tile)
+    read by the batched GEMVs, and without them, give bit-identical logits
+    and ids: the copies only change how the kernels load the same values."""
     ids = synth.token_ids(5, batch * 3, cfg.vocab).reshape(batch, 3).astype(np.uint32)
     out = []
     for interleave in (True, False):
         model = Q4Llama(device, cfg, 2, 16, max_tokens=1, batch=batch, interleave=interleave)
         assert (model.layers[0]["qkv"].sb is not None) == interleave
+        assert (model.layers[0]["gate_up"].wt is not None) == (interleave and batch > 1)
         got = []
         for pos in range(3):
             model.step(ids[:, pos:pos + 1], pos)
@@ -624,7 +647,8 @@ def test_interleaved_scale_bias_tables_change_no_result(device, cfg, batch):
 
 
 def test_llama_forward_checks_the_interleaved_tables(device):
-    """A misaligned or short interleaved table is rejected before any work."""
+    """A misaligned or short interleaved table or tiled word copy, and tiled
+    words without the interleaved table, are rejected before any work."""
     model = Q4Llama(device, TINY, 1, 16, max_tokens=4, batch=2)
     b = model.buf
     sb = model._layer_table[1].gate_up.sb
@@ -635,6 +659,15 @@ def test_llama_forward_checks_the_interleaved_tables(device):
     with pytest.raises(_lib.HipError, match="interleaved scale/bias"):
         model._forward(1, b["ids"], b["positions"])
     model._layer_table[1].gate_up.sb = sb
+    wt = model._layer_table[1].o.wt
+    model._layer_table[1].o.sb = None
+    with pytest.raises(_lib.HipError, match="need the interleaved"):
+        model._forward(1, b["ids"], b["positions"])
+    model._layer_table[1].o.sb = model.layers[1]["o"].sb.ptr
+    model._layer_table[1].o.wt = wt + 16
+    with pytest.raises(_lib.HipError, match="tiled words"):
+        model._forward(1, b["ids"], b["positions"])
+    model._layer_table[1].o.wt = wt
     model.step(np.ones((2, 1), np.uint32), 0)
 
 
