@@ -647,11 +647,13 @@ void launch_gemv_mfma_m(hipStream_t stream, uint32_t cus, const GemvArgs &a);
 
 // Chunk width: 4 group pairs when each wavefront's slice allows it (one
 // 16-byte scale and one bias load per 8 groups), else 2, else 1, at most
-// half the slice. Interleaved scales and biases (a.sb) are read at 2 and 1
-// pairs per chunk, for the prologue / epilogue pairs of the decoder's GEMVs.
-// At 4 pairs the separate arrays take two loads as well, and two loads from
-// the interleaved table measured slower (config-5 decode 2,611 -> 2,596 tok/s).
-// Tiled words (a.wt) are read at every width.
+// half the slice. With interleaved scales and biases (a.sb) the widest is 2
+// pairs, read with one load per chunk: at 4 pairs the separate arrays take
+// two loads, and two loads from the interleaved table measured slower (config-5
+// decode 2,611 -> 2,596 tok/s), while 2 pairs from the table instead of 4
+// from the arrays took the down projection 12.9 -> 11.5-12.0 us and the LM
+// head 65.3 -> 63.7 us (same outputs). Tiled words (a.wt) are read at every
+// width.
 template <int M>
 inline void launch_gemv_mfma_dispatch(hipStream_t stream, uint32_t cus, const GemvArgs &a) {
     const uint32_t groups = a.k / kGroup;
@@ -670,7 +672,7 @@ inline void launch_gemv_mfma_dispatch(hipStream_t stream, uint32_t cus, const Ge
     const uint32_t blocks = need < cap ? need : cap;
     const uint32_t rounds = (task_tiles + blocks * slots - 1) / (blocks * slots);
     int ch = 1;
-    for (const int c : {4, 2, 1}) {
+    for (const int c : {a.sb != nullptr ? 2 : 4, 2, 1}) {
         if (gs % (2 * c) != 0) continue;
         const uint32_t total = rounds * (gs / (2 * c));
         if (total % 2 == 0 || total >= 5) {
