@@ -606,13 +606,13 @@ inline void launch_gemv_mfma_t(hipStream_t stream, uint32_t cus, const GemvArgs 
 
 // Launches chunk width C with operand layouts `lay` (LAYS: the layouts other
 // than the plain one are built for this prologue / epilogue pair). Four-pair
-// chunks read the separate scale and bias arrays (two loads either way).
+// chunks only run without the interleaved table (the dispatcher takes two
+// pairs when it is given), so they read the plain layout.
 template <int M, int P, int E, int C, bool LAYS>
 inline void launch_gemv_mfma_lay(hipStream_t stream, uint32_t cus, const GemvArgs &a, uint32_t ksplit, int lay) {
-    if constexpr (LAYS) {
-        constexpr int sb = C == 4 ? 0 : kLaySb;
-        if (lay == (kLaySb | kLayTiled)) return launch_gemv_mfma_t<M, P, E, C, sb | kLayTiled>(stream, cus, a, ksplit);
-        if (lay == kLaySb) return launch_gemv_mfma_t<M, P, E, C, sb>(stream, cus, a, ksplit);
+    if constexpr (LAYS && C <= 2) {
+        if (lay == (kLaySb | kLayTiled)) return launch_gemv_mfma_t<M, P, E, C, kLaySb | kLayTiled>(stream, cus, a, ksplit);
+        if (lay == kLaySb) return launch_gemv_mfma_t<M, P, E, C, kLaySb>(stream, cus, a, ksplit);
     }
     launch_gemv_mfma_t<M, P, E, C, 0>(stream, cus, a, ksplit);
 }
@@ -652,8 +652,8 @@ void launch_gemv_mfma_m(hipStream_t stream, uint32_t cus, const GemvArgs &a);
 // two loads, and two loads from the interleaved table measured slower (config-5
 // decode 2,611 -> 2,596 tok/s), while 2 pairs from the table instead of 4
 // from the arrays took the down projection 12.9 -> 11.5-12.0 us and the LM
-// head 65.3 -> 63.7 us (same outputs). Tiled words (a.wt) are read at every
-// width.
+// head 65.3 -> 63.7 us (same outputs). Tiled words (a.wt) come with the
+// table, so they are read at 2 and 1 pairs per chunk.
 template <int M>
 inline void launch_gemv_mfma_dispatch(hipStream_t stream, uint32_t cus, const GemvArgs &a) {
     const uint32_t groups = a.k / kGroup;
