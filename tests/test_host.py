@@ -158,6 +158,11 @@ def test_calls_without_a_device_return_errors_not_crashes():
     assert "fh_device_create" in _lib.last_error()
     assert lib.fh_synchronize(None) == _lib.ERR_INVALID_ARGUMENT
     assert lib.fh_q4_matmul(None, None, 1, 64, 64, None, None, None, 1, 64, None, 1) == _lib.ERR_INVALID_ARGUMENT
+    # the load-time weight copies of the decoder
+    assert lib.fh_q4_interleave(None, None, None, 16, 128, 64, None) == _lib.ERR_INVALID_ARGUMENT
+    assert "fh_q4_interleave" in _lib.last_error()
+    assert lib.fh_q4_tile(None, None, 16, 128, 64, 0, None) == _lib.ERR_INVALID_ARGUMENT
+    assert "fh_q4_tile" in _lib.last_error()
     assert lib.fh_device_destroy(None) == _lib.OK
     n = ctypes.c_int(-1)
     assert lib.fh_device_count(ctypes.byref(n)) == _lib.OK and n.value >= 0
