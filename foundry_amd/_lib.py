@@ -167,6 +167,7 @@ SIGNATURES = {
     "fh_argmax": [_vp, _vp, _i64, _i64, _vp],
     "fh_advance_positions": [_vp, _vp, _i64, _i64],
     "fh_append_token": [_vp, _vp, _i64, _vp, _vp, _i64, _i64],
+    "fh_append_token_advance": [_vp, _vp, _i64, _vp, _vp, _i64, _i64, _i64],
     "fh_llama_forward": [_vp, _vp, _i64, _vp, _vp, _vp],
     "fh_copy_strided": [_vp, _int, _vp, ctypes.POINTER(View), _vp],
     "fh_to_dtype": [_vp, _int, _vp, ctypes.POINTER(View), _int, _vp],

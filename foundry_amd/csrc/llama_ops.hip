@@ -307,6 +307,18 @@ __global__ void advance_kernel(uint32_t *__restrict__ p, uint32_t n, uint32_t by
     if (i < n) p[i] += by;
 }
 
+// append_token_kernel, then position += by, in one launch: thread r reads its
+// token and position before it writes the advanced position, so the two may
+// share memory (no __restrict__ on them).
+__global__ void append_advance_kernel(const uint32_t *token, uint32_t rows, uint32_t *__restrict__ log,
+                                      uint32_t *position, uint32_t base, uint32_t capacity, uint32_t by) {
+    const uint32_t r = blockIdx.x * blockDim.x + threadIdx.x;
+    if (r >= rows) return;
+    const uint32_t p = position[r], t = token[r], idx = p - base;
+    if (p >= base && idx < capacity) log[static_cast<uint64_t>(r) * capacity + idx] = t;
+    position[r] = p + by;
+}
+
 // Long aligned rows take two passes: kArgmaxSegs blocks per row each reduce
 // one segment to (value bits, index) in the device's partial area, then one
 // wavefront per row picks the winner among the segments. (max, lowest index)
@@ -558,5 +570,26 @@ extern "C" int fh_append_token(fh_device *dev, const uint32_t *token, int64_t ro
         hipLaunchKernelGGL(append_token_kernel, dim3(static_cast<uint32_t>((rows + 63) / 64)), dim3(64), 0,
                            dev->stream, token, static_cast<uint32_t>(rows), log, position,
                            static_cast<uint32_t>(base), static_cast<uint32_t>(capacity));
+    });
+}
+
+extern "C" int fh_append_token_advance(fh_device *dev, const uint32_t *token, int64_t rows, uint32_t *log,
+                                       uint32_t *position, int64_t base, int64_t capacity, int64_t by) {
+    const char *fn = "fh_append_token_advance";
+    if (int rc = check_usable(dev, fn)) return rc;
+    if (int rc = fh_check_dims(fn, {rows, base, capacity, by})) return rc;
+    if (rows == 0) return FH_OK;
+    if (static_cast<uint64_t>(rows) * static_cast<uint64_t>(capacity) > 0xFFFFFFFFull)
+        return fail(FH_ERR_UNSUPPORTED, "%s: rows * capacity must fit in 32 bits", fn);
+    if (int rc = check_range(dev, token, static_cast<uint64_t>(rows) * 4, fn, "token")) return rc;
+    if (int rc = check_range(dev, position, static_cast<uint64_t>(rows) * 4, fn, "position")) return rc;
+    if (capacity > 0)
+        if (int rc = check_range(dev, log, static_cast<uint64_t>(rows) * capacity * 4, fn, "log")) return rc;
+    if (int rc = set_current(dev, fn)) return rc;
+    return dispatch(dev, fn, [&] {
+        hipLaunchKernelGGL(append_advance_kernel, dim3(static_cast<uint32_t>((rows + 63) / 64)), dim3(64), 0,
+                           dev->stream, token, static_cast<uint32_t>(rows), log, position,
+                           static_cast<uint32_t>(base), static_cast<uint32_t>(capacity),
+                           static_cast<uint32_t>(by));
     });
 }

@@ -424,9 +424,8 @@ class Q4Llama:
         self.dev.capture_begin()
         try:
             self._forward(1, self.buf["next"], self.buf["pos1"])
-            _lib.call("fh_append_token", d, self._p(self.buf["next"]), self.batch, self._p(log),
-                      self._p(self.buf["pos1"]), self.seq_len - 1, capacity)
-            _lib.call("fh_advance_positions", d, self._p(self.buf["pos1"]), self.batch, 1)
+            _lib.call("fh_append_token_advance", d, self._p(self.buf["next"]), self.batch, self._p(log),
+                      self._p(self.buf["pos1"]), self.seq_len - 1, capacity, 1)
         except Exception:
             self.dev.capture_end()
             raise

@@ -462,6 +462,14 @@ int fh_append_token(fh_device *dev, const uint32_t *token, int64_t rows, uint32_
 /* positions[i] += by for i < n, on the device's stream. */
 int fh_advance_positions(fh_device *dev, uint32_t *positions, int64_t n, int64_t by);
 
+/* fh_append_token(dev, token, rows, log, position, base, capacity), then
+ * fh_advance_positions(dev, position, rows, by), as one launch: the decode
+ * step's token record and position bump (src/generate/mod.rs:45-90), one
+ * dispatch fewer per replayed step. With capacity 0 nothing is logged and
+ * log may be null. token and position may share memory. */
+int fh_append_token_advance(fh_device *dev, const uint32_t *token, int64_t rows, uint32_t *log,
+                            uint32_t *position, int64_t base, int64_t capacity, int64_t by);
+
 /* ======================================================================
  * The decoder forward issued from native code: the layer loop that a
  * caller would otherwise drive op by op, so an eager prefill is not bound

@@ -646,6 +646,60 @@ def test_interleaved_scale_bias_tables_change_no_result(device, cfg, batch):
         assert np.array_equal(na, nb)
 
 
+@pytest.mark.parametrize("hidden,vocab", [(1024, 40001), (3072, 40000)])
+def test_one_row_greedy_id_ties_and_nan(device, hidden, vocab):
+    """The greedy id of a one-sequence step (the one-block argmax over 40001
+    logits, the two-pass one over 40000) equals numpy's argmax of the
+    logits; a copy of the winning LM-head row planted at a lower index ties
+    and must win; the same copy with a NaN scale is never taken."""
+    cfg = LlamaConfig(n_layers=1, hidden=hidden, n_heads=hidden // 128, n_kv_heads=max(2, hidden // 384),
+                      head_dim=128, ffn=2048, vocab=vocab)
+    model = Q4Llama(device, cfg, 3, 16, max_tokens=1, batch=1)
+    e = model.embed
+    assert e.sb is not None
+    ids = np.array([[cfg.vocab - 2]], np.uint32)  # the planted rows below are not the input's
+
+    def run():
+        model.step(ids, 0)
+        logits = down(device, model.buf["logits"], np.uint16, cfg.vocab)
+        return logits, int(down(device, model.buf["next"], np.uint32, 1)[0])
+
+    def as_f32(bits):
+        return (bits.astype(np.uint32) << 16).view(np.float32)
+
+    logits, nxt = run()
+    assert nxt == int(np.argmax(as_f32(logits)))
+    if nxt == 0:
+        pytest.skip("the winner is row 0: no lower row to plant a tie at")
+    # a copy of row nxt at a lower row j and at the last row: a three-way tie
+    j, last, k = nxt // 2, cfg.vocab - 1, cfg.hidden
+    wq = down(device, e.wq, np.uint32, cfg.vocab * k // 8).reshape(cfg.vocab, k // 8)
+    sc = down(device, e.s, np.uint16, cfg.vocab * k // 64).reshape(cfg.vocab, k // 64)
+    bi = down(device, e.b, np.uint16, cfg.vocab * k // 64).reshape(cfg.vocab, k // 64)
+    for src in (wq, sc, bi):
+        src[j] = src[nxt]
+        src[last] = src[nxt]
+
+    def upload_rows():
+        model._upload(e.wq, wq)
+        model._upload(e.s, sc)
+        model._upload(e.b, bi)
+        _lib.call("fh_q4_interleave", device.handle, ctypes.c_void_p(e.s.ptr), ctypes.c_void_p(e.b.ptr), cfg.vocab,
+                  k, 64, ctypes.c_void_p(e.sb.ptr))
+
+    upload_rows()
+    logits2, nxt2 = run()
+    assert logits2[j] == logits2[nxt] == logits2[last]
+    assert np.array_equal(np.delete(logits2, [j, last]), np.delete(logits, [j, last]))
+    assert nxt2 == j
+    # a NaN scale in the planted row: its logit is NaN and never taken
+    sc[j, 0] = 0x7FC0
+    upload_rows()
+    logits3, nxt3 = run()
+    assert np.isnan(as_f32(logits3[j:j + 1])[0])
+    assert nxt3 == nxt
+
+
 def test_llama_forward_checks_the_interleaved_tables(device):
     """A misaligned or short interleaved table or tiled word copy, and tiled
     words without the interleaved table, are rejected before any work."""
@@ -682,6 +736,45 @@ def test_append_token_rows(device):
     want = np.zeros((4, 4), np.uint32)
     want[0, 0], want[1, 2] = 11, 22  # row 2 (position 4 < base) and row 3 (index 4 = capacity) write nothing
     assert np.array_equal(down(device, log, np.uint32, 16).reshape(4, 4), want)
+
+
+def test_append_token_advance_equals_the_two_calls(device):
+    """fh_append_token_advance leaves the log and the positions that
+    fh_append_token then fh_advance_positions leave; with capacity 0 it only
+    advances, and a token array that is the position array is read before the
+    advance is written."""
+    rows, cap, base = 70, 6, 5  # two blocks of 64 threads
+    rng = np.random.default_rng(7)
+    tok_h = rng.integers(0, 1 << 32, rows, dtype=np.uint32)
+    pos_h = rng.integers(0, base + cap + 3, rows, dtype=np.uint32)
+    tok = up(device, tok_h)
+    pos_a, pos_b = up(device, pos_h), up(device, pos_h)
+    log_a, log_b = device.zeros(4 * rows * cap), device.zeros(4 * rows * cap)
+    for _ in range(2):
+        _lib.call("fh_append_token", device.handle, ctypes.c_void_p(tok.ptr), rows, ctypes.c_void_p(log_a.ptr),
+                  ctypes.c_void_p(pos_a.ptr), base, cap)
+        _lib.call("fh_advance_positions", device.handle, ctypes.c_void_p(pos_a.ptr), rows, 3)
+        _lib.call("fh_append_token_advance", device.handle, ctypes.c_void_p(tok.ptr), rows,
+                  ctypes.c_void_p(log_b.ptr), ctypes.c_void_p(pos_b.ptr), base, cap, 3)
+    want_log = down(device, log_a, np.uint32, rows * cap)
+    assert np.count_nonzero(want_log) > rows // 2
+    assert np.array_equal(down(device, log_b, np.uint32, rows * cap), want_log)
+    assert np.array_equal(down(device, pos_b, np.uint32, rows), pos_h + 6)
+    assert np.array_equal(down(device, pos_a, np.uint32, rows), pos_h + 6)
+    # capacity 0: no log, positions still advance
+    _lib.call("fh_append_token_advance", device.handle, ctypes.c_void_p(tok.ptr), rows, None,
+              ctypes.c_void_p(pos_b.ptr), base, 0, 1)
+    assert np.array_equal(down(device, pos_b, np.uint32, rows), pos_h + 7)
+    # token aliasing position: the log holds each row's position before the advance
+    same = up(device, np.full(rows, base + 2, np.uint32))
+    log_c = device.zeros(4 * rows * cap)
+    _lib.call("fh_append_token_advance", device.handle, ctypes.c_void_p(same.ptr), rows, ctypes.c_void_p(log_c.ptr),
+              ctypes.c_void_p(same.ptr), base, cap, 1)
+    got = down(device, log_c, np.uint32, rows * cap).reshape(rows, cap)
+    want = np.zeros((rows, cap), np.uint32)
+    want[:, 2] = base + 2
+    assert np.array_equal(got, want)
+    assert np.array_equal(down(device, same, np.uint32, rows), np.full(rows, base + 3, np.uint32))
 
 
 def test_checkpoint_model_equals_random_init(device, tmp_path):

@@ -163,6 +163,8 @@ def test_calls_without_a_device_return_errors_not_crashes():
     assert "fh_q4_interleave" in _lib.last_error()
     assert lib.fh_q4_tile(None, None, 16, 128, 64, 0, None) == _lib.ERR_INVALID_ARGUMENT
     assert "fh_q4_tile" in _lib.last_error()
+    assert lib.fh_append_token_advance(None, None, 1, None, None, 0, 0, 1) == _lib.ERR_INVALID_ARGUMENT
+    assert "fh_append_token_advance" in _lib.last_error()
     assert lib.fh_device_destroy(None) == _lib.OK
     n = ctypes.c_int(-1)
     assert lib.fh_device_count(ctypes.byref(n)) == _lib.OK and n.value >= 0
