@@ -985,7 +985,7 @@ __global__ __launch_bounds__(kShortThreads) void attn_decode_short_kernel(
     constexpr int KPS = kAttnChunk / SLOTS;  // keys per slot
     static_assert(HD == 64 || HD == 128, "a wavefront holds a chunk's key fragments in registers");
     static_assert(G <= kAttnMaxGroup && (G + 2) * PPH <= kShortThreads, "RoPE lanes fit the block");
-    static_assert((DB == 16 || DB == 32) && HD % DB == 0, "4 or 8 key slots");
+    static_assert((DB == 8 || DB == 16 || DB == 32) && HD % DB == 0, "16, 8 or 4 key slots");
     __shared__ __align__(16) uint16_t qb[G][HD];
     __shared__ __align__(16) uint16_t knew[HD];
     __shared__ __align__(16) float sc[kShortWaves][kAttnChunk][HP];  // raw dot products, lane = key
@@ -1168,8 +1168,8 @@ __global__ __launch_bounds__(kShortThreads) void attn_decode_short_kernel(
         for (int g = 0; g < G; ++g)
 #pragma unroll
             for (int k = 0; k < 2; ++k) {
-                if constexpr (SLOTS == 8) {
-                    acc[g][k] = group_sum<8>(acc[g][k]);
+                if constexpr (SLOTS >= 8) {
+                    acc[g][k] = group_sum<SLOTS>(acc[g][k]);
                 } else {
                     acc[g][k] += dpp_mov<0xB1>(acc[g][k]);
                     acc[g][k] += dpp_mov<0x4E>(acc[g][k]);
@@ -1308,7 +1308,7 @@ constexpr uint32_t kDecodeShortMaxLen = FH_DECODE_SHORT_MAX_LEN;
 static_assert(kDecodeShortMaxLen <= kShortKeys, "one chunk per wavefront");
 
 #ifndef FH_DECODE_SHORT_DIMS
-#define FH_DECODE_SHORT_DIMS 16
+#define FH_DECODE_SHORT_DIMS 8
 #endif
 constexpr int kShortDims = FH_DECODE_SHORT_DIMS;  // V dims per block
 
