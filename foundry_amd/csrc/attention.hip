@@ -985,7 +985,7 @@ __global__ __launch_bounds__(kShortThreads) void attn_decode_short_kernel(
     constexpr int KPS = kAttnChunk / SLOTS;  // keys per slot
     static_assert(HD == 64 || HD == 128, "a wavefront holds a chunk's key fragments in registers");
     static_assert(G <= kAttnMaxGroup && (G + 2) * PPH <= kShortThreads, "RoPE lanes fit the block");
-    static_assert((DB == 8 || DB == 16 || DB == 32) && HD % DB == 0, "16, 8 or 4 key slots");
+    static_assert((DB == 4 || DB == 8 || DB == 16 || DB == 32) && HD % DB == 0, "32, 16, 8 or 4 key slots");
     __shared__ __align__(16) uint16_t qb[G][HD];
     __shared__ __align__(16) uint16_t knew[HD];
     __shared__ __align__(16) float sc[kShortWaves][kAttnChunk][HP];  // raw dot products, lane = key
@@ -1140,6 +1140,24 @@ __global__ __launch_bounds__(kShortThreads) void attn_decode_short_kernel(
 #pragma unroll
         for (int h = 0; h < G; ++h) pw[wave][h][lane] = bf(rne(e[h] / sg[h]));
         __builtin_amdgcn_wave_barrier();  // this wavefront's probabilities before its reads
+        if constexpr (KPS == 2) {
+            float v0[2], v1[2];
+#pragma unroll
+            for (int u = 0; u < 2; ++u) {
+                const uint32_t jk = c0 + KPS * vs + u;
+                const uint32_t w = jk < pos ? vr[u] : (jk == pos ? vnew : 0u);
+                v0[u] = bf(w & 0xFFFFu);
+                v1[u] = bf(w >> 16);
+            }
+#pragma unroll
+            for (int g = 0; g < G; ++g) {
+                const float2 p2 = *reinterpret_cast<const float2 *>(&pw[wave][g][KPS * vs]);
+                acc[g][0] += p2.x * v0[0];
+                acc[g][1] += p2.x * v1[0];
+                acc[g][0] += p2.y * v0[1];
+                acc[g][1] += p2.y * v1[1];
+            }
+        }
 #pragma unroll
         for (int t4 = 0; t4 < KPS / 4; ++t4) {
             float v0[4], v1[4];
@@ -1308,7 +1326,7 @@ constexpr uint32_t kDecodeShortMaxLen = FH_DECODE_SHORT_MAX_LEN;
 static_assert(kDecodeShortMaxLen <= kShortKeys, "one chunk per wavefront");
 
 #ifndef FH_DECODE_SHORT_DIMS
-#define FH_DECODE_SHORT_DIMS 8
+#define FH_DECODE_SHORT_DIMS 4
 #endif
 constexpr int kShortDims = FH_DECODE_SHORT_DIMS;  // V dims per block
 
