@@ -1332,8 +1332,13 @@ constexpr int kShortDims = FH_DECODE_SHORT_DIMS;  // V dims per block
 
 template <int HD, int G>
 static void launch_decode_short(hipStream_t stream, uint32_t rows, const AttnArgs &x) {
+    // one wavefront per 64-key chunk the cache can hold (positions beyond
+    // max_len take no chunk), and at least the RoPE and value lanes
+    const uint32_t chunk_waves = (x.max_len + kAttnChunk - 1) / kAttnChunk;
+    const uint32_t rope_waves = ((G + 2) * (HD / 8) + 63) / 64;
+    const uint32_t waves = chunk_waves > rope_waves ? chunk_waves : rope_waves;
     const dim3 grid(x.n_kv * (HD / kShortDims), rows);
-    hipLaunchKernelGGL((attn_decode_short_kernel<HD, G, kShortDims>), grid, dim3(kShortThreads), 0, stream, x.q_src, x.cos_tab,
+    hipLaunchKernelGGL((attn_decode_short_kernel<HD, G, kShortDims>), grid, dim3(64 * waves), 0, stream, x.q_src, x.cos_tab,
                        x.sin_tab, x.positions, x.pos_limit, x.k_cache, x.v_cache, x.row_stride, x.n_heads, x.n_kv,
                        x.max_len, x.scale, x.out);
 }
