@@ -1336,7 +1336,10 @@ static void launch_decode_short(hipStream_t stream, uint32_t rows, const AttnArg
     // max_len take no chunk), and at least the RoPE and value lanes
     const uint32_t chunk_waves = (x.max_len + kAttnChunk - 1) / kAttnChunk;
     const uint32_t rope_waves = ((G + 2) * (HD / 8) + 63) / 64;
-    const uint32_t waves = chunk_waves > rope_waves ? chunk_waves : rope_waves;
+    // the output (and zero-output) writers are threads tid < G * kShortDims
+    const uint32_t out_waves = (G * kShortDims + 63) / 64;
+    uint32_t waves = chunk_waves > rope_waves ? chunk_waves : rope_waves;
+    if (out_waves > waves) waves = out_waves;
     const dim3 grid(x.n_kv * (HD / kShortDims), rows);
     hipLaunchKernelGGL((attn_decode_short_kernel<HD, G, kShortDims>), grid, dim3(64 * waves), 0, stream, x.q_src, x.cos_tab,
                        x.sin_tab, x.positions, x.pos_limit, x.k_cache, x.v_cache, x.row_stride, x.n_heads, x.n_kv,

@@ -120,8 +120,10 @@ static int launch_rows(fh_device *dev, const char *fn, const uint32_t *wq,
     if (n_out == 0 || k == 0) return FH_OK;
     const uint32_t words = static_cast<uint32_t>(k / 8);
     // fewer rows than CUs x 4 (B = 64: 16 blocks) keep q4_rows_kernel's wider
-    // grid: 2.75 against 2.89 us at B = 64
-    if (words % 64 == 0 && (words / 64 == 6 || words / 64 == 8) &&
+    // grid: 2.75 against 2.89 us at B = 64. An empty table (rows == 0) also
+    // takes q4_rows_kernel, which loads nothing for an id >= rows: the wave
+    // kernel reads row 0 for such ids, and an empty table has no row 0.
+    if (rows > 0 && words % 64 == 0 && (words / 64 == 6 || words / 64 == 8) &&
         n_out >= static_cast<int64_t>(kEmbedWaves) * dev->compute_units) {
         const uint32_t blocks = static_cast<uint32_t>((n_out + kEmbedWaves - 1) / kEmbedWaves);
         return dispatch(dev, fn, [&] {

@@ -1,0 +1,467 @@
+// q4 prefill GEMM with weights fed straight to the matrix cores:
+// Y[m, r] = sum_j X[m, j] * RNE_bf16(s[r, j/64] * q[r, j] + b[r, j/64]).
+// Replaces matmul_tiled (src/metal/kernels/matmul.metal:29-65) behind
+// Linear::forward (src/nn/linear.rs:22-35) for prompt-length row counts whose
+// 256 x 256 output tiles fill the chip.
+//
+// Design for CDNA4 (one 512-thread block per CU, 256 x 256 output tile, K
+// step 64 = one quantisation group):
+// - Eight wavefronts, two per SIMD, and both issue MFMAs all the time: on
+//   gfx950 one wavefront issues a v_mfma_f32_32x32x16_bf16 at most every 32
+//   clocks, and a second wavefront on the same SIMD doubles the rate
+//   (measured: 2.2 PFLOP/s with one wavefront per SIMD, 4.4 with two).
+//   Wavefront w owns X rows [128 (w / 4), +128) and output columns
+//   [64 (w % 4), +64): a 128 x 64 tile, 4 x 2 accumulators (128 registers).
+// - Weights skip LDS. Lane (col, h) of a 32-column B tile loads the 16 bytes
+//   of its weight row that hold k = 32 h .. 32 h + 31 of the group (one
+//   buffer_load_dwordx4) and dequantises them in registers; MFMA sub-step j
+//   takes k = 32 h + 8 j .. + 7, and the X fragments are read in the same k
+//   order, so every product is the plain GEMM's.
+// - The dequantisation of the next sub-step (46 VALU instructions), the
+//   next X fragments' LDS reads and the loads of later steps are interleaved
+//   with each sub-step's eight MFMAs (sched_group_barrier), so they issue in
+//   the MFMAs' shadow instead of in a phase of their own.
+// - X goes through LDS in three stages (per wavefront group of 128 rows, row
+//   pitch 72 bf16: conflict-free 16-byte fragment reads): step s + 2's X is
+//   stored while step s computes and step s + 1's first fragments are read
+//   at the end of step s, so one barrier per step suffices.
+// - Dequantisation: exact nibble -> float (v_cvt_f32_ubyte of masked
+//   bytes), fma(s, q, b), RNE to bf16: the fh_q4_dequant value whenever s*q
+//   is finite.
+// - The bf16 epilogue goes through LDS so that each lane stores 16
+//   contiguous bytes of an output row (1 KiB per wavefront instruction)
+//   instead of 2-byte values 8 KiB apart.
+// - Tiles are dealt to XCDs in rectangles (blocks go round-robin over the 8
+//   XCDs): the 32 blocks of one XCD share their X rows and weight rows in
+//   that XCD's L2.
+#include <type_traits>
+
+#include "device.hpp"
+#include "q4_common.hpp"
+
+namespace fh {
+
+namespace {
+
+constexpr int kDThreads = 512;
+constexpr int kDBM = 256, kDBN = 256, kDBK = 64;
+constexpr int kDPitch = kDBK + 8;                 // bf16 per X row in LDS
+constexpr int kDRows = kDBM / 2;                  // X rows per wavefront group
+constexpr int kDStage = kDRows * kDPitch;         // bf16 per group stage
+constexpr int kDStages = 3;
+constexpr uint32_t kDXLds = 2u * kDStages * kDStage * 2u;  // bytes, both groups
+// Scales and biases go through LDS in chunks of 8 groups (8 K steps), two
+// chunk buffers: [buffer][column][group][scale, bias], 4 bytes per group.
+// (Loaded per step and per lane they cost 4 loads that each touch 32 cache
+// lines for 256 useful bytes, and took 40% of the kernel.)
+constexpr int kDSbGroups = 8;
+constexpr uint32_t kDSbBuf = kDBN * kDSbGroups * 4;             // bytes per chunk buffer
+constexpr uint32_t kDSbLds = 2 * kDSbBuf;
+constexpr uint32_t kDLoopLds = kDXLds + kDSbLds;
+// bf16 epilogue: each wavefront's 128 x 64 tile, row pitch 72
+constexpr int kDOutPitch = 64 + 8;
+constexpr uint32_t kDOutLds = 8u * 128u * kDOutPitch * 2u;
+constexpr uint32_t kDLds = kDLoopLds > kDOutLds ? kDLoopLds : kDOutLds;
+constexpr uint32_t kXcds = 8;
+
+typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8_t;
+typedef __attribute__((ext_vector_type(16))) float f32x16_t;
+
+// w & 0x0F0F0F0F as one v_and_b32 the compiler cannot fold into the byte
+// conversions that follow (it would extract every nibble with its own
+// v_bfe_u32, one more instruction per weight).
+__device__ __forceinline__ uint32_t low_nibbles(uint32_t w) {
+    uint32_t r;
+    asm("v_and_b32 %0, 0x0f0f0f0f, %1" : "=v"(r) : "v"(w));
+    return r;
+}
+
+template <int I>
+__device__ __forceinline__ float ubyte_f32(uint32_t v) {
+    return static_cast<float>((v >> (8 * I)) & 0xFFu);
+}
+
+// 8 weights of one packed word (nibble e = weight e) -> bf16x8 in order.
+__device__ __forceinline__ bf16x8_t dequant8(uint32_t w, float s, float b) {
+    const uint32_t lo = low_nibbles(w);       // nibbles 0, 2, 4, 6 in bytes 0..3
+    const uint32_t hi = low_nibbles(w >> 4);  // nibbles 1, 3, 5, 7
+    uint4 o;
+    o.x = f32x2_to_bf16x2_rne(fmaf(s, ubyte_f32<0>(lo), b), fmaf(s, ubyte_f32<0>(hi), b));
+    o.y = f32x2_to_bf16x2_rne(fmaf(s, ubyte_f32<1>(lo), b), fmaf(s, ubyte_f32<1>(hi), b));
+    o.z = f32x2_to_bf16x2_rne(fmaf(s, ubyte_f32<2>(lo), b), fmaf(s, ubyte_f32<2>(hi), b));
+    o.w = f32x2_to_bf16x2_rne(fmaf(s, ubyte_f32<3>(lo), b), fmaf(s, ubyte_f32<3>(hi), b));
+    return __builtin_bit_cast(bf16x8_t, o);
+}
+
+// One thread's X pieces of one step.
+struct XSet {
+    uint4 p0, p1, p2, p3;
+};
+
+// One lane's packed weights of one step: for each of its two B tiles, the 4
+// words of the group half it feeds.
+struct WSet {
+    uint4 w[2];
+};
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void *p, uint64_t bytes) {
+    // raw buffer (stride 0) over `bytes`; 0x00020000 is the gfx9 32-bit data
+    // format word
+    const uint32_t records = bytes < 0xFFFFFFFFull ? static_cast<uint32_t>(bytes) : 0xFFFFFFFFu;
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(p), static_cast<short>(0), static_cast<int>(records),
+                                             0x00020000);
+}
+
+__device__ __forceinline__ uint4 buf_load16(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+    return __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r, static_cast<int>(voff),
+                                                                           static_cast<int>(soff), 0));
+}
+
+// sched_group_barrier masks
+constexpr int kSgMfma = 0x008, kSgValu = 0x002, kSgVmemRead = 0x020, kSgDsRead = 0x100, kSgDsWrite = 0x200;
+
+}  // namespace
+
+// Block L of the 1-D grid -> tile (tm, tn): L's XCD (L mod 8) takes a run of
+// consecutive tiles in a grouped order (gm tile rows at a time, then every
+// tile column), so each XCD works on a compact rectangle. A bijection for
+// any tile count.
+__device__ __forceinline__ void direct_tile(uint32_t L, uint32_t tiles_m, uint32_t tiles_n, uint32_t gm,
+                                            uint32_t *tm, uint32_t *tn) {
+    const uint32_t total = tiles_m * tiles_n;
+    const uint32_t xcd = L % kXcds, slot = L / kXcds;
+    const uint32_t base = total / kXcds, rem = total % kXcds;
+    const uint32_t v = xcd * base + (xcd < rem ? xcd : rem) + slot;
+    const uint32_t group = gm * tiles_n;
+    const uint32_t g = v / group, r = v % group;
+    const uint32_t rows_left = tiles_m - g * gm;
+    const uint32_t gm_eff = rows_left < gm ? rows_left : gm;
+    *tm = g * gm + r % gm_eff;
+    *tn = r / gm_eff;
+}
+
+// y_mode: 0 bf16 through the LDS epilogue (n % 8 == 0, y 16-byte aligned),
+// 1 bf16 stored per value, 2 f32 stored per value.
+__global__ __launch_bounds__(kDThreads) void q4_gemm_direct_kernel(
+    const uint16_t *__restrict__ x, uint32_t x_ld, const uint32_t *__restrict__ wq,
+    const uint16_t *__restrict__ scales, const uint16_t *__restrict__ biases, uint32_t m, uint32_t n, uint32_t k,
+    void *__restrict__ y, int y_mode, uint32_t tiles_m, uint32_t tiles_n, uint32_t gm) {
+    extern __shared__ __attribute__((aligned(16))) uint16_t smem[];
+    const uint32_t tid = threadIdx.x;
+    const uint32_t lane = tid & 63;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const uint32_t grp = wave >> 2, wc = wave & 3;
+    uint32_t tm, tn;
+    direct_tile(blockIdx.x, tiles_m, tiles_n, gm, &tm, &tn);
+    const uint32_t m0 = tm * kDBM, n0 = tn * kDBN;
+    const uint32_t kw = k / 8, kg = k / kGroup;
+    const uint32_t steps = k / kDBK;
+    const uint32_t h = lane >> 5;
+
+    uint16_t *const xs_base = smem + grp * kDStages * kDStage;  // this group's stages
+
+    // X staging: thread t of the group stages pieces t + 256 i (i < 4) of the
+    // group's 128 x 64 step tile, 8 pieces of 16 bytes per row. Rows past m
+    // read row m - 1 (their outputs are never stored).
+    const uint32_t t = tid & 255;
+    uint32_t xoff[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        uint32_t row = m0 + grp * kDRows + (t >> 3) + 32 * i;
+        row = row < m ? row : m - 1;
+        xoff[i] = (row * x_ld + (t & 7) * 8) * 2;
+    }
+    const uint32_t xdst = (t >> 3) * kDPitch + (t & 7) * 8;  // piece i: + 32 i rows
+    // weights: B tile jj's column for this lane; rows past n read row 0
+    uint32_t woff[2];
+#pragma unroll
+    for (int jj = 0; jj < 2; ++jj) {
+        uint32_t col = n0 + wc * 64 + jj * 32 + (lane & 31);
+        col = col < n ? col : 0;
+        woff[jj] = (col * kw + 4 * h) * 4;
+    }
+    // scale/bias chunks: thread t loads the 8 scales (group 0) or biases
+    // (group 1) of tile column t % 256 for one chunk: 16 bytes per 8 steps
+    uint32_t sbcol = n0 + (tid & 255);
+    sbcol = sbcol < n ? sbcol : 0;
+    const uint32_t sbgoff = sbcol * kg * 2;
+    const uint32_t chunks = kg / kDSbGroups;
+    char *const sb_lds = reinterpret_cast<char *>(smem) + kDXLds;
+    // this lane's dword of B tile jj in a chunk buffer, group 0
+    uint32_t sbread[2];
+#pragma unroll
+    for (int jj = 0; jj < 2; ++jj) sbread[jj] = (wc * 64 + jj * 32 + (lane & 31)) * kDSbGroups * 4;
+
+    // Loads are buffer loads: a per-lane 32-bit byte offset plus the step's
+    // offset as a scalar (readfirstlane keeps it scalar), so no lane keeps a
+    // 64-bit address of its own.
+    const __amdgpu_buffer_rsrc_t rx = buffer_rsrc(x, static_cast<uint64_t>(m) * x_ld * 2);
+    const __amdgpu_buffer_rsrc_t rw = buffer_rsrc(wq, static_cast<uint64_t>(n) * k / 2);
+    const __amdgpu_buffer_rsrc_t rs = buffer_rsrc(scales, static_cast<uint64_t>(n) * kg * 2);
+    const __amdgpu_buffer_rsrc_t rb = buffer_rsrc(biases, static_cast<uint64_t>(n) * kg * 2);
+    const uint32_t last = steps - 1;
+    auto load_x = [&](uint32_t st) {
+        const uint32_t so = __builtin_amdgcn_readfirstlane((st < last ? st : last) * kDBK * 2);
+        XSet r;
+        r.p0 = buf_load16(rx, xoff[0], so);
+        r.p1 = buf_load16(rx, xoff[1], so);
+        r.p2 = buf_load16(rx, xoff[2], so);
+        r.p3 = buf_load16(rx, xoff[3], so);
+        return r;
+    };
+    auto store_x = [&](const XSet &r, uint32_t st) {
+        uint16_t *xs = xs_base + (st % kDStages) * kDStage + xdst;
+        *reinterpret_cast<uint4 *>(xs) = r.p0;
+        *reinterpret_cast<uint4 *>(xs + 32 * kDPitch) = r.p1;
+        *reinterpret_cast<uint4 *>(xs + 64 * kDPitch) = r.p2;
+        *reinterpret_cast<uint4 *>(xs + 96 * kDPitch) = r.p3;
+    };
+    auto load_w = [&](WSet &ws, uint32_t st) {
+        st = st < last ? st : last;
+        const uint32_t wso = __builtin_amdgcn_readfirstlane(st * 32);
+#pragma unroll
+        for (int jj = 0; jj < 2; ++jj) ws.w[jj] = buf_load16(rw, woff[jj], wso);
+    };
+    // chunk c's 16 bytes for this thread (chunks past the last re-read it)
+    auto load_sb = [&](uint32_t c) {
+        c = c < chunks ? c : chunks - 1;
+        return buf_load16(grp ? rb : rs, sbgoff, __builtin_amdgcn_readfirstlane(c * kDSbGroups * 2));
+    };
+    // ... stored as [column][group][scale, bias] into chunk c's buffer
+    auto store_sb = [&](const uint4 &v, uint32_t c) {
+        uint16_t *dst = reinterpret_cast<uint16_t *>(sb_lds + (c & 1) * kDSbBuf + (tid & 255) * kDSbGroups * 4) + grp;
+        const uint32_t d[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+        for (int g = 0; g < kDSbGroups; ++g) dst[2 * g] = static_cast<uint16_t>(d[g / 2] >> (16 * (g % 2)));
+    };
+    // step st's (scale | bias << 16) for this lane's two B tiles
+    auto read_sb = [&](uint32_t st, uint32_t (&sb)[2]) {
+        const char *base = sb_lds + ((st / kDSbGroups) & 1) * kDSbBuf + (st % kDSbGroups) * 4;
+#pragma unroll
+        for (int jj = 0; jj < 2; ++jj) sb[jj] = *reinterpret_cast<const uint32_t *>(base + sbread[jj]);
+    };
+    // sub-step j's B fragments of both tiles from a step's weights
+    auto dequant = [&](const WSet &ws, const uint32_t (&sb)[2], int j, bf16x8_t (&b)[2]) {
+#pragma unroll
+        for (int jj = 0; jj < 2; ++jj) {
+            const float s = __uint_as_float(sb[jj] << 16);
+            const float bb = __uint_as_float(sb[jj] & 0xFFFF0000u);
+            const uint32_t w = j == 0 ? ws.w[jj].x : j == 1 ? ws.w[jj].y : j == 2 ? ws.w[jj].z : ws.w[jj].w;
+            b[jj] = dequant8(w, s, bb);
+        }
+    };
+    // A fragment of lane l for sub-step j of tile i: row 32 i + l % 32,
+    // k = 32 h + 8 j .. + 7
+    const uint32_t frag = (lane & 31) * kDPitch + 32 * h;
+    auto read_a = [&](uint32_t st, int j, bf16x8_t (&a)[4]) {
+        const uint16_t *xs = xs_base + (st % kDStages) * kDStage + frag + 8 * j;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) a[i] = *reinterpret_cast<const bf16x8_t *>(xs + i * 32 * kDPitch);
+    };
+
+    f32x16_t acc[4][2];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int jj = 0; jj < 2; ++jj)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[i][jj][r] = 0.f;
+
+    // Prologue: X(0), X(1) staged; X(2) and the weights of steps 0, 1 in
+    // flight; sub-step (0, 0)'s B fragments and sub-steps (0, 0), (0, 1)'s A
+    // fragments ready. The last loads issued are X(2), then W(1), as at the
+    // end of every step (X(st + 3) at its start, W(st + 2) at its end), so
+    // the loop's wait counts are those of the steady state.
+    WSet w0, w1;
+    uint4 sbr = load_sb(0);
+    XSet xr = load_x(0);
+    __builtin_amdgcn_sched_barrier(0);
+    load_w(w0, 0);
+    __builtin_amdgcn_sched_barrier(0);
+    store_sb(sbr, 0);
+    store_x(xr, 0);
+    __builtin_amdgcn_sched_barrier(0);
+    xr = load_x(1);
+    __builtin_amdgcn_sched_barrier(0);
+    store_x(xr, 1);
+    __builtin_amdgcn_sched_barrier(0);
+    xr = load_x(2);
+    __builtin_amdgcn_sched_barrier(0);
+    load_w(w1, 1);
+    __builtin_amdgcn_sched_barrier(0);
+    bf16x8_t b[2][2], a[2][4];
+    uint32_t sb0[2], sb1[2];
+    __syncthreads();
+    read_sb(0, sb0);
+    dequant(w0, sb0, 0, b[0]);
+    read_a(0, 0, a[0]);
+    read_a(0, 1, a[1]);
+
+    // Step st, sub-step j: the eight MFMAs of (st, j), interleaved with
+    // - the dequantisation of the next sub-step ((st, j + 1), or (st + 1, 0)),
+    // - the A reads of the sub-step after next ((st, j + 2), or (st + 1, j - 2)),
+    // - at j = 0: the store of X(st + 2) (loaded during step st - 1) and the
+    //   load of X(st + 3); at j = 3: the load of W(st + 2) into the set that
+    //   W(st) used (its last sub-step was dequantised at j = 2);
+    // - at j = 1: the LDS read of step st + 1's scales and biases; in the
+    //   first step of a chunk (st % 8 == 0) the load of chunk st / 8 + 1, and
+    //   in its fifth step the store of that chunk into the other buffer
+    //   (read from step st + 4 on; its previous contents, chunk st / 8 - 1,
+    //   were last read in step st - 5).
+    // One barrier per step, after sub-step 3: it publishes X(st + 2) and
+    // retires every read of the stage the next step's store reuses.
+    // q = st % 8 is a compile-time constant: the chunk loop below runs its
+    // eight steps unrolled, so no load sits under a branch (a branch's join
+    // would wait for every load in flight).
+    auto step = [&](uint32_t st, auto qc, WSet &cur, WSet &nxt, const uint32_t (&sbc)[2], uint32_t (&sbn)[2]) {
+        constexpr uint32_t q = decltype(qc)::value;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            bf16x8_t (&ac)[4] = a[j % 2];
+            bf16x8_t (&bc)[2] = b[j % 2];
+            bf16x8_t (&bn)[2] = b[(j + 1) % 2];
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int jj = 0; jj < 2; ++jj)
+                    acc[i][jj] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ac[i], bc[jj], acc[i][jj], 0, 0, 0);
+            if (j == 0) {
+                store_x(xr, st + 2);
+                xr = load_x(st + 3);
+            }
+            if (j == 1) {
+                read_sb(st + 1, sbn);
+                if (q == 0) sbr = load_sb(st / kDSbGroups + 1);
+                if (q == 4) store_sb(sbr, st / kDSbGroups + 1);
+            }
+            if (j < 3)
+                dequant(cur, sbc, j + 1, bn);
+            else
+                dequant(nxt, sbn, 0, bn);
+            if (j < 2)
+                read_a(st, j + 2, ac);
+            else
+                read_a(st + 1, j - 2, ac);
+            if (j == 3) load_w(cur, st + 2);
+            // 8 MFMAs, each followed by its share of the sub-step's other work
+            if (j == 0) {
+                __builtin_amdgcn_sched_group_barrier(kSgMfma, 1, 0);
+                __builtin_amdgcn_sched_group_barrier(kSgDsWrite, 4, 0);
+                __builtin_amdgcn_sched_group_barrier(kSgMfma, 1, 0);
+                __builtin_amdgcn_sched_group_barrier(kSgVmemRead, 4, 0);
+            } else if (j == 3) {
+                __builtin_amdgcn_sched_group_barrier(kSgMfma, 1, 0);
+                __builtin_amdgcn_sched_group_barrier(kSgVmemRead, 6, 0);
+            }
+#pragma unroll
+            for (int q = 0; q < 8; ++q) {
+                if ((j == 0 && q >= 2) || (j == 3 && q >= 1) || (j == 1 || j == 2))
+                    __builtin_amdgcn_sched_group_barrier(kSgMfma, 1, 0);
+                __builtin_amdgcn_sched_group_barrier(kSgValu, 6, 0);
+                if (q % 2 == 1) __builtin_amdgcn_sched_group_barrier(kSgDsRead, 1, 0);
+            }
+            // each sub-step is its own scheduling region, so that loads keep
+            // their sub-step (and the X loads their place before the weight
+            // loads, which the next step's wait counts rely on)
+            __builtin_amdgcn_sched_barrier(0);
+            if (j == 3) {
+                __syncthreads();
+                __builtin_amdgcn_sched_barrier(0);
+            }
+        }
+    };
+    for (uint32_t st = 0; st < steps; st += kDSbGroups) {
+        step(st, std::integral_constant<uint32_t, 0>{}, w0, w1, sb0, sb1);
+        step(st + 1, std::integral_constant<uint32_t, 1>{}, w1, w0, sb1, sb0);
+        step(st + 2, std::integral_constant<uint32_t, 2>{}, w0, w1, sb0, sb1);
+        step(st + 3, std::integral_constant<uint32_t, 3>{}, w1, w0, sb1, sb0);
+        step(st + 4, std::integral_constant<uint32_t, 4>{}, w0, w1, sb0, sb1);
+        step(st + 5, std::integral_constant<uint32_t, 5>{}, w1, w0, sb1, sb0);
+        step(st + 6, std::integral_constant<uint32_t, 6>{}, w0, w1, sb0, sb1);
+        step(st + 7, std::integral_constant<uint32_t, 7>{}, w1, w0, sb1, sb0);
+    }
+
+    const uint32_t row_base = m0 + grp * kDRows + 4 * h;
+    if (y_mode == 0) {
+        // bf16 via LDS: the wavefront's 128 x 64 tile, row-major (pitch 72),
+        // then 16-byte row pieces: 8 lanes per 128-byte row, 8 rows per store
+        uint16_t *const os = smem + wave * 128 * kDOutPitch;
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int jj = 0; jj < 2; ++jj)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const uint32_t row = i * 32 + 8 * (r / 4) + 4 * h + (r % 4);
+                    os[row * kDOutPitch + jj * 32 + (lane & 31)] = static_cast<uint16_t>(f32_to_bf16_rne(acc[i][jj][r]));
+                }
+        __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this wavefront's own LDS writes
+        __builtin_amdgcn_wave_barrier();
+        const uint32_t col = n0 + wc * 64 + (lane & 7) * 8;
+        uint16_t *const yb = static_cast<uint16_t *>(y);
+#pragma unroll
+        for (int p = 0; p < 16; ++p) {
+            const uint32_t r = p * 8 + (lane >> 3);
+            const uint32_t row = m0 + grp * kDRows + r;
+            const uint4 v = *reinterpret_cast<const uint4 *>(os + r * kDOutPitch + (lane & 7) * 8);
+            if (row < m && col < n) *reinterpret_cast<uint4 *>(yb + static_cast<uint64_t>(row) * n + col) = v;
+        }
+        return;
+    }
+#pragma unroll
+    for (int jj = 0; jj < 2; ++jj) {
+        const uint32_t col = n0 + wc * 64 + jj * 32 + (lane & 31);
+        if (col >= n) continue;
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const uint32_t row = row_base + i * 32 + 8 * (r / 4) + (r % 4);
+                if (row >= m) continue;
+                const uint64_t o = static_cast<uint64_t>(row) * n + col;
+                if (y_mode == 2)
+                    static_cast<float *>(y)[o] = acc[i][jj][r];
+                else
+                    static_cast<uint16_t *>(y)[o] = static_cast<uint16_t>(f32_to_bf16_rne(acc[i][jj][r]));
+            }
+    }
+}
+
+// Launches the direct-weight GEMM when it applies: at least one 256 x 256
+// tile per CU (the 2048 x 8192 x 3072 gate/up shape has exactly 256), k a
+// multiple of 512 (whole scale/bias chunks) and every per-lane byte offset
+// within 32 bits. Returns false otherwise.
+bool launch_q4_gemm_direct(hipStream_t stream, uint32_t cus, const uint16_t *x, uint32_t x_ld, const uint32_t *wq,
+                           const uint16_t *s, const uint16_t *b, uint32_t m, uint32_t n, uint32_t k, void *y,
+                           int y_is_f32) {
+    const uint32_t tiles_m = (m + kDBM - 1) / kDBM, tiles_n = (n + kDBN - 1) / kDBN;
+    const uint64_t tiles = static_cast<uint64_t>(tiles_m) * tiles_n;
+    // k % 512: whole scale/bias chunks of 8 groups (and whole pairs of steps)
+    if (tiles < cus || tiles > 0x7FFFFFFFull || k % (kDSbGroups * kDBK) != 0 || k == 0 || m == 0) return false;
+    if (static_cast<uint64_t>(m) * x_ld * 2 >= (1ull << 32) || static_cast<uint64_t>(n) * k / 2 >= (1ull << 32))
+        return false;
+    static bool lds_opt_in = false;
+    if (!lds_opt_in) {
+        (void)hipFuncSetAttribute(reinterpret_cast<const void *>(q4_gemm_direct_kernel),
+                                  hipFuncAttributeMaxDynamicSharedMemorySize, kDLds);
+        lds_opt_in = true;
+    }
+    // rows of tiles per XCD rectangle: the count that minimises the X and
+    // weight bytes one XCD brings in (gm tile rows of X, per_xcd / gm tile
+    // columns of weights)
+    const uint64_t per_xcd = (tiles + kXcds - 1) / kXcds;
+    const double x_tile = 256.0 * k * 2, w_tile = 256.0 * (k / 2 + 4 * (k / 64));
+    uint32_t gm = 1;
+    double best = 1e300;
+    for (uint32_t g = 1; g <= tiles_m && g <= per_xcd; ++g) {
+        const double cols = static_cast<double>((per_xcd + g - 1) / g);
+        const double bytes = g * x_tile + (cols < tiles_n ? cols : tiles_n) * w_tile;
+        if (bytes < best) best = bytes, gm = g;
+    }
+    const int y_mode = y_is_f32 ? 2 : (n % 8 == 0 && (reinterpret_cast<uintptr_t>(y) & 15) == 0) ? 0 : 1;
+    hipLaunchKernelGGL(q4_gemm_direct_kernel, dim3(static_cast<uint32_t>(tiles)), dim3(kDThreads), kDLds, stream, x,
+                       x_ld, wq, s, b, m, n, k, y, y_mode, tiles_m, tiles_n, gm);
+    return true;
+}
+
+}  // namespace fh

@@ -116,22 +116,28 @@ __global__ __launch_bounds__(kThreads) void binary_kernel(const typename Float<D
 template <int DT, bool AMAX>
 __global__ __launch_bounds__(kThreads) void reduce_kernel(const typename Float<DT>::T *__restrict__ src, View rows,
                                                           uint32_t dim_size, int64_t dim_stride,
-                                                          typename Float<DT>::T *__restrict__ dst) {
+                                                          typename Float<DT>::T *__restrict__ dst,
+                                                          uint32_t n_rows) {
     __shared__ float part[kThreads];
     const uint32_t t = threadIdx.x;
-    const int64_t base = at(blockIdx.x, rows);
-    float acc = AMAX ? -INFINITY : 0.0f;
-    for (uint32_t k = t; k < dim_size; k += kThreads) {
-        const float x = Float<DT>::get(src, base + static_cast<int64_t>(k) * dim_stride);
-        acc = AMAX ? fmaxf(acc, x) : acc + x;
-    }
-    part[t] = acc;
-    __syncthreads();
-    for (uint32_t w = kThreads / 2; w > 0; w /= 2) {
-        if (t < w) part[t] = AMAX ? fmaxf(part[t], part[t + w]) : part[t] + part[t + w];
+    // blocks stride over the output rows: the grid is capped so that its
+    // work-item count stays below 2^32 however many rows there are
+    for (uint32_t row = blockIdx.x; row < n_rows; row += gridDim.x) {
+        const int64_t base = at(row, rows);
+        float acc = AMAX ? -INFINITY : 0.0f;
+        for (uint32_t k = t; k < dim_size; k += kThreads) {
+            const float x = Float<DT>::get(src, base + static_cast<int64_t>(k) * dim_stride);
+            acc = AMAX ? fmaxf(acc, x) : acc + x;
+        }
+        __syncthreads();  // the previous row's tree has read part[]
+        part[t] = acc;
         __syncthreads();
+        for (uint32_t w = kThreads / 2; w > 0; w /= 2) {
+            if (t < w) part[t] = AMAX ? fmaxf(part[t], part[t + w]) : part[t] + part[t + w];
+            __syncthreads();
+        }
+        if (t == 0) Float<DT>::put(dst, row, part[0]);
     }
-    if (t == 0) Float<DT>::put(dst, blockIdx.x, part[0]);
 }
 
 // argmax_rows (src/metal/kernels/reduce.metal:42-78): a thread keeps its
@@ -140,29 +146,32 @@ __global__ __launch_bounds__(kThreads) void reduce_kernel(const typename Float<D
 template <int DT>
 __global__ __launch_bounds__(kThreads) void argmax_kernel(const typename Float<DT>::T *__restrict__ src, View rows,
                                                           uint32_t dim_size, int64_t dim_stride,
-                                                          uint32_t *__restrict__ dst) {
+                                                          uint32_t *__restrict__ dst, uint32_t n_rows) {
     __shared__ float val[kThreads];
     __shared__ uint32_t idx[kThreads];
     const uint32_t t = threadIdx.x;
-    const int64_t base = at(blockIdx.x, rows);
-    float best = -INFINITY;
-    uint32_t best_i = 0;
-    for (uint32_t k = t; k < dim_size; k += kThreads) {
-        const float x = Float<DT>::get(src, base + static_cast<int64_t>(k) * dim_stride);
-        if (x > best) best = x, best_i = k;
-    }
-    val[t] = best;
-    idx[t] = best_i;
-    __syncthreads();
-    for (uint32_t w = kThreads / 2; w > 0; w /= 2) {
-        if (t < w) {
-            const float o = val[t + w];
-            const uint32_t oi = idx[t + w];
-            if (o > val[t] || (o == val[t] && oi < idx[t])) val[t] = o, idx[t] = oi;
+    for (uint32_t row = blockIdx.x; row < n_rows; row += gridDim.x) {  // as reduce_kernel
+        const int64_t base = at(row, rows);
+        float best = -INFINITY;
+        uint32_t best_i = 0;
+        for (uint32_t k = t; k < dim_size; k += kThreads) {
+            const float x = Float<DT>::get(src, base + static_cast<int64_t>(k) * dim_stride);
+            if (x > best) best = x, best_i = k;
         }
+        __syncthreads();  // the previous row's tree has read val[], idx[]
+        val[t] = best;
+        idx[t] = best_i;
         __syncthreads();
+        for (uint32_t w = kThreads / 2; w > 0; w /= 2) {
+            if (t < w) {
+                const float o = val[t + w];
+                const uint32_t oi = idx[t + w];
+                if (o > val[t] || (o == val[t] && oi < idx[t])) val[t] = o, idx[t] = oi;
+            }
+            __syncthreads();
+        }
+        if (t == 0) dst[row] = idx[0];
     }
-    if (t == 0) dst[blockIdx.x] = idx[0];
 }
 
 // Batched matmul over strided operands. A block owns a 32 x 32 output tile
@@ -486,29 +495,31 @@ extern "C" int fh_reduce(fh_device *dev, int op, int dtype, const void *src, con
     const int64_t stride = view->strides[dim];
     const uint32_t size = static_cast<uint32_t>(dim_size);
     return dispatch(dev, fn, [&] {
-        const dim3 grid(static_cast<uint32_t>(rows)), block(kThreads);
+        // at most 2^20 blocks (2^28 work-items); the kernels stride over the rest
+        const uint32_t n_rows = static_cast<uint32_t>(rows);
+        const dim3 grid(n_rows < (1u << 20) ? n_rows : (1u << 20)), block(kThreads);
         if (dtype == FH_F32) {
             auto *s = static_cast<const float *>(src);
             if (op == FH_SUM)
                 hipLaunchKernelGGL((reduce_kernel<FH_F32, false>), grid, block, 0, dev->stream, s, rv, size, stride,
-                                   static_cast<float *>(dst));
+                                   static_cast<float *>(dst), n_rows);
             else if (op == FH_AMAX)
                 hipLaunchKernelGGL((reduce_kernel<FH_F32, true>), grid, block, 0, dev->stream, s, rv, size, stride,
-                                   static_cast<float *>(dst));
+                                   static_cast<float *>(dst), n_rows);
             else
                 hipLaunchKernelGGL(argmax_kernel<FH_F32>, grid, block, 0, dev->stream, s, rv, size, stride,
-                                   static_cast<uint32_t *>(dst));
+                                   static_cast<uint32_t *>(dst), n_rows);
         } else {
             auto *s = static_cast<const uint16_t *>(src);
             if (op == FH_SUM)
                 hipLaunchKernelGGL((reduce_kernel<FH_BF16, false>), grid, block, 0, dev->stream, s, rv, size, stride,
-                                   static_cast<uint16_t *>(dst));
+                                   static_cast<uint16_t *>(dst), n_rows);
             else if (op == FH_AMAX)
                 hipLaunchKernelGGL((reduce_kernel<FH_BF16, true>), grid, block, 0, dev->stream, s, rv, size, stride,
-                                   static_cast<uint16_t *>(dst));
+                                   static_cast<uint16_t *>(dst), n_rows);
             else
                 hipLaunchKernelGGL(argmax_kernel<FH_BF16>, grid, block, 0, dev->stream, s, rv, size, stride,
-                                   static_cast<uint32_t *>(dst));
+                                   static_cast<uint32_t *>(dst), n_rows);
         }
     });
 }
@@ -551,6 +562,9 @@ extern "C" int fh_matmul(fh_device *dev, int dtype, const void *lhs, const fh_vi
     if (int rc = set_current(dev, fn)) return rc;
     const dim3 grid((s.n + kMmTile - 1) / kMmTile, (s.m + kMmTile - 1) / kMmTile, static_cast<uint32_t>(batch));
     if (grid.y > 65535) return fail(FH_ERR_INDEX_TOO_LARGE, "%s: m=%u exceeds the grid", fn, s.m);
+    // grid.x * 256 work-items must stay below 2^32
+    if (static_cast<uint64_t>(grid.x) * kThreads > 0xFFFFFFFFull)
+        return fail(FH_ERR_INDEX_TOO_LARGE, "%s: n=%u exceeds the grid", fn, s.n);
     return dispatch(dev, fn, [&] {
         if (dtype == FH_F32)
             hipLaunchKernelGGL(matmul_kernel<FH_F32>, grid, dim3(kThreads), 0, dev->stream,

@@ -174,10 +174,16 @@ class RefLlama:
         c, s = self.cos[pos][:, None, :], self.sin[pos][:, None, :]
         return rne(rne(x * c) + rne(rot * s))
 
-    def forward(self, ids, positions, batch=1):
+    def forward(self, ids, positions, batch=1, trace=None):
         """Returns the last position's logits (float32 of bf16 values). The
         sequence is one of `batch` run together: every linear call has batch
-        x len(ids) rows, the LM head `batch` (one last row per sequence)."""
+        x len(ids) rows, the LM head `batch` (one last row per sequence).
+        With a dict `trace`, layer l's module outputs are stored under
+        "l.<name>": qkv (the fused q/k/v projection, before RoPE), attn (the
+        attention output, o_proj's input), o (o_proj's output), h_attn (the
+        residual after attention), act (silu(gate) * up, down_proj's input),
+        mlp (down_proj's output) and h (the layer's output); "norm" holds the
+        final RMSNorm of the last row, the LM head's input."""
         c = self.cfg
         t = len(ids)
         rows = batch * t
@@ -201,12 +207,19 @@ class RefLlama:
                 kv = hh // group
                 out[:, hh, :] = sdpa(q[:, hh, :], self.k[li][kv, :ctx, :], self.v[li][kv, :ctx, :], pos, scale)
             a = self.linear(out.reshape(t, -1), L["o"], rows)
-            h = rne(h + a)
-            x = self.rms_norm(h, L["post_norm"])
+            h_attn = rne(h + a)
+            x = self.rms_norm(h_attn, L["post_norm"])
             gu = self.linear(x, L["gate_up"], rows)
             act = silu_mul(gu[:, :c.ffn], gu[:, c.ffn:])
-            h = rne(h + self.linear(act, L["down"], rows))
+            mlp = self.linear(act, L["down"], rows)
+            h = rne(h_attn + mlp)
+            if trace is not None:
+                for name, val in (("qkv", qkv), ("attn", out.reshape(t, -1)), ("o", a), ("h_attn", h_attn),
+                                  ("act", act), ("mlp", mlp), ("h", h)):
+                    trace[f"{li}.{name}"] = val
         x = self.rms_norm(h, self.final_norm)
+        if trace is not None:
+            trace["norm"] = x[-1:]
         return self.linear(x[-1:], self.embed_f, batch)[0]
 
     def generate(self, prompt, new_tokens, top_k=5, batch=1):
@@ -220,6 +233,7 @@ class RefLlama:
         logits = self.forward(ids, np.arange(len(ids)), batch)
         self.prefill_s = time.perf_counter() - t0
         self.first_logits = logits
+        self.step_logits = [logits]  # the logits that chose each token
         tokens, tops = [], []
         t0 = time.perf_counter()
         for step in range(new_tokens):
@@ -229,8 +243,45 @@ class RefLlama:
                 break
             p = len(prompt) + step
             logits = self.forward([tokens[-1]], np.array([p]), batch)
+            self.step_logits.append(logits)
         self.decode_s = time.perf_counter() - t0  # new_tokens - 1 single-token forwards
         return np.array(tokens, dtype=np.uint32), tops
+
+
+def compare_close(actual, expected, atol, rtol=1e-2):
+    """src/eval/compare.rs:54-91 and CloseReport::passed (:27-36): an element
+    is close when |a - e| <= atol + rtol * max(|a|, |e|); non-finite elements
+    on either side count against; the comparison passes when no element is
+    non-finite and at least 999 per mille are close. rtol is the reference's
+    RTOL (src/eval/mod.rs:53)."""
+    a = np.asarray(actual, np.float32).ravel()
+    e = np.asarray(expected, np.float32).ravel()
+    if a.shape != e.shape:
+        raise ValueError(f"element counts differ: {a.size} against {e.size}")
+    finite = np.isfinite(a) & np.isfinite(e)
+    err = np.abs(a - e)
+    bound = np.float32(atol) + np.float32(rtol) * np.maximum(np.abs(a), np.abs(e))
+    close = finite & (err <= bound)
+    n, n_close, n_bad = a.size, int(np.count_nonzero(close)), int(np.count_nonzero(~finite))
+    return {"numel": n, "close_count": n_close, "close_fraction": n_close / n if n else 1.0,
+            "non_finite_count": n_bad, "max_abs_error": float(err[finite].max()) if finite.any() else 0.0,
+            "passed": close_passed(n, n_close, n_bad)}
+
+
+def close_passed(numel, close_count, non_finite_count) -> bool:
+    """CloseReport::passed (src/eval/compare.rs:27-36): no non-finite element
+    and close_count * 1000 >= numel * 999."""
+    return non_finite_count == 0 and close_count * 1000 >= numel * 999
+
+
+def module_atol(name: str) -> float:
+    """src/models/llama/model.rs:362-368: by the module name's last part."""
+    last = name.rsplit(".", 1)[-1]
+    if last == "embed_tokens":
+        return 1e-3
+    if last in ("q_proj", "k_proj", "o_proj"):
+        return 2e-2
+    return 1e-2
 
 
 def argmax(values) -> int:

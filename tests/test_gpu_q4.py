@@ -206,6 +206,28 @@ def test_embed_empty(device):
     assert out.shape == (0, 64)
 
 
+@pytest.mark.parametrize("k", [3072, 4096])
+def test_embed_empty_table_writes_zero_rows(device, k):
+    """A table of 0 rows makes every id out of range: each output row is zero
+    (index_select_rows, src/metal/kernels/index_select.metal:11-29), and no
+    table byte is read. 1024 ids is past the row count at which the gather
+    takes its one-wavefront-per-row kernel for k = 3072 and 4096."""
+    n_ids = 1024
+    ids = np.arange(n_ids, dtype=np.uint32)
+    ids_t = up(device, ids, DType.U32)
+    table = device.empty(256)  # a live allocation that the call must not read
+    out = device.empty(n_ids * k * 2)
+    sentinel = np.full(n_ids * k, 0x7FC1, dtype=np.uint16)
+    _lib.call("fh_upload", device.handle, ctypes.c_void_p(out.ptr), sentinel.ctypes.data_as(ctypes.c_void_p),
+              sentinel.nbytes)
+    _lib.call("fh_q4_embed", device.handle, ctypes.c_void_p(table.ptr), ctypes.c_void_p(table.ptr),
+              ctypes.c_void_p(table.ptr), 0, k, 64, ctypes.c_void_p(ids_t.storage.ptr), n_ids,
+              ctypes.c_void_p(out.ptr))
+    got = np.empty(n_ids * k, dtype=np.uint16)
+    _lib.call("fh_download", device.handle, got.ctypes.data_as(ctypes.c_void_p), ctypes.c_void_p(out.ptr), got.nbytes)
+    assert not got.any(), "an empty table must give all-zero rows"
+
+
 # ---------------- GEMV (m <= 8) ----------------
 
 @pytest.mark.parametrize(
@@ -251,6 +273,26 @@ def test_gemm_parity(device, oracle, m, n, k):
 def test_gemm_config3_shapes_sampled(device, oracle):
     run_linear(device, oracle, 2048, 8192, 3072, seed=3, sample=(96, 8192))
     run_linear(device, oracle, 2048, 3072, 8192, seed=4, sample=(96, 3072))
+
+
+# Shapes with at least one 256 x 256 tile per CU take the ping-pong kernel
+# (q4_gemm_pp.hip): ragged last tile rows and columns (rows past m and weight
+# rows past n are read clamped and never stored), a row stride above k, and
+# the 8B-shape prefill's gate/up and down widths. Rows compared: the first
+# 16 and the last 48 (the ragged tile), every column.
+@pytest.mark.parametrize("m,n,k,x_ld", [(2085, 8288, 1024, 1024), (2048, 8192, 1024, 1096),
+                                        (4096, 14336, 512, 512), (4096, 4096, 1920, 1920)])
+def test_gemm_pingpong_ragged_and_strided(device, oracle, m, n, k, x_ld):
+    seed = 7000 + m + n + k
+    wq, s, b = synth.q4_weights(seed, n, k)
+    x = synth.bf16_normal(seed + 1, (m, x_ld))
+    w = weight(device, wq, s, b)
+    xt = up(device, x, DType.BF16)
+    y32 = matmul_raw(device, xt, w, m, k, x_ld, _lib.F32)
+    y16 = matmul_raw(device, xt, w, m, k, x_ld, _lib.BF16)
+    rows = np.concatenate([np.arange(16), np.arange(m - 48, m)])
+    y64 = oracle.linear_f64(np.ascontiguousarray(x[rows, :k]), wq, s, b)
+    check_matmul(y32[rows], y16[rows], y64)
 
 
 # Prompt-length rows whose tiles leave CUs idle split K (up to 8 ranges of

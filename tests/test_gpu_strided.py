@@ -349,6 +349,27 @@ def test_reductions_match_the_restated_order(device, dtype):
         assert np.array_equal(i, np.array([int(np.flatnonzero(r == r.max())[0]) for r in rows])), dim
 
 
+def test_reductions_over_more_rows_than_the_grid():
+    """More output rows (2^20 + 37) than the reduce grid's 2^20 blocks: the
+    blocks stride over the rows, and every row is still reduced in the
+    restated order (a row of 3: thread t takes element t, then the tree)."""
+    from foundry_amd.device import HipDevice
+
+    dev = HipDevice(0)
+    try:
+        rows = (1 << 20) + 37
+        x = (np.arange(rows * 3, dtype=np.int64) % 251).astype(np.float32).reshape(rows, 3) - 125.0
+        t = Tensor.from_numpy(dev, x, DType.F32)
+        s = t.sum_keepdim(dev, 1).to_numpy(dev).ravel()
+        m = t.amax_keepdim(dev, 1).to_numpy(dev).ravel()
+        i = t.argmax_keepdim(dev, 1).to_numpy(dev).ravel()
+        assert np.array_equal(s, (x[:, 0] + x[:, 1]) + x[:, 2])
+        assert np.array_equal(m, x.max(axis=1))
+        assert np.array_equal(i, x.argmax(axis=1).astype(np.uint32))
+    finally:
+        dev.close()
+
+
 @pytest.mark.parametrize("dtype", [DType.F32, DType.BF16])
 def test_matmul_on_strided_batches(device, dtype):
     rng = np.random.default_rng(10)

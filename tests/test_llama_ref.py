@@ -344,3 +344,61 @@ def test_linear_takes_each_kernels_weight_value():
     # the row count of the model's call, not of x, decides (a batch of sequences)
     x = R.rne(rng.standard_normal((1, 256)).astype(np.float32))
     assert np.array_equal(m.linear(x, w, rows=16), R.rne(x @ R.rne(w).T))
+
+
+def test_compare_close_reference_cases():
+    """src/eval/compare.rs:137-240: the absolute bound is inclusive, the
+    relative bound scales with the larger magnitude, non-finite elements are
+    counted apart (neither close nor in the maximum error), element counts
+    must agree, and passing needs 999 per mille close and nothing non-finite."""
+    r = R.compare_close([0.0, 0.0], [0.5, 0.75], atol=0.5, rtol=0.0)
+    assert (r["numel"], r["close_count"], r["close_fraction"], r["non_finite_count"], r["max_abs_error"]) == \
+        (2, 1, 0.5, 0, 0.75)
+    r = R.compare_close([2.0, 3.0], [1.0, 1.0], atol=0.0, rtol=0.5)
+    assert (r["close_count"], r["max_abs_error"]) == (1, 2.0)
+    r = R.compare_close([np.nan, 1.0, np.inf], [1.0, 1.0, 1.0], atol=1e-3, rtol=1e-2)
+    assert (r["numel"], r["close_count"], r["non_finite_count"], r["max_abs_error"]) == (3, 1, 2, 0.0)
+    assert r["close_fraction"] == 1.0 / 3.0 and not r["passed"]
+    with pytest.raises(ValueError):
+        R.compare_close([1.0], [1.0, 2.0], atol=1e-3)
+    assert [R.close_passed(1000, c, b) for c, b in ((1000, 0), (999, 0), (998, 0), (999, 1))] == \
+        [True, True, False, False]
+    # the reference's RTOL is the default, and 999 close of 1000 passes
+    e = np.ones(1000, np.float32)
+    a = e.copy()
+    a[0] = 2.0
+    assert R.compare_close(a, e, atol=1e-2)["passed"]
+    a[1] = 2.0
+    assert not R.compare_close(a, e, atol=1e-2)["passed"]
+
+
+def test_module_atol_by_the_last_name_part():
+    """src/models/llama/model.rs:362-368 and its test below it."""
+    assert [R.module_atol(n) for n in ("model.embed_tokens", "model.layers.0.self_attn.q_proj",
+                                       "model.layers.0.self_attn.k_proj", "model.layers.0.self_attn.o_proj",
+                                       "model.layers.0.self_attn.v_proj", "model.layers.0.mlp.down_proj",
+                                       "lm_head")] == [1e-3, 2e-2, 2e-2, 2e-2, 1e-2, 1e-2, 1e-2]
+
+
+def test_forward_trace_holds_each_module_output():
+    """The traced module outputs of a tiny model chain into each other: h_attn
+    = RNE(h_in + o), h = RNE(h_attn + mlp), o is o_proj applied to attn, and
+    the logits are the head applied to the traced final norm."""
+    from foundry_amd.llama import LlamaConfig, embed_weights, final_norm_weight, layer_weights
+
+    cfg = LlamaConfig(2, 128, 2, 1, 64, 192, 300)
+    m = R.RefLlama(cfg, embed_weights(cfg, 3, 7.5), [layer_weights(cfg, 3, l, 7.5) for l in range(2)],
+                   final_norm_weight(cfg, 3), 16)
+    trace = {}
+    ids = [5, 7, 11]
+    logits = m.forward(ids, np.arange(3), trace=trace)
+    h_in = R.rne(m.embed_f[np.asarray(ids)])
+    for l in range(2):
+        assert np.array_equal(trace[f"{l}.h_attn"], R.rne(h_in + trace[f"{l}.o"]))
+        assert np.array_equal(trace[f"{l}.o"], m.linear(trace[f"{l}.attn"], m.layers[l]["o"]))
+        assert np.array_equal(trace[f"{l}.h"], R.rne(trace[f"{l}.h_attn"] + trace[f"{l}.mlp"]))
+        assert np.array_equal(trace[f"{l}.mlp"], m.linear(trace[f"{l}.act"], m.layers[l]["down"]))
+        assert trace[f"{l}.qkv"].shape == (3, cfg.qkv_rows)
+        h_in = trace[f"{l}.h"]
+    assert np.array_equal(trace["norm"], m.rms_norm(h_in, m.final_norm)[-1:])
+    assert np.array_equal(logits, m.linear(trace["norm"], m.embed_f)[0])
