@@ -21,10 +21,13 @@
 //   next X fragments' LDS reads and the loads of later steps are interleaved
 //   with each sub-step's eight MFMAs (sched_group_barrier), so they issue in
 //   the MFMAs' shadow instead of in a phase of their own.
-// - X goes through LDS in three stages (per wavefront group of 128 rows, row
-//   pitch 72 bf16: conflict-free 16-byte fragment reads): step s + 2's X is
-//   stored while step s computes and step s + 1's first fragments are read
-//   at the end of step s, so one barrier per step suffices.
+// - X goes through LDS in four stages per wavefront group of 128 rows,
+//   brought by LDS DMA (buffer_load ... lds: no registers, no ds_write):
+//   step s + 3's X is requested while step s computes and step s + 1's first
+//   fragments are read at the end of step s, so one barrier per step
+//   suffices. Rows are 128 bytes with their 16-byte pieces XOR-swizzled by
+//   the row index, so 16-byte fragment reads are conflict-free without
+//   padding (the DMA writes 64 consecutive 16-byte slots).
 // - Dequantisation: exact nibble -> float (v_cvt_f32_ubyte of masked
 //   bytes), fma(s, q, b), RNE to bf16: the fh_q4_dequant value whenever s*q
 //   is finite.
@@ -45,10 +48,10 @@ namespace {
 
 constexpr int kDThreads = 512;
 constexpr int kDBM = 256, kDBN = 256, kDBK = 64;
-constexpr int kDPitch = kDBK + 8;                 // bf16 per X row in LDS
+constexpr int kDPitch = kDBK;                     // bf16 per X row in LDS (swizzled pieces)
 constexpr int kDRows = kDBM / 2;                  // X rows per wavefront group
 constexpr int kDStage = kDRows * kDPitch;         // bf16 per group stage
-constexpr int kDStages = 3;
+constexpr int kDStages = 4;
 constexpr uint32_t kDXLds = 2u * kDStages * kDStage * 2u;  // bytes, both groups
 // Scales and biases go through LDS in chunks of 8 groups (8 K steps), two
 // chunk buffers: [buffer][column][group][scale, bias], 4 bytes per group.
@@ -93,11 +96,6 @@ __device__ __forceinline__ bf16x8_t dequant8(uint32_t w, float s, float b) {
     return __builtin_bit_cast(bf16x8_t, o);
 }
 
-// One thread's X pieces of one step.
-struct XSet {
-    uint4 p0, p1, p2, p3;
-};
-
 // One lane's packed weights of one step: for each of its two B tiles, the 4
 // words of the group half it feeds.
 struct WSet {
@@ -118,7 +116,7 @@ __device__ __forceinline__ uint4 buf_load16(__amdgpu_buffer_rsrc_t r, uint32_t v
 }
 
 // sched_group_barrier masks
-constexpr int kSgMfma = 0x008, kSgValu = 0x002, kSgVmemRead = 0x020, kSgDsRead = 0x100, kSgDsWrite = 0x200;
+constexpr int kSgMfma = 0x008, kSgValu = 0x002, kSgVmemRead = 0x020, kSgDsRead = 0x100;
 
 }  // namespace
 
@@ -160,18 +158,19 @@ __global__ __launch_bounds__(kDThreads) void q4_gemm_direct_kernel(
 
     uint16_t *const xs_base = smem + grp * kDStages * kDStage;  // this group's stages
 
-    // X staging: thread t of the group stages pieces t + 256 i (i < 4) of the
-    // group's 128 x 64 step tile, 8 pieces of 16 bytes per row. Rows past m
-    // read row m - 1 (their outputs are never stored).
-    const uint32_t t = tid & 255;
+    // X staging by LDS DMA: wavefront (g, c) brings rows [32 c, 32 c + 32)
+    // of its group's 128-row step tile, as 4 chunks of 8 rows (1 KiB each,
+    // lane i -> row 8 q + i / 8, slot i % 8). Slot s of row r holds piece
+    // s ^ (r % 8), so a fragment read of 8 rows (one piece each) hits 32
+    // distinct banks.
     uint32_t xoff[4];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        uint32_t row = m0 + grp * kDRows + (t >> 3) + 32 * i;
+    for (int q = 0; q < 4; ++q) {
+        uint32_t row = m0 + grp * kDRows + wc * 32 + q * 8 + (lane >> 3);
         row = row < m ? row : m - 1;
-        xoff[i] = (row * x_ld + (t & 7) * 8) * 2;
+        const uint32_t piece = (lane & 7) ^ (lane >> 3);
+        xoff[q] = (row * x_ld + piece * 8) * 2;
     }
-    const uint32_t xdst = (t >> 3) * kDPitch + (t & 7) * 8;  // piece i: + 32 i rows
     // weights: B tile jj's column for this lane; rows past n read row 0
     uint32_t woff[2];
 #pragma unroll
@@ -200,21 +199,13 @@ __global__ __launch_bounds__(kDThreads) void q4_gemm_direct_kernel(
     const __amdgpu_buffer_rsrc_t rs = buffer_rsrc(scales, static_cast<uint64_t>(n) * kg * 2);
     const __amdgpu_buffer_rsrc_t rb = buffer_rsrc(biases, static_cast<uint64_t>(n) * kg * 2);
     const uint32_t last = steps - 1;
-    auto load_x = [&](uint32_t st) {
+    auto dma_x = [&](uint32_t st) {
         const uint32_t so = __builtin_amdgcn_readfirstlane((st < last ? st : last) * kDBK * 2);
-        XSet r;
-        r.p0 = buf_load16(rx, xoff[0], so);
-        r.p1 = buf_load16(rx, xoff[1], so);
-        r.p2 = buf_load16(rx, xoff[2], so);
-        r.p3 = buf_load16(rx, xoff[3], so);
-        return r;
-    };
-    auto store_x = [&](const XSet &r, uint32_t st) {
-        uint16_t *xs = xs_base + (st % kDStages) * kDStage + xdst;
-        *reinterpret_cast<uint4 *>(xs) = r.p0;
-        *reinterpret_cast<uint4 *>(xs + 32 * kDPitch) = r.p1;
-        *reinterpret_cast<uint4 *>(xs + 64 * kDPitch) = r.p2;
-        *reinterpret_cast<uint4 *>(xs + 96 * kDPitch) = r.p3;
+        uint16_t *xs = xs_base + (st % kDStages) * kDStage + wc * 32 * kDPitch;
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rx, (__attribute__((address_space(3))) void *)(xs + q * 8 * kDPitch), 16,
+                                                 static_cast<int>(xoff[q]), static_cast<int>(so), 0, 0);
     };
     auto load_w = [&](WSet &ws, uint32_t st) {
         st = st < last ? st : last;
@@ -252,9 +243,9 @@ __global__ __launch_bounds__(kDThreads) void q4_gemm_direct_kernel(
     };
     // A fragment of lane l for sub-step j of tile i: row 32 i + l % 32,
     // k = 32 h + 8 j .. + 7
-    const uint32_t frag = (lane & 31) * kDPitch + 32 * h;
+    const uint32_t frag = (lane & 31) * kDPitch + (((4 * h) ^ (lane & 7)) * 8);
     auto read_a = [&](uint32_t st, int j, bf16x8_t (&a)[4]) {
-        const uint16_t *xs = xs_base + (st % kDStages) * kDStage + frag + 8 * j;
+        const uint16_t *xs = xs_base + (st % kDStages) * kDStage + (frag ^ (8 * j));
 #pragma unroll
         for (int i = 0; i < 4; ++i) a[i] = *reinterpret_cast<const bf16x8_t *>(xs + i * 32 * kDPitch);
     };
@@ -267,28 +258,24 @@ __global__ __launch_bounds__(kDThreads) void q4_gemm_direct_kernel(
 #pragma unroll
             for (int r = 0; r < 16; ++r) acc[i][jj][r] = 0.f;
 
-    // Prologue: X(0), X(1) staged; X(2) and the weights of steps 0, 1 in
-    // flight; sub-step (0, 0)'s B fragments and sub-steps (0, 0), (0, 1)'s A
-    // fragments ready. The last loads issued are X(2), then W(1), as at the
+    // Prologue: X(0..2) staged, the weights of steps 0, 1 in flight;
+    // sub-step (0, 0)'s B fragments and sub-steps (0, 0), (0, 1)'s A
+    // fragments ready. The last loads issued are W(0), then W(1), as at the
     // end of every step (X(st + 3) at its start, W(st + 2) at its end), so
     // the loop's wait counts are those of the steady state.
     WSet w0, w1;
     uint4 sbr = load_sb(0);
-    XSet xr = load_x(0);
+    dma_x(0);
+    dma_x(1);
+    dma_x(2);
     __builtin_amdgcn_sched_barrier(0);
     load_w(w0, 0);
     __builtin_amdgcn_sched_barrier(0);
     store_sb(sbr, 0);
-    store_x(xr, 0);
-    __builtin_amdgcn_sched_barrier(0);
-    xr = load_x(1);
-    __builtin_amdgcn_sched_barrier(0);
-    store_x(xr, 1);
-    __builtin_amdgcn_sched_barrier(0);
-    xr = load_x(2);
     __builtin_amdgcn_sched_barrier(0);
     load_w(w1, 1);
     __builtin_amdgcn_sched_barrier(0);
+    __builtin_amdgcn_s_waitcnt(0);  // every DMA of X(0..2) has landed
     bf16x8_t b[2][2], a[2][4];
     uint32_t sb0[2], sb1[2];
     __syncthreads();
@@ -300,16 +287,16 @@ __global__ __launch_bounds__(kDThreads) void q4_gemm_direct_kernel(
     // Step st, sub-step j: the eight MFMAs of (st, j), interleaved with
     // - the dequantisation of the next sub-step ((st, j + 1), or (st + 1, 0)),
     // - the A reads of the sub-step after next ((st, j + 2), or (st + 1, j - 2)),
-    // - at j = 0: the store of X(st + 2) (loaded during step st - 1) and the
-    //   load of X(st + 3); at j = 3: the load of W(st + 2) into the set that
-    //   W(st) used (its last sub-step was dequantised at j = 2);
+    // - at j = 0: the DMA of X(st + 3) into the stage step st - 1 read; at
+    //   j = 3: the load of W(st + 2) into the set that W(st) used (its last
+    //   sub-step was dequantised at j = 2);
     // - at j = 1: the LDS read of step st + 1's scales and biases; in the
     //   first step of a chunk (st % 8 == 0) the load of chunk st / 8 + 1, and
     //   in its fifth step the store of that chunk into the other buffer
     //   (read from step st + 4 on; its previous contents, chunk st / 8 - 1,
     //   were last read in step st - 5).
     // One barrier per step, after sub-step 3: it publishes X(st + 2) and
-    // retires every read of the stage the next step's store reuses.
+    // retires every read of the stage the next step's DMA reuses.
     // q = st % 8 is a compile-time constant: the chunk loop below runs its
     // eight steps unrolled, so no load sits under a branch (a branch's join
     // would wait for every load in flight).
@@ -325,10 +312,7 @@ __global__ __launch_bounds__(kDThreads) void q4_gemm_direct_kernel(
 #pragma unroll
                 for (int jj = 0; jj < 2; ++jj)
                     acc[i][jj] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ac[i], bc[jj], acc[i][jj], 0, 0, 0);
-            if (j == 0) {
-                store_x(xr, st + 2);
-                xr = load_x(st + 3);
-            }
+            if (j == 0) dma_x(st + 3);
             if (j == 1) {
                 read_sb(st + 1, sbn);
                 if (q == 0) sbr = load_sb(st / kDSbGroups + 1);
@@ -345,10 +329,8 @@ __global__ __launch_bounds__(kDThreads) void q4_gemm_direct_kernel(
             if (j == 3) load_w(cur, st + 2);
             // 8 MFMAs, each followed by its share of the sub-step's other work
             if (j == 0) {
-                __builtin_amdgcn_sched_group_barrier(kSgMfma, 1, 0);
-                __builtin_amdgcn_sched_group_barrier(kSgDsWrite, 4, 0);
-                __builtin_amdgcn_sched_group_barrier(kSgMfma, 1, 0);
-                __builtin_amdgcn_sched_group_barrier(kSgVmemRead, 4, 0);
+                __builtin_amdgcn_sched_group_barrier(kSgMfma, 2, 0);
+                __builtin_amdgcn_sched_group_barrier(kSgVmemRead, 4, 0);  // the X DMA
             } else if (j == 3) {
                 __builtin_amdgcn_sched_group_barrier(kSgMfma, 1, 0);
                 __builtin_amdgcn_sched_group_barrier(kSgVmemRead, 6, 0);
@@ -365,7 +347,14 @@ __global__ __launch_bounds__(kDThreads) void q4_gemm_direct_kernel(
             // loads, which the next step's wait counts rely on)
             __builtin_amdgcn_sched_barrier(0);
             if (j == 3) {
-                __syncthreads();
+                // X(st + 2)'s DMA (issued in step st - 1) has landed: only
+                // W(st + 1), X(st + 3), W(st + 2) and at most one scale/bias
+                // chunk were issued after it (vmcnt(8)); this wavefront's LDS
+                // writes and reads are done (lgkmcnt(0)). The barrier is a
+                // bare s_barrier: a workgroup fence would also wait for the
+                // DMA of X(st + 3).
+                __builtin_amdgcn_s_waitcnt(0x0078);
+                __builtin_amdgcn_s_barrier();
                 __builtin_amdgcn_sched_barrier(0);
             }
         }
@@ -381,6 +370,10 @@ __global__ __launch_bounds__(kDThreads) void q4_gemm_direct_kernel(
         step(st + 7, std::integral_constant<uint32_t, 7>{}, w1, w0, sb1, sb0);
     }
 
+    // the DMAs of the last steps (re-reads of the last X tile) land before
+    // any wavefront reuses the LDS
+    __builtin_amdgcn_s_waitcnt(0x0f70);
+    __builtin_amdgcn_s_barrier();
     const uint32_t row_base = m0 + grp * kDRows + 4 * h;
     if (y_mode == 0) {
         // bf16 via LDS: the wavefront's 128 x 64 tile, row-major (pitch 72),
