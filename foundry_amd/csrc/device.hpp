@@ -42,7 +42,7 @@ constexpr uint64_t kPackAreaBytes = 8ull * 16384 * 2 + (16384 / 64) * 8 * 4 + 20
 // Bytes of each device's partial area: the f32 partial sums [ranges][rows][n]
 // of a GEMV split over K ranges, or [splits][m][n] of a GEMM split over K,
 // added in order by the matching combine kernel.
-constexpr uint64_t kPartialAreaBytes = 32ull << 20;
+constexpr uint64_t kPartialAreaBytes = 128ull << 20;
 // K splits of a prompt-length GEMM at most (their f32 partials share the area).
 constexpr uint32_t kMaxGemmSplits = 8;
 }  // namespace fh

@@ -301,17 +301,17 @@ __global__ __launch_bounds__(256) void gemm_split_reduce_kernel(const float *__r
 // gemm_split_reduce_kernel adds them in order. launch_q4_gemm_deferred stops
 // before that add and returns the split count (1: y was written), so that a
 // consumer of y can add the partials itself, in the same order.
-bool launch_q4_gemm_direct(hipStream_t stream, uint32_t cus, const uint16_t *x, uint32_t x_ld, const uint32_t *wq,
-                           const uint16_t *s, const uint16_t *b, uint32_t m, uint32_t n, uint32_t k, void *y,
-                           int y_is_f32);
+uint32_t launch_q4_gemm_direct(hipStream_t stream, uint32_t cus, const uint16_t *x, uint32_t x_ld,
+                               const uint32_t *wq, const uint16_t *s, const uint16_t *b, uint32_t m, uint32_t n,
+                               uint32_t k, void *y, int y_is_f32, void *area);
 
 uint32_t launch_q4_gemm_deferred(hipStream_t stream, uint32_t cus, const uint16_t *x, uint32_t x_ld,
                                  const uint32_t *wq, const uint16_t *s, const uint16_t *b, uint32_t m, uint32_t n,
                                  uint32_t k, void *y, int y_is_f32, void *area) {
     const uint64_t big = static_cast<uint64_t>((n + 255) / 256) * ((m + 255) / 256);
-    // 256 x 256 tiles fill the chip: weights straight to the matrix cores
-    // (q4_gemm_direct.hip)
-    if (launch_q4_gemm_direct(stream, cus, x, x_ld, wq, s, b, m, n, k, y, y_is_f32)) return 1;
+    // 256 x 256 tiles fill the chip, or 3/4 of it over two K ranges: weights
+    // straight to the matrix cores (q4_gemm_direct.hip)
+    if (const uint32_t d = launch_q4_gemm_direct(stream, cus, x, x_ld, wq, s, b, m, n, k, y, y_is_f32, area)) return d;
     if (big >= cus) {
         launch_gemm_tile<256, 256, 2, 4>(stream, x, x_ld, wq, s, b, m, n, k, y, y_is_f32, 1);
         return 1;

@@ -139,11 +139,13 @@ __device__ __forceinline__ void direct_tile(uint32_t L, uint32_t tiles_m, uint32
 }
 
 // y_mode: 0 bf16 through the LDS epilogue (n % 8 == 0, y 16-byte aligned),
-// 1 bf16 stored per value, 2 f32 stored per value.
+// 1 bf16 stored per value, 2 f32 stored per value. With gridDim.y = S > 1
+// the block takes K range blockIdx.y (k_len of the k columns, k = S k_len)
+// and writes its f32 partial tile to y[blockIdx.y][m][n] (y_mode 2).
 __global__ __launch_bounds__(kDThreads) void q4_gemm_direct_kernel(
     const uint16_t *__restrict__ x, uint32_t x_ld, const uint32_t *__restrict__ wq,
     const uint16_t *__restrict__ scales, const uint16_t *__restrict__ biases, uint32_t m, uint32_t n, uint32_t k,
-    void *__restrict__ y, int y_mode, uint32_t tiles_m, uint32_t tiles_n, uint32_t gm) {
+    void *__restrict__ y, int y_mode, uint32_t tiles_m, uint32_t tiles_n, uint32_t gm, uint32_t k_len) {
     extern __shared__ __attribute__((aligned(16))) uint16_t smem[];
     const uint32_t tid = threadIdx.x;
     const uint32_t lane = tid & 63;
@@ -152,8 +154,16 @@ __global__ __launch_bounds__(kDThreads) void q4_gemm_direct_kernel(
     uint32_t tm, tn;
     direct_tile(blockIdx.x, tiles_m, tiles_n, gm, &tm, &tn);
     const uint32_t m0 = tm * kDBM, n0 = tn * kDBN;
-    const uint32_t kw = k / 8, kg = k / kGroup;
-    const uint32_t steps = k / kDBK;
+    const uint32_t kw = k / 8, kg = k / kGroup;  // row strides (words, groups)
+    const uint32_t steps = k_len / kDBK;
+    {
+        const uint32_t k0 = blockIdx.y * k_len;
+        x += k0;
+        wq += k0 / 8;
+        scales += k0 / kGroup;
+        biases += k0 / kGroup;
+        y = static_cast<float *>(y) + static_cast<uint64_t>(blockIdx.y) * m * n;  // y_mode 2 when blockIdx.y > 0
+    }
     const uint32_t h = lane >> 5;
 
     uint16_t *const xs_base = smem + grp * kDStages * kDStage;  // this group's stages
@@ -184,7 +194,7 @@ __global__ __launch_bounds__(kDThreads) void q4_gemm_direct_kernel(
     uint32_t sbcol = n0 + (tid & 255);
     sbcol = sbcol < n ? sbcol : 0;
     const uint32_t sbgoff = sbcol * kg * 2;
-    const uint32_t chunks = kg / kDSbGroups;
+    const uint32_t chunks = k_len / kGroup / kDSbGroups;
     char *const sb_lds = reinterpret_cast<char *>(smem) + kDXLds;
     // this lane's dword of B tile jj in a chunk buffer, group 0
     uint32_t sbread[2];
@@ -420,19 +430,29 @@ __global__ __launch_bounds__(kDThreads) void q4_gemm_direct_kernel(
     }
 }
 
-// Launches the direct-weight GEMM when it applies: at least one 256 x 256
-// tile per CU (the 2048 x 8192 x 3072 gate/up shape has exactly 256), k a
-// multiple of 512 (whole scale/bias chunks) and every per-lane byte offset
-// within 32 bits. Returns false otherwise.
-bool launch_q4_gemm_direct(hipStream_t stream, uint32_t cus, const uint16_t *x, uint32_t x_ld, const uint32_t *wq,
-                           const uint16_t *s, const uint16_t *b, uint32_t m, uint32_t n, uint32_t k, void *y,
-                           int y_is_f32) {
+// Launches the direct-weight GEMM when it applies: 256 x 256 tiles that fill
+// the chip (the 2048 x 8192 x 3072 gate/up shape has exactly 256), or fill
+// at least 3/4 of it over two K ranges (the 2048 x 3072 x 8192 down shape:
+// 96 tiles, 192 blocks), k a multiple of 512 per range (whole scale/bias
+// chunks) and every per-lane byte offset within 32 bits. Returns 0 when it
+// does not apply, 1 when y was written, 2 when the two ranges' f32 partials
+// were left in `area` ([2][m][n], for the caller to add in order).
+uint32_t launch_q4_gemm_direct(hipStream_t stream, uint32_t cus, const uint16_t *x, uint32_t x_ld,
+                               const uint32_t *wq, const uint16_t *s, const uint16_t *b, uint32_t m, uint32_t n,
+                               uint32_t k, void *y, int y_is_f32, void *area) {
     const uint32_t tiles_m = (m + kDBM - 1) / kDBM, tiles_n = (n + kDBN - 1) / kDBN;
     const uint64_t tiles = static_cast<uint64_t>(tiles_m) * tiles_n;
+    uint32_t splits = 1;
+    if (tiles < cus) {
+        if (area == nullptr || 8 * tiles < 3ull * cus || k % (2 * kDSbGroups * kDBK) != 0 ||
+            2ull * m * n * 4 > kPartialAreaBytes)
+            return 0;
+        splits = 2;
+    }
     // k % 512: whole scale/bias chunks of 8 groups (and whole pairs of steps)
-    if (tiles < cus || tiles > 0x7FFFFFFFull || k % (kDSbGroups * kDBK) != 0 || k == 0 || m == 0) return false;
+    if (tiles > 0x7FFFFFFFull || k % (kDSbGroups * kDBK) != 0 || k == 0 || m == 0) return 0;
     if (static_cast<uint64_t>(m) * x_ld * 2 >= (1ull << 32) || static_cast<uint64_t>(n) * k / 2 >= (1ull << 32))
-        return false;
+        return 0;
     static bool lds_opt_in = false;
     if (!lds_opt_in) {
         (void)hipFuncSetAttribute(reinterpret_cast<const void *>(q4_gemm_direct_kernel),
@@ -443,7 +463,7 @@ bool launch_q4_gemm_direct(hipStream_t stream, uint32_t cus, const uint16_t *x, 
     // weight bytes one XCD brings in (gm tile rows of X, per_xcd / gm tile
     // columns of weights)
     const uint64_t per_xcd = (tiles + kXcds - 1) / kXcds;
-    const double x_tile = 256.0 * k * 2, w_tile = 256.0 * (k / 2 + 4 * (k / 64));
+    const double x_tile = 256.0 * k / splits * 2, w_tile = 256.0 * (k / 2 + 4 * (k / 64)) / splits;
     uint32_t gm = 1;
     double best = 1e300;
     for (uint32_t g = 1; g <= tiles_m && g <= per_xcd; ++g) {
@@ -451,10 +471,15 @@ bool launch_q4_gemm_direct(hipStream_t stream, uint32_t cus, const uint16_t *x, 
         const double bytes = g * x_tile + (cols < tiles_n ? cols : tiles_n) * w_tile;
         if (bytes < best) best = bytes, gm = g;
     }
+    if (splits > 1) {
+        hipLaunchKernelGGL(q4_gemm_direct_kernel, dim3(static_cast<uint32_t>(tiles), splits), dim3(kDThreads), kDLds,
+                           stream, x, x_ld, wq, s, b, m, n, k, area, 2, tiles_m, tiles_n, gm, k / splits);
+        return splits;
+    }
     const int y_mode = y_is_f32 ? 2 : (n % 8 == 0 && (reinterpret_cast<uintptr_t>(y) & 15) == 0) ? 0 : 1;
     hipLaunchKernelGGL(q4_gemm_direct_kernel, dim3(static_cast<uint32_t>(tiles)), dim3(kDThreads), kDLds, stream, x,
-                       x_ld, wq, s, b, m, n, k, y, y_mode, tiles_m, tiles_n, gm);
-    return true;
+                       x_ld, wq, s, b, m, n, k, y, y_mode, tiles_m, tiles_n, gm, k);
+    return 1;
 }
 
 }  // namespace fh
