@@ -396,19 +396,49 @@ def config5_parity(dev, cfg, seed, depth_ids, prompt_ids, first8, max_len):
     del one
     out = {"batch_invariance_seq0_prefill_logits_err": err(first8[0], first1),
            "batch_invariance_bit_identical_fraction": float(np.mean(first8[0] == first1))}
+    batch = depth_ids.shape[0]
     two = LlamaConfig(2, cfg.hidden, cfg.n_heads, cfg.n_kv_heads, cfg.head_dim, cfg.ffn, cfg.vocab)
-    m2 = Q4Llama(dev, two, seed, max_len, max_tokens=p, batch=depth_ids.shape[0])
-    got = m2.generate(prompt_ids, 2, depth=depth_ids)
-    step_logits = R.from_bf16(m2.logits())[0]
-    del m2
+    m2 = Q4Llama(dev, two, seed, max_len, max_tokens=p, batch=batch)
+    # greedy through the captured batch-8 decode step, reading sequence 0's
+    # logits after the prefill and after every step
+    m2.generate(prompt_ids, 1, depth=depth_ids)
+    gpu_logits = [R.from_bf16(m2.logits())[0]]
+    gpu_tokens = [int(m2.next_tokens()[0])]
+    graph = m2.capture_step()
+    for _ in range(CONFIG5_GREEDY - 1):
+        graph.launch()
+        gpu_logits.append(R.from_bf16(m2.logits())[0])
+        gpu_tokens.append(int(m2.next_tokens()[0]))
+    del graph, m2
     ref = R.RefLlama(two, embed_weights(two, seed), [layer_weights(two, seed, l) for l in range(2)],
                      final_norm_weight(two, seed), max_len)
-    ref.forward(list(np.concatenate([depth_ids[0], prompt_ids[0]])), np.arange(d + p), batch=depth_ids.shape[0])
-    want = ref.forward([int(got[0, 0])], np.array([d + p]), batch=depth_ids.shape[0])
-    out["restatement_2_layer_decode_step_logits_err"] = err(step_logits, want)
-    out["restatement_2_layer_top5_equal"] = R.top_ids(step_logits, 5) == R.top_ids(want, 5)
+    logits = ref.forward(list(np.concatenate([depth_ids[0], prompt_ids[0]])), np.arange(d + p), batch=batch)
+    exp_tokens, exp_tops = [], []
+    for i in range(CONFIG5_GREEDY):
+        exp_tokens.append(R.argmax(logits))
+        exp_tops.append(R.top_ids(logits, 5))
+        # step 1 is fed the GPU's token, so its logits compare like with like
+        # (the greedy rule below then follows the restatement's own tokens
+        # only while both agree)
+        feed = gpu_tokens[0] if i == 0 else exp_tokens[-1]
+        if i + 1 < CONFIG5_GREEDY:
+            logits = ref.forward([feed], np.array([d + p + i]), batch=batch)
+            if i == 0:
+                out["restatement_2_layer_decode_step_logits_err"] = err(gpu_logits[1], logits)
+                out["restatement_2_layer_top5_equal"] = R.top_ids(gpu_logits[1], 5) == R.top_ids(logits, 5)
+                if gpu_tokens[0] != exp_tokens[0]:
+                    break
+    n = len(exp_tokens)
+    gpu_tops = [R.top_ids(l, 5) for l in gpu_logits[:n]]
+    out["restatement_2_layer_greedy_seq0"] = {
+        **R.compare_generation(np.array(gpu_tokens[:n]), gpu_tops, np.array(exp_tokens), exp_tops),
+        "gpu_tokens": gpu_tokens[:n], "reference_arithmetic_tokens": exp_tokens}
     out["s"] = time.perf_counter() - t0
     return out
+
+
+# greedy steps of config 5's 2-layer restatement comparison (sequence 0)
+CONFIG5_GREEDY = 8
 
 
 def bench_decode_batched(dev, new_tokens: int, seed: int = 0, batch: int = 8, depth: int = 2048,
@@ -500,6 +530,33 @@ def greedy_agreement(model, cfg, seed, prompt, tokens, n):
                   "top5_gpu": R.top_ids(gpu_logits.astype(np.float32), 5),
                   "top5_reference_arithmetic": R.top_ids(ref_logits.astype(np.float32), 5),
                   "distinct_greedy_tokens": int(len(set(got.tolist())))}
+    # the batch-1 decode step itself (the captured graph the bench replays:
+    # dot2 GEMVs with the RMSNorm prologue and SiLU epilogue, the one-launch
+    # attention) from the prefill's token, against the restatement's step
+    # from the same token (its step_logits[1])
+    decode_step = None
+    if n > 1 and int(got[0]) == int(exp_tokens[0]):
+        graph = model.capture_step()
+        graph.launch()
+        step = R.from_bf16(model.logits()).astype(np.float64)
+        want = ref.step_logits[1].astype(np.float64)
+        decode_step = {"logits_max_abs_err_rel": float(np.max(np.abs(step - want)) / np.max(np.abs(want))),
+                       "top5_gpu": R.top_ids(step.astype(np.float32), 5),
+                       "top5_reference_arithmetic": R.top_ids(want.astype(np.float32), 5)}
+    # what the prefill GEMM's bf16 weight tiles cost against fp32 dequantised
+    # weights throughout (BASELINE's dequant arithmetic): the restatement's
+    # first-step logits both ways, and the GPU's against the fp32 one
+    saved = R.GEMV_MAX_ROWS
+    try:
+        R.GEMV_MAX_ROWS = 1 << 30
+        ref.reset()
+        f32_logits = ref.forward(list(int(i) for i in prompt), np.arange(len(prompt))).astype(np.float64)
+    finally:
+        R.GEMV_MAX_ROWS = saved
+    scale = np.max(np.abs(f32_logits))
+    drift = {"restatement_bf16_vs_fp32_weights_logits_err": float(np.max(np.abs(ref_logits - f32_logits)) / scale),
+             "gpu_vs_fp32_weight_restatement_logits_err": float(np.max(np.abs(gpu_logits - f32_logits)) / scale),
+             "top5_fp32_weights": R.top_ids(f32_logits.astype(np.float32), 5)}
     report = R.compare_generation(got, [[]] * n, exp_tokens, exp_tops)
     if report["first_divergence"] is not None:
         d = report["first_divergence"]
@@ -508,6 +565,8 @@ def greedy_agreement(model, cfg, seed, prompt, tokens, n):
         gpu_tops[d] = R.top_ids(R.from_bf16(model.logits()), 5)
         report = R.compare_generation(got, gpu_tops, exp_tokens, exp_tops)
     report["first_step"] = first_step
+    report["decode_step"] = decode_step
+    report["prefill_weight_rounding_drift"] = drift
     report["cpu_s"] = time.perf_counter() - t0
     # the restatement's own speed on this host (numpy fp32, one process)
     report["cpu_reference"] = {"threads": int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1)),

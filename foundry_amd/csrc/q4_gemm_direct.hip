@@ -54,7 +54,9 @@ constexpr int kDStage = kDRows * kDPitch;         // bf16 per group stage
 constexpr int kDStages = 4;
 constexpr uint32_t kDXLds = 2u * kDStages * kDStage * 2u;  // bytes, both groups
 // Scales and biases go through LDS in chunks of 8 groups (8 K steps), two
-// chunk buffers: [buffer][column][group][scale, bias], 4 bytes per group.
+// chunk buffers: [buffer][group][column][scale, bias], 4 bytes per (group,
+// column), so the 32 columns a wavefront reads per step are consecutive
+// dwords (no bank conflicts).
 // (Loaded per step and per lane they cost 4 loads that each touch 32 cache
 // lines for 256 useful bytes, and took 40% of the kernel.)
 constexpr int kDSbGroups = 8;
@@ -66,6 +68,14 @@ constexpr int kDOutPitch = 64 + 8;
 constexpr uint32_t kDOutLds = 8u * 128u * kDOutPitch * 2u;
 constexpr uint32_t kDLds = kDLoopLds > kDOutLds ? kDLoopLds : kDOutLds;
 constexpr uint32_t kXcds = 8;
+// Weight register sets: W(st) is requested kDWSets steps before its step
+// (at the end of step st - kDWSets), into the set W(st - kDWSets) used. Four
+// sets (three steps of lead, 244 VGPRs) measured no faster than two.
+#ifndef FH_DIRECT_WSETS
+#define FH_DIRECT_WSETS 2
+#endif
+constexpr int kDWSets = FH_DIRECT_WSETS;
+static_assert(kDWSets == 2 || kDWSets == 4, "the 8-step chunk loop cycles through the sets");
 
 typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8_t;
 typedef __attribute__((ext_vector_type(16))) float f32x16_t;
@@ -171,14 +181,16 @@ __global__ __launch_bounds__(kDThreads) void q4_gemm_direct_kernel(
     // X staging by LDS DMA: wavefront (g, c) brings rows [32 c, 32 c + 32)
     // of its group's 128-row step tile, as 4 chunks of 8 rows (1 KiB each,
     // lane i -> row 8 q + i / 8, slot i % 8). Slot s of row r holds piece
-    // s ^ (r % 8), so a fragment read of 8 rows (one piece each) hits 32
-    // distinct banks.
+    // s ^ ((r / 2) % 8): a 128-byte row covers half the 64 banks, so the 16
+    // rows of one 16-lane fragment read (one piece each) start at 16
+    // distinct 4-bank offsets, (r % 2) * 32 + 4 * slot, and hit all 64
+    // banks once. (With s ^ (r % 8), rows r and r + 8 of a read collided.)
     uint32_t xoff[4];
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
         uint32_t row = m0 + grp * kDRows + wc * 32 + q * 8 + (lane >> 3);
         row = row < m ? row : m - 1;
-        const uint32_t piece = (lane & 7) ^ (lane >> 3);
+        const uint32_t piece = (lane & 7) ^ ((4 * q + (lane >> 4)) & 7);
         xoff[q] = (row * x_ld + piece * 8) * 2;
     }
     // weights: B tile jj's column for this lane; rows past n read row 0
@@ -199,7 +211,7 @@ __global__ __launch_bounds__(kDThreads) void q4_gemm_direct_kernel(
     // this lane's dword of B tile jj in a chunk buffer, group 0
     uint32_t sbread[2];
 #pragma unroll
-    for (int jj = 0; jj < 2; ++jj) sbread[jj] = (wc * 64 + jj * 32 + (lane & 31)) * kDSbGroups * 4;
+    for (int jj = 0; jj < 2; ++jj) sbread[jj] = (wc * 64 + jj * 32 + (lane & 31)) * 4;
 
     // Loads are buffer loads: a per-lane 32-bit byte offset plus the step's
     // offset as a scalar (readfirstlane keeps it scalar), so no lane keeps a
@@ -228,16 +240,16 @@ __global__ __launch_bounds__(kDThreads) void q4_gemm_direct_kernel(
         c = c < chunks ? c : chunks - 1;
         return buf_load16(grp ? rb : rs, sbgoff, __builtin_amdgcn_readfirstlane(c * kDSbGroups * 2));
     };
-    // ... stored as [column][group][scale, bias] into chunk c's buffer
+    // ... stored as [group][column][scale, bias] into chunk c's buffer
     auto store_sb = [&](const uint4 &v, uint32_t c) {
-        uint16_t *dst = reinterpret_cast<uint16_t *>(sb_lds + (c & 1) * kDSbBuf + (tid & 255) * kDSbGroups * 4) + grp;
+        uint16_t *dst = reinterpret_cast<uint16_t *>(sb_lds + (c & 1) * kDSbBuf + (tid & 255) * 4) + grp;
         const uint32_t d[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
-        for (int g = 0; g < kDSbGroups; ++g) dst[2 * g] = static_cast<uint16_t>(d[g / 2] >> (16 * (g % 2)));
+        for (int g = 0; g < kDSbGroups; ++g) dst[g * kDBN * 2] = static_cast<uint16_t>(d[g / 2] >> (16 * (g % 2)));
     };
     // step st's (scale | bias << 16) for this lane's two B tiles
     auto read_sb = [&](uint32_t st, uint32_t (&sb)[2]) {
-        const char *base = sb_lds + ((st / kDSbGroups) & 1) * kDSbBuf + (st % kDSbGroups) * 4;
+        const char *base = sb_lds + ((st / kDSbGroups) & 1) * kDSbBuf + (st % kDSbGroups) * kDBN * 4;
 #pragma unroll
         for (int jj = 0; jj < 2; ++jj) sb[jj] = *reinterpret_cast<const uint32_t *>(base + sbread[jj]);
     };
@@ -252,8 +264,8 @@ __global__ __launch_bounds__(kDThreads) void q4_gemm_direct_kernel(
         }
     };
     // A fragment of lane l for sub-step j of tile i: row 32 i + l % 32,
-    // k = 32 h + 8 j .. + 7
-    const uint32_t frag = (lane & 31) * kDPitch + (((4 * h) ^ (lane & 7)) * 8);
+    // k = 32 h + 8 j .. + 7, i.e. piece 4 h + j in slot (4 h + j) ^ (l / 2 % 8)
+    const uint32_t frag = (lane & 31) * kDPitch + (((4 * h) ^ ((lane >> 1) & 7)) * 8);
     auto read_a = [&](uint32_t st, int j, bf16x8_t (&a)[4]) {
         const uint16_t *xs = xs_base + (st % kDStages) * kDStage + (frag ^ (8 * j));
 #pragma unroll
@@ -268,29 +280,28 @@ __global__ __launch_bounds__(kDThreads) void q4_gemm_direct_kernel(
 #pragma unroll
             for (int r = 0; r < 16; ++r) acc[i][jj][r] = 0.f;
 
-    // Prologue: X(0..2) staged, the weights of steps 0, 1 in flight;
-    // sub-step (0, 0)'s B fragments and sub-steps (0, 0), (0, 1)'s A
-    // fragments ready. The last loads issued are W(0), then W(1), as at the
-    // end of every step (X(st + 3) at its start, W(st + 2) at its end), so
-    // the loop's wait counts are those of the steady state.
-    WSet w0, w1;
+    // Prologue: X(0..2) staged, the weights of steps 0 .. kDWSets - 1
+    // loaded; sub-step (0, 0)'s B fragments and sub-steps (0, 0), (0, 1)'s A
+    // fragments ready.
+    WSet ws[kDWSets];
     uint4 sbr = load_sb(0);
     dma_x(0);
     dma_x(1);
     dma_x(2);
     __builtin_amdgcn_sched_barrier(0);
-    load_w(w0, 0);
+    load_w(ws[0], 0);
     __builtin_amdgcn_sched_barrier(0);
     store_sb(sbr, 0);
     __builtin_amdgcn_sched_barrier(0);
-    load_w(w1, 1);
+#pragma unroll
+    for (int i = 1; i < kDWSets; ++i) load_w(ws[i], i);
     __builtin_amdgcn_sched_barrier(0);
     __builtin_amdgcn_s_waitcnt(0);  // every DMA of X(0..2) has landed
     bf16x8_t b[2][2], a[2][4];
     uint32_t sb0[2], sb1[2];
     __syncthreads();
     read_sb(0, sb0);
-    dequant(w0, sb0, 0, b[0]);
+    dequant(ws[0], sb0, 0, b[0]);
     read_a(0, 0, a[0]);
     read_a(0, 1, a[1]);
 
@@ -298,8 +309,8 @@ __global__ __launch_bounds__(kDThreads) void q4_gemm_direct_kernel(
     // - the dequantisation of the next sub-step ((st, j + 1), or (st + 1, 0)),
     // - the A reads of the sub-step after next ((st, j + 2), or (st + 1, j - 2)),
     // - at j = 0: the DMA of X(st + 3) into the stage step st - 1 read; at
-    //   j = 3: the load of W(st + 2) into the set that W(st) used (its last
-    //   sub-step was dequantised at j = 2);
+    //   j = 3: the load of W(st + kDWSets) into the set that W(st) used (its
+    //   last sub-step was dequantised at j = 2);
     // - at j = 1: the LDS read of step st + 1's scales and biases; in the
     //   first step of a chunk (st % 8 == 0) the load of chunk st / 8 + 1, and
     //   in its fifth step the store of that chunk into the other buffer
@@ -336,7 +347,7 @@ __global__ __launch_bounds__(kDThreads) void q4_gemm_direct_kernel(
                 read_a(st, j + 2, ac);
             else
                 read_a(st + 1, j - 2, ac);
-            if (j == 3) load_w(cur, st + 2);
+            if (j == 3) load_w(cur, st + kDWSets);
             // 8 MFMAs, each followed by its share of the sub-step's other work
             if (j == 0) {
                 __builtin_amdgcn_sched_group_barrier(kSgMfma, 2, 0);
@@ -358,26 +369,27 @@ __global__ __launch_bounds__(kDThreads) void q4_gemm_direct_kernel(
             __builtin_amdgcn_sched_barrier(0);
             if (j == 3) {
                 // X(st + 2)'s DMA (issued in step st - 1) has landed: only
-                // W(st + 1), X(st + 3), W(st + 2) and at most one scale/bias
-                // chunk were issued after it (vmcnt(8)); this wavefront's LDS
+                // W(st - 1 + kDWSets), X(st + 3), W(st + kDWSets) and, in the
+                // first step of a chunk, one scale/bias chunk were issued
+                // after it (vmcnt(8), or 9); this wavefront's LDS
                 // writes and reads are done (lgkmcnt(0)). The barrier is a
                 // bare s_barrier: a workgroup fence would also wait for the
                 // DMA of X(st + 3).
-                __builtin_amdgcn_s_waitcnt(0x0078);
+                __builtin_amdgcn_s_waitcnt(q == 0 ? 0x0079 : 0x0078);
                 __builtin_amdgcn_s_barrier();
                 __builtin_amdgcn_sched_barrier(0);
             }
         }
     };
     for (uint32_t st = 0; st < steps; st += kDSbGroups) {
-        step(st, std::integral_constant<uint32_t, 0>{}, w0, w1, sb0, sb1);
-        step(st + 1, std::integral_constant<uint32_t, 1>{}, w1, w0, sb1, sb0);
-        step(st + 2, std::integral_constant<uint32_t, 2>{}, w0, w1, sb0, sb1);
-        step(st + 3, std::integral_constant<uint32_t, 3>{}, w1, w0, sb1, sb0);
-        step(st + 4, std::integral_constant<uint32_t, 4>{}, w0, w1, sb0, sb1);
-        step(st + 5, std::integral_constant<uint32_t, 5>{}, w1, w0, sb1, sb0);
-        step(st + 6, std::integral_constant<uint32_t, 6>{}, w0, w1, sb0, sb1);
-        step(st + 7, std::integral_constant<uint32_t, 7>{}, w1, w0, sb1, sb0);
+        step(st, std::integral_constant<uint32_t, 0>{}, ws[0 % kDWSets], ws[1 % kDWSets], sb0, sb1);
+        step(st + 1, std::integral_constant<uint32_t, 1>{}, ws[1 % kDWSets], ws[2 % kDWSets], sb1, sb0);
+        step(st + 2, std::integral_constant<uint32_t, 2>{}, ws[2 % kDWSets], ws[3 % kDWSets], sb0, sb1);
+        step(st + 3, std::integral_constant<uint32_t, 3>{}, ws[3 % kDWSets], ws[4 % kDWSets], sb1, sb0);
+        step(st + 4, std::integral_constant<uint32_t, 4>{}, ws[4 % kDWSets], ws[5 % kDWSets], sb0, sb1);
+        step(st + 5, std::integral_constant<uint32_t, 5>{}, ws[5 % kDWSets], ws[6 % kDWSets], sb1, sb0);
+        step(st + 6, std::integral_constant<uint32_t, 6>{}, ws[6 % kDWSets], ws[7 % kDWSets], sb0, sb1);
+        step(st + 7, std::integral_constant<uint32_t, 7>{}, ws[7 % kDWSets], ws[8 % kDWSets], sb1, sb0);
     }
 
     // the DMAs of the last steps (re-reads of the last X tile) land before

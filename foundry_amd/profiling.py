@@ -38,15 +38,17 @@ def kernel_stats(directory: str):
 
 
 def trace_medians(directory: str):
-    """[(name, grid, block, dispatches, median_us, total_ms)] from the
-    per-dispatch rows of a *_kernel_trace.csv, grouped by kernel and grid."""
+    """[(name, grid, block, dispatches, median_us, mean_us, total_ms)] from
+    the per-dispatch rows of a *_kernel_trace.csv, grouped by kernel and
+    grid."""
     groups = {}
     for r in _rows(os.path.join(directory, "**", "*kernel_trace.csv")):
         key = (r["Kernel_Name"], f'{r["Grid_Size_X"]} x {r["Grid_Size_Y"]} x {r["Grid_Size_Z"]}',
                r["Workgroup_Size_X"])
         groups.setdefault(key, []).append((int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3)
-    out = [(k[0], k[1], k[2], len(v), statistics.median(v), sum(v) / 1e3) for k, v in groups.items()]
-    return sorted(out, key=lambda t: -t[5])
+    out = [(k[0], k[1], k[2], len(v), statistics.median(v), statistics.mean(v), sum(v) / 1e3)
+           for k, v in groups.items()]
+    return sorted(out, key=lambda t: -t[6])
 
 
 def counters_by_kernel(directory: str, kernel_substring: str):
@@ -83,11 +85,11 @@ def main(argv):
             print(f"| {name[:90]} | {calls} | {avg / 1e3:.2f} | {total / 1e6:.3f} |")
         return 0
     if len(argv) >= 2 and argv[0] == "trace":
-        print("| Kernel | grid | block | dispatches | median us | total ms |")
-        print("|---|---|---|---|---|---|")
-        for name, grid, block, n, med, total in trace_medians(argv[1]):
+        print("| Kernel | grid | block | dispatches | median us | mean us | total ms |")
+        print("|---|---|---|---|---|---|---|")
+        for name, grid, block, n, med, mean, total in trace_medians(argv[1]):
             short = name.split("(")[0][:80]
-            print(f"| `{short}` | {grid} | {block} | {n} | {med:.2f} | {total:.3f} |")
+            print(f"| `{short}` | {grid} | {block} | {n} | {med:.2f} | {mean:.2f} | {total:.3f} |")
         return 0
     if len(argv) >= 3 and argv[0] == "counters":
         for (kernel, grid), d in sorted(counters_by_kernel(argv[1], argv[2]).items()):
