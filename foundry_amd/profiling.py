@@ -3,13 +3,14 @@
     python -m foundry_amd.profiling stats <dir>        # kernel-trace --stats CSV
     python -m foundry_amd.profiling trace <dir>        # per-dispatch medians from the kernel trace
     python -m foundry_amd.profiling counters <dir> <kernel-substring>   # --pmc values per dispatch
-    python -m foundry_amd.profiling traffic <fetch_dir> <write_dir> <kernel-substring>
+    python -m foundry_amd.profiling traffic <fetch_dir> <write_dir> <kernel-substring> [grid-size]
 
 ``traffic`` takes two ``rocprofv3 --pmc`` runs of the same command, one with
 FETCH_SIZE and one with WRITE_SIZE (KiB per dispatch), each of which also ran
 ``bench.py --calibrate-copy`` (a device-to-device copy of a known byte count).
 Each counter is scaled by known bytes / what the counter read for the copy
-kernel, then averaged over the dispatches of the named kernel.
+kernel, then averaged over the dispatches of the named kernel (of the given
+total grid size, in work-items, when one is given).
 """
 from __future__ import annotations
 
@@ -62,15 +63,16 @@ def counters_by_kernel(directory: str, kernel_substring: str):
     return {k: {c: (statistics.mean(v), len(v)) for c, v in d.items()} for k, d in acc.items()}
 
 
-def counter_per_dispatch(directory: str, counter: str, kernel_substring: str):
+def counter_per_dispatch(directory: str, counter: str, kernel_substring: str, grid: str | None = None):
     vals = [float(r["Counter_Value"]) for r in _rows(os.path.join(directory, "**", "*counter_collection.csv"))
-            if r["Counter_Name"] == counter and kernel_substring in r["Kernel_Name"]]
+            if r["Counter_Name"] == counter and kernel_substring in r["Kernel_Name"]
+            and (grid is None or r["Grid_Size"] == grid)]
     return vals
 
 
-def scaled_bytes(directory: str, counter: str, kernel_substring: str):
+def scaled_bytes(directory: str, counter: str, kernel_substring: str, grid: str | None = None):
     """Mean bytes per dispatch of the kernel, scaled by the copy calibration."""
-    kernel = counter_per_dispatch(directory, counter, kernel_substring)
+    kernel = counter_per_dispatch(directory, counter, kernel_substring, grid)
     copy = counter_per_dispatch(directory, counter, COPY_KERNEL)
     if not kernel or not copy:
         raise RuntimeError(f"{counter}: no dispatches of {kernel_substring!r} or of the copy kernel in {directory}")
@@ -98,8 +100,9 @@ def main(argv):
                 print(f"  {name}={mean:.6g} (mean of {n} dispatches)")
         return 0
     if len(argv) >= 4 and argv[0] == "traffic":
-        fetch, fscale, n1 = scaled_bytes(argv[1], "FETCH_SIZE", argv[3])
-        write, wscale, n2 = scaled_bytes(argv[2], "WRITE_SIZE", argv[3])
+        grid = argv[4] if len(argv) >= 5 else None
+        fetch, fscale, n1 = scaled_bytes(argv[1], "FETCH_SIZE", argv[3], grid)
+        write, wscale, n2 = scaled_bytes(argv[2], "WRITE_SIZE", argv[3], grid)
         print(f"fetch_bytes_per_dispatch={fetch:.0f} (scale {fscale:.4f}, {n1} dispatches)")
         print(f"write_bytes_per_dispatch={write:.0f} (scale {wscale:.4f}, {n2} dispatches)")
         print(f"traffic_bytes_per_dispatch={fetch + write:.0f}")

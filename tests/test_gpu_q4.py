@@ -275,14 +275,15 @@ def test_gemm_config3_shapes_sampled(device, oracle):
     run_linear(device, oracle, 2048, 3072, 8192, seed=4, sample=(96, 3072))
 
 
-# Shapes with at least one 256 x 256 tile per CU take the ping-pong kernel
-# (q4_gemm_pp.hip): ragged last tile rows and columns (rows past m and weight
-# rows past n are read clamped and never stored), a row stride above k, and
-# the 8B-shape prefill's gate/up and down widths. Rows compared: the first
-# 16 and the last 48 (the ragged tile), every column.
+# Shapes with at least one 256 x 256 tile per CU take the direct-weight
+# kernel (q4_gemm_direct.hip) when k is a multiple of 512, else the LDS-staged
+# one (q4_gemm.hip, k = 1920): ragged last tile rows and columns (rows past m
+# and weight rows past n are read clamped and never stored), a row stride
+# above k, and the 8B-shape prefill's gate/up and down widths. Rows compared:
+# the first 16 and the last 48 (the ragged tile), every column.
 @pytest.mark.parametrize("m,n,k,x_ld", [(2085, 8288, 1024, 1024), (2048, 8192, 1024, 1096),
                                         (4096, 14336, 512, 512), (4096, 4096, 1920, 1920)])
-def test_gemm_pingpong_ragged_and_strided(device, oracle, m, n, k, x_ld):
+def test_gemm_full_chip_ragged_and_strided(device, oracle, m, n, k, x_ld):
     seed = 7000 + m + n + k
     wq, s, b = synth.q4_weights(seed, n, k)
     x = synth.bf16_normal(seed + 1, (m, x_ld))
@@ -292,6 +293,29 @@ def test_gemm_pingpong_ragged_and_strided(device, oracle, m, n, k, x_ld):
     y16 = matmul_raw(device, xt, w, m, k, x_ld, _lib.BF16)
     rows = np.concatenate([np.arange(16), np.arange(m - 48, m)])
     y64 = oracle.linear_f64(np.ascontiguousarray(x[rows, :k]), wq, s, b)
+    check_matmul(y32[rows], y16[rows], y64)
+
+
+# Prompt-length GEMMs with fewer 256 x 256 tiles than CUs: the direct-weight
+# kernel over two K ranges (2048 x 3072 x 8192, ragged 2000 x 3000 x 8192,
+# 512 x 16384 x 3072) or the LDS-staged kernel split over K (1024 x 4096 x
+# 8192), the ranges' f32 partials added in order by the reduce kernel. Rows
+# compared: the first 16, 32 sampled, the last 48; every column. A second
+# run is bit-identical.
+@pytest.mark.parametrize("m,n,k", [(2048, 3072, 8192), (2000, 3000, 8192), (512, 16384, 3072), (1024, 4096, 8192)])
+def test_gemm_split_ranges_sampled_and_repeatable(device, oracle, m, n, k):
+    seed = 9000 + m + n + k
+    wq, s, b = synth.q4_weights(seed, n, k)
+    x = synth.bf16_normal(seed + 1, (m, k))
+    w = weight(device, wq, s, b)
+    xt = up(device, x, DType.BF16)
+    y32 = matmul_raw(device, xt, w, m, k, k, _lib.F32)
+    y16 = matmul_raw(device, xt, w, m, k, k, _lib.BF16)
+    again = matmul_raw(device, xt, w, m, k, k, _lib.F32)
+    assert np.array_equal(y32.view(np.uint32), again.view(np.uint32)), "split-K sums differ between runs"
+    rng = np.random.default_rng(seed)
+    rows = np.unique(np.concatenate([np.arange(16), rng.integers(16, m - 48, 32), np.arange(m - 48, m)]))
+    y64 = oracle.linear_f64(np.ascontiguousarray(x[rows]), wq, s, b)
     check_matmul(y32[rows], y16[rows], y64)
 
 
