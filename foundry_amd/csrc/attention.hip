@@ -34,7 +34,10 @@
 //       rows.
 //   fh_attention with head_dim 128 uses attn_pv_tile_kernel instead: the
 //   query-row tiles of the scores, P.V on the matrix cores (M and S combined
-//   over each row's chunks in another fixed order).
+//   over each row's chunks in another fixed order). A prompt-length call
+//   whose 256-pair query tiles fill half the device takes one launch of
+//   attn_flash_kernel instead (attention_flash.hip): both passes over the
+//   keys in one block per tile, no workspace.
 //   Every output element is a sum in a fixed order, so results do not
 //   change from run to run.
 // splits and slices make rows * n_kv * (blocks per pair) about
@@ -53,6 +56,12 @@
 #endif
 
 namespace fh {
+
+// The one-pass prefill kernel (attention_flash.hip); false when it does not
+// apply to the shape.
+bool launch_attention_flash(hipStream_t stream, uint32_t cus, const uint16_t *q, const uint32_t *positions,
+                            uint32_t rows, const uint16_t *k_cache, const uint16_t *v_cache, uint32_t n_heads,
+                            uint32_t n_kv, uint32_t head_dim, uint32_t max_len, float scale, uint16_t *out);
 
 constexpr int kAttnChunk = 64;
 constexpr int kAttnThreads = 256;
@@ -1458,8 +1467,13 @@ extern "C" int fh_attention(fh_device *dev, const uint16_t *q, const uint16_t *k
                      const_cast<uint16_t *>(v_cache), 0, static_cast<uint32_t>(n_heads),
                      static_cast<uint32_t>(n_kv), static_cast<uint32_t>(max_len), scale,
                      static_cast<char *>(workspace), out};
+    // prompt-length calls that fill the device: the one-pass kernel
+    // (attention_flash.hip), which leaves the workspace untouched
     return dispatch(dev, fn, [&] {
-        launch_attention_shape<false>(head_dim, n_heads / n_kv, dev->stream, static_cast<uint32_t>(tokens), a, x);
+        if (!launch_attention_flash(dev->stream, dev->compute_units, q, positions, static_cast<uint32_t>(tokens),
+                                    k_cache, v_cache, static_cast<uint32_t>(n_heads), static_cast<uint32_t>(n_kv),
+                                    static_cast<uint32_t>(head_dim), static_cast<uint32_t>(max_len), scale, out))
+            launch_attention_shape<false>(head_dim, n_heads / n_kv, dev->stream, static_cast<uint32_t>(tokens), a, x);
     });
 }
 

@@ -117,16 +117,17 @@ def test_rope_out_of_range_position_writes_nothing(device):
     assert not down(device, vc, np.uint16, c.n_kv_heads * max_len * c.head_dim).any()
 
 
-def attention_ref(q, kc, vc, pos, scale):
-    """Per (token, head) restatement of the reference SDPA rounding points.
+def attention_ref(q, kc, vc, pos, scale, rows=None):
+    """Per (token, head) restatement of the reference SDPA rounding points
+    (for the given token rows only, when given: the others are left zero).
     Also returns, per (token, head), the output shift one probability
     rounding the other way can cause: ulp(max p) * max|v|."""
     t, n_heads, _ = q.shape
     group = n_heads // kc.shape[0]
     qf, kf, vf = R.from_bf16(q), R.from_bf16(kc), R.from_bf16(vc)
-    out = np.empty(q.shape, np.float32)
-    flip = np.empty((t, n_heads), np.float32)
-    for i in range(t):
+    out = np.zeros(q.shape, np.float32)
+    flip = np.zeros((t, n_heads), np.float32)
+    for i in (range(t) if rows is None else rows):
         ctx = min(int(pos[i]) + 1, kc.shape[1])
         for h in range(n_heads):
             kv = h // group
@@ -189,6 +190,36 @@ def test_attention(device, n_heads, n_kv, hd, t, max_len):
     got, scale, _ = run_attention(device, q, kc, vc, pos)
     ref, flip = attention_ref(q, kc, vc, pos, scale)
     assert_attention_close(got, ref, flip, pos.tolist())
+
+
+# Prompt-length calls whose query tiles (256 / G rows, one block per tile and
+# KV head) fill at least half the device take the one-pass kernel
+# (attention_flash.hip): group sizes 4 (Llama-3.1-8B: 64-row tiles), 3
+# (Llama-3.2-3B: 85-row tiles, ragged last tile) and 8; a prompt after depth
+# rows (positions past + t), a context that is not a multiple of the 64-key
+# blocks, and a position past the cache (it attends the whole cache). Rows
+# compared: the first and last of a few tiles, sampled others, every head.
+FLASH_CASES = [(32, 8, 1024, 2048, 1024), (24, 8, 1400, 1500, 90), (32, 4, 1024, 1100, 70)]
+
+
+@pytest.mark.parametrize("n_heads,n_kv,t,max_len,past", FLASH_CASES)
+def test_attention_one_pass_prefill(device, n_heads, n_kv, t, max_len, past):
+    hd = 128
+    g = n_heads // n_kv
+    qt = 256 // g
+    q = synth.bf16_normal(26, (t, n_heads, hd))
+    kc = synth.bf16_normal(27, (n_kv, max_len, hd))
+    vc = synth.bf16_normal(28, (n_kv, max_len, hd))
+    pos = (past + np.arange(t)).astype(np.uint32)
+    pos[t // 2] = max_len + 5  # past the cache: the whole cache
+    got, scale, _ = run_attention(device, q, kc, vc, pos)
+    rng = np.random.default_rng(t + max_len)
+    rows = sorted(set([0, 1, qt - 1, qt, t // 2, t - 2, t - 1, ((t - 1) // qt) * qt] +
+                      rng.integers(0, t, 12).tolist()))
+    ref, flip = attention_ref(q, kc, vc, pos, scale, rows)
+    assert_attention_close(got[rows], ref[rows], flip[rows], rows)
+    again, _, _ = run_attention(device, q, kc, vc, pos)
+    assert np.array_equal(got, again), "one-pass attention differs between runs"
 
 
 def test_attention_workspace_reuse(device):
