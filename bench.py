@@ -31,7 +31,8 @@ sequential-k fp32 accumulation, bf16 RNE) on the config-1 GEMV, on this
 host's cores, for a bounded number of calls.
 
 Single legs, for kernel traces and counters: --gemm-only, --floors-only,
---decode-only, --batched-only.
+--decode-only, --batched-only, and --eager-steps N (config 4, or config 5
+with --batched-only: the decode steps launched op by op).
 """
 from __future__ import annotations
 
@@ -508,6 +509,36 @@ def bench_decode_batched(dev, new_tokens: int, seed: int = 0, batch: int = 8, de
     }
 
 
+def eager_decode_steps(dev, steps: int, batched: bool, seed: int = 0):
+    """Config 4 (or config 5 when `batched`) set up as bench_decode /
+    bench_decode_batched do (the depth rows of config 5 are left out: the
+    caches hold the prompt), then `steps` decode steps launched op by op
+    (Q4Llama.eager_step): the same kernels as the captured step, for kernel
+    traces taken without graph replay."""
+    from foundry_amd.llama import LlamaConfig, Q4Llama
+
+    if batched:
+        cfg, batch = LlamaConfig.llama_3_1_8b(), 8
+        ids = synth.token_ids(seed, batch * 4096, cfg.vocab).reshape(batch, 4096)
+        prompt = ids[:, 2048:]
+        model = Q4Llama(dev, cfg, seed, 4096 + steps + 1, max_tokens=2048, batch=batch)
+        model.step(ids[:, :2048], 0)  # depth rows: context 4096 at the first step
+        model.step(prompt, 2048)
+    else:
+        cfg, batch = LlamaConfig.llama_3_2_3b(), 1
+        prompt = synth.token_ids(0, 512, cfg.vocab)
+        model = Q4Llama(dev, cfg, seed, len(prompt) + steps + 1, max_tokens=len(prompt))
+        model.prefill(prompt)
+    dev.synchronize()
+    dev.timer_begin()
+    for _ in range(steps):
+        model.eager_step()
+    ms = dev.timer_end()
+    return {"config": "Llama-3.1-8B shape, batch 8, context 4096" if batched else "Llama-3.2-3B shape, batch 1",
+            "eager_steps": steps, "ms_per_eager_step": ms / steps,
+            "next_tokens": model.next_tokens()[:4].tolist()}
+
+
 def greedy_agreement(model, cfg, seed, prompt, tokens, n):
     """Greedy agreement with the CPU restatement of the reference's forward
     (oracle/llama_ref.py) over the first n new tokens, by the reference's rule
@@ -638,6 +669,10 @@ def main() -> int:
                     help="only the two config-3 GEMMs (for kernel traces and counters); prints their JSON")
     ap.add_argument("--floors-only", action="store_true",
                     help="only the launch and read floors; prints their JSON")
+    ap.add_argument("--eager-steps", type=int, default=0,
+                    help="only config 4 (or with --batched-only config 5): the prompt, then this many decode "
+                         "steps launched op by op instead of as a graph (for kernel traces: the profiler's "
+                         "graph interception has crashed on the replayed legs); prints their JSON")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not supported "
@@ -648,6 +683,11 @@ def main() -> int:
         calibrate_copy()
     dev = HipDevice(0)
     small = max(5, args.steps // 5)
+    if args.eager_steps > 0:
+        d = eager_decode_steps(dev, args.eager_steps, batched=args.batched_only)
+        dev.close()
+        print(json.dumps(d), flush=True)
+        return 0
     if args.decode_only or args.batched_only or args.gemm_only or args.floors_only:
         if args.decode_only:
             d = bench_decode(dev, max(2, args.decode_tokens), args.agreement)
