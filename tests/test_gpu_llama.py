@@ -308,6 +308,50 @@ def test_decode_attention(device, n_heads, n_kv, hd, batch, max_len):
         assert_attention_close(got[b:b + 1], ref, flip, (b, p))
 
 
+def test_decode_attention_dirty_workspace(device):
+    """The chunked decode P.V (8 sequences x 8 KV heads x 4096 keys) leaves
+    f32 partials per chunk in the workspace for the combine pass, which reads
+    only the row's active chunks: a workspace full of 0xFF bytes (NaN
+    partials) and repeated calls give the output of a zeroed one, bit for
+    bit, for rows of 1 to 8 active chunks."""
+    n_heads, n_kv, hd, batch, max_len = 32, 8, 128, 8, 4096
+    qkv = synth.bf16_normal(24, (batch, (n_heads + 2 * n_kv) * hd))
+    kc = synth.bf16_normal(25, (batch, n_kv, max_len, hd))
+    vc = synth.bf16_normal(26, (batch, n_kv, max_len, hd))
+    pos = np.array([4095, 0, 511, 512, 1023, 2600, 3583, 3584], dtype=np.uint32)
+    c = LlamaConfig(n_layers=1, hidden=n_heads * hd, n_heads=n_heads, n_kv_heads=n_kv, head_dim=hd, ffn=64,
+                    vocab=16)
+    cos, sin = rope_tables(c, max_len)
+    s = [up(device, a) for a in (qkv, cos, sin, pos, tile_k(kc), vc)]
+    nbytes = _lib.decode_attention_workspace_bytes(batch, n_heads, n_kv, hd, max_len)
+
+    def run(ws):
+        out = device.empty(batch * n_heads * hd * 2)
+        _lib.call("fh_decode_attention", device.handle, ctypes.c_void_p(s[0].ptr), batch, n_heads, n_kv, hd,
+                  ctypes.c_void_p(s[1].ptr), ctypes.c_void_p(s[2].ptr), max_len, ctypes.c_void_p(s[3].ptr),
+                  ctypes.c_void_p(s[4].ptr), ctypes.c_void_p(s[5].ptr), max_len, ctypes.c_float(0.0883883461356163),
+                  ctypes.c_void_p(ws.ptr), nbytes, ctypes.c_void_p(out.ptr))
+        return down(device, out, np.uint16, batch * n_heads * hd)
+
+    first = run(device.zeros(nbytes))
+    dirty = up(device, np.full(nbytes, 0xFF, np.uint8))
+    for _ in range(3):
+        assert np.array_equal(run(dirty), first)
+    # the same keys and values again (the cache already holds each row's new
+    # key and value): the restated attention
+    kgot = untile_k(down(device, s[4], np.uint16, kc.size).reshape(kc.shape))
+    vgot = down(device, s[5], np.uint16, vc.size).reshape(vc.shape)
+    xf = R.from_bf16(qkv)
+    rc, rs = R.rope_tables(hd, c.rope_theta, (32.0, 1.0, 4.0, 8192), max_len)
+    bits = lambda a: (a.view(np.uint32) >> 16).astype(np.uint16)
+    got = first.reshape(batch, n_heads, hd)
+    for b in range(batch):
+        p = int(pos[b])
+        q = rope_ref(xf[b:b + 1, :n_heads * hd].reshape(1, n_heads, hd), np.array([p]), rc, rs)
+        ref, flip = attention_ref(bits(q), kgot[b], vgot[b], np.array([p]), 0.0883883461356163)
+        assert_attention_close(got[b:b + 1], ref, flip, (b, p))
+
+
 @pytest.mark.parametrize("max_len", [32, 1100, 4096])  # one launch, sliced and chunked P.V
 def test_decode_attention_out_of_range_position(device, max_len):
     n_heads, n_kv, hd = 4, 2, 64
