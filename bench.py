@@ -190,6 +190,16 @@ def bench_gemv(dev, n, k, copies, steps, warmup, seed, launches=None):
             "median_over_replays": MEDIAN_REPLAYS, "ms_per_step": ms_step}
 
 
+def bench_lm_head(dev, steps, warmup):
+    """The LM-head GEMV (128256 x 3072, 222 MB per launch). Cold: 3 weight
+    copies cycled, so each launch's weights were last read two launches (444
+    MB) earlier, more than the 256 MB MALL holds; warm: one copy. 12 launches
+    per replay, so the individually timed replays' medians carry one graph
+    launch per 12 GEMVs rather than per 3."""
+    return {"lm_head_gemv_cold": bench_gemv(dev, 128256, 3072, 3, steps, warmup, seed=3, launches=12),
+            "lm_head_gemv_warm": bench_gemv(dev, 128256, 3072, 1, steps, warmup, seed=3, launches=12)}
+
+
 _TABLES: dict = {}
 
 
@@ -669,6 +679,8 @@ def main() -> int:
                     help="only the two config-3 GEMMs (for kernel traces and counters); prints their JSON")
     ap.add_argument("--floors-only", action="store_true",
                     help="only the launch and read floors; prints their JSON")
+    ap.add_argument("--lm-head-only", action="store_true",
+                    help="only the LM-head GEMV (128256 x 3072) cold and warm legs; prints their JSON")
     ap.add_argument("--eager-steps", type=int, default=0,
                     help="only config 4 (or with --batched-only config 5): the prompt, then this many decode "
                          "steps launched op by op instead of as a graph (for kernel traces: the profiler's "
@@ -688,7 +700,7 @@ def main() -> int:
         dev.close()
         print(json.dumps(d), flush=True)
         return 0
-    if args.decode_only or args.batched_only or args.gemm_only or args.floors_only:
+    if args.decode_only or args.batched_only or args.gemm_only or args.floors_only or args.lm_head_only:
         if args.decode_only:
             d = bench_decode(dev, max(2, args.decode_tokens), args.agreement)
         elif args.batched_only:
@@ -696,6 +708,8 @@ def main() -> int:
         elif args.gemm_only:
             d = {"gemm_gate_up": bench_gemm(dev, 2048, 8192, 3072, args.steps, args.warmup, seed=7),
                  "gemm_down": bench_gemm(dev, 2048, 3072, 8192, args.steps, args.warmup, seed=9)}
+        elif args.lm_head_only:
+            d = bench_lm_head(dev, args.steps, args.warmup)
         else:
             d = bench_floors(dev, args.steps, args.warmup)
         dev.close()
@@ -707,8 +721,7 @@ def main() -> int:
     secondary = {}
     if not args.quick:
         secondary["gemv_warm"] = bench_gemv(dev, 8192, 3072, 1, small, 2, seed=1, launches=args.copies)
-        secondary["lm_head_gemv_cold"] = bench_gemv(dev, 128256, 3072, 3, small, 2, seed=3)
-        secondary["lm_head_gemv_warm"] = bench_gemv(dev, 128256, 3072, 1, small, 2, seed=3, launches=3)
+        secondary.update(bench_lm_head(dev, small, 2))
         print(f"[bench] gemv warm {secondary['gemv_warm']['GB_per_s']:.0f} GB/s; lm head cold "
               f"{secondary['lm_head_gemv_cold']['GB_per_s']:.0f}, warm {secondary['lm_head_gemv_warm']['GB_per_s']:.0f} GB/s",
               flush=True)

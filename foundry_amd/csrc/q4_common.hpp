@@ -55,4 +55,20 @@ __device__ __forceinline__ float q4_dequant_fma(float s, uint32_t q, float b) {
     return fmaf(s, static_cast<float>(q), b);
 }
 
+// Loads of bytes a launch reads once (the weights and scale/bias tables the
+// one-row-per-lane-group decode GEMV streams): the nontemporal hint (`nt`)
+// marks them as streaming for the caches. Measured on a cold 14.2 MB GEMV:
+// 5.40 -> 5.26 us; the batch-1 decode step 1.010 -> 0.964 ms. (The same hint
+// made the matrix-core GEMV and the decode attention's K/V reads slower.)
+typedef __attribute__((ext_vector_type(4))) uint32_t stream_u32x4_t;
+typedef __attribute__((ext_vector_type(2))) uint32_t stream_u32x2_t;
+
+__device__ __forceinline__ uint4 load_stream16(const uint4 *p) {
+    return __builtin_bit_cast(uint4, __builtin_nontemporal_load(reinterpret_cast<const stream_u32x4_t *>(p)));
+}
+
+__device__ __forceinline__ uint2 load_stream8(const uint2 *p) {
+    return __builtin_bit_cast(uint2, __builtin_nontemporal_load(reinterpret_cast<const stream_u32x2_t *>(p)));
+}
+
 }  // namespace fh

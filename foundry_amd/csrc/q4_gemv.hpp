@@ -162,11 +162,11 @@ __global__ __launch_bounds__(kGemvThreads) void q4_gemv_kernel(
         for (int u = 0; u < CPL; ++u) {
             const uint32_t c = c0 + u * L;
             if (FULL || c < chunks) {
-                buf.w[u] = wrow[u * L];
+                buf.w[u] = load_stream16(wrow + u * L);
                 if constexpr (SB) {
                     // group c / 2 is half (c / 2) & 1 of pair c / 4 (the bf16
                     // conversion takes the low half)
-                    const uint2 v = irow[c / 4];
+                    const uint2 v = load_stream8(irow + c / 4);
                     const uint32_t sh = (c & 2u) * 8u;
                     buf.s[u] = v.x >> sh;
                     buf.b[u] = v.y >> sh;
