@@ -8,6 +8,7 @@
 #include <new>
 
 #include "device.hpp"
+#include "q4_common.hpp"
 
 namespace fh {
 
@@ -123,11 +124,12 @@ int zero_fill(fh_device *dev, const char *fn, void *ptr, uint64_t nbytes) {
 }
 
 // The read probe: every thread loads 4 x 16 bytes, contiguous per wavefront
-// (all four requested before any is used); each wavefront folds its loads
-// into one XOR word that its lane 0 writes, so no block-wide barrier or
-// reduction sits between the last load and the end. 512 threads x 4 loads
-// per block was the fastest single-launch read of 14.2 MB in a sweep of
-// block sizes (64-1024) and loads per thread (2-16).
+// (all four requested before any is used), with the nontemporal hint the
+// decode GEMV's weight loads carry (222 MB read: 37.4 -> 34.1 us); each
+// wavefront folds its loads into one XOR word that its lane 0 writes, so no
+// block-wide barrier or reduction sits between the last load and the end.
+// 512 threads x 4 loads per block was the fastest single-launch read of
+// 14.2 MB in a sweep of block sizes (64-1024) and loads per thread (2-16).
 constexpr uint32_t kProbeThreads = 512;
 constexpr uint32_t kProbeUnroll = 4;
 constexpr uint64_t kProbeBlockBytes = kProbeThreads * 16ull * kProbeUnroll;
@@ -140,7 +142,7 @@ __global__ __launch_bounds__(kProbeThreads) void read_probe_kernel(const uint4 *
 #pragma unroll
     for (uint32_t u = 0; u < kProbeUnroll; ++u) {
         const uint64_t i = base + u * kProbeThreads;
-        v[u] = src[i < pieces ? i : pieces - 1];
+        v[u] = load_stream16(src + (i < pieces ? i : pieces - 1));
     }
     uint32_t x = 0;
 #pragma unroll

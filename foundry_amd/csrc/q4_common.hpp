@@ -55,11 +55,13 @@ __device__ __forceinline__ float q4_dequant_fma(float s, uint32_t q, float b) {
     return fmaf(s, static_cast<float>(q), b);
 }
 
-// Loads of bytes a launch reads once (the weights and scale/bias tables the
-// one-row-per-lane-group decode GEMV streams): the nontemporal hint (`nt`)
-// marks them as streaming for the caches. Measured on a cold 14.2 MB GEMV:
-// 5.40 -> 5.26 us; the batch-1 decode step 1.010 -> 0.964 ms. (The same hint
-// made the matrix-core GEMV and the decode attention's K/V reads slower.)
+// Loads of bytes a launch reads once (the weights a decode GEMV streams):
+// the nontemporal hint (`nt`) marks them as streaming for the caches.
+// Measured: the cold 14.2 MB one-row GEMV 5.40 -> 5.26 us (weights and its
+// scale/bias table), the batch-1 decode step 1.010 -> 0.964 ms, the batch-8
+// step 2.819 -> 2.805 ms (the matrix-core GEMV's weights only: on its
+// scale/bias table the hint cost 3.5%, and on the decode attention's K/V
+// reads it was no faster).
 typedef __attribute__((ext_vector_type(4))) uint32_t stream_u32x4_t;
 typedef __attribute__((ext_vector_type(2))) uint32_t stream_u32x2_t;
 

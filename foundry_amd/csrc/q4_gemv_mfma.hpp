@@ -227,12 +227,12 @@ __global__ __launch_bounds__(kMfThreads) void q4_gemv_mfma_kernel(
                 wt + ((static_cast<uint64_t>(tile) * wt_pairs + wt_p0 + p0) * 16 + col) * 16 + quarter * 4);
             if (dead) wp = reinterpret_cast<const uint4 *>(wt);
 #pragma unroll
-            for (int c2 = 0; c2 < CH; ++c2) cb.w[c2] = wp[c2 * 64];
+            for (int c2 = 0; c2 < CH; ++c2) cb.w[c2] = load_stream16(wp + c2 * 64);
         } else {
             const uint4 *wp = reinterpret_cast<const uint4 *>(wq + row * w_ld + p0 * 16 + quarter * 4);
             if (dead) wp = reinterpret_cast<const uint4 *>(wq);
 #pragma unroll
-            for (int c2 = 0; c2 < CH; ++c2) cb.w[c2] = wp[c2 * 4];
+            for (int c2 = 0; c2 < CH; ++c2) cb.w[c2] = load_stream16(wp + c2 * 4);
         }
         const uint16_t *sp = scales + row * sb_ld + p0 * 2, *bp = biases + row * sb_ld + p0 * 2;
         if (dead) sp = scales, bp = biases;
