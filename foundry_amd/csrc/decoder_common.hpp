@@ -13,6 +13,15 @@ namespace fh {
 __device__ __forceinline__ uint16_t rne(float v) { return static_cast<uint16_t>(f32_to_bf16_rne(v)); }
 __device__ __forceinline__ float bf(uint16_t b) { return bf16_to_f32(b); }
 
+// act(g) * u of LlamaMlp (src/models/llama/mlp.rs:49-58) on bf16 g and u:
+// RNE(RNE(g / (1 + exp(-g))) * u), the rounding of the reference's separate
+// silu and mul ops. Every kernel that forms the activation uses this.
+__device__ __forceinline__ uint16_t silu_mul1(uint16_t gb, uint16_t ub) {
+    const float g = bf(gb), u = bf(ub);
+    const float den = expf(-g) + 1.0f;
+    return rne(bf(rne(g / den)) * u);
+}
+
 // Elements i .. i + 7 of a GEMM split over K (f32 partials [splits][...],
 // `stride` elements apart, i a multiple of 4): each the RNE to bf16 of its
 // partials added in split order, the sum gemm_split_reduce_kernel forms;

@@ -26,6 +26,9 @@ void launch_rms_norm_partials(hipStream_t stream, const float *part, uint32_t sp
                               uint16_t *y);
 void launch_silu_mul_partials(hipStream_t stream, const float *part, uint32_t splits, uint32_t rows, uint32_t f,
                               uint16_t *out);
+bool launch_q4_gemm_direct_silu(hipStream_t stream, uint32_t cus, const uint16_t *x, uint32_t x_ld,
+                                const uint32_t *wq, const uint16_t *s, const uint16_t *b, uint32_t m, uint32_t f,
+                                uint32_t k, uint16_t *act);
 int rope_kv(fh_device *dev, const char *fn, const uint16_t *qkv, const float *part, uint32_t splits,
             uint64_t part_stride, int64_t tokens, int64_t n_heads, int64_t n_kv, int64_t head_dim,
             const uint16_t *cos_tab, const uint16_t *sin_tab, int64_t table_len, const uint32_t *positions,
@@ -189,8 +192,9 @@ int add_norm(fh_device *d, const fh_llama_model &m, int64_t rows, const uint16_t
     });
 }
 
-// Above 8 rows: gate_up = m.x [Wgate; Wup]^T; act = silu(gate) * up, the
-// SiLU forming gate and up from the GEMM's split partials (linear_deferred).
+// Above 8 rows: gate_up = m.x [Wgate; Wup]^T; act = silu(gate) * up, in the
+// GEMM's epilogue where its tiles fill the chip, else the SiLU forming gate
+// and up from the GEMM's output or split partials (linear_deferred).
 int linear_silu(fh_device *d, const fh_llama_model &m, int64_t rows, const fh_q4_weight &w) {
     const char *fn = "fh_llama_forward";
     if (m.ffn % 8 != 0 || !aligned16(m.act)) {
@@ -201,6 +205,15 @@ int linear_silu(fh_device *d, const fh_llama_model &m, int64_t rows, const fh_q4
     }
     FH_TRY(check_gemm(d, fn, m.x, rows, m.hidden, w, m.gate_up));
     FH_TRY(fh::check_range(d, m.act, static_cast<uint64_t>(rows) * m.ffn * 2, fn, "act"));
+    // prompt-length rows whose tiles fill the chip: the activation in the
+    // GEMM's epilogue (no gate/up tensor, no SiLU launch)
+    bool fused = false;
+    FH_TRY(fh::dispatch(d, fn, [&] {
+        fused = fh::launch_q4_gemm_direct_silu(d->stream, d->compute_units, m.x, static_cast<uint32_t>(m.hidden), w.wq,
+                                               w.scales, w.biases, static_cast<uint32_t>(rows),
+                                               static_cast<uint32_t>(m.ffn), static_cast<uint32_t>(m.hidden), m.act);
+    }));
+    if (fused) return FH_OK;
     uint32_t splits = 1;
     FH_TRY(gemm_deferred(d, fn, m.x, rows, m.hidden, w, m.gate_up, &splits));
     if (splits == 1) return fh_silu_mul(d, m.gate_up, rows, m.ffn, m.act);

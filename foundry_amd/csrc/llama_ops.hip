@@ -177,16 +177,11 @@ __global__ __launch_bounds__(256) void rope_kv_kernel(
     }
 }
 
-// out = RNE(RNE(g / (1 + exp(-g))) * u), gu row = [g (F) | u (F)].
+// out = RNE(RNE(g / (1 + exp(-g))) * u) (silu_mul1), gu row = [g (F) | u (F)].
 // Block (256 pieces of 8 outputs, row): with vec (f % 8 == 0, operands
 // 16-byte aligned) a thread reads 16 bytes of g and of u and writes 16
 // bytes; otherwise it walks its 8 outputs one at a time. Rows past the grid's
 // y extent (65535) loop.
-__device__ __forceinline__ uint16_t silu_mul1(uint16_t gb, uint16_t ub) {
-    const float g = bf(gb), u = bf(ub);
-    const float den = expf(-g) + 1.0f;
-    return rne(bf(rne(g / den)) * u);
-}
 
 // With part (vec only), g and u are formed from the f32 partials of the
 // gate/up GEMM (split_sum8), which stands in for its reduce.

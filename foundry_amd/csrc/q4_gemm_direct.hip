@@ -39,6 +39,7 @@
 //   that XCD's L2.
 #include <type_traits>
 
+#include "decoder_common.hpp"
 #include "device.hpp"
 #include "q4_common.hpp"
 
@@ -149,9 +150,13 @@ __device__ __forceinline__ void direct_tile(uint32_t L, uint32_t tiles_m, uint32
 }
 
 // y_mode: 0 bf16 through the LDS epilogue (n % 8 == 0, y 16-byte aligned),
-// 1 bf16 stored per value, 2 f32 stored per value. With gridDim.y = S > 1
-// the block takes K range blockIdx.y (k_len of the k columns, k = S k_len)
-// and writes its f32 partial tile to y[blockIdx.y][m][n] (y_mode 2).
+// 1 bf16 stored per value, 2 f32 stored per value, 3 the MLP activation:
+// the weight rows are [gate (f) | up (f)] (n = 2 f, f % 128 == 0), tile
+// column tn covers gate rows [128 tn, +128) and the matching up rows, and y
+// is act [m][f] = silu_mul1(RNE(gate), RNE(up)) (y 16-byte aligned). With
+// gridDim.y = S > 1 the block takes K range blockIdx.y (k_len of the k
+// columns, k = S k_len) and writes its f32 partial tile to y[blockIdx.y][m][n]
+// (y_mode 2).
 __global__ __launch_bounds__(kDThreads) void q4_gemm_direct_kernel(
     const uint16_t *__restrict__ x, uint32_t x_ld, const uint32_t *__restrict__ wq,
     const uint16_t *__restrict__ scales, const uint16_t *__restrict__ biases, uint32_t m, uint32_t n, uint32_t k,
@@ -164,6 +169,11 @@ __global__ __launch_bounds__(kDThreads) void q4_gemm_direct_kernel(
     uint32_t tm, tn;
     direct_tile(blockIdx.x, tiles_m, tiles_n, gm, &tm, &tn);
     const uint32_t m0 = tm * kDBM, n0 = tn * kDBN;
+    // weight row of the tile's column lc (mode 3: gate rows, then their up rows)
+    const uint32_t f = n / 2;
+    auto weight_row = [&](uint32_t lc) {
+        return y_mode == 3 ? (lc < kDBN / 2 ? tn * (kDBN / 2) + lc : f + tn * (kDBN / 2) + lc - kDBN / 2) : n0 + lc;
+    };
     const uint32_t kw = k / 8, kg = k / kGroup;  // row strides (words, groups)
     const uint32_t steps = k_len / kDBK;
     {
@@ -197,13 +207,13 @@ __global__ __launch_bounds__(kDThreads) void q4_gemm_direct_kernel(
     uint32_t woff[2];
 #pragma unroll
     for (int jj = 0; jj < 2; ++jj) {
-        uint32_t col = n0 + wc * 64 + jj * 32 + (lane & 31);
+        uint32_t col = weight_row(wc * 64 + jj * 32 + (lane & 31));
         col = col < n ? col : 0;
         woff[jj] = (col * kw + 4 * h) * 4;
     }
     // scale/bias chunks: thread t loads the 8 scales (group 0) or biases
     // (group 1) of tile column t % 256 for one chunk: 16 bytes per 8 steps
-    uint32_t sbcol = n0 + (tid & 255);
+    uint32_t sbcol = weight_row(tid & 255);
     sbcol = sbcol < n ? sbcol : 0;
     const uint32_t sbgoff = sbcol * kg * 2;
     const uint32_t chunks = k_len / kGroup / kDSbGroups;
@@ -397,6 +407,44 @@ __global__ __launch_bounds__(kDThreads) void q4_gemm_direct_kernel(
     __builtin_amdgcn_s_waitcnt(0x0f70);
     __builtin_amdgcn_s_barrier();
     const uint32_t row_base = m0 + grp * kDRows + 4 * h;
+    if (y_mode == 3) {
+        // every wavefront's 128 x 64 tile to LDS as bf16 (pitch 72); then
+        // the group's 256 threads form its 128 x 128 activations, gate
+        // column c from wavefront c / 64 and up column c from wavefront
+        // 2 + c / 64, 16 output bytes per piece
+        uint16_t *const os = smem + wave * 128 * kDOutPitch;
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int jj = 0; jj < 2; ++jj)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const uint32_t row = i * 32 + 8 * (r / 4) + 4 * h + (r % 4);
+                    os[row * kDOutPitch + jj * 32 + (lane & 31)] = static_cast<uint16_t>(f32_to_bf16_rne(acc[i][jj][r]));
+                }
+        __syncthreads();
+        const uint16_t *const gs = smem + grp * 4 * 128 * kDOutPitch;
+        uint16_t *const yb = static_cast<uint16_t *>(y);
+        const uint32_t gt = tid & 255;
+#pragma unroll
+        for (int p = 0; p < 8; ++p) {
+            const uint32_t piece = p * 256 + gt, r = piece / 16, c = (piece % 16) * 8;
+            const uint16_t *g = gs + (c / 64) * 128 * kDOutPitch + r * kDOutPitch + c % 64;
+            const uint4 gv = *reinterpret_cast<const uint4 *>(g);
+            const uint4 uv = *reinterpret_cast<const uint4 *>(g + 2 * 128 * kDOutPitch);
+            const uint32_t gw[4] = {gv.x, gv.y, gv.z, gv.w}, uw[4] = {uv.x, uv.y, uv.z, uv.w};
+            uint32_t ow[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+                ow[e] = silu_mul1(gw[e] & 0xFFFFu, uw[e] & 0xFFFFu) |
+                        (static_cast<uint32_t>(silu_mul1(gw[e] >> 16, uw[e] >> 16)) << 16);
+            const uint32_t row = m0 + grp * kDRows + r;
+            if (row < m)
+                *reinterpret_cast<uint4 *>(yb + static_cast<uint64_t>(row) * f + tn * (kDBN / 2) + c) =
+                    make_uint4(ow[0], ow[1], ow[2], ow[3]);
+        }
+        return;
+    }
     if (y_mode == 0) {
         // bf16 via LDS: the wavefront's 128 x 64 tile, row-major (pitch 72),
         // then 16-byte row pieces: 8 lanes per 128-byte row, 8 rows per store
@@ -442,6 +490,32 @@ __global__ __launch_bounds__(kDThreads) void q4_gemm_direct_kernel(
     }
 }
 
+// Rows of tiles per XCD rectangle: the count that minimises the X and
+// weight bytes one XCD brings in (gm tile rows of X, per_xcd / gm tile
+// columns of weights; a tile reads k_len columns of 256 rows of each).
+static uint32_t xcd_rect_rows(uint64_t tiles, uint32_t tiles_m, uint32_t tiles_n, uint32_t k_len) {
+    const uint64_t per_xcd = (tiles + kXcds - 1) / kXcds;
+    const double x_tile = 256.0 * k_len * 2, w_tile = 256.0 * (k_len / 2 + 4 * (k_len / 64));
+    uint32_t gm = 1;
+    double best = 1e300;
+    for (uint32_t g = 1; g <= tiles_m && g <= per_xcd; ++g) {
+        const double cols = static_cast<double>((per_xcd + g - 1) / g);
+        const double bytes = g * x_tile + (cols < tiles_n ? cols : tiles_n) * w_tile;
+        if (bytes < best) best = bytes, gm = g;
+    }
+    return gm;
+}
+
+// The kernel's dynamic LDS above the default limit, requested once.
+static void direct_lds_opt_in() {
+    static bool done = false;
+    if (!done) {
+        (void)hipFuncSetAttribute(reinterpret_cast<const void *>(q4_gemm_direct_kernel),
+                                  hipFuncAttributeMaxDynamicSharedMemorySize, kDLds);
+        done = true;
+    }
+}
+
 // Launches the direct-weight GEMM when it applies: 256 x 256 tiles that fill
 // the chip (the 2048 x 8192 x 3072 gate/up shape has exactly 256), or fill
 // at least 3/4 of it over two K ranges (the 2048 x 3072 x 8192 down shape:
@@ -465,24 +539,8 @@ uint32_t launch_q4_gemm_direct(hipStream_t stream, uint32_t cus, const uint16_t 
     if (tiles > 0x7FFFFFFFull || k % (kDSbGroups * kDBK) != 0 || k == 0 || m == 0) return 0;
     if (static_cast<uint64_t>(m) * x_ld * 2 >= (1ull << 32) || static_cast<uint64_t>(n) * k / 2 >= (1ull << 32))
         return 0;
-    static bool lds_opt_in = false;
-    if (!lds_opt_in) {
-        (void)hipFuncSetAttribute(reinterpret_cast<const void *>(q4_gemm_direct_kernel),
-                                  hipFuncAttributeMaxDynamicSharedMemorySize, kDLds);
-        lds_opt_in = true;
-    }
-    // rows of tiles per XCD rectangle: the count that minimises the X and
-    // weight bytes one XCD brings in (gm tile rows of X, per_xcd / gm tile
-    // columns of weights)
-    const uint64_t per_xcd = (tiles + kXcds - 1) / kXcds;
-    const double x_tile = 256.0 * k / splits * 2, w_tile = 256.0 * (k / 2 + 4 * (k / 64)) / splits;
-    uint32_t gm = 1;
-    double best = 1e300;
-    for (uint32_t g = 1; g <= tiles_m && g <= per_xcd; ++g) {
-        const double cols = static_cast<double>((per_xcd + g - 1) / g);
-        const double bytes = g * x_tile + (cols < tiles_n ? cols : tiles_n) * w_tile;
-        if (bytes < best) best = bytes, gm = g;
-    }
+    direct_lds_opt_in();
+    const uint32_t gm = xcd_rect_rows(tiles, tiles_m, tiles_n, k / splits);
     if (splits > 1) {
         hipLaunchKernelGGL(q4_gemm_direct_kernel, dim3(static_cast<uint32_t>(tiles), splits), dim3(kDThreads), kDLds,
                            stream, x, x_ld, wq, s, b, m, n, k, area, 2, tiles_m, tiles_n, gm, k / splits);
@@ -492,6 +550,28 @@ uint32_t launch_q4_gemm_direct(hipStream_t stream, uint32_t cus, const uint16_t 
     hipLaunchKernelGGL(q4_gemm_direct_kernel, dim3(static_cast<uint32_t>(tiles)), dim3(kDThreads), kDLds, stream, x,
                        x_ld, wq, s, b, m, n, k, y, y_mode, tiles_m, tiles_n, gm, k);
     return 1;
+}
+
+// act [m][f] = silu_mul1 of the [gate; up] GEMM (n = 2 f weight rows) in one
+// launch (y_mode 3), when its 256-row x 128-pair tiles fill the chip with no
+// K split, f % 128 == 0, k % 512 == 0, act 16-byte aligned and every byte
+// offset within 32 bits. Returns false when it does not apply.
+bool launch_q4_gemm_direct_silu(hipStream_t stream, uint32_t cus, const uint16_t *x, uint32_t x_ld,
+                                const uint32_t *wq, const uint16_t *s, const uint16_t *b, uint32_t m, uint32_t f,
+                                uint32_t k, uint16_t *act) {
+    const uint32_t n = 2 * f;
+    const uint32_t tiles_m = (m + kDBM - 1) / kDBM, tiles_n = f / (kDBN / 2);
+    const uint64_t tiles = static_cast<uint64_t>(tiles_m) * tiles_n;
+    if (f == 0 || f % (kDBN / 2) != 0 || m == 0 || tiles < cus || tiles > 0x7FFFFFFFull || k == 0 ||
+        k % (kDSbGroups * kDBK) != 0 || (reinterpret_cast<uintptr_t>(act) & 15) != 0)
+        return false;
+    if (static_cast<uint64_t>(m) * x_ld * 2 >= (1ull << 32) || static_cast<uint64_t>(n) * k / 2 >= (1ull << 32))
+        return false;
+    direct_lds_opt_in();
+    const uint32_t gm = xcd_rect_rows(tiles, tiles_m, tiles_n, k);  // a tile reads 256 weight rows either way
+    hipLaunchKernelGGL(q4_gemm_direct_kernel, dim3(static_cast<uint32_t>(tiles)), dim3(kDThreads), kDLds, stream, x,
+                       x_ld, wq, s, b, m, n, k, act, 3, tiles_m, tiles_n, gm, k);
+    return true;
 }
 
 }  // namespace fh

@@ -19,6 +19,9 @@ uint32_t gemv_rows_per_launch(uint32_t k, bool norm);
 void launch_q4_gemm(hipStream_t stream, uint32_t cus, const uint16_t *x, uint32_t x_ld, const uint32_t *wq,
                     const uint16_t *s, const uint16_t *b, uint32_t m, uint32_t n, uint32_t k,
                     void *y, int y_is_f32, void *area);
+bool launch_q4_gemm_direct_silu(hipStream_t stream, uint32_t cus, const uint16_t *x, uint32_t x_ld,
+                                const uint32_t *wq, const uint16_t *s, const uint16_t *b, uint32_t m, uint32_t f,
+                                uint32_t k, uint16_t *act);
 
 // Row counts up to this go to the GEMV.
 constexpr int64_t kGemvMaxRows = 8;
@@ -388,6 +391,36 @@ int q4_matmul_rmsnorm(fh_device *dev, const uint16_t *x, const uint16_t *residua
 
 // fh_q4_gate_up_silu with the weight's optional interleaved scale/bias table
 // and tiled words (in the SiLU pairing: fh_q4_tile with silu_pairs = 1).
+// Prompt-length rows: the [gate; up] GEMM with the activation in its
+// epilogue (launch_q4_gemm_direct_silu), where that kernel applies.
+int gate_up_silu_gemm(fh_device *dev, const char *fn, const uint16_t *x, int64_t m, int64_t k, const uint32_t *wq,
+                      const uint16_t *scales, const uint16_t *biases, int64_t n, int64_t group, uint16_t *act) {
+    if (int rc = check_usable(dev, fn)) return rc;
+    if (int rc = check_q4_table(dev, fn, wq, scales, biases, n, k, group)) return rc;
+    if (m > 65535ll * 128) return fail(FH_ERR_INDEX_TOO_LARGE, "%s: m > 65535*128 rows", fn);
+    if (reinterpret_cast<uintptr_t>(x) % 16 != 0 || reinterpret_cast<uintptr_t>(act) % 16 != 0 || k % 8 != 0)
+        return fail(FH_ERR_INVALID_ARGUMENT, "%s: above %lld rows x and act must be 16-byte aligned and k %% 8 == 0",
+                    fn, (long long)kGemvMaxRows);
+    const uint64_t x_bytes = static_cast<uint64_t>(m) * k * 2, act_bytes = static_cast<uint64_t>(m) * (n / 2) * 2;
+    if (int rc = check_range(dev, x, x_bytes, fn, "x")) return rc;
+    if (int rc = check_range(dev, act, act_bytes, fn, "act")) return rc;
+    if (overlaps(x, x_bytes, act, act_bytes)) return fail(FH_ERR_INVALID_ARGUMENT, "%s: act overlaps x", fn);
+    if (int rc = set_current(dev, fn)) return rc;
+    bool done = false;
+    if (int rc = dispatch(dev, fn, [&] {
+            done = launch_q4_gemm_direct_silu(dev->stream, dev->compute_units, x, static_cast<uint32_t>(k), wq, scales,
+                                              biases, static_cast<uint32_t>(m), static_cast<uint32_t>(n / 2),
+                                              static_cast<uint32_t>(k), act);
+        }))
+        return rc;
+    if (!done)
+        return fail(FH_ERR_UNSUPPORTED,
+                    "%s: %lld rows x f=%lld x k=%lld: the fused GEMM needs tiles of 256 rows x 128 pairs that fill "
+                    "the chip, f %% 128 == 0 and k %% 512 == 0; use the unfused ops",
+                    fn, (long long)m, (long long)(n / 2), (long long)k);
+    return FH_OK;
+}
+
 int q4_gate_up_silu(fh_device *dev, const uint16_t *x, const uint16_t *residual, uint16_t *residual_out,
                     const uint16_t *norm_weight, float eps, int64_t m, int64_t k, const uint32_t *wq,
                     const uint16_t *scales, const uint16_t *biases, const uint32_t *sb, const uint32_t *wt,
@@ -395,6 +428,8 @@ int q4_gate_up_silu(fh_device *dev, const uint16_t *x, const uint16_t *residual,
     const char *fn = "fh_q4_gate_up_silu";
     if (n % 2 != 0) return fail(FH_ERR_INVALID_ARGUMENT, "%s: n=%lld is not [gate; up] rows", fn, (long long)n);
     const bool norm = norm_weight != nullptr;
+    if (m > kGemvMaxRows && !norm && residual == nullptr && residual_out == nullptr)
+        return gate_up_silu_gemm(dev, fn, x, m, k, wq, scales, biases, n, group, act);
     if (int rc = check_fused(dev, fn, m, k, wq, scales, biases, n, group, act, FH_BF16, n / 2, norm)) return rc;
     if (int rc = check_sb(dev, fn, sb, n, k)) return rc;
     if (int rc = check_wt(dev, fn, wt, sb, n, k)) return rc;

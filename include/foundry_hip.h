@@ -390,7 +390,8 @@ int fh_decode_attention_noalloc(fh_device *dev, const uint16_t *qkv, int64_t bat
                                 uint16_t *out);
 
 /* Decode-step fusions of the q4 Linear (m <= 8 rows, the GEMV; larger m
- * returns FH_ERR_UNSUPPORTED -- use the unfused ops). Same arithmetic as the
+ * returns FH_ERR_UNSUPPORTED -- use the unfused ops -- except
+ * fh_q4_gate_up_silu without a norm weight, below). Same arithmetic as the
  * unfused sequence, with no intermediate tensor in memory:
  *   fh_q4_matmul_rmsnorm: y = fh_rms_norm(x, residual, residual_out,
  *     norm_weight, eps) @ W^T (src/nn/norm.rs:32-50 then src/nn/linear.rs:
@@ -402,7 +403,12 @@ int fh_decode_attention_noalloc(fh_device *dev, const uint16_t *qkv, int64_t bat
  *     (n = 2f): act[:, j] = RNE(RNE(g_j / (exp(-g_j) + 1)) * u_j) with g, u
  *     the bf16 outputs of the linear (src/models/llama/mlp.rs:49-58); act:
  *     [m, f] bf16. x' = x, or with norm_weight, the RMSNorm above (residual
- *     arguments as for fh_q4_matmul_rmsnorm).
+ *     arguments as for fh_q4_matmul_rmsnorm). Above 8 rows, without a norm
+ *     weight or residual: the prompt GEMM with the activation in its
+ *     epilogue, when its tiles of 256 rows x 128 gate/up pairs fill the GPU
+ *     (f % 128 == 0, k % 512 == 0; x and act 16-byte aligned, act not
+ *     overlapping x); other shapes return FH_ERR_UNSUPPORTED. Bit-identical
+ *     to fh_q4_matmul then fh_silu_mul.
  * The q4 operands follow fh_q4_matmul (group 64); x 16-byte aligned. */
 int fh_q4_matmul_rmsnorm(fh_device *dev, const uint16_t *x, const uint16_t *residual,
                          uint16_t *residual_out, const uint16_t *norm_weight, float eps, int64_t m,

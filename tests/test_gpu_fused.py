@@ -15,6 +15,9 @@ Bars:
   the matrix-core GEMV with the same K split: a task there is 16 weight rows,
   or 8 gate rows and their 8 up rows, so f need only be a multiple of 8
   (f = 1000 below).
+- fh_q4_gate_up_silu above 8 rows (no norm): the direct GEMM with the
+  activation in its epilogue, bit-identical to fh_q4_matmul (the same kernel
+  and K order) followed by fh_silu_mul.
 - fh_q4_matmul_rmsnorm: the prologue sums h^2 in another order than
   fh_rms_norm, and sums each staged chunk of x in pairs, so a normalised value
   or a chunk sum can differ in its last bit. Bars: the fp32 output within 2e-3
@@ -124,6 +127,28 @@ def test_gate_up_silu(device, m, k, f, same_shape):
         gf, wf = R.from_bf16(got), R.from_bf16(want)
         row_max = np.abs(wf).max(axis=1, keepdims=True)
         assert np.mean(got == want) >= 0.99 and (np.abs(gf - wf) <= row_max * 2.0**-7).all()
+
+
+@pytest.mark.parametrize("m,k,f", [(2048, 3072, 4096), (1000, 2048, 8192), (4096, 4096, 14336)])
+def test_gate_up_silu_prompt_rows(device, m, k, f):
+    """Above 8 rows the activation is formed in the prompt GEMM's epilogue
+    (tiles of 256 rows x 128 gate/up column pairs that fill the chip), with
+    no gate/up tensor in memory: bit-identical to fh_q4_matmul on [gate; up]
+    followed by fh_silu_mul. m = 1000 leaves a ragged last row tile; f = 14336
+    is the 8B shape's FFN."""
+    x = synth.bf16_normal(75 + m, (m, k))
+    _, w = q4(device, 85 + m, 2 * f, k)
+    sx = up(device, x)
+    act = device.empty(m * f * 2)
+    _lib.call("fh_q4_gate_up_silu", device.handle, P(sx), None, None, None, ctypes.c_float(EPS), m, k, P(w[0]),
+              P(w[1]), P(w[2]), 2 * f, 64, P(act))
+    gu = device.empty(m * 2 * f * 2)
+    _lib.call("fh_q4_matmul", device.handle, P(sx), m, k, k, P(w[0]), P(w[1]), P(w[2]), 2 * f, 64, P(gu), _lib.BF16)
+    want = device.empty(m * f * 2)
+    _lib.call("fh_silu_mul", device.handle, P(gu), m, f, P(want))
+    got, want = down(device, act, np.uint16, m * f), down(device, want, np.uint16, m * f)
+    assert np.array_equal(got, want)
+    assert np.count_nonzero(got) > got.size // 2  # a real activation, not a cleared buffer
 
 
 @pytest.mark.parametrize("m", [1, 3])
