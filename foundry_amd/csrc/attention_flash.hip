@@ -63,23 +63,37 @@ __device__ __forceinline__ uint32_t fl_slot(uint32_t k) {
 // The reference compiles its Metal kernels with the default options
 // (src/metal/mod.rs:109-128: no MTLCompileOptions), under which Metal's fast
 // math is on: its exp (unary.metal:6) and divide (binary.metal:14) are not
-// the correctly rounded functions. Here exp(x) is v_exp_f32 of x * log2(e)
-// and p = e * (1 / S), the same class of approximation; with expf and a
-// true division the one-pass kernel takes 1.8x as long (the VALU work per
-// score bounds it). FH_FLASH_EXP2=0 / FH_FLASH_RCP=0 select those.
+// the correctly rounded functions. Here exp(s - m) is v_exp_f32 of one fma,
+// b * (scale log2 e) - mb * (scale log2 e) for s = b * scale (b = RNE(q.k))
+// and m = mb * scale, and p = e * (1 / S): the same class of approximation.
+// With expf of s - m and a true division the one-pass kernel takes 1.8x as
+// long (the VALU work per score bounds it). FH_FLASH_EXP2=0 / FH_FLASH_RCP=0
+// select those.
 #ifndef FH_FLASH_EXP2
 #define FH_FLASH_EXP2 1
 #endif
 #ifndef FH_FLASH_RCP
 #define FH_FLASH_RCP 1
 #endif
-__device__ __forceinline__ float fl_exp(float x) {
+// exp(b * scale - mb * scale) as ex(b, ex.base(mb)); b may be -inf, mb
+// is finite
+struct FlExp {
+    float scale, c1;  // c1 = scale * log2(e)
+    __device__ float base(float mb) const {
 #if FH_FLASH_EXP2
-    return __builtin_amdgcn_exp2f(x * 1.44269504088896341f);
+        return -(mb * c1);
 #else
-    return expf(x);
+        return __fmul_rn(mb, scale);
 #endif
-}
+    }
+    __device__ float operator()(float b, float base_) const {
+#if FH_FLASH_EXP2
+        return __builtin_amdgcn_exp2f(fmaf(b, c1, base_));
+#else
+        return expf(__fmul_rn(b, scale) - base_);
+#endif
+    }
+};
 
 }  // namespace
 
@@ -195,10 +209,13 @@ __global__ __launch_bounds__(kFlThreads) void attn_flash_kernel(
         }
         return d;
     };
-    // s_j = RNE(q.k_j) * scale, or -inf past the pair's context (MASK: the
-    // block reaches past some live pair's context)
+    // b_j = RNE(q.k_j) (the score is s_j = b_j * scale; the scale is applied
+    // inside the exp argument, and the max over b is the max over s), or -inf
+    // past the pair's context (MASK: the block reaches past some live pair's
+    // context)
+    const FlExp ex{scale, scale * 1.44269504088896341f};
     auto score_of = [&](const fl_f32x16_t &d, uint32_t kb, int t, int r, auto mask) {
-        const float sv = __fmul_rn(bf(rne(d[r])), scale);
+        const float sv = bf(rne(d[r]));
         if constexpr (decltype(mask)::value) {
             const uint32_t j = kb * kFlKeys + 32 * t + 8 * (r / 4) + 4 * h + (r % 4);
             return j < ctx ? sv : -INFINITY;
@@ -208,7 +225,7 @@ __global__ __launch_bounds__(kFlThreads) void attn_flash_kernel(
     using Masked = std::integral_constant<bool, true>;
     using Unmasked = std::integral_constant<bool, false>;
 
-    // Pass 1: running (max, sum of exp) over this lane's keys of the pair
+    // Pass 1: running (max of b, sum of exp(s - m)) over this lane's keys of the pair
     float m = -INFINITY, l = 0.f;
     stage_k(0, 0);
     __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0)
@@ -228,10 +245,11 @@ __global__ __launch_bounds__(kFlThreads) void attn_flash_kernel(
                 }
                 const float mn = fmaxf(m, mt);
                 if (mn != -INFINITY) {
+                    const float o = ex.base(mn);
                     float sum = 0.f;
 #pragma unroll
-                    for (int r = 0; r < 16; ++r) sum += fl_exp(sv[r] - mn);
-                    l = l * fl_exp(m - mn) + sum;
+                    for (int r = 0; r < 16; ++r) sum += ex(sv[r], o);
+                    l = l * ex(m, o) + sum;
                     m = mn;
                 }
             }
@@ -249,13 +267,17 @@ __global__ __launch_bounds__(kFlThreads) void attn_flash_kernel(
         const float mo = __shfl_xor(m, 32, 64), lo = __shfl_xor(l, 32, 64);
         const float m0 = h ? mo : m, l0 = h ? lo : l, m1 = h ? m : mo, l1 = h ? l : lo;
         M = fmaxf(m0, m1);
-        S = M == -INFINITY ? 1.f : (m0 == -INFINITY ? 0.f : l0 * fl_exp(m0 - M)) + (m1 == -INFINITY ? 0.f : l1 * fl_exp(m1 - M));
+        const float o = M == -INFINITY ? 0.f : ex.base(M);
+        S = M == -INFINITY ? 1.f : (m0 == -INFINITY ? 0.f : l0 * ex(m0, o)) + (m1 == -INFINITY ? 0.f : l1 * ex(m1, o));
     }
+    // a pair with no key (a dead lane) gets exp(-inf) = 0 everywhere, not NaN
+    const float oM = M == -INFINITY ? 0.f : ex.base(M);
 #if FH_FLASH_RCP
     const float rS = 1.f / S;
 #endif
 
-    // Pass 2: p_j = RNE(exp(s_j - M) / S), acc += P V over 4 tiles of 32 dims
+    // Pass 2: p_j = RNE(exp(s_j - M) / S) (masked keys: exp(-inf) = 0), acc +=
+    // P V over 4 tiles of 32 dims
     fl_f32x16_t acc[4];
 #pragma unroll
     for (int dt = 0; dt < 4; ++dt)
@@ -284,11 +306,9 @@ __global__ __launch_bounds__(kFlThreads) void attn_flash_kernel(
                 const fl_f32x16_t &d = dsc;
                 const float s0 = score_of(d, kb, t, r, mask), s1 = score_of(d, kb, t, r + 1, mask);
 #if FH_FLASH_RCP
-                const float p0 = s0 == -INFINITY ? 0.f : fl_exp(s0 - M) * rS;
-                const float p1 = s1 == -INFINITY ? 0.f : fl_exp(s1 - M) * rS;
+                const float p0 = ex(s0, oM) * rS, p1 = ex(s1, oM) * rS;
 #else
-                const float p0 = s0 == -INFINITY ? 0.f : fl_exp(s0 - M) / S;
-                const float p1 = s1 == -INFINITY ? 0.f : fl_exp(s1 - M) / S;
+                const float p0 = ex(s0, oM) / S, p1 = ex(s1, oM) / S;
 #endif
                 pw[r / 2] = f32x2_to_bf16x2_rne(p0, p1);
             }
