@@ -61,7 +61,8 @@ namespace fh {
 // apply to the shape.
 bool launch_attention_flash(hipStream_t stream, uint32_t cus, const uint16_t *q, const uint32_t *positions,
                             uint32_t rows, const uint16_t *k_cache, const uint16_t *v_cache, uint32_t n_heads,
-                            uint32_t n_kv, uint32_t head_dim, uint32_t max_len, float scale, uint16_t *out);
+                            uint32_t n_kv, uint32_t head_dim, uint32_t max_len, float scale, uint16_t *out,
+                            uint32_t batch, uint64_t seq_cache);
 
 constexpr int kAttnChunk = 64;
 constexpr int kAttnThreads = 256;
@@ -1472,7 +1473,8 @@ extern "C" int fh_attention(fh_device *dev, const uint16_t *q, const uint16_t *k
     return dispatch(dev, fn, [&] {
         if (!launch_attention_flash(dev->stream, dev->compute_units, q, positions, static_cast<uint32_t>(tokens),
                                     k_cache, v_cache, static_cast<uint32_t>(n_heads), static_cast<uint32_t>(n_kv),
-                                    static_cast<uint32_t>(head_dim), static_cast<uint32_t>(max_len), scale, out))
+                                    static_cast<uint32_t>(head_dim), static_cast<uint32_t>(max_len), scale, out, 1,
+                                    0))
             launch_attention_shape<false>(head_dim, n_heads / n_kv, dev->stream, static_cast<uint32_t>(tokens), a, x);
     });
 }

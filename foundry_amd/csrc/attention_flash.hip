@@ -97,14 +97,17 @@ struct FlExp {
 
 }  // namespace
 
-// Block (KV head, query tile): rows r0 .. r0 + 256 / G - 1 of one sequence
-// over its cache (K tiled in groups of 16 keys, k_tile; V [max_len][128]).
-// positions[r]: the row's position; it attends keys 0 .. min(pos, max_len - 1).
+// Block (KV head, sequence, query tile): rows r0 .. r0 + 256 / G - 1 of
+// sequence blockIdx.y (`rows` rows each, its cache seq_cache elements after
+// the previous one's; K tiled in groups of 16 keys, k_tile; V [max_len][128])
+// over its cache. positions[r]: the row's position; it attends keys 0 ..
+// min(pos, max_len - 1). Tiles go out last first: a prompt's later rows
+// attend more keys, and the longest blocks then start first.
 template <int G>
 __global__ __launch_bounds__(kFlThreads) void attn_flash_kernel(
     const uint16_t *__restrict__ q, const uint32_t *__restrict__ positions, uint32_t rows,
-    const uint16_t *__restrict__ k_cache, const uint16_t *__restrict__ v_cache, uint32_t n_heads, uint32_t max_len,
-    float scale, uint16_t *__restrict__ out) {
+    const uint16_t *__restrict__ k_cache, const uint16_t *__restrict__ v_cache, uint64_t seq_cache, uint32_t n_heads,
+    uint32_t max_len, float scale, uint16_t *__restrict__ out) {
     constexpr uint32_t QT = 256 / G;   // query rows per block
     constexpr uint32_t LIVE = QT * G;  // (row, head) pairs of the block
     // K blocks: [key][16 pieces of 8 dims], piece slot s of key k holding
@@ -116,7 +119,15 @@ __global__ __launch_bounds__(kFlThreads) void attn_flash_kernel(
     // the wavefronts' longest contexts, read before V^T buffer 1 is first written
     uint32_t *const wmax = reinterpret_cast<uint32_t *>(&vls[1][0]);
     const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, h = lane >> 5;
-    const uint32_t kvh = blockIdx.x, r0 = blockIdx.y * QT, h0 = kvh * G;
+    const uint32_t kvh = blockIdx.x, sq = blockIdx.y, r0 = (gridDim.z - 1 - blockIdx.z) * QT, h0 = kvh * G;
+    {
+        const uint64_t rows0 = static_cast<uint64_t>(sq) * rows;  // the sequence's first row
+        q += rows0 * n_heads * kFlHd;
+        out += rows0 * n_heads * kFlHd;
+        positions += rows0;
+        k_cache += sq * seq_cache;
+        v_cache += sq * seq_cache;
+    }
     const uint16_t *const kc = k_cache + static_cast<uint64_t>(kvh) * max_len * kFlHd;
     const uint16_t *const vc = v_cache + static_cast<uint64_t>(kvh) * max_len * kFlHd;
 
@@ -351,23 +362,34 @@ __global__ __launch_bounds__(kFlThreads) void attn_flash_kernel(
     }
 }
 
-// Launches the one-pass kernel for head_dim 128 and G = n_heads / n_kv of
-// 1 .. 8 when its blocks (n_kv per query tile) fill at least half the CUs;
-// returns false otherwise (the caller takes the two-kernel path).
-bool launch_attention_flash(hipStream_t stream, uint32_t cus, const uint16_t *q, const uint32_t *positions,
-                            uint32_t rows, const uint16_t *k_cache, const uint16_t *v_cache, uint32_t n_heads,
-                            uint32_t n_kv, uint32_t head_dim, uint32_t max_len, float scale, uint16_t *out) {
+// Whether the one-pass kernel takes `rows` prompt rows of one sequence:
+// head_dim 128, G = n_heads / n_kv of 1 .. 8, and its blocks (n_kv per query
+// tile) fill at least half the CUs.
+bool attention_flash_applies(uint32_t cus, uint32_t rows, uint32_t n_heads, uint32_t n_kv, uint32_t head_dim) {
     if (head_dim != kFlHd || n_kv == 0 || n_heads % n_kv != 0) return false;
     const uint32_t g = n_heads / n_kv;
     if (g < 1 || g > 8) return false;
-    const uint32_t qt = 256 / g;
-    const uint64_t tiles = (rows + qt - 1) / qt;
-    if (tiles * n_kv * 2 < cus || tiles > 65535) return false;
-    const dim3 grid(n_kv, static_cast<uint32_t>(tiles));
+    const uint64_t tiles = (rows + 256 / g - 1) / (256 / g);
+    return tiles * n_kv * 2 >= cus && tiles <= 65535;
+}
+
+// Launches the one-pass kernel over `batch` sequences of `rows` rows (q, out
+// and positions consecutive per sequence, caches seq_cache elements apart)
+// when attention_flash_applies to one sequence; returns false otherwise (the
+// caller takes the two-kernel path). Every block is the one a launch per
+// sequence would run, so the outputs are those of per-sequence launches.
+bool launch_attention_flash(hipStream_t stream, uint32_t cus, const uint16_t *q, const uint32_t *positions,
+                            uint32_t rows, const uint16_t *k_cache, const uint16_t *v_cache, uint32_t n_heads,
+                            uint32_t n_kv, uint32_t head_dim, uint32_t max_len, float scale, uint16_t *out,
+                            uint32_t batch, uint64_t seq_cache) {
+    if (batch == 0 || batch > 65535 || !attention_flash_applies(cus, rows, n_heads, n_kv, head_dim)) return false;
+    const uint32_t g = n_heads / n_kv;
+    const uint32_t tiles = (rows + 256 / g - 1) / (256 / g);
+    const dim3 grid(n_kv, batch, tiles);
 #define FH_FLASH_G(GG)                                                                                          \
     case GG:                                                                                                    \
         hipLaunchKernelGGL(attn_flash_kernel<GG>, grid, dim3(kFlThreads), 0, stream, q, positions, rows, k_cache, \
-                           v_cache, n_heads, max_len, scale, out);                                              \
+                           v_cache, seq_cache, n_heads, max_len, scale, out);                                   \
         return true;
     switch (g) {
         FH_FLASH_G(1)

@@ -29,6 +29,11 @@ void launch_silu_mul_partials(hipStream_t stream, const float *part, uint32_t sp
 bool launch_q4_gemm_direct_silu(hipStream_t stream, uint32_t cus, const uint16_t *x, uint32_t x_ld,
                                 const uint32_t *wq, const uint16_t *s, const uint16_t *b, uint32_t m, uint32_t f,
                                 uint32_t k, uint16_t *act);
+bool attention_flash_applies(uint32_t cus, uint32_t rows, uint32_t n_heads, uint32_t n_kv, uint32_t head_dim);
+bool launch_attention_flash(hipStream_t stream, uint32_t cus, const uint16_t *q, const uint32_t *positions,
+                            uint32_t rows, const uint16_t *k_cache, const uint16_t *v_cache, uint32_t n_heads,
+                            uint32_t n_kv, uint32_t head_dim, uint32_t max_len, float scale, uint16_t *out,
+                            uint32_t batch, uint64_t seq_cache);
 int rope_kv(fh_device *dev, const char *fn, const uint16_t *qkv, const float *part, uint32_t splits,
             uint64_t part_stride, int64_t tokens, int64_t n_heads, int64_t n_kv, int64_t head_dim,
             const uint16_t *cos_tab, const uint16_t *sin_tab, int64_t table_len, const uint32_t *positions,
@@ -235,6 +240,15 @@ int attention(fh_device *d, const fh_llama_model &m, const fh_llama_layer &L, in
     const int64_t hq = m.n_heads * m.head_dim;
     const int64_t qkv_n = (m.n_heads + 2 * m.n_kv_heads) * m.head_dim;
     const int64_t seq_cache = m.n_kv_heads * m.max_len * m.head_dim;  // one sequence's cache, elements
+    // where each sequence's call would take the one-pass kernel, the
+    // sequences share one launch of it (its blocks are the per-sequence
+    // launches' blocks, longest first across the batch) after every RoPE
+    const bool one_launch =
+        m.batch > 1 && m.batch <= 65535 && m.max_len <= 0xFFFFFFFFll &&
+        fh::attention_flash_applies(d->compute_units, static_cast<uint32_t>(seq_tokens),
+                                    static_cast<uint32_t>(m.n_heads), static_cast<uint32_t>(m.n_kv_heads),
+                                    static_cast<uint32_t>(m.head_dim)) &&
+        aligned16(m.q) && aligned16(m.attn) && aligned16(L.k_cache) && aligned16(L.v_cache);
     for (int64_t sq = 0; sq < m.batch; ++sq) {
         const int64_t r0 = sq * seq_tokens;
         uint16_t *kc = L.k_cache + sq * seq_cache, *vc = L.v_cache + sq * seq_cache;
@@ -243,11 +257,27 @@ int attention(fh_device *d, const fh_llama_model &m, const fh_llama_layer &L, in
                            static_cast<uint64_t>(m.batch * seq_tokens * qkv_n), seq_tokens, m.n_heads, m.n_kv_heads,
                            m.head_dim, m.cos_tab, m.sin_tab, m.max_len, positions + r0, kc, vc, m.max_len,
                            m.q + r0 * hq));
-        FH_TRY(fh_attention(d, m.q + r0 * hq, kc, vc, positions + r0, seq_tokens, m.n_heads, m.n_kv_heads,
-                            m.head_dim, m.max_len, m.scale, m.attn_workspace, m.attn_workspace_bytes,
-                            m.attn + r0 * hq));
+        if (!one_launch)
+            FH_TRY(fh_attention(d, m.q + r0 * hq, kc, vc, positions + r0, seq_tokens, m.n_heads, m.n_kv_heads,
+                                m.head_dim, m.max_len, m.scale, m.attn_workspace, m.attn_workspace_bytes,
+                                m.attn + r0 * hq));
     }
-    return FH_OK;
+    if (!one_launch) return FH_OK;
+    const char *fn = "fh_llama_forward";
+    const uint64_t rows_bytes = static_cast<uint64_t>(m.batch) * seq_tokens * hq * 2;
+    const uint64_t cache_bytes = static_cast<uint64_t>(m.batch) * seq_cache * 2;
+    FH_TRY(fh::check_range(d, m.q, rows_bytes, fn, "q"));
+    FH_TRY(fh::check_range(d, m.attn, rows_bytes, fn, "attn"));
+    FH_TRY(fh::check_range(d, L.k_cache, cache_bytes, fn, "k_cache"));
+    FH_TRY(fh::check_range(d, L.v_cache, cache_bytes, fn, "v_cache"));
+    FH_TRY(fh::check_range(d, positions, static_cast<uint64_t>(m.batch) * seq_tokens * 4, fn, "positions"));
+    return fh::dispatch(d, fn, [&] {
+        fh::launch_attention_flash(d->stream, d->compute_units, m.q, positions, static_cast<uint32_t>(seq_tokens),
+                                   L.k_cache, L.v_cache, static_cast<uint32_t>(m.n_heads),
+                                   static_cast<uint32_t>(m.n_kv_heads), static_cast<uint32_t>(m.head_dim),
+                                   static_cast<uint32_t>(m.max_len), m.scale, m.attn, static_cast<uint32_t>(m.batch),
+                                   static_cast<uint64_t>(seq_cache));
+    });
 }
 
 }  // namespace

@@ -639,6 +639,37 @@ def test_llama_forward_equals_the_op_sequence(device, batch, t):
         assert np.array_equal(got, exp), f"{what}: {np.count_nonzero(got != exp)} of {got.size} differ"
 
 
+# head_dim 128, 32 / 8 heads: 1024 prompt rows per sequence make 16 query
+# tiles x 8 KV heads, enough for the one-pass prefill attention per sequence
+FLASH = LlamaConfig(n_layers=1, hidden=4096, n_heads=32, n_kv_heads=8, head_dim=128, ffn=1024, vocab=1000)
+
+
+def test_llama_forward_one_attention_launch_for_the_batch(device):
+    """Two sequences of 1024 prompt rows: fh_llama_forward runs the one-pass
+    attention once for both (its blocks are those of one launch per
+    sequence, longest query tiles first), and the logits, hidden states and
+    next ids are bit-identical to the forward issued op by op (fh_attention
+    per sequence)."""
+    batch, t, c = 2, 1024, FLASH
+    model = Q4Llama(device, c, 6, t, max_tokens=t, batch=batch)
+    b = model.buf
+    model._upload(b["ids"], np.ascontiguousarray(synth.token_ids(12, batch * t, c.vocab), dtype=np.uint32))
+    model._upload(b["positions"], np.tile(np.arange(t, dtype=np.uint32), batch))
+
+    def state():
+        return (down(device, b["logits"], np.uint16, batch * c.vocab),
+                down(device, b["attn"], np.uint16, batch * t * c.n_heads * c.head_dim),
+                down(device, b["next"], np.uint32, batch))
+
+    model._forward(t, b["ids"], b["positions"])
+    native = state()
+    _op_by_op_forward(model, t)
+    ops = state()
+    for got, exp, what in zip(native, ops, ("logits", "attn", "next")):
+        assert np.array_equal(got, exp), f"{what}: {np.count_nonzero(got != exp)} of {got.size} differ"
+    assert np.count_nonzero(native[1]) > native[1].size // 2
+
+
 def test_q4_interleave_layout(device):
     """fh_q4_interleave: dword 2p of a row holds the scales of groups 2p and
     2p + 1 (group 2p in the low half), dword 2p + 1 their biases; shapes it
