@@ -35,9 +35,9 @@ bool launch_attention_flash(hipStream_t stream, uint32_t cus, const uint16_t *q,
                             uint32_t n_kv, uint32_t head_dim, uint32_t max_len, float scale, uint16_t *out,
                             uint32_t batch, uint64_t seq_cache);
 int rope_kv(fh_device *dev, const char *fn, const uint16_t *qkv, const float *part, uint32_t splits,
-            uint64_t part_stride, int64_t tokens, int64_t n_heads, int64_t n_kv, int64_t head_dim,
+            uint64_t part_stride, int64_t seq_tokens, int64_t n_heads, int64_t n_kv, int64_t head_dim,
             const uint16_t *cos_tab, const uint16_t *sin_tab, int64_t table_len, const uint32_t *positions,
-            uint16_t *k_cache, uint16_t *v_cache, int64_t max_len, uint16_t *q_out);
+            uint16_t *k_cache, uint16_t *v_cache, int64_t max_len, uint16_t *q_out, int64_t batch);
 int q4_down_pack(fh_device *dev, const char *fn, const uint16_t *x, int64_t m, int64_t x_ld, const uint32_t *wq,
                  const uint16_t *scales, const uint16_t *biases, const uint32_t *sb, const uint32_t *wt, int64_t n,
                  int64_t k, const uint16_t *res, uint16_t *res_out, const uint16_t *norm_weight, float eps,
@@ -242,27 +242,28 @@ int attention(fh_device *d, const fh_llama_model &m, const fh_llama_layer &L, in
     const int64_t seq_cache = m.n_kv_heads * m.max_len * m.head_dim;  // one sequence's cache, elements
     // where each sequence's call would take the one-pass kernel, the
     // sequences share one launch of it (its blocks are the per-sequence
-    // launches' blocks, longest first across the batch) after every RoPE
+    // launches' blocks, longest first across the batch)
     const bool one_launch =
         m.batch > 1 && m.batch <= 65535 && m.max_len <= 0xFFFFFFFFll &&
         fh::attention_flash_applies(d->compute_units, static_cast<uint32_t>(seq_tokens),
                                     static_cast<uint32_t>(m.n_heads), static_cast<uint32_t>(m.n_kv_heads),
                                     static_cast<uint32_t>(m.head_dim)) &&
         aligned16(m.q) && aligned16(m.attn) && aligned16(L.k_cache) && aligned16(L.v_cache);
-    for (int64_t sq = 0; sq < m.batch; ++sq) {
-        const int64_t r0 = sq * seq_tokens;
-        uint16_t *kc = L.k_cache + sq * seq_cache, *vc = L.v_cache + sq * seq_cache;
-        const float *part = qkv_splits > 1 ? static_cast<const float *>(d->partial_area) + r0 * qkv_n : nullptr;
-        FH_TRY(fh::rope_kv(d, "fh_llama_forward", m.qkv + r0 * qkv_n, part, qkv_splits,
-                           static_cast<uint64_t>(m.batch * seq_tokens * qkv_n), seq_tokens, m.n_heads, m.n_kv_heads,
-                           m.head_dim, m.cos_tab, m.sin_tab, m.max_len, positions + r0, kc, vc, m.max_len,
-                           m.q + r0 * hq));
-        if (!one_launch)
-            FH_TRY(fh_attention(d, m.q + r0 * hq, kc, vc, positions + r0, seq_tokens, m.n_heads, m.n_kv_heads,
-                                m.head_dim, m.max_len, m.scale, m.attn_workspace, m.attn_workspace_bytes,
-                                m.attn + r0 * hq));
+    // the RoPE and cache writes of every sequence in one launch
+    const float *part = qkv_splits > 1 ? static_cast<const float *>(d->partial_area) : nullptr;
+    FH_TRY(fh::rope_kv(d, "fh_llama_forward", m.qkv, part, qkv_splits,
+                       static_cast<uint64_t>(m.batch * seq_tokens * qkv_n), seq_tokens, m.n_heads, m.n_kv_heads,
+                       m.head_dim, m.cos_tab, m.sin_tab, m.max_len, positions, L.k_cache, L.v_cache, m.max_len, m.q,
+                       m.batch));
+    if (!one_launch) {
+        for (int64_t sq = 0; sq < m.batch; ++sq) {
+            const int64_t r0 = sq * seq_tokens;
+            FH_TRY(fh_attention(d, m.q + r0 * hq, L.k_cache + sq * seq_cache, L.v_cache + sq * seq_cache,
+                                positions + r0, seq_tokens, m.n_heads, m.n_kv_heads, m.head_dim, m.max_len, m.scale,
+                                m.attn_workspace, m.attn_workspace_bytes, m.attn + r0 * hq));
+        }
+        return FH_OK;
     }
-    if (!one_launch) return FH_OK;
     const char *fn = "fh_llama_forward";
     const uint64_t rows_bytes = static_cast<uint64_t>(m.batch) * seq_tokens * hq * 2;
     const uint64_t cache_bytes = static_cast<uint64_t>(m.batch) * seq_cache * 2;

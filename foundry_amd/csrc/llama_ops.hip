@@ -142,9 +142,13 @@ __global__ __launch_bounds__(256) void rope_kv_kernel(
     const uint16_t *__restrict__ cos_tab, const uint16_t *__restrict__ sin_tab, uint32_t table_len,
     const uint32_t *__restrict__ positions, uint16_t *__restrict__ k_cache,
     uint16_t *__restrict__ v_cache, uint32_t max_len, uint16_t *__restrict__ q_out,
-    const float *__restrict__ part, uint32_t splits, uint64_t part_stride) {
+    const float *__restrict__ part, uint32_t splits, uint64_t part_stride, uint32_t seq_tokens, uint64_t seq_cache) {
     const uint32_t t = blockIdx.x;
     const uint32_t pos = positions[t];
+    // token t belongs to sequence t / seq_tokens, whose caches start seq_cache
+    // elements after the previous sequence's
+    k_cache += (t / seq_tokens) * seq_cache;
+    v_cache += (t / seq_tokens) * seq_cache;
     // positions are device data the host cannot check: a position outside the
     // cache or the tables writes nothing
     if (pos >= max_len || pos >= table_len) return;
@@ -437,12 +441,14 @@ namespace fh {
 // split over K: `splits` slices [tokens][width] that are part_stride floats
 // apart inside the device's partial area.
 int rope_kv(fh_device *dev, const char *fn, const uint16_t *qkv, const float *part, uint32_t splits,
-            uint64_t part_stride, int64_t tokens, int64_t n_heads, int64_t n_kv, int64_t head_dim,
+            uint64_t part_stride, int64_t seq_tokens, int64_t n_heads, int64_t n_kv, int64_t head_dim,
             const uint16_t *cos_tab, const uint16_t *sin_tab, int64_t table_len, const uint32_t *positions,
-            uint16_t *k_cache, uint16_t *v_cache, int64_t max_len, uint16_t *q_out) {
+            uint16_t *k_cache, uint16_t *v_cache, int64_t max_len, uint16_t *q_out, int64_t batch) {
     if (int rc = check_usable(dev, fn)) return rc;
-    if (int rc = fh_check_dims(fn, {tokens, n_heads, n_kv, head_dim, table_len, max_len})) return rc;
+    if (int rc = fh_check_dims(fn, {seq_tokens, n_heads, n_kv, head_dim, table_len, max_len, batch})) return rc;
+    const int64_t tokens = seq_tokens * batch;  // batch sequences' rows, one after another
     if (tokens == 0) return FH_OK;
+    if (tokens > 0x7FFFFFFFll) return fail(FH_ERR_INDEX_TOO_LARGE, "%s: %lld rows", fn, (long long)tokens);
     if (n_kv == 0 || n_heads % n_kv != 0 || head_dim % 16 != 0 || head_dim == 0)
         return fail(FH_ERR_INVALID_ARGUMENT, "%s: heads %lld/%lld, head_dim %lld", fn,
                     (long long)n_heads, (long long)n_kv, (long long)head_dim);
@@ -463,9 +469,9 @@ int rope_kv(fh_device *dev, const char *fn, const uint16_t *qkv, const float *pa
     if (int rc = check_range(dev, cos_tab, static_cast<uint64_t>(table_len) * head_dim * 2, fn, "cos")) return rc;
     if (int rc = check_range(dev, sin_tab, static_cast<uint64_t>(table_len) * head_dim * 2, fn, "sin")) return rc;
     if (int rc = check_range(dev, positions, static_cast<uint64_t>(tokens) * 4, fn, "positions")) return rc;
-    const uint64_t cache = static_cast<uint64_t>(n_kv) * max_len * head_dim * 2;
-    if (int rc = check_range(dev, k_cache, cache, fn, "k_cache")) return rc;
-    if (int rc = check_range(dev, v_cache, cache, fn, "v_cache")) return rc;
+    const uint64_t seq_cache = static_cast<uint64_t>(n_kv) * max_len * head_dim;  // elements per sequence
+    if (int rc = check_range(dev, k_cache, batch * seq_cache * 2, fn, "k_cache")) return rc;
+    if (int rc = check_range(dev, v_cache, batch * seq_cache * 2, fn, "v_cache")) return rc;
     if (int rc = check_range(dev, q_out, static_cast<uint64_t>(tokens) * n_heads * head_dim * 2, fn, "q_out")) return rc;
     if (int rc = set_current(dev, fn)) return rc;
     return dispatch(dev, fn, [&] {
@@ -473,7 +479,8 @@ int rope_kv(fh_device *dev, const char *fn, const uint16_t *qkv, const float *pa
                            dev->stream, qkv, static_cast<uint32_t>(n_heads),
                            static_cast<uint32_t>(n_kv), static_cast<uint32_t>(head_dim), cos_tab,
                            sin_tab, static_cast<uint32_t>(table_len), positions, k_cache, v_cache,
-                           static_cast<uint32_t>(max_len), q_out, part, splits, part_stride);
+                           static_cast<uint32_t>(max_len), q_out, part, splits, part_stride,
+                           static_cast<uint32_t>(seq_tokens), seq_cache);
     });
 }
 
@@ -485,7 +492,7 @@ extern "C" int fh_rope_kv(fh_device *dev, const uint16_t *qkv, int64_t tokens, i
                           uint16_t *k_cache, uint16_t *v_cache, int64_t max_len,
                           uint16_t *q_out) {
     return fh::rope_kv(dev, "fh_rope_kv", qkv, nullptr, 1u, 0u, tokens, n_heads, n_kv, head_dim, cos_tab, sin_tab,
-                       table_len, positions, k_cache, v_cache, max_len, q_out);
+                       table_len, positions, k_cache, v_cache, max_len, q_out, 1);
 }
 
 extern "C" int fh_silu_mul(fh_device *dev, const uint16_t *gate_up, int64_t rows, int64_t f,
