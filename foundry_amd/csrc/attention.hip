@@ -50,6 +50,7 @@
 // cost is the keys every block pulls through one CU (about 34 GB/s per CU
 // in the matrix-core fragment pattern), so it only pays for short caches.
 #include "decoder_common.hpp"
+#include "q4_gemv_mfma.hpp"
 
 #ifndef FH_PV_CHUNKED_MIN_KEYS
 #define FH_PV_CHUNKED_MIN_KEYS 16384
@@ -914,23 +915,28 @@ __global__ __launch_bounds__(kAttnThreads) void attn_pv_tile_kernel(
 // KV head, row); the 4 wavefronts each add a contiguous quarter of the row's
 // active chunks in order (8 loads issued before their adds), then the
 // quarters are added in order, so the sum is the same every run.
+// With img (img_rows = the launch's rows, 2..8), the block also writes its 64
+// outputs -- one quantisation group of the row, width % 64 == 0 -- into the
+// o projection's staged-x image in mf_pack_kernel's layout (fragments by
+// mf_slot, the group's X = sum of its values), and block (0, 0, 0) the zero
+// slot and X = 0 for rows img_rows..7: the matrix-core GEMV then copies the
+// image instead of staging x itself (q4_gemv_packed), with the same values.
 constexpr int kCombineOuts = 64;
 
 __global__ __launch_bounds__(kAttnThreads) void attn_combine_kernel(
     const uint32_t *__restrict__ positions, uint32_t pos_limit, uint32_t n_heads, uint32_t n_kv, uint32_t width,
     uint32_t max_len, uint32_t chunks, uint32_t chunk_keys, const float *__restrict__ part,
-    uint16_t *__restrict__ out) {
+    uint16_t *__restrict__ out, uint4 *__restrict__ img, uint32_t img_rows) {
     __shared__ float quarter_sum[kAttnWaves][kCombineOuts];
+    __shared__ __align__(16) uint16_t ob[kCombineOuts];
     const uint32_t tid = threadIdx.x, e = tid % kCombineOuts, qw = tid / kCombineOuts;
     const uint32_t i = blockIdx.x * kCombineOuts + e, kvh = blockIdx.y, r = blockIdx.z;
     const uint32_t pos = positions[r];
     uint16_t *orow = out + (static_cast<uint64_t>(r) * n_kv + kvh) * width;  // heads kvh*G.. of row r
-    if (pos >= pos_limit) {
-        if (qw == 0 && i < width) orow[i] = 0;
-        return;
-    }
+    // a position the cache or the tables cannot hold: zero output
+    const bool live = pos < pos_limit;
     const uint32_t ctx = pos < max_len ? pos + 1 : max_len;
-    const uint32_t nc = (ctx + chunk_keys - 1) / chunk_keys;
+    const uint32_t nc = live ? (ctx + chunk_keys - 1) / chunk_keys : 0u;
     const uint32_t per = (nc + kAttnWaves - 1) / kAttnWaves;
     const uint32_t c0 = qw * per, c1 = min(c0 + per, nc);
     const float *pr = part + (static_cast<uint64_t>(r) * n_kv + kvh) * chunks * width + (i < width ? i : 0);
@@ -945,11 +951,29 @@ __global__ __launch_bounds__(kAttnThreads) void attn_combine_kernel(
     }
     quarter_sum[qw][e] = o;
     __syncthreads();
-    if (qw == 0 && i < width) {
+    if (qw == 0) {
         float t = quarter_sum[0][e];
 #pragma unroll
         for (int w = 1; w < kAttnWaves; ++w) t += quarter_sum[w][e];
-        orow[i] = rne(t);
+        const uint16_t ov = live ? rne(t) : uint16_t{0};
+        if (i < width) orow[i] = ov;
+        ob[e] = ov;
+    }
+    if (img == nullptr) return;  // uniform over the launch
+    __syncthreads();
+    const uint32_t k = n_kv * width, ppr = k / 8;  // the o projection's x row
+    float *xs = reinterpret_cast<float *>(img + static_cast<uint64_t>(img_rows) * ppr + 2);
+    if (tid < 8) {  // pieces of the block's group: lanes 0..7, as the GEMV's own staging sums them
+        const uint32_t g = (kvh * width + blockIdx.x * kCombineOuts) / kGroup;
+        const uint4 p = gemv_permute(*reinterpret_cast<const uint4 *>(&ob[8 * tid]));
+        img[mf_slot_rt(img_rows, r, g * 8 + tid)] = p;
+        const float gsum = group_sum<8>(mf_piece_sum(p));
+        if (tid == 0) xs[g * 8 + r] = gsum;
+    }
+    if (blockIdx.x == 0 && blockIdx.y == 0 && blockIdx.z == 0) {
+        if (tid == 0) img[static_cast<uint64_t>(img_rows) * ppr] = make_uint4(0u, 0u, 0u, 0u);  // the zero slot
+        const uint32_t G = k / kGroup;
+        for (uint32_t j = tid; j < (8 - img_rows) * G; j += kAttnThreads) xs[(j % G) * 8 + img_rows + j / G] = 0.f;
     }
 }
 
@@ -1230,6 +1254,8 @@ struct AttnArgs {
     float scale;
     char *ws;
     uint16_t *out;
+    uint4 *img = nullptr;   // decode: the o projection's x image (attn_combine_kernel), or null
+    uint32_t img_rows = 0;  // its rows (the launch's rows)
 };
 
 template <int G, int P>
@@ -1277,7 +1303,7 @@ static void launch_attention(hipStream_t stream, uint32_t rows, const AttnLayout
         if (chunks > 1)
             hipLaunchKernelGGL(attn_combine_kernel, dim3((G * HD + kCombineOuts - 1) / kCombineOuts, x.n_kv, rows),
                                dim3(kAttnThreads), 0, stream, x.positions, x.pos_limit, x.n_heads, x.n_kv,
-                               static_cast<uint32_t>(G * HD), x.max_len, chunks, ck, part, x.out);
+                               static_cast<uint32_t>(G * HD), x.max_len, chunks, ck, part, x.out, nullptr, 0u);
         return;
     }
     if (a.chunks) {
@@ -1289,7 +1315,8 @@ static void launch_attention(hipStream_t stream, uint32_t rows, const AttnLayout
         if (chunks > 1)
             hipLaunchKernelGGL(attn_combine_kernel, dim3((G * HD + kCombineOuts - 1) / kCombineOuts, x.n_kv, rows),
                                dim3(kAttnThreads), 0, stream, x.positions, x.pos_limit, x.n_heads, x.n_kv,
-                               static_cast<uint32_t>(G * HD), x.max_len, chunks, ck, part, x.out);
+                               static_cast<uint32_t>(G * HD), x.max_len, chunks, ck, part, x.out,
+                               ROPE ? x.img : nullptr, ROPE ? x.img_rows : 0u);
         return;
     }
     switch (HD / a.slices / 2) {  // dim pairs per P.V block
@@ -1512,11 +1539,14 @@ namespace {
 
 // fh_decode_attention with its workspace either a caller allocation (checked
 // against the device's allocations) or the device's scratch array.
+// img (the device's pack area, img_rows = batch): also leave the o
+// projection's x image there when the chunked P.V's combine runs (*wrote).
 int decode_attention(const char *fn, fh_device *dev, const uint16_t *qkv, int64_t batch, int64_t n_heads,
                      int64_t n_kv, int64_t head_dim, const uint16_t *cos_tab, const uint16_t *sin_tab,
                      int64_t table_len, const uint32_t *positions, uint16_t *k_cache, uint16_t *v_cache,
                      int64_t max_len, float scale, void *workspace, uint64_t workspace_bytes, bool scratch_ws,
-                     uint16_t *out) {
+                     uint16_t *out, uint4 *img = nullptr, bool *wrote = nullptr) {
+    if (wrote) *wrote = false;
     if (int rc = check_usable(dev, fn)) return rc;
     if (int rc = fh_check_dims(fn, {batch, n_heads, n_kv, head_dim, table_len, max_len})) return rc;
     if (batch == 0) return FH_OK;
@@ -1553,22 +1583,50 @@ int decode_attention(const char *fn, fh_device *dev, const uint16_t *qkv, int64_
     if (int rc = check_range(dev, out, static_cast<uint64_t>(batch) * n_heads * head_dim * 2, fn, "out")) return rc;
     if (int rc = set_current(dev, fn)) return rc;
     const uint32_t limit = static_cast<uint32_t>(max_len < table_len ? max_len : table_len);
-    const AttnArgs x{qkv, cos_tab, sin_tab, positions, limit, k_cache, v_cache, row_stride,
-                     static_cast<uint32_t>(n_heads), static_cast<uint32_t>(n_kv), static_cast<uint32_t>(max_len),
-                     scale, static_cast<char *>(workspace), out};
+    AttnArgs x{qkv, cos_tab, sin_tab, positions, limit, k_cache, v_cache, row_stride,
+               static_cast<uint32_t>(n_heads), static_cast<uint32_t>(n_kv), static_cast<uint32_t>(max_len),
+               scale, static_cast<char *>(workspace), out};
+    // the image holds 2..8 rows of a width the pack area takes, in whole groups
+    const uint64_t img_k = static_cast<uint64_t>(n_heads) * head_dim;
+    if (img && batch >= 2 && batch <= 8 && img_k % kGroup == 0 && img_k <= kMfPackMaxK) {
+        x.img = img;
+        x.img_rows = static_cast<uint32_t>(batch);
+    }
     // short caches: one launch (no workspace use); otherwise scores, then P.V
     const bool short_cache = static_cast<uint64_t>(max_len) <= kDecodeShortMaxLen && head_dim != 256;
     dev->no_alloc = scratch_ws;
+    bool combined = false;
     const int rc = dispatch(dev, fn, [&] {
         if (!short_cache ||
             !launch_decode_short_shape(head_dim, n_heads / n_kv, dev->stream, static_cast<uint32_t>(batch), x))
-            launch_attention_shape<true>(head_dim, n_heads / n_kv, dev->stream, static_cast<uint32_t>(batch), a, x);
+            combined = launch_attention_shape<true>(head_dim, n_heads / n_kv, dev->stream,
+                                                    static_cast<uint32_t>(batch), a, x) &&
+                       a.chunks > 1;
     });
+    if (wrote) *wrote = rc == FH_OK && x.img != nullptr && combined;
     dev->no_alloc = false;
     return rc;
 }
 
 }  // namespace
+
+namespace fh {
+
+// fh_decode_attention for the batched decode step of fh_llama_forward: where
+// the chunked P.V's combine runs (and 2..8 rows), it also leaves the o
+// projection's x image in the device's pack area for q4_gemv_packed;
+// *wrote tells whether it did.
+int decode_attention_with_o_image(fh_device *dev, const uint16_t *qkv, int64_t batch, int64_t n_heads, int64_t n_kv,
+                                  int64_t head_dim, const uint16_t *cos_tab, const uint16_t *sin_tab,
+                                  int64_t table_len, const uint32_t *positions, uint16_t *k_cache,
+                                  uint16_t *v_cache, int64_t max_len, float scale, void *workspace,
+                                  uint64_t workspace_bytes, uint16_t *out, bool *wrote) {
+    return decode_attention("fh_llama_forward", dev, qkv, batch, n_heads, n_kv, head_dim, cos_tab, sin_tab,
+                            table_len, positions, k_cache, v_cache, max_len, scale, workspace, workspace_bytes, false,
+                            out, static_cast<uint4 *>(dev->pack_area), wrote);
+}
+
+}  // namespace fh
 
 extern "C" int fh_decode_attention(fh_device *dev, const uint16_t *qkv, int64_t batch, int64_t n_heads,
                                    int64_t n_kv, int64_t head_dim, const uint16_t *cos_tab,

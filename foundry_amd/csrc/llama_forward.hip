@@ -43,6 +43,13 @@ int q4_down_pack(fh_device *dev, const char *fn, const uint16_t *x, int64_t m, i
                  int64_t k, const uint16_t *res, uint16_t *res_out, const uint16_t *norm_weight, float eps,
                  const uint32_t *next_wq, const uint16_t *next_scales, const uint16_t *next_biases,
                  const uint32_t *next_sb, const uint32_t *next_wt, int64_t next_n, bool *packed);
+bool gemv_packed_applies(int64_t m, const uint32_t *wq, const uint16_t *scales, const uint16_t *biases,
+                         const uint32_t *sb, const uint32_t *wt, int64_t n, int64_t k);
+int decode_attention_with_o_image(fh_device *dev, const uint16_t *qkv, int64_t batch, int64_t n_heads, int64_t n_kv,
+                                  int64_t head_dim, const uint16_t *cos_tab, const uint16_t *sin_tab,
+                                  int64_t table_len, const uint32_t *positions, uint16_t *k_cache,
+                                  uint16_t *v_cache, int64_t max_len, float scale, void *workspace,
+                                  uint64_t workspace_bytes, uint16_t *out, bool *wrote);
 int q4_gemv_packed(fh_device *dev, const char *fn, int64_t m, const uint32_t *wq, const uint16_t *scales,
                    const uint16_t *biases, const uint32_t *sb, const uint32_t *wt, int64_t n, int64_t k, void *y,
                    int y_is_f32);
@@ -231,8 +238,17 @@ int linear_silu(fh_device *d, const fh_llama_model &m, int64_t rows, const fh_q4
 // q,k = rope(q,k); cache k,v; attn = sdpa(q, cache) for every sequence.
 // Above one token per sequence, qkv may be the q/k/v GEMM's split partials
 // (qkv_splits > 1, linear_deferred), which the RoPE then adds itself.
+// One token per sequence with o_image: where the decode attention's combine
+// runs it also leaves the o projection's x image in the pack area, and
+// *o_image tells whether it did.
 int attention(fh_device *d, const fh_llama_model &m, const fh_llama_layer &L, int64_t seq_tokens,
-              const uint32_t *positions, uint32_t qkv_splits) {
+              const uint32_t *positions, uint32_t qkv_splits, bool *o_image = nullptr) {
+    if (o_image) *o_image = false;
+    if (seq_tokens == 1 && o_image)
+        return fh::decode_attention_with_o_image(d, m.qkv, m.batch, m.n_heads, m.n_kv_heads, m.head_dim, m.cos_tab,
+                                                 m.sin_tab, m.max_len, positions, L.k_cache, L.v_cache, m.max_len,
+                                                 m.scale, m.decode_workspace, m.decode_workspace_bytes, m.attn,
+                                                 o_image);
     if (seq_tokens == 1)
         return fh_decode_attention(d, m.qkv, m.batch, m.n_heads, m.n_kv_heads, m.head_dim, m.cos_tab, m.sin_tab,
                                    m.max_len, positions, L.k_cache, L.v_cache, m.max_len, m.scale,
@@ -325,7 +341,13 @@ extern "C" int fh_llama_forward(fh_device *dev, const fh_llama_model *model, int
             FH_TRY(linear_norm(dev, m, pending, h, h_alt, L.input_norm, tokens, L.qkv, m.qkv));
             std::swap(h, h_alt);
         }
-        FH_TRY(attention(dev, m, L, seq_tokens, positions, qkv_splits));
+        // the batched decode step: the o projection can read its x as the
+        // image the attention's combine leaves in the pack area
+        bool o_image = false;
+        const bool want_o_image = fused && seq_tokens == 1 &&
+                                  fh::gemv_packed_applies(tokens, L.o.wq, L.o.scales, L.o.biases, L.o.sb, L.o.wt,
+                                                          L.o.n, L.o.k);
+        FH_TRY(attention(dev, m, L, seq_tokens, positions, qkv_splits, want_o_image ? &o_image : nullptr));
         if (!fused) {
             // o, then h += o and x = rms_norm(h); gate/up and SiLU; down (its
             // output is added by the next RMSNorm)
@@ -337,7 +359,11 @@ extern "C" int fh_llama_forward(fh_device *dev, const fh_llama_model *model, int
             pending = m.o;
             continue;
         }
-        FH_TRY(linear(dev, m.attn, tokens, hq, L.o, m.o));
+        if (o_image)
+            FH_TRY(fh::q4_gemv_packed(dev, fn, tokens, L.o.wq, L.o.scales, L.o.biases, L.o.sb, L.o.wt, L.o.n, L.o.k,
+                                      m.o, 0));
+        else
+            FH_TRY(linear(dev, m.attn, tokens, hq, L.o, m.o));
         {
             // act = silu_mul(rms_norm(o + h) [Wgate; Wup]^T) in one GEMV
             const fh_q4_weight &w = L.gate_up;

@@ -143,6 +143,14 @@ __device__ __forceinline__ uint32_t mf_slot(uint32_t m, uint32_t c) {
     return ((p * 4 + j) * 4 + (w >> 2)) * M + (m ^ mf_swz<M>(j));
 }
 
+// mf_slot for a row count known at run time (1..8), for writers of the
+// image outside the GEMV's templates.
+__device__ __forceinline__ uint32_t mf_slot_rt(uint32_t M, uint32_t m, uint32_t c) {
+    const uint32_t p = c >> 4, w = c & 15, j = w & 3;
+    const uint32_t swz = M == 8 ? 2 * j : M == 4 ? j : M == 2 ? (j >> 1) : 0u;
+    return ((p * 4 + j) * 4 + (w >> 2)) * M + (m ^ swz);
+}
+
 // M: x rows (1..8). CH: group pairs per chunk (1, 2 or 4). ksplit:
 // wavefronts per task (divides 16; k / 64 / ksplit is a multiple of 2 * CH).
 // LAY: operand layouts, a set of the bits below.

@@ -202,6 +202,18 @@ int q4_down_pack(fh_device *dev, const char *fn, const uint16_t *x, int64_t m, i
 
 // The RMSNorm'd GEMV of m rows on the image q4_down_pack left in the pack
 // area (weight [n, k], k the image's row length).
+// Whether q4_gemv_packed takes m rows (2..8) of this weight from an image
+// in the pack area: the matrix-core GEMV with the image prologue applies.
+bool gemv_packed_applies(int64_t m, const uint32_t *wq, const uint16_t *scales, const uint16_t *biases,
+                         const uint32_t *sb, const uint32_t *wt, int64_t n, int64_t k) {
+    if (m < 2 || m > 8 || n <= 0 || k <= 0 || n > 0x7FFFFFFFll || k > kMfPackMaxK) return false;
+    GemvArgs a{nullptr, static_cast<uint32_t>(k), wq, scales, biases, static_cast<uint32_t>(n),
+               static_cast<uint32_t>(k), nullptr, static_cast<uint32_t>(n), 0, kProRmsNorm, kEpiNone, GemvFusion{}};
+    a.sb = sb;
+    a.wt = wt;
+    return mf_eligible(static_cast<uint32_t>(m), a) && mf_rows_per_launch(a.k) >= m;
+}
+
 int q4_gemv_packed(fh_device *dev, const char *fn, int64_t m, const uint32_t *wq, const uint16_t *scales,
                    const uint16_t *biases, const uint32_t *sb, const uint32_t *wt, int64_t n, int64_t k, void *y,
                    int y_is_f32) {

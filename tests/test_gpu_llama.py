@@ -639,6 +639,35 @@ def test_llama_forward_equals_the_op_sequence(device, batch, t):
         assert np.array_equal(got, exp), f"{what}: {np.count_nonzero(got != exp)} of {got.size} differ"
 
 
+@pytest.mark.parametrize("batch", [8, 5])
+def test_llama_forward_decode_step_o_projection_from_the_combine(device, batch):
+    """One token per sequence over a 2048-position cache: the decode
+    attention takes the chunked P.V, whose combine also writes the o
+    projection's staged-x image, and the o GEMV copies it instead of staging
+    x (batch 8 and an odd batch, whose image rows are not swizzled). Logits,
+    hidden states and next ids are bit-identical to the forward issued op by
+    op (fh_decode_attention, then fh_q4_matmul on its output). (At 8 rows or
+    fewer the fused step alternates the hidden state between two buffers, so
+    the attention output stands in for it.)"""
+    model = Q4Llama(device, SPLIT, 7, 2048, max_tokens=1, batch=batch)
+    b, c = model.buf, SPLIT
+    model._upload(b["ids"], np.ascontiguousarray(synth.token_ids(13, batch, c.vocab), dtype=np.uint32))
+    rng = np.random.default_rng(batch)
+    model._upload(b["positions"], rng.integers(0, 2048, size=batch).astype(np.uint32))
+
+    def state():
+        return (down(device, b["logits"], np.uint16, batch * c.vocab),
+                down(device, b["attn"], np.uint16, batch * c.n_heads * c.head_dim),
+                down(device, b["next"], np.uint32, batch))
+
+    model._forward(1, b["ids"], b["positions"])
+    native = state()
+    _op_by_op_forward(model, 1)
+    ops = state()
+    for got, exp, what in zip(native, ops, ("logits", "attn", "next")):
+        assert np.array_equal(got, exp), f"{what}: {np.count_nonzero(got != exp)} of {got.size} differ"
+
+
 # head_dim 128, 32 / 8 heads: 1024 prompt rows per sequence make 16 query
 # tiles x 8 KV heads, enough for the one-pass prefill attention per sequence
 FLASH = LlamaConfig(n_layers=1, hidden=4096, n_heads=32, n_kv_heads=8, head_dim=128, ffn=1024, vocab=1000)
