@@ -15,7 +15,8 @@ on its own with a pair of HIP events on the device's stream (the replays are
 enqueued back to back), and the median replay is reported per launch
 (``median_us_per_launch``).
 
-Secondary lines (same method): the GEMV warm (one weight copy, in the MALL);
+Secondary lines (same method): the GEMV warm (one weight copy, which stays in
+the eight 4 MB L2s);
 the LM-head GEMV (N=128256, K=3072) cold (3 copies, 665 MB) and warm (one);
 the q4 embedding gather at B = 4096, 64 and 1, cold (3 tables, distinct ids)
 and warm (one table, the same ids); the two config-3 prefill GEMMs; the
@@ -31,6 +32,7 @@ sequential-k fp32 accumulation, bf16 RNE) on the config-1 GEMV, on this
 host's cores, for a bounded number of calls.
 
 Single legs, for kernel traces and counters: --gemm-only, --floors-only,
+--lm-head-only, --copy-sweep-only (the GEMV over 1 .. 48 weight copies),
 --decode-only, --batched-only, and --eager-steps N (config 4, or config 5
 with --batched-only: the decode steps launched op by op).
 """
@@ -169,7 +171,7 @@ def timed_graph(dev: HipDevice, enqueue, steps: int, warmup: int, median_replays
 def bench_gemv(dev, n, k, copies, steps, warmup, seed, launches=None):
     """`launches` GEMVs per replay (default one per copy), cycling through
     `copies` distinct weight copies: cold when the copies exceed the 256 MB
-    last-level cache (MALL), warm with one copy."""
+    last-level cache (MALL), warm with one copy (held in the L2s)."""
     w = Weights(dev, n, k, copies, seed)
     x = dev.storage_from_bytes(synth.bf16_normal(seed + 1, (1, k)).tobytes())
     y = dev.empty(2 * n)
@@ -252,6 +254,23 @@ def bench_gemm(dev, m, n, k, steps, warmup, seed):
     return {"m": m, "n": n, "k": k, "us_per_launch": ms * 1e3, "TFLOP_per_s": tflops,
             "frac_bf16_peak": tflops / BF16_PEAK_TFLOPS, "median_us_per_launch": med * 1e3,
             "median_TFLOP_per_s": 2.0 * m * n * k / (med * 1e-3) / 1e12}
+
+
+def bench_copy_sweep(dev, steps, warmup):
+    """Where the warm GEMV's speed comes from: 48 launches per replay cycling
+    through 1 .. 48 weight copies, for the config-1 shape (14.2 MB a copy)
+    and the config-4 gate/up shape (16384 x 3072, 28.3 MB). One or two copies
+    fit the eight 4 MB L2s; 8 copies of the first shape (113 MB) and of the
+    second (227 MB) fit only the 256 MB MALL; 48 and 24 copies fit neither."""
+    out = {}
+    for n, counts in ((8192, (1, 2, 4, 8, 16, 48)), (16384, (1, 2, 4, 8, 16, 24))):
+        for copies in counts:
+            r = bench_gemv(dev, n, 3072, copies, steps, warmup, seed=1, launches=48)
+            out[f"n{n}_copies{copies}"] = {"distinct_weight_MB": r["distinct_weight_bytes"] / 1e6,
+                                           "us_per_launch": r["us_per_launch"],
+                                           "median_us_per_launch": r["median_us_per_launch"]}
+            print(f"[bench] n={n} copies={copies}: median {r['median_us_per_launch']:.2f} us", flush=True)
+    return out
 
 
 def bench_floors(dev, steps, warmup):
@@ -681,6 +700,9 @@ def main() -> int:
                     help="only the launch and read floors; prints their JSON")
     ap.add_argument("--lm-head-only", action="store_true",
                     help="only the LM-head GEMV (128256 x 3072) cold and warm legs; prints their JSON")
+    ap.add_argument("--copy-sweep-only", action="store_true",
+                    help="only the decode GEMV over 1 .. 48 weight copies (L2-, MALL- and HBM-resident "
+                         "weights); prints their JSON")
     ap.add_argument("--eager-steps", type=int, default=0,
                     help="only config 4 (or with --batched-only config 5): the prompt, then this many decode "
                          "steps launched op by op instead of as a graph (for kernel traces: the profiler's "
@@ -700,7 +722,8 @@ def main() -> int:
         dev.close()
         print(json.dumps(d), flush=True)
         return 0
-    if args.decode_only or args.batched_only or args.gemm_only or args.floors_only or args.lm_head_only:
+    if (args.decode_only or args.batched_only or args.gemm_only or args.floors_only or args.lm_head_only
+            or args.copy_sweep_only):
         if args.decode_only:
             d = bench_decode(dev, max(2, args.decode_tokens), args.agreement)
         elif args.batched_only:
@@ -710,6 +733,8 @@ def main() -> int:
                  "gemm_down": bench_gemm(dev, 2048, 3072, 8192, args.steps, args.warmup, seed=9)}
         elif args.lm_head_only:
             d = bench_lm_head(dev, args.steps, args.warmup)
+        elif args.copy_sweep_only:
+            d = bench_copy_sweep(dev, args.steps, args.warmup)
         else:
             d = bench_floors(dev, args.steps, args.warmup)
         dev.close()
