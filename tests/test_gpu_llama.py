@@ -673,17 +673,21 @@ def test_llama_forward_decode_step_o_projection_from_the_combine(device, batch):
 FLASH = LlamaConfig(n_layers=1, hidden=4096, n_heads=32, n_kv_heads=8, head_dim=128, ffn=1024, vocab=1000)
 
 
-def test_llama_forward_one_attention_launch_for_the_batch(device):
+@pytest.mark.parametrize("depth", [0, 384])
+def test_llama_forward_one_attention_launch_for_the_batch(device, depth):
     """Two sequences of 1024 prompt rows: fh_llama_forward runs the one-pass
     attention once for both (its blocks are those of one launch per
     sequence, longest query tiles first), and the logits, hidden states and
     next ids are bit-identical to the forward issued op by op (fh_attention
-    per sequence)."""
+    per sequence). depth: the second sequence's rows sit that many positions
+    further on (its cache below them zero, as allocated), so each sequence's
+    positions and cache are its own in the shared launch."""
     batch, t, c = 2, 1024, FLASH
-    model = Q4Llama(device, c, 6, t, max_tokens=t, batch=batch)
+    model = Q4Llama(device, c, 6, t + depth, max_tokens=t, batch=batch)
     b = model.buf
     model._upload(b["ids"], np.ascontiguousarray(synth.token_ids(12, batch * t, c.vocab), dtype=np.uint32))
-    model._upload(b["positions"], np.tile(np.arange(t, dtype=np.uint32), batch))
+    model._upload(b["positions"], np.concatenate([np.arange(t, dtype=np.uint32),
+                                                  np.arange(depth, depth + t, dtype=np.uint32)]))
 
     def state():
         return (down(device, b["logits"], np.uint16, batch * c.vocab),
