@@ -639,8 +639,8 @@ def test_llama_forward_equals_the_op_sequence(device, batch, t):
         assert np.array_equal(got, exp), f"{what}: {np.count_nonzero(got != exp)} of {got.size} differ"
 
 
-@pytest.mark.parametrize("batch", [8, 5])
-def test_llama_forward_decode_step_o_projection_from_the_combine(device, batch):
+@pytest.mark.parametrize("batch,dead", [(8, False), (5, False), (5, True)])
+def test_llama_forward_decode_step_o_projection_from_the_combine(device, batch, dead):
     """One token per sequence over a 2048-position cache: the decode
     attention takes the chunked P.V, whose combine also writes the o
     projection's staged-x image, and the o GEMV copies it instead of staging
@@ -648,12 +648,17 @@ def test_llama_forward_decode_step_o_projection_from_the_combine(device, batch):
     hidden states and next ids are bit-identical to the forward issued op by
     op (fh_decode_attention, then fh_q4_matmul on its output). (At 8 rows or
     fewer the fused step alternates the hidden state between two buffers, so
-    the attention output stands in for it.)"""
+    the attention output stands in for it.) dead: sequence 0 sits at the
+    cache's length, so its attention output, and its rows of the image, are
+    zero."""
     model = Q4Llama(device, SPLIT, 7, 2048, max_tokens=1, batch=batch)
     b, c = model.buf, SPLIT
     model._upload(b["ids"], np.ascontiguousarray(synth.token_ids(13, batch, c.vocab), dtype=np.uint32))
     rng = np.random.default_rng(batch)
-    model._upload(b["positions"], rng.integers(0, 2048, size=batch).astype(np.uint32))
+    positions = rng.integers(0, 2048, size=batch).astype(np.uint32)
+    if dead:
+        positions[0] = 2048
+    model._upload(b["positions"], positions)
 
     def state():
         return (down(device, b["logits"], np.uint16, batch * c.vocab),
@@ -666,6 +671,8 @@ def test_llama_forward_decode_step_o_projection_from_the_combine(device, batch):
     ops = state()
     for got, exp, what in zip(native, ops, ("logits", "attn", "next")):
         assert np.array_equal(got, exp), f"{what}: {np.count_nonzero(got != exp)} of {got.size} differ"
+    hq = c.n_heads * c.head_dim
+    assert not dead or not native[1][:hq].any()
 
 
 # head_dim 128, 32 / 8 heads: 1024 prompt rows per sequence make 16 query
